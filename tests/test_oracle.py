@@ -1,0 +1,260 @@
+"""CPU tier: pin the oracle against the reference's golden vectors and against
+what the mathematics fixes (brute-force nearest point, round trips, invariants).
+
+Golden vectors: tests/golden/*.npz, written by tests/golden/make_golden.py from
+the reference's own functions (core/e8_quantizer.py, core/entropy_coder.py,
+core/compact_storage.py, core/gpu_ans.py, llm/compressed_kv_cache.py,
+core/pipeline.py).
+"""
+import itertools
+import json
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+G = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def load(name):
+    return np.load(os.path.join(G, name))
+
+
+def _avx512_numpy():
+    try:
+        import numpy._core._multiarray_umath as mu
+        return "AVX512_SKX" in mu.__cpu_features__ and mu.__cpu_features__["AVX512_SKX"]
+    except Exception:
+        return False
+
+
+# ----------------------------------------------------------------- E8 ----
+
+def test_e8_golden():
+    g = load("e8.npz")
+    np.testing.assert_array_equal(O.encode_d8(g["x"]), g["d8"])
+    np.testing.assert_array_equal(O.encode_e8(g["x"]), g["e8"])
+
+
+def test_symbols_golden():
+    g = load("e8.npz")
+    cos, free, c8h = O.e8_to_symbols(g["e8"])
+    np.testing.assert_array_equal(cos, g["coset"])
+    np.testing.assert_array_equal(free, g["free"])
+    np.testing.assert_array_equal(c8h, g["c8h"])
+    np.testing.assert_array_equal(O.symbols_to_e8(cos, free, c8h), g["back"])
+
+
+def test_compute_scale_golden():
+    g = load("e8.npz")
+    mine = [O.compute_scale(s2, b) for s2 in (1.0, 0.37, 12.5, 3e-5) for b in (3, 4, 5)]
+    np.testing.assert_array_equal(np.array(mine), g["scales"])
+
+
+def _e8_shell():
+    """All E8 points with |c|_inf <= 2 near the origin (integer and half-integer cosets)."""
+    pts = []
+    for v in itertools.product(range(-2, 3), repeat=8):
+        if sum(v) % 2 == 0 and sum(abs(t) for t in v) <= 4:
+            pts.append(v)
+    for v in itertools.product((-1.5, -0.5, 0.5, 1.5), repeat=8):
+        if (sum(v) - 4) % 2 == 0:  # sum of (v - 1/2) even
+            pts.append(v)
+    return np.array(pts, dtype=np.float64)
+
+
+def test_e8_brute_force_nearest():
+    """encode_e8 returns a nearest E8 point (distance ties allowed) -- checked
+    against exhaustive search over the lattice points around the origin."""
+    rng = np.random.default_rng(0)
+    shell = _e8_shell()
+    x = (rng.random((400, 8)) - 0.5).astype(np.float32) * 1.6
+    q = O.encode_e8(x).astype(np.float64)
+    d = ((x[:, None, :].astype(np.float64) - shell[None]) ** 2).sum(-1).min(1)
+    dq = ((x.astype(np.float64) - q) ** 2).sum(-1)
+    assert np.all(dq <= d + 1e-6)
+    valid, _ = O.validate_e8(q.astype(np.float32))
+    assert valid.all()
+
+
+def test_d8_brute_force_and_parity():
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal((2000, 8)) * 3).astype(np.float32)
+    r = O.encode_d8(x)
+    assert np.all(np.mod(r.sum(-1), 2) == 0)
+    # nearest D8 point: rounding with one minimal-cost flip
+    rr = np.rint(x)
+    base = ((x - rr) ** 2).sum(-1)
+    odd = (rr.sum(-1) % 2) != 0
+    flip = (1 - 2 * np.abs(x - rr)).min(-1)
+    best = base + np.where(odd, flip, 0)
+    got = ((x - r) ** 2).sum(-1)
+    np.testing.assert_allclose(got, best, rtol=0, atol=1e-5)
+
+
+def test_e8_tie_rules():
+    # exact distance tie between cosets: c1 (integer coset) wins (dist1 <= dist2)
+    x = np.full((1, 8), 0.25, np.float32)
+    q = O.encode_e8(x)
+    assert np.all(q == 0)
+    # rounding is half-to-even
+    x = np.array([[0.5, 1.5, 2.5, -0.5, -1.5, 0, 0, 0]], np.float32)
+    assert O.encode_d8(x)[0, :5].tolist() in ([0, 2, 2, 0, -2], [1, 2, 2, 0, -2], [0, 2, 2, 0, -1])
+
+
+# ------------------------------------------------------ compact storage ----
+
+def test_compact_golden():
+    g = load("compact.npz")
+    for b in (3, 4, 5):
+        np.testing.assert_array_equal(O.pack_e8(g[f"q{b}"], b), g[f"packed{b}"])
+        np.testing.assert_array_equal(O.unpack_e8(g[f"raw{b}"], b), g[f"unpacked{b}"])
+
+
+def test_compact_known_answers_and_rejects():
+    # handcrafted points of core/compact_storage.py:398-414, round trip bit-exact
+    for b in (3, 4, 5):
+        R = 2 ** (b - 1)
+        lo, hi = -R, R - 1
+        cases = [[0] * 8, [1, 1, 0, 0, 0, 0, 0, 0], [-1, 1, 0, 0, 0, 0, 0, 0], [1, 0, 0, 0, 0, 0, 0, 1],
+                 [hi, hi - 2, 0, 0, 0, 0, 0, 0], [lo, lo, 0, 0, 0, 0, 0, 0], [0.5] * 8, [-0.5] * 8,
+                 [1.5, -0.5, 0.5, 0.5, 0.5, 0.5, 0.5, 0.5]]
+        q = np.array([c for c in cases if O.check_representable(np.array([c], np.float32), b)[0]], np.float32)
+        np.testing.assert_array_equal(O.unpack_e8(O.pack_e8(q, b), b), q)
+    # strict rejection (core/compact_storage.py:472-478)
+    for bad in ([1.0, 0, 0, 0, 0, 0, 0, 0], [1.0, 0.5, 0, 0, 0, 0, 0, 0], [13.0, -13.0, 0, 0, 0, 0, 0, 0],
+                [8.0, 8.0, 0, 0, 0, 0, 0, 0], [-9.0, -9.0, 0, 0, 0, 0, 0, 0]):
+        with pytest.raises(ValueError):
+            O.pack_e8(np.array([bad], np.float32), 4)
+
+
+# -------------------------------------------------------------- argsort ----
+
+@pytest.mark.skipif(not _avx512_numpy(), reason="tie order restated for numpy's AVX512 argsort")
+def test_argsort_matches_numpy_exhaustive_small():
+    for n in range(1, 9):
+        for vals in itertools.product((0, 1, 2), repeat=n):
+            a = np.array(vals, dtype=np.int64)
+            np.testing.assert_array_equal(O.argsort(a, np.iinfo(np.int64).max), np.argsort(a))
+
+
+@pytest.mark.skipif(not _avx512_numpy(), reason="tie order restated for numpy's AVX512 argsort")
+def test_argsort_matches_numpy_random():
+    rng = np.random.default_rng(2)
+    for n in list(range(9, 80)) + [100, 127, 128, 129, 200, 255, 256]:
+        for _ in range(40):
+            a = -rng.integers(0, int(rng.integers(2, 9)), size=n)
+            np.testing.assert_array_equal(O.argsort(a.astype(np.int64), np.iinfo(np.int64).max),
+                                          np.argsort(a.astype(np.int64)))
+            np.testing.assert_array_equal(O.argsort(a.astype(np.int64), np.iinfo(np.int32).max),
+                                          np.argsort(a.astype(np.int32)))
+
+
+# ----------------------------------------------------------------- rANS ----
+
+def _ragged(g, key, i):
+    off = g[key + "_off"]
+    return g[key][off[i]:off[i + 1]]
+
+
+def test_build_table_golden():
+    g = load("rans.npz")
+    n = len(g["tab_lo"])
+    for i in range(n):
+        counts = _ragged(g, "tab_counts", i)
+        freqs = g["tab_freqs"][g["tab_counts_off"][i]:g["tab_counts_off"][i + 1]]
+        lo = int(g["tab_lo"][i])
+        t = O.build_rans_table(counts, list(range(lo, lo + len(counts))))
+        np.testing.assert_array_equal(t.freqs, freqs, err_msg=f"table case {i}")
+        np.testing.assert_array_equal(t.lookup, g["tab_lookup"][i])
+        assert t.freqs.sum() == O.L and (t.freqs >= 1).all()
+
+
+def test_rans_encode_golden():
+    g = load("rans.npz")
+    for i in range(len(g["enc_lo"])):
+        syms = _ragged(g, "enc_syms", i)
+        counts = _ragged(g, "enc_counts", i)
+        words = _ragged(g, "enc_words", i)
+        lo = int(g["enc_lo"][i])
+        t = O.build_rans_table(counts, list(range(lo, lo + len(counts))))
+        w, st, nb = O.rans_encode(syms, t)
+        np.testing.assert_array_equal(w, words, err_msg=f"stream {i}")
+        assert st == g["enc_state"][i] and nb == g["enc_nbits"][i]
+        np.testing.assert_array_equal(O.rans_decode(w, nb, st, t, len(syms)), syms)
+
+
+def test_rans_roundtrip_reference_distributions():
+    """core/gpu_ans.py:382-424 distributions, decode(encode(s)) == s."""
+    rng = np.random.default_rng(42)
+    cases = [(list(range(-5, 6)), [1, 3, 10, 30, 50, 60, 50, 30, 10, 3, 1]),
+             (list(range(5)), [500, 10, 3, 2, 1]), (list(range(8)), [13, 12, 13, 12, 13, 12, 13, 12]),
+             ([0, 1], [70, 30]), (list(range(-3, 4)), [1, 1, 1, 200, 1, 1, 1])]
+    for alph, counts in cases:
+        counts = np.array(counts, np.int64)
+        t = O.build_rans_table(counts, alph)
+        s = rng.choice(alph, size=2000, p=counts / counts.sum())
+        w, st, nb = O.rans_encode(s, t)
+        assert 1024 <= st < 2048
+        np.testing.assert_array_equal(O.rans_decode(w, nb, st, t, len(s)), s)
+
+
+def test_rans_empty_and_out_of_alphabet():
+    t = O.build_rans_table(np.array([3, 5, 2], np.int64), [0, 1, 2])
+    w, st, nb = O.rans_encode(np.zeros(0, np.int64), t)
+    assert st == 1024 and nb == 0 and w.tolist() == [0]
+    # symbols outside the alphabet encode as their nearest entry (core/gpu_ans.py:116-119)
+    w, st, nb = O.rans_encode(np.array([-7, 9, 1]), t)
+    np.testing.assert_array_equal(O.rans_decode(w, nb, st, t, 3), [0, 2, 1])
+
+
+def test_table_alphabet_limit():
+    with pytest.raises(ValueError):
+        O.build_rans_table(np.ones(1025, np.int64), list(range(1025)))
+
+
+# ---------------------------------------------------------------- chunk ----
+
+def test_compress_chunk_golden():
+    g = load("cache.npz")
+    for ci in range(int(g["n_cases"])):
+        p = f"c{ci}_"
+        t = g[p + "input"]
+        bits = int(g[p + "bits"])
+        # the scale the reference stored, recomputed in fp32 from its fp16 copy is not enough
+        # for bit-exactness: derive sigma2 the way the oracle does and compare at tolerance,
+        # then run the codec with the oracle's scale and compare everything downstream.
+        ch = O.compress_chunk(t, bits)
+        np.testing.assert_array_equal(ch.scales, g[p + "scales"])
+        np.testing.assert_array_equal(ch.decompressed, g[p + "decompressed"])
+        np.testing.assert_array_equal(ch.coset_packed, g[p + "coset_packed"])
+        assert ch.coset_counts == tuple(g[p + "coset_counts"])
+        np.testing.assert_array_equal(ch.bitstream, g[p + "bitstream"])
+        np.testing.assert_array_equal(np.array(ch.word_offsets), g[p + "word_offsets"])
+        meta = np.array([(s.coset, s.idx, s.n_symbols) for s in ch.streams]).reshape(-1, 3)
+        np.testing.assert_array_equal(meta, g[p + "stream_meta"])
+        np.testing.assert_array_equal([s.state for s in ch.streams], g[p + "states"])
+        np.testing.assert_array_equal([s.n_bits for s in ch.streams], g[p + "nbits"])
+        assert ch.compressed_bytes == int(g[p + "compressed_bytes"])
+        np.testing.assert_array_equal(O.decompress_chunk(ch), g[p + "rebuilt"])
+
+
+# ------------------------------------------------------------------ RHT ----
+
+def test_rht_golden():
+    g = load("rht.npz")
+    for s, sg in zip(g["seeds"], g["signs"]):
+        np.testing.assert_array_equal(O.rht_signs(128, int(s)), sg)
+    y = O.fwht(g["x"] * O.rht_signs(128, 7))
+    np.testing.assert_allclose(y, g["y"], rtol=0, atol=2e-6)
+    # self-inverse and orthogonal
+    x = g["x"].astype(np.float64)
+    np.testing.assert_allclose(O.fwht(O.fwht(x)), x, atol=1e-12)
+    np.testing.assert_allclose((O.fwht(x) ** 2).sum(-1), (x ** 2).sum(-1), rtol=1e-12)
+
+
+def test_golden_meta():
+    m = json.load(open(os.path.join(G, "meta.json")))
+    assert m["cpu_capability"] and m["numpy"]
