@@ -1,0 +1,195 @@
+/*
+ * latticequant_amd.h -- C ABI of the MI355X (gfx950) E8 + rANS compressed-KV path.
+ *
+ * Conventions
+ *   - Every pointer argument named d_* is device memory; h_* is host memory.
+ *   - Every entry point is stream-ordered on the hipStream_t it receives and
+ *     returns an int status (LQ_OK = 0, negative = error, see lq_status_string).
+ *   - Nothing here allocates device memory: outputs and workspaces are passed
+ *     in by the caller, sized with the *_workspace_size helpers.
+ *   - Nothing here synchronises the stream except the functions that say so.
+ *   - Geometry of a "chunk" follows CompressedKVCache._compress_tensor
+ *     (reference llm/compressed_kv_cache.py:176-287): a (B, H, T, hd) tensor is
+ *     n_heads = B*H heads of bph = T*hd/8 contiguous 8-dim vectors.  A batch of
+ *     chunks with identical geometry is processed per call; chunk c's input
+ *     vectors start at c * n_heads * bph.
+ *   - Checkpoint blocks: the stream (coset c, coordinate i) of a chunk is the
+ *     reference's rANS stream; its symbols are additionally grouped by vector
+ *     block of LQ_BLK vectors so that encode and decode run one block per lane.
+ *     The bitstream words themselves are the reference's, bit for bit.
+ */
+#ifndef LATTICEQUANT_AMD_H
+#define LATTICEQUANT_AMD_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LQ_L 1024          /* rANS precision (reference core/gpu_ans.py:44-45) */
+#define LQ_BLK 512         /* vectors per checkpoint block */
+#define LQ_MAXSYM 264      /* alphabet capacity of a chunk table (int8 symbols + 4 guard entries) */
+#define LQ_STREAMS 16      /* 2 cosets x 8 coordinate streams per chunk */
+
+/* status codes */
+#define LQ_OK 0
+#define LQ_ERR_ARG -1
+#define LQ_ERR_LAUNCH -2
+#define LQ_ERR_ALPHABET -3     /* alphabet > L=1024: the reference never terminates */
+#define LQ_ERR_RANGE -4        /* lattice symbol outside int8 */
+
+/* per-chunk status bits written by the device */
+#define LQ_ST_SYM_OVERFLOW 1   /* a lattice symbol did not fit int8 */
+#define LQ_ST_ALPHABET 2       /* a stream alphabet exceeded L */
+#define LQ_ST_TIE_UNPINNED 4   /* table of > 256 symbols hit an argsort tie at a cut */
+
+/* dtype codes for activations */
+#define LQ_F16 0
+#define LQ_BF16 1
+#define LQ_F32 2
+
+/* Device table of one rANS stream (chunk tables and generic tables).
+ * enc[s] = freq | cum << 11 | nb << 21 where nb = 11 - bitlen(freq). */
+typedef struct {
+    int32_t lo;          /* alphabet[0]; the alphabet is lo .. lo + n_sym - 1 */
+    int32_t n_sym;       /* 0 when the stream is absent (its coset is empty) */
+    int32_t n_symbols;   /* number of symbols in the stream */
+    int32_t status;
+    uint32_t enc[LQ_MAXSYM];
+} lq_table;
+
+int lq_version(void);
+const char *lq_status_string(int code);
+/* HIP runtime version this library is running against (hipRuntimeGetVersion). */
+int lq_hip_runtime_version(void);
+
+/* ---------------------------------------------------------------- E8 ---- */
+
+/* encode_e8 / encode_d8 on fp32 (n, 8).  mode 0: E8, 1: D8.
+ * Replaces core/e8_quantizer.py:20-83 (encode_d8, encode_e8). */
+int lq_e8_encode_f32(const float *d_x, int64_t n, int mode, float *d_out, hipStream_t s);
+
+/* e8_to_symbols on fp32 E8 points: coset (n) and 8 int32 symbols per vector
+ * (7 free coordinates + floor(c7/2)).  Replaces core/entropy_coder.py:46-68. */
+int lq_e8_to_symbols(const float *d_q, int64_t n, int32_t *d_coset, int32_t *d_sym8, hipStream_t s);
+
+/* symbols_to_e8.  Replaces core/entropy_coder.py:71-89. */
+int lq_symbols_to_e8(const int32_t *d_coset, const int32_t *d_sym8, int64_t n, float *d_q, hipStream_t s);
+
+/* Per-head sigma^2 = mean(x^2), fp32 scale sqrt(2*pi*e*sigma^2*4^-b) (1 if
+ * sigma^2 < 1e-12) and its fp16 copy; bits per chunk.  Also the per-head
+ * fast-division flag consumed by lq_chunk_quantize.  d_work: 2*n_heads_total doubles.
+ * Replaces llm/compressed_kv_cache.py:188-196. */
+int lq_head_scales(const void *d_x, int dtype, int64_t n_chunks, int64_t n_heads, int64_t bph,
+                   const int32_t *d_chunk_bits, double *d_work, float *d_sigma2, float *d_scale32,
+                   uint16_t *d_scale16, int32_t *d_fastdiv, hipStream_t s);
+
+/* Fast-division flags for caller-supplied fp32 scales (exhaustive check of all
+ * 2048 fp16 significands per head).  Same d_fastdiv layout as above. */
+int lq_scale_fastdiv(const float *d_scale32, int64_t n_heads_total, int dtype, int32_t *d_fastdiv,
+                     hipStream_t s);
+
+/* Quantize a batch of chunks: x / scale -> E8 nearest point -> symbols.
+ * Writes, per chunk: int8 symbols grouped per LQ_BLK block as coset-0 columns
+ * then coset-1 columns (d_sym, n_chunks * nblk * LQ_BLK * 8 bytes), the coset
+ * bitmap in the reference's LSB-first byte order (d_coset_bits,
+ * n_chunks * nblk * LQ_BLK / 8 bytes), the coset-1 count per block (d_blk_n1),
+ * the 16 x 256 symbol histograms (d_hist, must be zero on entry) and status
+ * bits.  d_deq (nullable) receives q * scale32 in deq_dtype, the value
+ * update() returns.  Replaces llm/compressed_kv_cache.py:199-231,270. */
+int lq_chunk_quantize(const void *d_x, int dtype, int64_t n_chunks, int64_t n_heads, int64_t bph,
+                      const float *d_scale32, const int32_t *d_fastdiv, int8_t *d_sym,
+                      uint8_t *d_coset_bits, uint32_t *d_blk_n1, uint32_t *d_hist, int32_t *d_status,
+                      void *d_deq, int deq_dtype, hipStream_t s);
+
+/* ------------------------------------------------------------------ rANS -- */
+
+/* Chunk tables from the histograms: alphabet range(min-2, max+2) and
+ * build_rans_table normalisation with numpy's argsort tie order.
+ * Replaces llm/compressed_kv_cache.py:242-250 + core/gpu_ans.py:62-98. */
+int lq_chunk_tables(const uint32_t *d_hist, int64_t n_chunks, lq_table *d_tables, int32_t *d_status,
+                    hipStream_t s);
+
+/* Workspace of the chunk encoder, in bytes. */
+int64_t lq_chunk_encode_workspace(int64_t n_chunks, int64_t n_vectors);
+
+/* Encode every stream of a batch of chunks (one lane per block and stream).
+ * Outputs per (chunk, stream, block): bit offset in the stream (d_blk_off) and
+ * decoder checkpoint state (d_blk_state); per (chunk, stream): n_bits,
+ * final state and word offset inside the chunk bitstream; per chunk: total
+ * words (d_chunk_words).  Words are written by lq_chunk_pack.
+ * Replaces llm/compressed_kv_cache.py:236-263 + core/gpu_ans.py:105-139. */
+int lq_chunk_encode(const int8_t *d_sym, const uint32_t *d_blk_n1, int64_t n_chunks, int64_t n_vectors,
+                    const lq_table *d_tables, void *d_work, uint32_t *d_blk_off, uint16_t *d_blk_state,
+                    int64_t *d_stream_nbits, int32_t *d_stream_state, int64_t *d_stream_woff,
+                    int64_t *d_chunk_words, hipStream_t s);
+
+/* Write the merged bitstreams: chunk c's words start at d_words + d_chunk_base[c]
+ * (caller-chosen, e.g. an exclusive prefix of d_chunk_words).  Each stream is
+ * the reference's layout: LSB-first bits, n_words + 1 words, last word zero. */
+int lq_chunk_pack(int64_t n_chunks, int64_t n_vectors, const lq_table *d_tables, const void *d_work,
+                  const uint32_t *d_blk_off, const int64_t *d_stream_nbits, const int64_t *d_stream_woff,
+                  const int64_t *d_chunk_base, uint32_t *d_words, hipStream_t s);
+
+/* Decode + dequantize a batch of chunks to (B, H, T, hd) in out_dtype:
+ * fp16(q * float(scale16[head])).  d_lut_work: n_chunks * 16 * 1024 uint16.
+ * Replaces llm/compressed_kv_cache.py:289-332 (_decompress_chunk). */
+int lq_chunk_decode(const uint32_t *d_words, const int64_t *d_chunk_base, const int64_t *d_stream_woff,
+                    const uint32_t *d_blk_off, const uint16_t *d_blk_state, const uint8_t *d_coset_bits,
+                    const uint32_t *d_blk_n1, const lq_table *d_tables, const uint16_t *d_scale16,
+                    int64_t n_chunks, int64_t n_heads, int64_t bph, uint16_t *d_lut_work, void *d_out,
+                    int out_dtype, hipStream_t s);
+
+/* Generic tables (build_rans_table API): n_tables histograms of n_sym[t] <= 1024
+ * counts at d_counts + d_count_off[t].  Outputs freqs / cumfreqs (n_sym+1) at the
+ * same offsets (+t for cum), lookup (1024 per table) and status per table.
+ * Replaces core/gpu_ans.py:62-98. */
+int lq_build_tables(const int64_t *d_counts, const int64_t *d_count_off, const int32_t *d_n_sym,
+                    int32_t n_tables, int32_t *d_freqs, int32_t *d_cum, int32_t *d_lookup, int32_t *d_status,
+                    hipStream_t s);
+
+/* Serial rANS encode of n_streams streams of symbol indices (one lane each).
+ * Stream t: d_idx + d_sym_off[t], length d_n[t], table freqs/cum at
+ * d_tab_off[t].  Words go to d_words + d_word_off[t] (capacity
+ * 10*n/32 + 2 words each); state and n_bits per stream.
+ * d_scratch: same total capacity as d_words.  Replaces core/gpu_ans.py:105-139. */
+int lq_rans_encode_streams(const int32_t *d_idx, const int64_t *d_sym_off, const int64_t *d_n,
+                           const int32_t *d_freqs, const int32_t *d_cum, const int64_t *d_tab_off,
+                           int32_t n_streams, uint32_t *d_scratch, uint32_t *d_words, const int64_t *d_word_off,
+                           int64_t *d_state, int64_t *d_nbits, hipStream_t s);
+
+/* One lane per stream decode with the reference's bit-position guard; writes
+ * int64 symbol values.  Replaces _rans_decode_kernel (core/gpu_ans.py:175-235). */
+int lq_rans_decode_streams(const int32_t *d_bits, const int32_t *d_bit_off, const int32_t *d_nbits,
+                           const int32_t *d_init, const int32_t *d_ndec, const int32_t *d_lookup,
+                           const int32_t *d_freqs, const int32_t *d_cum, const int32_t *d_alphabet,
+                           const int32_t *d_tid, int32_t max_sym, const int32_t *d_out_off, int32_t n_streams,
+                           int64_t *d_out, hipStream_t s);
+
+/* -------------------------------------------------------- compact form --- */
+
+/* Fixed-rate unpack + dequant, b in {3,4,5}: out = fp16((coord + 0.5*coset) * scale[head_idx]).
+ * Replaces _unpack_e8_4bit_kernel (core/triton_dequant.py:45-132). */
+int lq_unpack_compact(const uint8_t *d_packed, int bits, int64_t n, const float *d_scales,
+                      const int32_t *d_head_idx, uint16_t *d_out, hipStream_t s);
+
+/* Fixed-rate pack of in-range E8 points, b in {3,4,5} (core/compact_storage.py:87-154).
+ * d_ok (n) receives 1 for a valid in-range point; invalid points are written as zero bytes. */
+int lq_pack_compact(const float *d_q, int bits, int64_t n, uint8_t *d_packed, int32_t *d_ok, hipStream_t s);
+
+/* Single-pass repr/fallback merge: block i is decoded from packed[rank_repr(i)]
+ * when mask[i] != 0 else copied from fallback[rank_fb(i)]; ranks are computed
+ * in-kernel.  head = i / bph.  Replaces _fused_merge_4bit_vec_kernel
+ * (llm/fused_triton_merge.py:33-130), with unpack_e8's floor-mod parity.
+ * d_work: lq_merge_workspace(total) bytes. */
+int64_t lq_merge_workspace(int64_t total_blocks);
+int lq_fused_merge(const uint8_t *d_packed, int bits, const uint16_t *d_fallback, const uint8_t *d_mask,
+                   const float *d_scales, int64_t total_blocks, int64_t bph, void *d_work, uint16_t *d_out,
+                   hipStream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LATTICEQUANT_AMD_H */

@@ -1,0 +1,238 @@
+"""Batched E8 + rANS chunk codec on the GPU (host orchestration of the HIP kernels).
+
+A *chunk* is what one ``CompressedKVCache._compress_tensor`` call produces in
+the reference (llm/compressed_kv_cache.py:176-287): a (B, H, T, hd) tensor is
+split into n_heads = B*H heads of bph = T*hd/8 eight-dim vectors; each head
+gets a per-head scale; vectors are quantized to E8, symbolised (coset bit, 7
+free coordinates, floor(c7/2)) and the 16 coordinate streams (2 cosets x 8)
+are rANS coded with per-stream tables.
+
+This module keeps a batch of equally shaped chunks resident on the device:
+
+  write:  sigma^2/scales -> quantize (+histograms, coset bitmap, int8 symbols)
+          -> tables -> block-parallel encode -> bitstream assembly
+  read:   LUT build -> checkpointed decode fused with dequantisation
+
+Nothing here synchronises with the host unless ``exact_size=True`` (the
+bitstream arena is then allocated at its exact size) or a host view is asked
+for.  All compute runs in the kernels of liblatticequant_amd.so.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Optional
+
+import numpy as np
+import torch
+
+from . import _lib as L
+
+
+def _i(n):
+    return int(n)
+
+
+@dataclass
+class EncodedBatch:
+    """Device-resident compressed form of n_chunks chunks of one geometry."""
+    n_chunks: int
+    n_heads: int
+    bph: int
+    shape: tuple                 # per-chunk (B, H, T, hd)
+    bits: torch.Tensor           # (C,) int32
+    scale32: torch.Tensor        # (C*H,) fp32, the scale the quantizer divided by
+    scale16: torch.Tensor        # (C*H,) fp16, what the chunk stores
+    sigma2: Optional[torch.Tensor]
+    coset_bits: torch.Tensor     # (C, nblk*BLK/8) uint8, reference LSB-first order
+    blk_n1: torch.Tensor         # (C, nblk) int32
+    tables: torch.Tensor         # (C*16, TABLE_BYTES) uint8 (lq_table)
+    blk_off: torch.Tensor        # (C*16*nblk,) int32 (uint32 bit offsets)
+    blk_state: torch.Tensor      # (C*16*nblk,) int16 (uint16 decoder states)
+    stream_nbits: torch.Tensor   # (C*16,) int64
+    stream_state: torch.Tensor   # (C*16,) int32
+    stream_woff: torch.Tensor    # (C*16,) int64 word offset inside the chunk
+    chunk_words: torch.Tensor    # (C,) int64
+    chunk_base: torch.Tensor     # (C,) int64 word offset of each chunk in `words`
+    words: torch.Tensor          # (arena,) int32 merged bitstreams
+    status: torch.Tensor         # (C,) int32 LQ_ST_* bits
+    hist: Optional[torch.Tensor] = None
+    extra: dict = field(default_factory=dict)
+
+    @property
+    def n_vectors(self) -> int:
+        return self.n_heads * self.bph
+
+    @property
+    def nblk(self) -> int:
+        return (self.n_vectors + L.LQ_BLK - 1) // L.LQ_BLK
+
+    # ---- byte accounting -------------------------------------------------
+    def reference_bytes(self) -> torch.Tensor:
+        """Bytes the reference counts per chunk (llm/compressed_kv_cache.py:113-119):
+        int32 bitstream words + packed coset bits + fp16 scales.  (C,) int64 on device."""
+        return self.chunk_words * 4 + (self.n_vectors + 7) // 8 + 2 * self.n_heads
+
+    def side_bytes(self) -> torch.Tensor:
+        """Bytes this format adds per chunk: compact tables (lo, n_sym: 4 B + 2 B per
+        symbol), block checkpoints (4 B offset + 2 B state per stream and block),
+        per-block coset counts (2 B)."""
+        t = self.tables.view(torch.int32).view(-1, L.TABLE_BYTES // 4)
+        nsym = t[:, 1].to(torch.int64).view(self.n_chunks, L.LQ_STREAMS)
+        present = (nsym > 0).to(torch.int64)
+        tab = (4 * present + 2 * nsym).sum(1)
+        ck = 6 * present.sum(1) * self.nblk
+        return tab + ck + 2 * self.nblk
+
+
+def _zeros(n, dtype, dev):
+    return torch.zeros(int(n), dtype=dtype, device=dev)
+
+
+def _empty(n, dtype, dev):
+    return torch.empty(int(n), dtype=dtype, device=dev)
+
+
+def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, deq_out: bool = False,
+                 exact_size: bool = True, words_out: Optional[torch.Tensor] = None):
+    """Compress a batch of chunks.
+
+    x: (C, B, H, T, hd) fp16 / bf16 / fp32 CUDA tensor, hd % 8 == 0.
+    bits: int or (C,) sequence of bits per dimension per chunk (3, 4, 5, ...).
+    scale32: optional (C*B*H,) fp32 scales (otherwise from sigma^2 on the device).
+    deq_out: also return q * scale32 in x's dtype (what update() hands to attention).
+    exact_size: allocate the bitstream arena at its exact size (one host sync);
+      else at a no-sync upper bound (10 bits per symbol).
+    words_out: caller-provided arena (int32) large enough for the upper bound.
+    Returns (EncodedBatch, deq or None)."""
+    lib = L.lib()
+    if x.dim() != 5:
+        raise ValueError("x must be (n_chunks, B, H, T, hd)")
+    if not x.is_cuda:
+        raise ValueError("x must be a CUDA (ROCm) tensor")
+    x = x.contiguous()
+    C, B, H, T, hd = x.shape
+    if hd % 8:
+        raise ValueError("head_dim must be a multiple of 8")
+    dev = x.device
+    nh, bph = B * H, T * hd // 8
+    V = nh * bph
+    nblk = (V + L.LQ_BLK - 1) // L.LQ_BLK
+    dt = L.dtype_code(x.dtype)
+    s = L.stream_ptr(dev)
+    if isinstance(bits, int):
+        bits_t = torch.full((C,), bits, dtype=torch.int32, device=dev)
+    else:
+        bits_t = torch.as_tensor(list(bits), dtype=torch.int32).to(dev)
+    fastdiv = _empty(C * nh, torch.int32, dev)
+    sigma2 = None
+    if scale32 is None:
+        work = _empty(2 * C * nh, torch.float64, dev)
+        sigma2 = _empty(C * nh, torch.float32, dev)
+        scale32 = _empty(C * nh, torch.float32, dev)
+        scale16 = _empty(C * nh, torch.float16, dev)
+        L.check(lib.lq_head_scales(x.data_ptr(), dt, C, nh, bph, bits_t.data_ptr(), work.data_ptr(), sigma2.data_ptr(),
+                                   scale32.data_ptr(), scale16.data_ptr(), fastdiv.data_ptr(), s), "lq_head_scales")
+    else:
+        scale32 = scale32.to(device=dev, dtype=torch.float32).contiguous().view(-1)
+        if scale32.numel() != C * nh:
+            raise ValueError("scale32 must hold one scale per head of every chunk")
+        scale16 = scale32.to(torch.float16)
+        L.check(lib.lq_scale_fastdiv(scale32.data_ptr(), C * nh, dt, fastdiv.data_ptr(), s), "lq_scale_fastdiv")
+    sym = _empty(C * nblk * L.LQ_BLK * 8, torch.int8, dev)
+    coset_bits = _zeros(C * nblk * L.LQ_BLK // 8, torch.uint8, dev)
+    blk_n1 = _empty(C * nblk, torch.int32, dev)
+    hist = _zeros(C * L.LQ_STREAMS * 256, torch.int32, dev)
+    status = _zeros(C, torch.int32, dev)
+    deq = torch.empty_like(x) if deq_out else None
+    L.check(lib.lq_chunk_quantize(x.data_ptr(), dt, C, nh, bph, scale32.data_ptr(), fastdiv.data_ptr(), sym.data_ptr(),
+                                  coset_bits.data_ptr(), blk_n1.data_ptr(), hist.data_ptr(), status.data_ptr(),
+                                  L.ptr(deq), dt, s), "lq_chunk_quantize")
+    tables = _empty(C * L.LQ_STREAMS * L.TABLE_BYTES, torch.uint8, dev)
+    L.check(lib.lq_chunk_tables(hist.data_ptr(), C, tables.data_ptr(), status.data_ptr(), s), "lq_chunk_tables")
+    ws = lib.lq_chunk_encode_workspace(C, V)
+    work = _empty(ws, torch.uint8, dev)
+    ntask = C * L.LQ_STREAMS * nblk
+    blk_off = _empty(ntask, torch.int32, dev)
+    blk_state = _empty(ntask, torch.int16, dev)
+    stream_nbits = _empty(C * L.LQ_STREAMS, torch.int64, dev)
+    stream_state = _empty(C * L.LQ_STREAMS, torch.int32, dev)
+    stream_woff = _empty(C * L.LQ_STREAMS, torch.int64, dev)
+    chunk_words = _empty(C, torch.int64, dev)
+    L.check(lib.lq_chunk_encode(sym.data_ptr(), blk_n1.data_ptr(), C, V, tables.data_ptr(), work.data_ptr(),
+                                blk_off.data_ptr(), blk_state.data_ptr(), stream_nbits.data_ptr(),
+                                stream_state.data_ptr(), stream_woff.data_ptr(), chunk_words.data_ptr(), s),
+            "lq_chunk_encode")
+    chunk_base = torch.cumsum(chunk_words, 0) - chunk_words
+    bound = C * ((10 * 8 * V + 31) // 32 + 2 * L.LQ_STREAMS)
+    if words_out is not None:
+        if words_out.numel() < bound:
+            raise ValueError(f"words_out holds {words_out.numel()} words, needs {bound}")
+        words = words_out
+    elif exact_size:
+        words = _empty(max(1, int(chunk_words.sum().item())), torch.int32, dev)
+    else:
+        words = _empty(bound, torch.int32, dev)
+    L.check(lib.lq_chunk_pack(C, V, tables.data_ptr(), work.data_ptr(), blk_off.data_ptr(), stream_nbits.data_ptr(),
+                              stream_woff.data_ptr(), chunk_base.data_ptr(), words.data_ptr(), s), "lq_chunk_pack")
+    enc = EncodedBatch(n_chunks=C, n_heads=nh, bph=bph, shape=(B, H, T, hd), bits=bits_t, scale32=scale32,
+                       scale16=scale16, sigma2=sigma2, coset_bits=coset_bits.view(C, -1), blk_n1=blk_n1.view(C, -1),
+                       tables=tables, blk_off=blk_off, blk_state=blk_state, stream_nbits=stream_nbits,
+                       stream_state=stream_state, stream_woff=stream_woff, chunk_words=chunk_words,
+                       chunk_base=chunk_base, words=words, status=status, hist=hist)
+    return enc, deq
+
+
+def decode_batch(enc: EncodedBatch, out_dtype: torch.dtype = torch.float16, out: Optional[torch.Tensor] = None,
+                 lut_work: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Decompress every chunk of the batch: (C, B, H, T, hd) in out_dtype,
+    fp16(q * float(scale16[head])) as _decompress_chunk computes it
+    (llm/compressed_kv_cache.py:289-332)."""
+    lib = L.lib()
+    dev = enc.words.device
+    C = enc.n_chunks
+    if out is None:
+        out = torch.empty((C,) + tuple(enc.shape), dtype=out_dtype, device=dev)
+    if lut_work is None:
+        lut_work = _empty(C * L.LQ_STREAMS * L.LQ_L, torch.int16, dev)
+    L.check(lib.lq_chunk_decode(enc.words.data_ptr(), enc.chunk_base.data_ptr(), enc.stream_woff.data_ptr(),
+                                enc.blk_off.data_ptr(), enc.blk_state.data_ptr(), enc.coset_bits.data_ptr(),
+                                enc.blk_n1.data_ptr(), enc.tables.data_ptr(), enc.scale16.data_ptr(), C, enc.n_heads,
+                                enc.bph, lut_work.data_ptr(), out.data_ptr(), L.dtype_code(out.dtype),
+                                L.stream_ptr(dev)), "lq_chunk_decode")
+    return out
+
+
+# ------------------------------------------------------------- host views --
+
+def host_tables(enc: EncodedBatch):
+    """(C*16) list of (lo, n_sym, n_symbols, status, freqs np.int32) read back from the device."""
+    t = enc.tables.view(torch.int32).view(-1, L.TABLE_BYTES // 4).cpu().numpy()
+    out = []
+    for row in t:
+        lo, n_sym, n_symbols, st = (int(v) for v in row[:4])
+        enc_w = row[4:4 + n_sym].view(np.uint32)
+        out.append((lo, n_sym, n_symbols, st, (enc_w & 0x7ff).astype(np.int32)))
+    return out
+
+
+def chunk_streams_host(enc: EncodedBatch, c: int):
+    """Per present stream of chunk c: dict(coset, idx, n, lo, freqs, words, state, n_bits)."""
+    tabs = host_tables(enc)
+    nbits = enc.stream_nbits.cpu().numpy()
+    state = enc.stream_state.cpu().numpy()
+    woff = enc.stream_woff.cpu().numpy()
+    base = int(enc.chunk_base[c].item())
+    nw = int(enc.chunk_words[c].item())
+    words = enc.words[base:base + nw].cpu().numpy().view(np.uint32)
+    res = []
+    for st in range(L.LQ_STREAMS):
+        sid = c * L.LQ_STREAMS + st
+        lo, n_sym, n_symbols, stt, freqs = tabs[sid]
+        if n_sym == 0:
+            continue
+        w0 = int(woff[sid])
+        nb = int(nbits[sid])
+        res.append(dict(coset=st // 8, idx=st % 8, n=n_symbols, lo=lo, freqs=freqs,
+                        words=words[w0:w0 + (nb + 31) // 32 + 1].copy(), state=int(state[sid]), n_bits=nb,
+                        word_offset=w0, status=stt))
+    return res

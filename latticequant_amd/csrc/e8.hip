@@ -1,0 +1,325 @@
+// E8 lattice kernels for gfx950: nearest-point search, symbolisation,
+// per-head scales and the chunk quantizer of the compressed-KV write path.
+#include "lq_device.h"
+
+using namespace lq;
+
+namespace {
+
+// ------------------------------------------------------------ encode API --
+
+__global__ void k_e8_encode(const float* __restrict__ x, int64_t n, int mode, float* __restrict__ out) {
+    int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (v >= n) return;
+    float xv[8], r[8];
+    load8(x, LQ_F32, v, xv);
+    if (mode == 1) {
+        d8_round(xv, r);
+    } else {
+        int cos = e8_nearest(xv, r);
+        float off = cos ? 0.5f : 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) r[i] = r[i] + off;
+    }
+    store8(out, LQ_F32, v, r);
+}
+
+// e8_to_symbols (core/entropy_coder.py:46-68) on arbitrary float points.
+__global__ void k_e8_to_symbols(const float* __restrict__ q, int64_t n, int32_t* __restrict__ coset,
+                                int32_t* __restrict__ sym8) {
+    int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (v >= n) return;
+    float p[8];
+    load8(q, LQ_F32, v, p);
+    int half = fabsf(p[0] - rintf(p[0])) > 0.25f;
+    coset[v] = half;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        float t = half ? p[i] - 0.5f : p[i];
+        int32_t c = (int32_t)rintf(t);
+        sym8[8 * v + i] = i < 7 ? c : (c >> 1);   // floor(c7 / 2)
+    }
+}
+
+// symbols_to_e8 (core/entropy_coder.py:71-89).
+__global__ void k_symbols_to_e8(const int32_t* __restrict__ coset, const int32_t* __restrict__ sym8, int64_t n,
+                                float* __restrict__ q) {
+    int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (v >= n) return;
+    const int32_t* s = sym8 + 8 * v;
+    int32_t sum7 = 0;
+    float o[8];
+    float off = coset[v] == 1 ? 0.5f : 0.f;
+#pragma unroll
+    for (int i = 0; i < 7; i++) { sum7 += s[i]; o[i] = (float)s[i] + off; }
+    o[7] = (float)(2 * s[7] + (sum7 & 1)) + off;
+    store8(q, LQ_F32, v, o);
+}
+
+// ---------------------------------------------------------- head scales --
+
+// Partial sums of x^2 per head in double: grid (heads, parts).
+__global__ void k_head_sumsq(const void* __restrict__ x, int dtype, int64_t vec_per_head, int parts,
+                             double* __restrict__ work) {
+    int64_t h = blockIdx.x;
+    int p = blockIdx.y;
+    int64_t per = (vec_per_head + parts - 1) / parts;
+    int64_t v0 = (int64_t)p * per, v1 = v0 + per < vec_per_head ? v0 + per : vec_per_head;
+    double acc = 0.0;
+    for (int64_t v = v0 + threadIdx.x; v < v1; v += blockDim.x) {
+        float xv[8];
+        load8(x, dtype, h * vec_per_head + v, xv);
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc += (double)xv[i] * (double)xv[i];
+    }
+    __shared__ double red[256];
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int s = blockDim.x / 2; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) work[h * parts + p] = red[0];
+}
+
+// Exhaustive check that the three-op division equals IEEE division for every
+// fp16 significand M in [1, 2047] (every fp16 value is M * 2^E, and both forms
+// are invariant under that power of two).  One block of 256 threads per head.
+__device__ void fastdiv_check(float s, int32_t* flag) {
+    __shared__ int bad;
+    if (threadIdx.x == 0) bad = 0;
+    __syncthreads();
+    float r = 1.0f / s;
+    int mine = 0;
+    for (int m = 1 + threadIdx.x; m < 2048; m += blockDim.x) {
+        float xv = (float)m;
+        float qi = xv / s;
+        float qf = div_scaled(xv, s, r, true);
+        mine |= __float_as_uint(qi) != __float_as_uint(qf);
+    }
+    if (mine) atomicOr(&bad, 1);
+    __syncthreads();
+    if (threadIdx.x == 0) *flag = bad ? 0 : 1;
+}
+
+// sigma^2, scales (llm/compressed_kv_cache.py:189-196) and fast-division flag.
+__global__ void k_head_finalize(const double* __restrict__ work, int parts, int64_t elems_per_head,
+                                int64_t n_heads, const int32_t* __restrict__ chunk_bits, int dtype,
+                                float* __restrict__ sigma2, float* __restrict__ scale32,
+                                uint16_t* __restrict__ scale16, int32_t* __restrict__ fastdiv) {
+    int64_t h = blockIdx.x;
+    __shared__ float sc;
+    if (threadIdx.x == 0) {
+        double acc = 0.0;
+        for (int p = 0; p < parts; p++) acc += work[h * parts + p];
+        float s2 = (float)(acc / (double)elems_per_head);
+        int b = chunk_bits[h / n_heads];
+        float pw = ldexpf(1.0f, -2 * b);                 // 4.0 ** -b, exact
+        float tv = (0x1.114580p+4f * s2) * pw;           // RN32(f32(2*pi*e) * s2) * 4^-b
+        float s = sqrtf(tv);
+        if (s2 < 0x1.197998p-40f) s = 1.0f;              // sigma2 < f32(1e-12)
+        sigma2[h] = s2;
+        scale32[h] = s;
+        scale16[h] = f2h(s);
+        sc = s;
+    }
+    __syncthreads();
+    if (dtype == LQ_F16) {
+        fastdiv_check(sc, fastdiv + h);
+    } else if (threadIdx.x == 0) {
+        fastdiv[h] = 0;
+    }
+}
+
+__global__ void k_scale_fastdiv(const float* __restrict__ scale32, int dtype, int32_t* __restrict__ fastdiv) {
+    int64_t h = blockIdx.x;
+    if (dtype == LQ_F16) {
+        fastdiv_check(scale32[h], fastdiv + h);
+    } else if (threadIdx.x == 0) {
+        fastdiv[h] = 0;
+    }
+}
+
+// -------------------------------------------------------- chunk quantize --
+
+constexpr int kQThreads = 256;
+constexpr int kQBlocksPerWG = 4;
+
+// One workgroup quantizes kQBlocksPerWG consecutive LQ_BLK-vector blocks of one
+// chunk.  Per block it writes the coset bitmap (wave ballots, i.e. the
+// reference's LSB-first pack_coset_bits layout), the coset-1 count and the int8
+// symbols as coset-0 columns followed by coset-1 columns, staged in LDS so the
+// global stores are 16-byte and contiguous.  Histograms accumulate in LDS and
+// are flushed once per workgroup.
+__global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
+    const void* __restrict__ x, int dtype, int64_t n_heads, int64_t bph, int64_t nblk,
+    const float* __restrict__ scale32, const int32_t* __restrict__ fastdiv, int8_t* __restrict__ sym,
+    uint8_t* __restrict__ coset_bits, uint32_t* __restrict__ blk_n1, uint32_t* __restrict__ hist,
+    int32_t* __restrict__ status, void* __restrict__ deq, int deq_dtype) {
+    __shared__ uint32_t shist[LQ_STREAMS * 256];
+    __shared__ __align__(16) int8_t stage[kBlk * 8];
+    __shared__ unsigned long long masks[kBlk / 64];
+    __shared__ int sflag;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int64_t wg_per_chunk = (nblk + kQBlocksPerWG - 1) / kQBlocksPerWG;
+    const int64_t chunk = blockIdx.x / wg_per_chunk;
+    const int64_t b0 = (blockIdx.x % wg_per_chunk) * kQBlocksPerWG;
+    const int64_t V = n_heads * bph;
+
+    for (int i = tid; i < LQ_STREAMS * 256; i += kQThreads) shist[i] = 0;
+    if (tid == 0) sflag = 0;
+    __syncthreads();
+
+    int flag = 0;
+    for (int bi = 0; bi < kQBlocksPerWG; bi++) {
+        const int64_t blk = b0 + bi;
+        if (blk >= nblk) break;
+        const int64_t vbase = blk * kBlk;
+        const int valid = (int)((V - vbase) < kBlk ? (V - vbase) : kBlk);
+        int8_t sy[2][8];
+        int cs[2];
+        // pass 1: quantize two vectors per thread
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int vl = r * kQThreads + tid;
+            cs[r] = 0;
+            if (vl < valid) {
+                const int64_t v = vbase + vl;
+                const int64_t h = chunk * n_heads + v / bph;
+                const float s = scale32[h];
+                const bool fast = fastdiv[h] != 0;
+                const float rs = 1.0f / s;
+                float xv[8], t[8], ic[8];
+                load8(x, dtype, chunk * V + v, xv);
+#pragma unroll
+                for (int i = 0; i < 8; i++) t[i] = div_scaled(xv[i], s, rs, fast);
+                int c = e8_nearest(t, ic);
+                cs[r] = c;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    int32_t iv = (int32_t)ic[i];
+                    int32_t sv = i < 7 ? iv : (iv >> 1);
+                    if (sv < -128 || sv > 127) { flag = 1; sv = sv < -128 ? -128 : 127; }
+                    sy[r][i] = (int8_t)sv;
+                }
+                if (deq) {
+                    float off = c ? 0.5f : 0.f, y[8];
+#pragma unroll
+                    for (int i = 0; i < 8; i++) y[i] = (ic[i] + off) * s;
+                    store8(deq, deq_dtype, chunk * V + v, y);
+                }
+            }
+            unsigned long long m = __ballot(cs[r]);
+            if (lane == 0) masks[r * 4 + wave] = m;
+        }
+        __syncthreads();
+        int n1 = 0;
+#pragma unroll
+        for (int k = 0; k < kBlk / 64; k++) n1 += __popcll(masks[k]);
+        const int n0 = valid - n1;
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int vl = r * kQThreads + tid;
+            if (vl < valid) {
+                const int word = r * 4 + wave;
+                int before = 0;
+                for (int k = 0; k < word; k++) before += __popcll(masks[k]);
+                unsigned long long m = masks[word];
+                int below = __popcll(m & ((1ull << lane) - 1ull));
+                int rank1 = before + below;
+                int rank0 = vl - rank1;
+                const int c = cs[r];
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    int pos = c ? 8 * n0 + i * n1 + rank1 : i * n0 + rank0;
+                    stage[pos] = sy[r][i];
+                    atomicAdd(&shist[(c * 8 + i) * 256 + ((int)sy[r][i] + 128)], 1u);
+                }
+            }
+        }
+        __syncthreads();
+        // copy-out: symbols, coset bitmap, block count
+        {
+            const int64_t gblk = chunk * nblk + blk;
+            const int nbytes = valid * 8;
+            uint4* dst = reinterpret_cast<uint4*>(sym + gblk * (int64_t)kBlk * 8);
+            const uint4* src = reinterpret_cast<const uint4*>(stage);
+            for (int i = tid; i * 16 < nbytes; i += kQThreads) dst[i] = src[i];
+            unsigned long long* cb = reinterpret_cast<unsigned long long*>(coset_bits + gblk * (kBlk / 8));
+            if (tid < kBlk / 64) cb[tid] = masks[tid];
+            if (tid == 0) blk_n1[gblk] = (uint32_t)n1;
+        }
+        __syncthreads();
+    }
+    if (flag) atomicOr(&sflag, 1);
+    __syncthreads();
+    uint32_t* gh = hist + chunk * (LQ_STREAMS * 256);
+    for (int i = tid; i < LQ_STREAMS * 256; i += kQThreads) {
+        uint32_t c = shist[i];
+        if (c) atomicAdd(gh + i, c);
+    }
+    if (tid == 0 && sflag) atomicOr(status + chunk, LQ_ST_SYM_OVERFLOW);
+}
+
+inline int launch_status() { return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_LAUNCH; }
+
+}  // namespace
+
+extern "C" {
+
+int lq_e8_encode_f32(const float* d_x, int64_t n, int mode, float* d_out, hipStream_t s) {
+    if (n < 0 || (mode != 0 && mode != 1)) return LQ_ERR_ARG;
+    if (n == 0) return LQ_OK;
+    hipLaunchKernelGGL(k_e8_encode, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, d_x, n, mode, d_out);
+    return launch_status();
+}
+
+int lq_e8_to_symbols(const float* d_q, int64_t n, int32_t* d_coset, int32_t* d_sym8, hipStream_t s) {
+    if (n < 0) return LQ_ERR_ARG;
+    if (n == 0) return LQ_OK;
+    hipLaunchKernelGGL(k_e8_to_symbols, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, d_q, n, d_coset, d_sym8);
+    return launch_status();
+}
+
+int lq_symbols_to_e8(const int32_t* d_coset, const int32_t* d_sym8, int64_t n, float* d_q, hipStream_t s) {
+    if (n < 0) return LQ_ERR_ARG;
+    if (n == 0) return LQ_OK;
+    hipLaunchKernelGGL(k_symbols_to_e8, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, d_coset, d_sym8, n, d_q);
+    return launch_status();
+}
+
+int lq_head_scales(const void* d_x, int dtype, int64_t n_chunks, int64_t n_heads, int64_t bph,
+                   const int32_t* d_chunk_bits, double* d_work, float* d_sigma2, float* d_scale32,
+                   uint16_t* d_scale16, int32_t* d_fastdiv, hipStream_t s) {
+    if (n_chunks <= 0 || n_heads <= 0 || bph <= 0 || dtype < 0 || dtype > 2) return LQ_ERR_ARG;
+    const int64_t H = n_chunks * n_heads;
+    const int parts = 2;
+    hipLaunchKernelGGL(k_head_sumsq, dim3((unsigned)H, parts), dim3(256), 0, s, d_x, dtype, bph, parts, d_work);
+    hipLaunchKernelGGL(k_head_finalize, dim3((unsigned)H), dim3(256), 0, s, d_work, parts, bph * 8, n_heads,
+                       d_chunk_bits, dtype, d_sigma2, d_scale32, d_scale16, d_fastdiv);
+    return launch_status();
+}
+
+int lq_scale_fastdiv(const float* d_scale32, int64_t n_heads_total, int dtype, int32_t* d_fastdiv, hipStream_t s) {
+    if (n_heads_total <= 0) return LQ_ERR_ARG;
+    hipLaunchKernelGGL(k_scale_fastdiv, dim3((unsigned)n_heads_total), dim3(256), 0, s, d_scale32, dtype, d_fastdiv);
+    return launch_status();
+}
+
+int lq_chunk_quantize(const void* d_x, int dtype, int64_t n_chunks, int64_t n_heads, int64_t bph,
+                      const float* d_scale32, const int32_t* d_fastdiv, int8_t* d_sym, uint8_t* d_coset_bits,
+                      uint32_t* d_blk_n1, uint32_t* d_hist, int32_t* d_status, void* d_deq, int deq_dtype,
+                      hipStream_t s) {
+    if (n_chunks <= 0 || n_heads <= 0 || bph <= 0 || dtype < 0 || dtype > 2) return LQ_ERR_ARG;
+    const int64_t V = n_heads * bph;
+    const int64_t nblk = (V + kBlk - 1) / kBlk;
+    const int64_t wg = n_chunks * ((nblk + kQBlocksPerWG - 1) / kQBlocksPerWG);
+    hipLaunchKernelGGL(k_chunk_quantize, dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x, dtype, n_heads, bph, nblk,
+                       d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, d_hist, d_status, d_deq, deq_dtype);
+    return launch_status();
+}
+
+}  // extern "C"

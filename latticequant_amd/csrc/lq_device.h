@@ -1,0 +1,164 @@
+// Device helpers shared by the LatticeQuant gfx950 kernels.
+//
+// All fp32 arithmetic that decides a lattice point is written so that it
+// rounds exactly where the reference's torch ops round (the library is built
+// with -ffp-contract=off; FMAs appear only where written explicitly).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "latticequant_amd.h"
+
+namespace lq {
+
+constexpr int kL = LQ_L;
+constexpr int kBlk = LQ_BLK;
+constexpr int kCapW = (10 * LQ_BLK + 31) / 32;   // scratch words per (stream, block) task
+
+// torch.arange(8, dtype=f32) * 1e-7  ==  RN32(i * f32(1e-7))   (core/e8_quantizer.py:42-44)
+__device__ __forceinline__ float tiebreak(int i) {
+    constexpr float tb[8] = {0.0f,           0x1.ad7f2ap-24f, 0x1.ad7f2ap-23f, 0x1.421f60p-22f,
+                             0x1.ad7f2ap-22f, 0x1.0c6f7ap-21f, 0x1.421f60p-21f, 0x1.77cf44p-21f};
+    return tb[i];
+}
+
+// ---------------------------------------------------------------- dtypes --
+__device__ __forceinline__ float h2f(uint16_t u) { return __half2float(__ushort_as_half(u)); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
+__device__ __forceinline__ float bf2f(uint16_t u) { return __uint_as_float((uint32_t)u << 16); }
+__device__ __forceinline__ uint16_t f2bf(float f) {   // round to nearest even, quiet NaN
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// Load one 8-dim vector (index v) of an fp16 / bf16 / fp32 array as fp32.
+__device__ __forceinline__ void load8(const void* base, int dtype, int64_t v, float x[8]) {
+    if (dtype == LQ_F32) {
+        const float4* p = reinterpret_cast<const float4*>(base) + 2 * v;
+        float4 a = p[0], b = p[1];
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    } else {
+        uint4 r = reinterpret_cast<const uint4*>(base)[v];
+        uint32_t w[4] = {r.x, r.y, r.z, r.w};
+        for (int i = 0; i < 4; i++) {
+            uint16_t lo = (uint16_t)(w[i] & 0xffffu), hi = (uint16_t)(w[i] >> 16);
+            x[2 * i] = dtype == LQ_F16 ? h2f(lo) : bf2f(lo);
+            x[2 * i + 1] = dtype == LQ_F16 ? h2f(hi) : bf2f(hi);
+        }
+    }
+}
+
+__device__ __forceinline__ void store8(void* base, int dtype, int64_t v, const float y[8]) {
+    if (dtype == LQ_F32) {
+        float4* p = reinterpret_cast<float4*>(base) + 2 * v;
+        p[0] = make_float4(y[0], y[1], y[2], y[3]);
+        p[1] = make_float4(y[4], y[5], y[6], y[7]);
+    } else {
+        uint32_t w[4];
+        for (int i = 0; i < 4; i++) {
+            uint16_t lo = dtype == LQ_F16 ? f2h(y[2 * i]) : f2bf(y[2 * i]);
+            uint16_t hi = dtype == LQ_F16 ? f2h(y[2 * i + 1]) : f2bf(y[2 * i + 1]);
+            w[i] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        reinterpret_cast<uint4*>(base)[v] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+__device__ __forceinline__ uint16_t f2dtype(float f, int dtype) { return dtype == LQ_F16 ? f2h(f) : f2bf(f); }
+
+// ------------------------------------------------------------------- E8 ---
+
+// Nearest D8 point (core/e8_quantizer.py:20-58): round half-even, and when the
+// coordinate sum is odd move the coordinate with the smallest
+// RN(RN(1 - 2|r|) + tiebreak_i) (first index on ties) one step away from x.
+__device__ __forceinline__ void d8_round(const float x[8], float r[8]) {
+    float res[8];
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) { r[i] = rintf(x[i]); s += r[i]; }
+    float best = 0.f;
+    int idx = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        res[i] = x[i] - r[i];
+        float two = 2.0f * fabsf(res[i]);
+        float fc = 1.0f - two;
+        float adj = fc + tiebreak(i);
+        if (i == 0 || adj < best) { best = adj; idx = i; }
+    }
+    if (((int64_t)s) & 1) {
+        float rv = res[0];
+#pragma unroll
+        for (int i = 1; i < 8; i++) rv = (idx == i) ? res[i] : rv;
+        float sg = rv > 0.f ? 1.f : (rv < 0.f ? -1.f : 1.f);
+#pragma unroll
+        for (int i = 0; i < 8; i++) r[i] = (idx == i) ? r[i] + sg : r[i];
+    }
+}
+
+// Nearest E8 point (core/e8_quantizer.py:61-83).  Returns the integer
+// coordinates of the chosen coset representative (c1 itself, or c2 - 1/2) and
+// the coset bit; the squared distances are summed left to right like torch's
+// CPU sum over an 8-wide row.
+__device__ __forceinline__ int e8_nearest(const float x[8], float ic[8]) {
+    float r1[8], r2[8], y[8];
+    d8_round(x, r1);
+#pragma unroll
+    for (int i = 0; i < 8; i++) y[i] = x[i] - 0.5f;
+    d8_round(y, r2);
+    float d1 = 0.f, d2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        float a = x[i] - r1[i];
+        float b = x[i] - (r2[i] + 0.5f);
+        float a2 = a * a, b2 = b * b;
+        d1 = (i == 0) ? a2 : d1 + a2;
+        d2 = (i == 0) ? b2 : d2 + b2;
+    }
+    bool use1 = d1 <= d2;
+#pragma unroll
+    for (int i = 0; i < 8; i++) ic[i] = use1 ? r1[i] : r2[i];
+    return use1 ? 0 : 1;
+}
+
+// x / s rounded to nearest.  The three-op form (q0 = x*r, e = fma(-q0, s, x),
+// q1 = fma(e, r, q0)) is used only for heads whose scale passed the exhaustive
+// check of lq_scale_fastdiv; otherwise IEEE division.
+__device__ __forceinline__ float div_scaled(float x, float s, float r, bool fast) {
+    if (fast) {
+        float q0 = x * r;
+        float e = __builtin_fmaf(-q0, s, x);
+        return __builtin_fmaf(e, r, q0);
+    }
+    return x / s;
+}
+
+// ---------------------------------------------------------------- rANS ---
+
+__device__ __forceinline__ uint32_t enc_pack(uint32_t f, uint32_t cum) {
+    uint32_t bl = 32u - (uint32_t)__clz((int)f);   // bit length of f
+    uint32_t nb = 11u - bl;
+    return f | (cum << 11) | (nb << 21);
+}
+__device__ __forceinline__ uint32_t enc_f(uint32_t e) { return e & 0x7ffu; }
+__device__ __forceinline__ uint32_t enc_c(uint32_t e) { return (e >> 11) & 0x3ffu; }
+__device__ __forceinline__ uint32_t enc_nb(uint32_t e) { return (e >> 21) & 0xfu; }
+
+// One encoder step (core/gpu_ans.py:124-128): k renormalisation bits leave
+// through *k / *bits (low k bits of x), then x = L + cum + (x >> k) - f.
+__device__ __forceinline__ uint32_t enc_step(uint32_t x, uint32_t e, uint32_t* k_out) {
+    uint32_t f = enc_f(e), nb = enc_nb(e);
+    uint32_t thr = f << nb;
+    uint32_t k = nb - 1u + (x >= thr ? 1u : 0u);
+    *k_out = k;
+    return (x >> k) + (uint32_t)kL + enc_c(e) - f;
+}
+
+// Bit-length helper for x in [1, 2^31).
+__device__ __forceinline__ uint32_t bitlen(uint32_t x) { return 32u - (uint32_t)__clz((int)x); }
+
+}  // namespace lq

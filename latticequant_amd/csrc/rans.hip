@@ -1,0 +1,823 @@
+// rANS kernels for gfx950: table construction, block-parallel encode of the
+// reference's bit-wise streams, bitstream assembly and checkpointed decode.
+//
+// Stream format (reference core/gpu_ans.py:105-139): L = 1024, state in
+// [1024, 2048), one renormalisation bit at a time; the encoder runs over the
+// symbols in reverse and the emitted bit list is reversed and packed LSB-first
+// into uint32 words, followed by one zero word.
+//
+// Parallel encode: the state after a symbol depends only on the high bits of
+// the state before it, so encoder trajectories from different starting states
+// merge.  A lane that owns block g tracks the interval [lo, hi] of every state
+// that can enter it, starting from the full range a few symbols earlier (in
+// encode order); once lo == hi the entering state is known exactly, whatever
+// the true history.  If the interval has not collapsed the window grows, up to
+// the end of the stream where the state is exactly L.  Results are therefore
+// exact, and identical to a serial encode.
+#include "lq_device.h"
+
+using namespace lq;
+
+namespace {
+
+inline int launch_status() { return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_LAUNCH; }
+
+// ---------------------------------------------------------------------------
+// numpy.argsort tie order.  numpy's argsort on x86 AVX512 hosts runs
+// x86-simd-sort: for n <= 256, a bitonic network over 8-lane registers padded
+// with the type maximum, in which each comparator leaves equal keys in place.
+// Executed here stage by stage in LDS, one comparator per thread.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ void cmpx(int64_t* k, int16_t* a, int p, int q) {
+    int64_t kp = k[p], kq = k[q];
+    if (kp > kq) {
+        k[p] = kq; k[q] = kp;
+        int16_t t = a[p]; a[p] = a[q]; a[q] = t;
+    }
+}
+
+// first lane of each of the 4 comparators of an in-register stage with partner i ^ m
+__device__ __forceinline__ int pair_lane(int m, int p) {
+    switch (m) {
+        case 1: return 2 * p;                      // 0 2 4 6
+        case 2: case 3: return (p & 1) | ((p >> 1) << 2);   // 0 1 4 5
+        default: return p;                         // m = 4, 7: 0 1 2 3
+    }
+}
+
+__device__ void reg_stage(int64_t* k, int16_t* a, int nv, int m) {
+    for (int t = threadIdx.x; t < nv * 4; t += blockDim.x) {
+        int reg = t >> 2, i = pair_lane(m, t & 3);
+        cmpx(k, a, reg * 8 + i, reg * 8 + (i ^ m));
+    }
+    __syncthreads();
+}
+
+// keys k[0..n) (int64), pad = value larger than every key; result in a[0..n).
+__device__ void net_argsort(int64_t* k, int16_t* a, int n) {
+    int nv = 1;
+    while (nv * 8 < n) nv *= 2;
+    for (int i = threadIdx.x; i < nv * 8; i += blockDim.x) {
+        if (i >= n) k[i] = INT64_MAX;
+        a[i] = (int16_t)(i < n ? i : -1);
+    }
+    __syncthreads();
+    const int s8[6] = {1, 3, 1, 7, 2, 1};
+    for (int st = 0; st < 6; st++) reg_stage(k, a, nv, s8[st]);
+    for (int per = 2; per <= nv; per *= 2) {
+        for (int t = threadIdx.x; t < nv * 4; t += blockDim.x) {   // mirror compare across registers
+            int grp = t / (per * 4), rem = t % (per * 4);
+            int i = rem / 8, l = rem % 8, off = grp * per;
+            cmpx(k, a, 8 * (off + i) + l, 8 * (off + per - 1 - i) + 7 - l);
+        }
+        __syncthreads();
+        for (int num = per / 2; num >= 2; num /= 2) {               // register half cleaners
+            for (int t = threadIdx.x; t < nv * 4; t += blockDim.x) {
+                int grp = t / (per * 4), rem = t % (per * 4);
+                int l = rem % 8, q = rem / 8;
+                int jj = q / (num / 2), i = q % (num / 2);
+                int r1 = grp * per + jj * num + i;
+                cmpx(k, a, 8 * r1 + l, 8 * (r1 + num / 2) + l);
+            }
+            __syncthreads();
+        }
+        reg_stage(k, a, nv, 4);
+        reg_stage(k, a, nv, 2);
+        reg_stage(k, a, nv, 1);
+    }
+}
+
+// Stable order (key, index) for n > 256, where numpy runs a SIMD quicksort
+// whose tie order is not restated; the caller flags ties at a cut.
+__device__ void rank_argsort(const int64_t* k, int16_t* a, int n) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        int64_t ki = k[i];
+        int r = 0;
+        for (int j = 0; j < n; j++) r += (k[j] < ki) || (k[j] == ki && j < i);
+        a[r] = (int16_t)i;
+    }
+    __syncthreads();
+}
+
+// build_rans_table normalisation (core/gpu_ans.py:62-86) on LDS arrays.
+// counts[n] (int64), freqs[n] (int32) out.  Needs k[>=1024], a[>=1024] scratch.
+// Returns status bits (LQ_ST_TIE_UNPINNED) in *st.
+__device__ void normalise(const int64_t* counts, int n, int32_t* freqs, int64_t* k, int16_t* a, int* st) {
+    __shared__ int64_t s_total;
+    __shared__ int s_diff;
+    if (threadIdx.x == 0) {
+        int64_t t = 0;
+        for (int i = 0; i < n; i++) t += counts[i];
+        s_total = t;
+    }
+    __syncthreads();
+    const int64_t total = s_total;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        if (total == 0) {
+            freqs[i] = 1;
+        } else {
+            double f = (double)counts[i] / (double)total * (double)kL;   // (counts / total * L)
+            int32_t t = (int32_t)f;                                       // .astype(int32)
+            freqs[i] = t < 1 ? 1 : t;
+        }
+    }
+    __syncthreads();
+    for (;;) {
+        if (threadIdx.x == 0) {
+            int64_t sum = 0;
+            for (int i = 0; i < n; i++) sum += freqs[i];
+            s_diff = (int)(kL - sum);
+        }
+        __syncthreads();
+        const int diff = s_diff;
+        if (diff == 0) break;
+        for (int i = threadIdx.x; i < n; i += blockDim.x) k[i] = diff > 0 ? -counts[i] : -(int64_t)freqs[i];
+        __syncthreads();
+        if (n <= 256) {
+            net_argsort(k, a, n);
+        } else {
+            rank_argsort(k, a, n);
+        }
+        if (threadIdx.x == 0) {
+            int m = diff > 0 ? diff : -diff;
+            if (n > 256 && (m % n) != 0) {   // a tie across the cut makes numpy's choice matter
+                int c = m % n;
+                if (k[a[c - 1]] == k[a[c]]) *st |= LQ_ST_TIE_UNPINNED;
+            }
+            if (diff > 0) {
+                for (int j = 0; j < m; j++) freqs[a[j % n]] += 1;
+            } else {
+                for (int j = 0; j < m; j++) {
+                    int idx = a[j % n];
+                    if (freqs[idx] > 1) freqs[idx] -= 1;
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------ chunk tables --
+
+__global__ __launch_bounds__(256) void k_chunk_tables(const uint32_t* __restrict__ hist, lq_table* __restrict__ tables,
+                                                      int32_t* __restrict__ status) {
+    __shared__ int64_t counts[LQ_MAXSYM];
+    __shared__ int32_t freqs[LQ_MAXSYM];
+    __shared__ int64_t keys[256];
+    __shared__ int16_t perm[LQ_MAXSYM];
+    __shared__ uint32_t h[256];
+    __shared__ int s_min, s_max, s_st;
+    __shared__ uint32_t s_tot;
+    const int64_t sid = blockIdx.x;   // chunk * 16 + stream
+    const int tid = threadIdx.x;
+    h[tid] = hist[sid * 256 + tid];
+    if (tid == 0) { s_min = 256; s_max = -1; s_tot = 0; s_st = 0; }
+    __syncthreads();
+    if (h[tid]) { atomicMin(&s_min, tid); atomicMax(&s_max, tid); atomicAdd(&s_tot, h[tid]); }
+    __syncthreads();
+    lq_table* T = tables + sid;
+    if (s_max < 0) {
+        if (tid == 0) { T->lo = 0; T->n_sym = 0; T->n_symbols = 0; T->status = 0; }
+        return;
+    }
+    const int lo = s_min - 128 - 2;
+    const int n = s_max - s_min + 5;
+    for (int i = tid; i < n; i += 256) {
+        int b = lo + i + 128;
+        counts[i] = (b >= 0 && b < 256) ? (int64_t)h[b] : 0;
+    }
+    __syncthreads();
+    // n <= 260; arrays for the network hold 256 keys, so n in 257..260 takes the rank path
+    __shared__ int64_t kbig[LQ_MAXSYM];
+    normalise(counts, n, freqs, n <= 256 ? keys : kbig, perm, &s_st);
+    if (tid == 0) {
+        uint32_t cum = 0;
+        for (int i = 0; i < n; i++) {
+            T->enc[i] = enc_pack((uint32_t)freqs[i], cum);
+            cum += (uint32_t)freqs[i];
+        }
+        T->lo = lo;
+        T->n_sym = n;
+        T->n_symbols = (int32_t)s_tot;
+        T->status = s_st;
+        if (s_st) atomicOr(status + sid / LQ_STREAMS, s_st);
+    }
+}
+
+// ------------------------------------------------------------ chunk encode --
+//
+// Task = (chunk, stream st = coset * 8 + coord, block g), one lane each; a
+// 256-thread workgroup holds 16 consecutive blocks x 16 streams of one chunk.
+
+struct Col {
+    const int8_t* p;
+    int n;
+};
+
+__device__ __forceinline__ Col column(const int8_t* sym, const uint32_t* blk_n1, int64_t chunk, int64_t nblk,
+                                      int64_t V, int64_t h, int c, int idx) {
+    uint32_t n1 = blk_n1[chunk * nblk + h];
+    int64_t valid = V - h * kBlk < kBlk ? V - h * kBlk : kBlk;
+    int n0 = (int)valid - (int)n1;
+    const int8_t* base = sym + (chunk * nblk + h) * (int64_t)kBlk * 8;
+    Col col;
+    col.p = c ? base + 8 * n0 + idx * (int)n1 : base + idx * n0;
+    col.n = c ? (int)n1 : n0;
+    return col;
+}
+
+// enc entry of symbol value v (int8) in table of stream st
+__device__ __forceinline__ uint32_t enc_of(const uint32_t* enc, int lo, int v) { return enc[v - lo]; }
+
+// Interval step: every state in [lo, hi] encodes the symbol; the image is
+// exact when the interval lies on one side of the renormalisation threshold,
+// otherwise the whole image range of the symbol.
+__device__ __forceinline__ void hull_step(uint32_t& lo, uint32_t& hi, uint32_t e) {
+    uint32_t f = enc_f(e), nb = enc_nb(e);
+    uint32_t thr = f << nb;
+    uint32_t base = (uint32_t)kL + enc_c(e) - f;
+    if (hi < thr || lo >= thr) {
+        uint32_t k = nb - 1u + (lo >= thr ? 1u : 0u);
+        lo = (lo >> k) + base;
+        hi = (hi >> k) + base;
+    } else {
+        lo = f + base;
+        hi = 2u * f - 1u + base;
+    }
+}
+
+struct EncWork {  // offsets into the encode workspace
+    int64_t bits, scratch, total;
+};
+
+__host__ __device__ inline EncWork enc_layout(int64_t n_chunks, int64_t n_vectors) {
+    int64_t nblk = (n_vectors + kBlk - 1) / kBlk;
+    int64_t tasks = n_chunks * LQ_STREAMS * nblk;
+    EncWork w;
+    w.bits = 0;
+    w.scratch = ((tasks * 4 + 255) / 256) * 256;
+    w.total = w.scratch + tasks * (int64_t)kCapW * 4;
+    return w;
+}
+
+__global__ __launch_bounds__(256) void k_chunk_encode(const int8_t* __restrict__ sym, const uint32_t* __restrict__ blk_n1,
+                                                      int64_t nblk, int64_t V, const lq_table* __restrict__ tables,
+                                                      uint32_t* __restrict__ blk_bits, uint32_t* __restrict__ scratch,
+                                                      uint16_t* __restrict__ blk_state) {
+    __shared__ uint32_t senc[LQ_STREAMS][LQ_MAXSYM];
+    __shared__ int slo[LQ_STREAMS], snsym[LQ_STREAMS];
+    const int tid = threadIdx.x;
+    const int64_t groups = (nblk + 15) / 16;
+    const int64_t chunk = blockIdx.x / groups;
+    const int64_t g = (blockIdx.x % groups) * 16 + (tid >> 4);
+    const int st = tid & 15;
+    const lq_table* T = tables + chunk * LQ_STREAMS;
+    for (int i = tid; i < LQ_STREAMS * LQ_MAXSYM; i += 256) {
+        int s = i / LQ_MAXSYM, j = i % LQ_MAXSYM;
+        senc[s][j] = j < T[s].n_sym ? T[s].enc[j] : 0u;
+    }
+    if (tid < LQ_STREAMS) { slo[tid] = T[tid].lo; snsym[tid] = T[tid].n_sym; }
+    __syncthreads();
+    if (g >= nblk) return;
+    const int64_t task = (chunk * LQ_STREAMS + st) * nblk + g;
+    if (snsym[st] == 0) {  // absent stream (empty coset)
+        blk_bits[task] = 0;
+        blk_state[task] = (uint16_t)kL;
+        return;
+    }
+    const int c = st >> 3, idx = st & 7;
+    const uint32_t* enc = senc[st];
+    const int lo_sym = slo[st];
+
+    // ---- state entering block g (encode order runs from the stream end down)
+    uint32_t x = kL;
+    int window = 24;
+    for (;;) {
+        // top of the window: `window` symbols after block g, or the stream end
+        int64_t h = g + 1;
+        int need = window;
+        while (h < nblk) {
+            int nc = column(sym, blk_n1, chunk, nblk, V, h, c, idx).n;
+            if (need <= nc) break;
+            need -= nc;
+            h++;
+        }
+        bool exact = h >= nblk;
+        uint32_t lo = kL, hi = exact ? (uint32_t)kL : 2u * kL - 1u;
+        int64_t hb = exact ? nblk - 1 : h;
+        int jtop = exact ? -1 : need - 1;
+        for (int64_t b = hb; b > g; b--) {
+            Col col = column(sym, blk_n1, chunk, nblk, V, b, c, idx);
+            int j0 = (b == hb && !exact) ? jtop : col.n - 1;
+            if (lo == hi) {
+                uint32_t xx = lo, k;
+                for (int j = j0; j >= 0; j--) xx = enc_step(xx, enc_of(enc, lo_sym, col.p[j]), &k);
+                lo = hi = xx;
+            } else {
+                for (int j = j0; j >= 0; j--) hull_step(lo, hi, enc_of(enc, lo_sym, col.p[j]));
+            }
+        }
+        if (lo == hi) { x = lo; break; }
+        window *= 8;
+    }
+
+    // ---- encode block g, bits right-aligned in the task's scratch region
+    Col col = column(sym, blk_n1, chunk, nblk, V, g, c, idx);
+    uint32_t* scr = scratch + task * (int64_t)kCapW;
+    int wpos = kCapW - 1;
+    uint64_t acc = 0;
+    uint32_t nacc = 0, total = 0;
+    for (int j = col.n - 1; j >= 0; j--) {
+        uint32_t k;
+        uint32_t e = enc_of(enc, lo_sym, col.p[j]);
+        uint32_t xin = x;
+        x = enc_step(x, e, &k);
+        // emitted group in final stream order is the k low bits of xin, most significant first
+        uint64_t r = ((uint64_t)__builtin_bitreverse32(xin) << k) >> 32;
+        acc = (acc << k) | r;
+        nacc += k;
+        total += k;
+        if (nacc >= 32) {
+            nacc -= 32;
+            scr[wpos--] = (uint32_t)(acc >> nacc);
+        }
+    }
+    if (nacc) scr[wpos] = (uint32_t)(acc << (32 - nacc));
+    blk_bits[task] = total;
+    blk_state[task] = (uint16_t)x;
+}
+
+// per (chunk, stream): exclusive prefix of block bit counts, n_bits, final state
+__global__ __launch_bounds__(256) void k_chunk_scan(const uint32_t* __restrict__ blk_bits, const uint16_t* __restrict__ blk_state,
+                                                    const lq_table* __restrict__ tables, int64_t nblk,
+                                                    uint32_t* __restrict__ blk_off, int64_t* __restrict__ stream_nbits,
+                                                    int32_t* __restrict__ stream_state) {
+    __shared__ uint64_t part[256];
+    const int64_t sid = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int64_t per = (nblk + 255) / 256;
+    const int64_t b0 = tid * per, b1 = b0 + per < nblk ? b0 + per : nblk;
+    const uint32_t* bb = blk_bits + sid * nblk;
+    uint64_t s = 0;
+    for (int64_t b = b0; b < b1; b++) s += bb[b];
+    part[tid] = s;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {   // inclusive Hillis-Steele scan
+        uint64_t v = tid >= off ? part[tid - off] : 0;
+        __syncthreads();
+        part[tid] += v;
+        __syncthreads();
+    }
+    uint64_t run = tid ? part[tid - 1] : 0;
+    for (int64_t b = b0; b < b1; b++) {
+        blk_off[sid * nblk + b] = (uint32_t)run;
+        run += bb[b];
+    }
+    if (tid == 255) {
+        bool present = tables[sid].n_sym > 0;
+        stream_nbits[sid] = present ? (int64_t)part[255] : 0;
+        stream_state[sid] = present ? (int32_t)blk_state[sid * nblk] : 0;
+    }
+}
+
+// per chunk: word offset of each present stream (n_words + 1 words each) and chunk total
+__global__ void k_chunk_offsets(const int64_t* __restrict__ stream_nbits, const lq_table* __restrict__ tables,
+                                int64_t n_chunks, int64_t* __restrict__ stream_woff, int64_t* __restrict__ chunk_words) {
+    int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= n_chunks) return;
+    int64_t w = 0;
+    for (int st = 0; st < LQ_STREAMS; st++) {
+        int64_t sid = c * LQ_STREAMS + st;
+        stream_woff[sid] = w;
+        if (tables[sid].n_sym > 0) w += (stream_nbits[sid] + 31) / 32 + 1;
+    }
+    chunk_words[c] = w;
+}
+
+// One wave per task: assemble the stream words whose first bit falls in block g.
+__global__ __launch_bounds__(256) void k_chunk_pack(int64_t n_tasks, int64_t nblk, const uint32_t* __restrict__ blk_bits,
+                                                    const uint32_t* __restrict__ scratch, const uint32_t* __restrict__ blk_off,
+                                                    const int64_t* __restrict__ stream_nbits,
+                                                    const int64_t* __restrict__ stream_woff,
+                                                    const int64_t* __restrict__ chunk_base, uint32_t* __restrict__ words) {
+    const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (task >= n_tasks) return;
+    const int64_t sid = task / nblk, g = task % nblk, chunk = sid / LQ_STREAMS;
+    const int64_t nbits = stream_nbits[sid];
+    const uint32_t b = blk_bits[task];
+    const int64_t off = blk_off[task];
+    uint32_t* out = words + chunk_base[chunk] + stream_woff[sid];
+    const int64_t w_first = (off + 31) / 32, w_end = (off + b + 31) / 32;
+    for (int64_t w = w_first + lane; w < w_end; w += 64) {
+        int64_t cur = 32 * w;
+        const int64_t end = 32 * w + 32 < nbits ? 32 * w + 32 : nbits;
+        uint32_t res = 0;
+        int64_t h = g;
+        int64_t ho = off;
+        uint32_t hb = b;
+        while (cur < end) {
+            while (cur >= ho + hb) { h++; ho = blk_off[sid * nblk + h]; hb = blk_bits[sid * nblk + h]; }
+            int64_t lim = end < ho + hb ? end : ho + hb;
+            int take = (int)(lim - cur);
+            int64_t sp = (int64_t)kCapW * 32 - hb + (cur - ho);
+            const uint32_t* scr = scratch + (sid * nblk + h) * (int64_t)kCapW;
+            int64_t wi = sp >> 5;
+            int sh = (int)(sp & 31);
+            uint64_t v = scr[wi];
+            if (sh + take > 32) v |= (uint64_t)scr[wi + 1] << 32;
+            v >>= sh;
+            uint32_t bits = take == 32 ? (uint32_t)v : (uint32_t)v & ((1u << take) - 1u);
+            res |= bits << (int)(cur - 32 * w);
+            cur += take;
+        }
+        out[w] = res;
+    }
+}
+
+// trailing zero word of every present stream
+__global__ void k_chunk_tail(int64_t n_streams, const lq_table* __restrict__ tables, const int64_t* __restrict__ stream_nbits,
+                             const int64_t* __restrict__ stream_woff, const int64_t* __restrict__ chunk_base,
+                             uint32_t* __restrict__ words) {
+    int64_t sid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (sid >= n_streams || tables[sid].n_sym == 0) return;
+    words[chunk_base[sid / LQ_STREAMS] + stream_woff[sid] + (stream_nbits[sid] + 31) / 32] = 0u;
+}
+
+// ------------------------------------------------------------ chunk decode --
+
+// slot -> symbol index LUT of every chunk stream (binary search over cumfreqs)
+__global__ __launch_bounds__(256) void k_chunk_lut(const lq_table* __restrict__ tables, uint16_t* __restrict__ lut) {
+    __shared__ uint32_t cum[LQ_MAXSYM + 1];
+    const int64_t sid = blockIdx.x;
+    const lq_table* T = tables + sid;
+    const int n = T->n_sym;
+    if (n == 0) return;
+    if (threadIdx.x == 0) {
+        uint32_t c = 0;
+        for (int i = 0; i < n; i++) { cum[i] = c; c += enc_f(T->enc[i]); }
+        cum[n] = c;
+    }
+    __syncthreads();
+    for (int slot = threadIdx.x; slot < kL; slot += 256) {
+        int lo = 0, hi = n - 1;   // largest s with cum[s] <= slot
+        while (lo < hi) {
+            int mid = (lo + hi + 1) >> 1;
+            if (cum[mid] <= (uint32_t)slot) lo = mid; else hi = mid - 1;
+        }
+        lut[sid * kL + slot] = (uint16_t)lo;
+    }
+}
+
+__device__ __forceinline__ int shfl_xor_i(int v, int m) { return __shfl_xor(v, m, 64); }
+
+// Workgroup: 16 blocks x 16 streams of one chunk.  Each lane decodes its
+// stream's symbols of one block from the block checkpoint; the 8 lanes of a
+// (block, coset) run in lockstep, so after step j they hold the 8 symbols of
+// the block's j-th vector of that coset, recover c7's parity with a 3-step
+// xor-shuffle and each store one dequantised coordinate.
+__global__ __launch_bounds__(256) void k_chunk_decode(const uint32_t* __restrict__ words, const int64_t* __restrict__ chunk_base,
+                                                      const int64_t* __restrict__ stream_woff, const uint32_t* __restrict__ blk_off,
+                                                      const uint16_t* __restrict__ blk_state, const uint8_t* __restrict__ coset_bits,
+                                                      const uint32_t* __restrict__ blk_n1, const lq_table* __restrict__ tables,
+                                                      const uint16_t* __restrict__ scale16, const uint16_t* __restrict__ lutg,
+                                                      int64_t n_heads, int64_t bph, int64_t nblk, void* __restrict__ out,
+                                                      int out_dtype) {
+    __shared__ uint16_t lut[LQ_STREAMS][kL];
+    __shared__ uint32_t senc[LQ_STREAMS][LQ_MAXSYM];
+    __shared__ uint16_t list[16][kBlk];
+    __shared__ int slo[LQ_STREAMS], snsym[LQ_STREAMS];
+    __shared__ int sn1[16];
+    const int tid = threadIdx.x;
+    const int64_t V = n_heads * bph;
+    const int64_t groups = (nblk + 15) / 16;
+    const int64_t chunk = blockIdx.x / groups;
+    const int64_t gbase = (blockIdx.x % groups) * 16;
+    const lq_table* T = tables + chunk * LQ_STREAMS;
+    {
+        const uint4* src = reinterpret_cast<const uint4*>(lutg + chunk * LQ_STREAMS * kL);
+        uint4* dst = reinterpret_cast<uint4*>(&lut[0][0]);
+        for (int i = tid; i < LQ_STREAMS * kL / 8; i += 256) dst[i] = src[i];
+    }
+    for (int i = tid; i < LQ_STREAMS * LQ_MAXSYM; i += 256) {
+        int s = i / LQ_MAXSYM, j = i % LQ_MAXSYM;
+        senc[s][j] = j < T[s].n_sym ? T[s].enc[j] : 0u;
+    }
+    if (tid < LQ_STREAMS) { slo[tid] = T[tid].lo; snsym[tid] = T[tid].n_sym; }
+    // coset index lists: thread (block b, part p) scans 32 vectors
+    {
+        const int b = tid >> 4, p = tid & 15;
+        const int64_t g = gbase + b;
+        uint32_t bits = 0;
+        int valid = 0;
+        if (g < nblk) {
+            bits = reinterpret_cast<const uint32_t*>(coset_bits + (chunk * nblk + g) * (kBlk / 8))[p];
+            int64_t vv = V - g * kBlk;
+            valid = (int)(vv < kBlk ? vv : kBlk);
+        }
+        int lo_v = p * 32;
+        int nv = valid - lo_v;
+        nv = nv < 0 ? 0 : (nv > 32 ? 32 : nv);
+        uint32_t vmask = nv == 32 ? 0xffffffffu : ((1u << nv) - 1u);
+        bits &= vmask;
+        int c1 = __popc(bits);
+        // exclusive prefix of coset-1 counts over the 16 parts of this block (lanes tid & ~15 .. )
+        int incl = c1;
+        for (int o = 1; o < 16; o <<= 1) {
+            int t = __shfl_up(incl, o, 16);
+            if (p >= o) incl += t;
+        }
+        int r1 = incl - c1;
+        int total1 = __shfl(incl, 15, 16);
+        int n0 = valid - total1;
+        int r0 = lo_v - r1;
+        for (int i = 0; i < nv; i++) {
+            int vl = lo_v + i;
+            if ((bits >> i) & 1u) list[b][n0 + r1++] = (uint16_t)vl;
+            else list[b][r0++] = (uint16_t)vl;
+        }
+        if (p == 0) sn1[b] = total1;
+    }
+    __syncthreads();
+
+    const int b = tid >> 4;
+    const int st = tid & 15;
+    const int64_t g = gbase + b;
+    if (g >= nblk || snsym[st] == 0) return;   // whole (block, coset) groups leave together
+    const int c = st >> 3, idx = st & 7;
+    const int64_t vv = V - g * kBlk;
+    const int valid = (int)(vv < kBlk ? vv : kBlk);
+    const int n1 = sn1[b], n0 = valid - n1;
+    const int ncnt = c ? n1 : n0;
+    const int lbase = c ? n0 : 0;
+    const int64_t task = (chunk * LQ_STREAMS + st) * nblk + g;
+    const uint32_t* wb = words + chunk_base[chunk] + stream_woff[chunk * LQ_STREAMS + st];
+    uint32_t x = blk_state[task];
+    const uint32_t bp = blk_off[task];
+    uint32_t nwi = bp >> 5;
+    uint64_t buf = 0;
+    uint32_t nbuf = 0;
+    if (ncnt > 0) {
+        buf = ((uint64_t)__builtin_bitreverse32(wb[nwi]) << 32) << (bp & 31);
+        nbuf = 32 - (bp & 31);
+        nwi++;
+    }
+    const uint16_t* L = lut[st];
+    const uint32_t* E = senc[st];
+    const int lo_sym = slo[st];
+    const float off = c ? 0.5f : 0.f;
+    const int64_t vbase = chunk * V + g * kBlk;
+    for (int j = 0; j < ncnt; j++) {
+        uint32_t slot = x & (kL - 1);
+        uint32_t s = L[slot];
+        uint32_t e = E[s];
+        x = enc_f(e) * (x >> 10) + slot - enc_c(e);
+        if (x < (uint32_t)kL) {
+            uint32_t k = (uint32_t)__clz((int)x) - 21u;
+            if (nbuf < k) {
+                buf |= ((uint64_t)__builtin_bitreverse32(wb[nwi++]) << 32) >> nbuf;
+                nbuf += 32;
+            }
+            x = (x << k) | (uint32_t)(buf >> (64 - k));
+            buf <<= k;
+            nbuf -= k;
+        }
+        int val = lo_sym + (int)s;
+        int contrib = idx < 7 ? val : 0;
+        contrib += shfl_xor_i(contrib, 1);
+        contrib += shfl_xor_i(contrib, 2);
+        contrib += shfl_xor_i(contrib, 4);
+        int coord = idx < 7 ? val : 2 * val + (contrib & 1);
+        int vl = list[b][lbase + j];
+        int64_t v = vbase + vl;
+        float sc = h2f(scale16[chunk * n_heads + (g * kBlk + vl) / bph]);
+        float y = ((float)coord + off) * sc;
+        if (out_dtype == LQ_F32) reinterpret_cast<float*>(out)[v * 8 + idx] = y;
+        else reinterpret_cast<uint16_t*>(out)[v * 8 + idx] = f2dtype(y, out_dtype);
+    }
+}
+
+// ------------------------------------------------------- generic tables --
+
+__global__ __launch_bounds__(256) void k_build_tables(const int64_t* __restrict__ counts, const int64_t* __restrict__ count_off,
+                                                      const int32_t* __restrict__ n_sym, int32_t* __restrict__ freqs_out,
+                                                      int32_t* __restrict__ cum_out, int32_t* __restrict__ lookup,
+                                                      int32_t* __restrict__ status) {
+    __shared__ int64_t cnt[kL];
+    __shared__ int32_t fr[kL];
+    __shared__ int64_t keys[kL];
+    __shared__ int16_t perm[kL];
+    __shared__ int s_st;
+    const int t = blockIdx.x;
+    const int n = n_sym[t];
+    const int64_t o = count_off[t];
+    if (n <= 0 || n > kL) {
+        if (threadIdx.x == 0) status[t] = LQ_ST_ALPHABET;
+        return;
+    }
+    for (int i = threadIdx.x; i < n; i += 256) cnt[i] = counts[o + i];
+    if (threadIdx.x == 0) s_st = 0;
+    __syncthreads();
+    normalise(cnt, n, fr, keys, perm, &s_st);
+    for (int i = threadIdx.x; i < n; i += 256) freqs_out[o + i] = fr[i];
+    if (threadIdx.x == 0) {
+        int32_t c = 0;
+        for (int i = 0; i < n; i++) {
+            cum_out[o + t + i] = c;
+            for (int j = c; j < c + fr[i]; j++) lookup[(int64_t)t * kL + j] = i;
+            c += fr[i];
+        }
+        cum_out[o + t + n] = c;
+        status[t] = s_st;
+    }
+}
+
+// ------------------------------------------------------ generic streams --
+
+// Serial encode of one stream per lane, then the bits are laid out in the
+// reference's word order (n_words + 1 words, last zero).
+__global__ void k_encode_streams(const int32_t* __restrict__ idx, const int64_t* __restrict__ sym_off,
+                                 const int64_t* __restrict__ nsym, const int32_t* __restrict__ freqs,
+                                 const int32_t* __restrict__ cum, const int64_t* __restrict__ tab_off, int32_t n_streams,
+                                 uint32_t* __restrict__ scratch, uint32_t* __restrict__ words,
+                                 const int64_t* __restrict__ word_off, int64_t* __restrict__ state_out,
+                                 int64_t* __restrict__ nbits_out) {
+    int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n_streams) return;
+    const int64_t n = nsym[t];
+    const int32_t* id = idx + sym_off[t];
+    const int32_t* F = freqs + tab_off[t];
+    const int32_t* C = cum + tab_off[t];
+    const int64_t cap = (10 * n + 31) / 32 + 2;
+    uint32_t* scr = scratch + word_off[t];
+    uint32_t* out = words + word_off[t];
+    int64_t wpos = cap - 1;
+    uint64_t acc = 0;
+    uint32_t nacc = 0;
+    int64_t total = 0;
+    uint32_t x = kL;
+    for (int64_t j = n - 1; j >= 0; j--) {
+        uint32_t f = (uint32_t)F[id[j]], cf = (uint32_t)C[id[j]];
+        uint32_t e = enc_pack(f, cf);
+        uint32_t k, xin = x;
+        x = enc_step(x, e, &k);
+        uint64_t r = ((uint64_t)__builtin_bitreverse32(xin) << k) >> 32;
+        acc = (acc << k) | r;
+        nacc += k;
+        total += k;
+        if (nacc >= 32) { nacc -= 32; scr[wpos--] = (uint32_t)(acc >> nacc); }
+    }
+    if (nacc) scr[wpos] = (uint32_t)(acc << (32 - nacc));
+    const int64_t nw = (total + 31) / 32;
+    const int64_t base = cap * 32 - total;   // scratch bit position of stream bit 0
+    for (int64_t w = 0; w < nw; w++) {
+        int64_t sp = base + 32 * w;
+        int64_t wi = sp >> 5;
+        int sh = (int)(sp & 31);
+        int take = (int)(total - 32 * w < 32 ? total - 32 * w : 32);
+        uint64_t v = scr[wi];
+        if (sh + take > 32) v |= (uint64_t)scr[wi + 1] << 32;
+        v >>= sh;
+        out[w] = take == 32 ? (uint32_t)v : (uint32_t)v & ((1u << take) - 1u);
+    }
+    out[nw] = 0u;
+    state_out[t] = x;
+    nbits_out[t] = total;
+}
+
+// _rans_decode_kernel semantics (core/gpu_ans.py:175-235): one stream per lane,
+// renormalisation reads min(needed, n_bits - bit_pos) bits.
+__global__ void k_decode_streams(const int32_t* __restrict__ bits, const int32_t* __restrict__ bit_off,
+                                 const int32_t* __restrict__ nbits, const int32_t* __restrict__ init,
+                                 const int32_t* __restrict__ ndec, const int32_t* __restrict__ lookup,
+                                 const int32_t* __restrict__ freqs, const int32_t* __restrict__ cum,
+                                 const int32_t* __restrict__ alphabet, const int32_t* __restrict__ tid_,
+                                 int32_t max_sym, const int32_t* __restrict__ out_off, int32_t n_streams,
+                                 int64_t* __restrict__ out) {
+    int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n_streams) return;
+    const uint32_t* wb = reinterpret_cast<const uint32_t*>(bits);
+    const int64_t boff = bit_off[t];
+    const int64_t nb = nbits[t];
+    const int n = ndec[t];
+    const int tb = tid_[t];
+    const int32_t* LU = lookup + (int64_t)tb * kL;
+    const int32_t* F = freqs + (int64_t)tb * max_sym;
+    const int32_t* C = cum + (int64_t)tb * max_sym;
+    const int32_t* A = alphabet + (int64_t)tb * max_sym;
+    int64_t* o = out + out_off[t];
+    uint32_t x = (uint32_t)init[t];
+    int64_t pos = 0;
+    for (int i = 0; i < n; i++) {
+        uint32_t slot = x & (kL - 1);
+        int si = LU[slot];
+        o[i] = A[si];
+        x = (uint32_t)F[si] * (x >> 10) + slot - (uint32_t)C[si];
+        if (x < (uint32_t)kL) {
+            int64_t k = (int64_t)__clz((int)x) - 21;
+            if (k > nb - pos) k = nb - pos;
+            for (int64_t q = 0; q < k; q++) {
+                int64_t ab = boff + pos + q;
+                x = (x << 1) | ((wb[ab >> 5] >> (ab & 31)) & 1u);
+            }
+            pos += k;
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int lq_chunk_tables(const uint32_t* d_hist, int64_t n_chunks, lq_table* d_tables, int32_t* d_status, hipStream_t s) {
+    if (n_chunks <= 0) return LQ_ERR_ARG;
+    hipLaunchKernelGGL(k_chunk_tables, dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, d_hist, d_tables, d_status);
+    return launch_status();
+}
+
+int64_t lq_chunk_encode_workspace(int64_t n_chunks, int64_t n_vectors) {
+    if (n_chunks <= 0 || n_vectors <= 0) return -1;
+    return enc_layout(n_chunks, n_vectors).total;
+}
+
+int lq_chunk_encode(const int8_t* d_sym, const uint32_t* d_blk_n1, int64_t n_chunks, int64_t n_vectors,
+                    const lq_table* d_tables, void* d_work, uint32_t* d_blk_off, uint16_t* d_blk_state,
+                    int64_t* d_stream_nbits, int32_t* d_stream_state, int64_t* d_stream_woff, int64_t* d_chunk_words,
+                    hipStream_t s) {
+    if (n_chunks <= 0 || n_vectors <= 0) return LQ_ERR_ARG;
+    const int64_t nblk = (n_vectors + kBlk - 1) / kBlk;
+    EncWork w = enc_layout(n_chunks, n_vectors);
+    uint32_t* bits = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(d_work) + w.bits);
+    uint32_t* scratch = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(d_work) + w.scratch);
+    const int64_t groups = (nblk + 15) / 16;
+    hipLaunchKernelGGL(k_chunk_encode, dim3((unsigned)(n_chunks * groups)), dim3(256), 0, s, d_sym, d_blk_n1, nblk,
+                       n_vectors, d_tables, bits, scratch, d_blk_state);
+    hipLaunchKernelGGL(k_chunk_scan, dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, bits, d_blk_state, d_tables,
+                       nblk, d_blk_off, d_stream_nbits, d_stream_state);
+    hipLaunchKernelGGL(k_chunk_offsets, dim3((unsigned)((n_chunks + 63) / 64)), dim3(64), 0, s, d_stream_nbits, d_tables,
+                       n_chunks, d_stream_woff, d_chunk_words);
+    return launch_status();
+}
+
+int lq_chunk_pack(int64_t n_chunks, int64_t n_vectors, const lq_table* d_tables, const void* d_work,
+                  const uint32_t* d_blk_off, const int64_t* d_stream_nbits, const int64_t* d_stream_woff,
+                  const int64_t* d_chunk_base, uint32_t* d_words, hipStream_t s) {
+    if (n_chunks <= 0 || n_vectors <= 0) return LQ_ERR_ARG;
+    const int64_t nblk = (n_vectors + kBlk - 1) / kBlk;
+    EncWork w = enc_layout(n_chunks, n_vectors);
+    const uint32_t* bits = reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(d_work) + w.bits);
+    const uint32_t* scratch = reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(d_work) + w.scratch);
+    const int64_t tasks = n_chunks * LQ_STREAMS * nblk;
+    hipLaunchKernelGGL(k_chunk_pack, dim3((unsigned)((tasks + 3) / 4)), dim3(256), 0, s, tasks, nblk, bits, scratch,
+                       d_blk_off, d_stream_nbits, d_stream_woff, d_chunk_base, d_words);
+    const int64_t ns = n_chunks * LQ_STREAMS;
+    hipLaunchKernelGGL(k_chunk_tail, dim3((unsigned)((ns + 255) / 256)), dim3(256), 0, s, ns, d_tables,
+                       d_stream_nbits, d_stream_woff, d_chunk_base, d_words);
+    return launch_status();
+}
+
+int lq_chunk_decode(const uint32_t* d_words, const int64_t* d_chunk_base, const int64_t* d_stream_woff,
+                    const uint32_t* d_blk_off, const uint16_t* d_blk_state, const uint8_t* d_coset_bits,
+                    const uint32_t* d_blk_n1, const lq_table* d_tables, const uint16_t* d_scale16, int64_t n_chunks,
+                    int64_t n_heads, int64_t bph, uint16_t* d_lut_work, void* d_out, int out_dtype, hipStream_t s) {
+    if (n_chunks <= 0 || n_heads <= 0 || bph <= 0 || out_dtype < 0 || out_dtype > 2) return LQ_ERR_ARG;
+    const int64_t V = n_heads * bph;
+    const int64_t nblk = (V + kBlk - 1) / kBlk;
+    hipLaunchKernelGGL(k_chunk_lut, dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, d_tables, d_lut_work);
+    const int64_t groups = (nblk + 15) / 16;
+    hipLaunchKernelGGL(k_chunk_decode, dim3((unsigned)(n_chunks * groups)), dim3(256), 0, s, d_words, d_chunk_base,
+                       d_stream_woff, d_blk_off, d_blk_state, d_coset_bits, d_blk_n1, d_tables, d_scale16, d_lut_work,
+                       n_heads, bph, nblk, d_out, out_dtype);
+    return launch_status();
+}
+
+int lq_build_tables(const int64_t* d_counts, const int64_t* d_count_off, const int32_t* d_n_sym, int32_t n_tables,
+                    int32_t* d_freqs, int32_t* d_cum, int32_t* d_lookup, int32_t* d_status, hipStream_t s) {
+    if (n_tables <= 0) return LQ_ERR_ARG;
+    hipLaunchKernelGGL(k_build_tables, dim3((unsigned)n_tables), dim3(256), 0, s, d_counts, d_count_off, d_n_sym, d_freqs,
+                       d_cum, d_lookup, d_status);
+    return launch_status();
+}
+
+int lq_rans_encode_streams(const int32_t* d_idx, const int64_t* d_sym_off, const int64_t* d_n, const int32_t* d_freqs,
+                           const int32_t* d_cum, const int64_t* d_tab_off, int32_t n_streams, uint32_t* d_scratch,
+                           uint32_t* d_words, const int64_t* d_word_off, int64_t* d_state, int64_t* d_nbits,
+                           hipStream_t s) {
+    if (n_streams <= 0) return LQ_ERR_ARG;
+    hipLaunchKernelGGL(k_encode_streams, dim3((unsigned)((n_streams + 63) / 64)), dim3(64), 0, s, d_idx, d_sym_off, d_n,
+                       d_freqs, d_cum, d_tab_off, n_streams, d_scratch, d_words, d_word_off, d_state, d_nbits);
+    return launch_status();
+}
+
+int lq_rans_decode_streams(const int32_t* d_bits, const int32_t* d_bit_off, const int32_t* d_nbits, const int32_t* d_init,
+                           const int32_t* d_ndec, const int32_t* d_lookup, const int32_t* d_freqs, const int32_t* d_cum,
+                           const int32_t* d_alphabet, const int32_t* d_tid, int32_t max_sym, const int32_t* d_out_off,
+                           int32_t n_streams, int64_t* d_out, hipStream_t s) {
+    if (n_streams <= 0 || max_sym <= 0) return LQ_ERR_ARG;
+    hipLaunchKernelGGL(k_decode_streams, dim3((unsigned)((n_streams + 63) / 64)), dim3(64), 0, s, d_bits, d_bit_off, d_nbits,
+                       d_init, d_ndec, d_lookup, d_freqs, d_cum, d_alphabet, d_tid, max_sym, d_out_off, n_streams, d_out);
+    return launch_status();
+}
+
+}  // extern "C"

@@ -1,0 +1,128 @@
+"""GPU parity of the E8 + rANS chunk codec against the CPU oracle.
+
+Bit-exact: lattice points, symbols, coset bitmap, tables, bitstream words,
+final states, n_bits; fp16 outputs bit-exact (the contract allows 1 ulp)."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+G = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+pytestmark = pytest.mark.gpu
+
+
+def _lq():
+    from latticequant_amd import codec, _lib
+    return codec, _lib
+
+
+def _e8_gpu(x, mode):
+    codec, L = _lq()
+    xt = torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+    out = torch.empty_like(xt)
+    L.check(L.lib().lq_e8_encode_f32(xt.data_ptr(), xt.shape[0], mode, out.data_ptr(), L.stream_ptr()), "e8")
+    return out.cpu().numpy()
+
+
+def test_e8_golden_gpu():
+    g = np.load(os.path.join(G, "e8.npz"))
+    np.testing.assert_array_equal(_e8_gpu(g["x"], 0), g["e8"])
+    np.testing.assert_array_equal(_e8_gpu(g["x"], 1), g["d8"])
+
+
+def test_e8_random_vs_oracle_gpu():
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((1 << 18, 8)) * rng.choice([0.3, 3, 30], size=(1 << 18, 1))).astype(np.float32)
+    np.testing.assert_array_equal(_e8_gpu(x, 0), O.encode_e8(x))
+
+
+def _compare_chunk(enc, c, ch, check_tables=True):
+    codec, L = _lq()
+    streams = codec.chunk_streams_host(enc, c)
+    assert len(streams) == len(ch.streams)
+    for sg, so in zip(streams, ch.streams):
+        assert (sg["coset"], sg["idx"], sg["n"]) == (so.coset, so.idx, so.n_symbols)
+        assert sg["lo"] == so.table.alphabet[0]
+        if check_tables:
+            np.testing.assert_array_equal(sg["freqs"], so.table.freqs)
+        assert sg["n_bits"] == so.n_bits and sg["state"] == so.state
+        np.testing.assert_array_equal(sg["words"], so.words)
+    nb = (ch.n_vectors + 7) // 8
+    np.testing.assert_array_equal(enc.coset_bits[c].cpu().numpy()[:nb], ch.coset_packed)
+    base = int(enc.chunk_base[c]); nw = int(enc.chunk_words[c])
+    np.testing.assert_array_equal(enc.words[base:base + nw].cpu().numpy().view(np.uint32), ch.bitstream)
+
+
+def test_chunk_golden_cases_gpu():
+    """The reference's own _compress_tensor outputs (tests/golden/cache.npz)."""
+    codec, L = _lq()
+    g = np.load(os.path.join(G, "cache.npz"))
+    for ci in range(int(g["n_cases"])):
+        p = f"c{ci}_"
+        t = g[p + "input"]
+        bits = int(g[p + "bits"])
+        ch = O.compress_chunk(t, bits)   # oracle == reference on these cases (tests/test_oracle.py)
+        x = torch.from_numpy(t).cuda()[None]
+        enc, deq = codec.encode_batch(x, bits, scale32=torch.from_numpy(ch.scales_f32), deq_out=True)
+        assert int(enc.status.item()) == 0
+        np.testing.assert_array_equal(deq[0].cpu().numpy(), g[p + "decompressed"])
+        _compare_chunk(enc, 0, ch)
+        np.testing.assert_array_equal(codec.decode_batch(enc)[0].cpu().numpy(), g[p + "rebuilt"])
+        # scales computed on the device
+        enc2, _ = codec.encode_batch(x, bits)
+        np.testing.assert_array_equal(enc2.scale16.cpu().numpy(), g[p + "scales"])
+
+
+@pytest.mark.parametrize("shape,bits,seed", [((1, 8, 256, 128), 4, 1), ((1, 8, 1024, 128), 3, 2),
+                                             ((2, 4, 300, 64), 5, 3), ((1, 8, 8192, 128), 4, 4)])
+def test_chunk_random_vs_oracle_gpu(shape, bits, seed):
+    codec, L = _lq()
+    g = torch.Generator().manual_seed(seed)
+    t = torch.randn(*shape, generator=g)
+    ch_idx = torch.randperm(shape[-1], generator=g)[:4]
+    t[..., ch_idx] *= 10.0
+    t = t.to(torch.float16)
+    tn = t.numpy()
+    ch = O.compress_chunk(tn, bits)
+    enc, deq = codec.encode_batch(t.cuda()[None], bits, scale32=torch.from_numpy(ch.scales_f32), deq_out=True)
+    assert int(enc.status.item()) == 0
+    np.testing.assert_array_equal(deq[0].cpu().numpy(), ch.decompressed)
+    _compare_chunk(enc, 0, ch)
+    np.testing.assert_array_equal(codec.decode_batch(enc)[0].cpu().numpy(), O.decompress_chunk(ch))
+    # device sigma^2 agrees with the oracle's float64 mean to fp32 rounding
+    enc2, _ = codec.encode_batch(t.cuda()[None], bits)
+    np.testing.assert_allclose(enc2.sigma2.cpu().numpy(), O.head_sigma2(tn), rtol=2e-7)
+
+
+def test_chunk_batch_and_roundtrip_gpu():
+    """Several chunks per call, mixed bit rates, bf16 input; decode(encode) == q * scale16."""
+    codec, L = _lq()
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(6, 1, 4, 96, 128, generator=g).to(torch.bfloat16)
+    bits = [3, 4, 5, 4, 3, 5]
+    enc, deq = codec.encode_batch(x.cuda(), bits, deq_out=True)
+    assert enc.status.cpu().numpy().tolist() == [0] * 6
+    out = codec.decode_batch(enc, out_dtype=torch.bfloat16)
+    for c in range(6):
+        sc32 = enc.scale32.view(6, -1)[c].cpu().numpy()
+        ch = O.compress_chunk(x[c].float().numpy(), bits[c], scales_f32=sc32)
+        _compare_chunk(enc, c, ch)
+        # bf16 read path: float(q) * float(scale16) rounded to bf16
+        q = torch.from_numpy(O.quantize_heads(x[c].float().numpy(), sc32))
+        sc = enc.scale16.view(6, -1)[c].float().cpu()
+        want = (q.view(4, -1, 8) * sc[:, None, None]).to(torch.bfloat16).view(1, 4, 96, 128)
+        assert torch.equal(out[c].cpu(), want)
+
+
+def test_empty_coset_and_zero_head_gpu():
+    codec, L = _lq()
+    t = torch.zeros(1, 2, 8, 64, dtype=torch.float16)
+    t[0, 1] = torch.randn(8, 64).half()
+    ch = O.compress_chunk(t.numpy(), 4)
+    enc, deq = codec.encode_batch(t.cuda()[None], 4, deq_out=True)
+    np.testing.assert_array_equal(enc.scale16.cpu().numpy(), ch.scales)
+    _compare_chunk(enc, 0, ch)
+    np.testing.assert_array_equal(codec.decode_batch(enc)[0].cpu().numpy(), O.decompress_chunk(ch))
