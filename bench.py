@@ -68,7 +68,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--group", type=int, default=8, help="chunks per kernel launch")
+    ap.add_argument("--group", type=int, default=64, help="chunks per kernel launch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-chunks", type=int, default=2)
     args = ap.parse_args()
@@ -89,10 +89,10 @@ def main():
     G = args.group
     groups = [(i, min(i + G, C)) for i in range(0, C, G)]
     V = HEADS * TOKENS * HD // 8
-    bound = G * ((10 * 8 * V + 31) // 32 + 2 * L.LQ_STREAMS)
+    bound = codec.words_bound(G, V)
     arenas = [torch.empty(bound, dtype=torch.int32, device=dev) for _ in groups]
     out = torch.empty_like(x)
-    luts = torch.empty(G * L.LQ_STREAMS * L.LQ_L, dtype=torch.int16, device=dev)
+    luts = torch.empty(G * L.LQ_STREAMS * L.LQ_L, dtype=torch.int32, device=dev)
     encs = [None] * len(groups)
 
     def write():

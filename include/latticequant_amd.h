@@ -80,7 +80,7 @@ int lq_symbols_to_e8(const int32_t *d_coset, const int32_t *d_sym8, int64_t n, f
 
 /* Per-head sigma^2 = mean(x^2), fp32 scale sqrt(2*pi*e*sigma^2*4^-b) (1 if
  * sigma^2 < 1e-12) and its fp16 copy; bits per chunk.  Also the per-head
- * fast-division flag consumed by lq_chunk_quantize.  d_work: 2*n_heads_total doubles.
+ * fast-division flag consumed by lq_chunk_quantize.  d_work: 4096 + n_heads_total doubles.
  * Replaces llm/compressed_kv_cache.py:188-196. */
 int lq_head_scales(const void *d_x, int dtype, int64_t n_chunks, int64_t n_heads, int64_t bph,
                    const int32_t *d_chunk_bits, double *d_work, float *d_sigma2, float *d_scale32,
@@ -134,12 +134,13 @@ int lq_chunk_pack(int64_t n_chunks, int64_t n_vectors, const lq_table *d_tables,
                   const int64_t *d_chunk_base, uint32_t *d_words, hipStream_t s);
 
 /* Decode + dequantize a batch of chunks to (B, H, T, hd) in out_dtype:
- * fp16(q * float(scale16[head])).  d_lut_work: n_chunks * 16 * 1024 uint16.
+ * fp16(q * float(scale16[head])).  d_lut_work: n_chunks * 16 * 1024 uint32.
+ * d_words must have 2 readable words after the last chunk's last stream.
  * Replaces llm/compressed_kv_cache.py:289-332 (_decompress_chunk). */
 int lq_chunk_decode(const uint32_t *d_words, const int64_t *d_chunk_base, const int64_t *d_stream_woff,
                     const uint32_t *d_blk_off, const uint16_t *d_blk_state, const uint8_t *d_coset_bits,
                     const uint32_t *d_blk_n1, const lq_table *d_tables, const uint16_t *d_scale16,
-                    int64_t n_chunks, int64_t n_heads, int64_t bph, uint16_t *d_lut_work, void *d_out,
+                    int64_t n_chunks, int64_t n_heads, int64_t bph, uint32_t *d_lut_work, void *d_out,
                     int out_dtype, hipStream_t s);
 
 /* Generic tables (build_rans_table API): n_tables histograms of n_sym[t] <= 1024

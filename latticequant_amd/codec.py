@@ -84,6 +84,12 @@ class EncodedBatch:
         return tab + ck + 2 * self.nblk
 
 
+def words_bound(n_chunks: int, n_vectors: int) -> int:
+    """Upper bound of the bitstream words of n_chunks chunks (10 bits per symbol,
+    n_words + 1 per stream) plus the decoder's 2-word read-ahead slack."""
+    return n_chunks * ((10 * 8 * n_vectors + 31) // 32 + 2 * L.LQ_STREAMS) + 2
+
+
 def _zeros(n, dtype, dev):
     return torch.zeros(int(n), dtype=dtype, device=dev)
 
@@ -126,7 +132,7 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
     fastdiv = _empty(C * nh, torch.int32, dev)
     sigma2 = None
     if scale32 is None:
-        work = _empty(2 * C * nh, torch.float64, dev)
+        work = _empty(4096 + C * nh, torch.float64, dev)
         sigma2 = _empty(C * nh, torch.float32, dev)
         scale32 = _empty(C * nh, torch.float32, dev)
         scale16 = _empty(C * nh, torch.float16, dev)
@@ -163,13 +169,13 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
                                 stream_state.data_ptr(), stream_woff.data_ptr(), chunk_words.data_ptr(), s),
             "lq_chunk_encode")
     chunk_base = torch.cumsum(chunk_words, 0) - chunk_words
-    bound = C * ((10 * 8 * V + 31) // 32 + 2 * L.LQ_STREAMS)
+    bound = words_bound(C, V)
     if words_out is not None:
         if words_out.numel() < bound:
             raise ValueError(f"words_out holds {words_out.numel()} words, needs {bound}")
         words = words_out
     elif exact_size:
-        words = _empty(max(1, int(chunk_words.sum().item())), torch.int32, dev)
+        words = _empty(int(chunk_words.sum().item()) + 2, torch.int32, dev)   # decoder read-ahead slack
     else:
         words = _empty(bound, torch.int32, dev)
     L.check(lib.lq_chunk_pack(C, V, tables.data_ptr(), work.data_ptr(), blk_off.data_ptr(), stream_nbits.data_ptr(),
@@ -193,7 +199,7 @@ def decode_batch(enc: EncodedBatch, out_dtype: torch.dtype = torch.float16, out:
     if out is None:
         out = torch.empty((C,) + tuple(enc.shape), dtype=out_dtype, device=dev)
     if lut_work is None:
-        lut_work = _empty(C * L.LQ_STREAMS * L.LQ_L, torch.int16, dev)
+        lut_work = _empty(C * L.LQ_STREAMS * L.LQ_L, torch.int32, dev)
     L.check(lib.lq_chunk_decode(enc.words.data_ptr(), enc.chunk_base.data_ptr(), enc.stream_woff.data_ptr(),
                                 enc.blk_off.data_ptr(), enc.blk_state.data_ptr(), enc.coset_bits.data_ptr(),
                                 enc.blk_n1.data_ptr(), enc.tables.data_ptr(), enc.scale16.data_ptr(), C, enc.n_heads,

@@ -296,7 +296,8 @@ int lq_head_scales(const void* d_x, int dtype, int64_t n_chunks, int64_t n_heads
                    uint16_t* d_scale16, int32_t* d_fastdiv, hipStream_t s) {
     if (n_chunks <= 0 || n_heads <= 0 || bph <= 0 || dtype < 0 || dtype > 2) return LQ_ERR_ARG;
     const int64_t H = n_chunks * n_heads;
-    const int parts = 2;
+    int64_t want = (4096 + H - 1) / H, cap = bph / 512 > 1 ? bph / 512 : 1;
+    const int parts = (int)(want < cap ? want : cap);
     hipLaunchKernelGGL(k_head_sumsq, dim3((unsigned)H, parts), dim3(256), 0, s, d_x, dtype, bph, parts, d_work);
     hipLaunchKernelGGL(k_head_finalize, dim3((unsigned)H), dim3(256), 0, s, d_work, parts, bph * 8, n_heads,
                        d_chunk_bits, dtype, d_sigma2, d_scale32, d_scale16, d_fastdiv);

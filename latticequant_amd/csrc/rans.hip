@@ -100,62 +100,136 @@ __device__ void rank_argsort(const int64_t* k, int16_t* a, int n) {
     __syncthreads();
 }
 
-// build_rans_table normalisation (core/gpu_ans.py:62-86) on LDS arrays.
-// counts[n] (int64), freqs[n] (int32) out.  Needs k[>=1024], a[>=1024] scratch.
-// Returns status bits (LQ_ST_TIE_UNPINNED) in *st.
-__device__ void normalise(const int64_t* counts, int n, int32_t* freqs, int64_t* k, int16_t* a, int* st) {
-    __shared__ int64_t s_total;
-    __shared__ int s_diff;
-    if (threadIdx.x == 0) {
-        int64_t t = 0;
-        for (int i = 0; i < n; i++) t += counts[i];
-        s_total = t;
-    }
+// Block-wide sum of v (blockDim.x multiple of 64, <= 1024).
+__device__ int64_t block_sum(int64_t v) {
+    __shared__ int64_t part[16];
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     __syncthreads();
-    const int64_t total = s_total;
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+    __syncthreads();
+    int64_t s = 0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); w++) s += part[w];
+    return s;
+}
+
+// One pass of the build_rans_table adjustment loop (core/gpu_ans.py:73-84)
+// with m = |diff|: j = 0 .. m-1 visits order[j % n], i.e. every entry
+// `full` = m / n times plus the first rem = m % n entries of the argsort order
+// once more; an increment adds its visits, a decrement leaves
+// max(f - visits, 1).  The argsort tie order only matters for the tie group
+// straddling position rem, and only if a different subset of that group would
+// change a frequency; the numpy network runs only then.
+__device__ void adjust_pass(const int64_t* counts, int n, int32_t* freqs, int diff, int64_t* k, int16_t* a,
+                            int64_t* kk, int8_t* inset, int* st) {
+    const int m = diff > 0 ? diff : -diff;
+    const int full = m / n, rem = m % n;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) kk[i] = diff > 0 ? -counts[i] : -(int64_t)freqs[i];
+    __syncthreads();
+    int matters = 0;
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        if (total == 0) {
-            freqs[i] = 1;
-        } else {
-            double f = (double)counts[i] / (double)total * (double)kL;   // (counts / total * L)
-            int32_t t = (int32_t)f;                                       // .astype(int32)
-            freqs[i] = t < 1 ? 1 : t;
-        }
+        const int64_t ki = kk[i];
+        int lt = 0, eq = 0;
+        for (int j = 0; j < n; j++) { lt += kk[j] < ki; eq += kk[j] == ki; }
+        const int8_t in = lt + eq <= rem ? 1 : (lt >= rem ? 0 : 2);
+        inset[i] = in;
+        if (in == 2 && (diff > 0 || freqs[i] - full > 1)) matters = 1;
     }
-    __syncthreads();
-    for (;;) {
-        if (threadIdx.x == 0) {
-            int64_t sum = 0;
-            for (int i = 0; i < n; i++) sum += freqs[i];
-            s_diff = (int)(kL - sum);
-        }
-        __syncthreads();
-        const int diff = s_diff;
-        if (diff == 0) break;
-        for (int i = threadIdx.x; i < n; i += blockDim.x) k[i] = diff > 0 ? -counts[i] : -(int64_t)freqs[i];
+    if (block_sum(matters) != 0) {
+        for (int i = threadIdx.x; i < n; i += blockDim.x) k[i] = kk[i];
         __syncthreads();
         if (n <= 256) {
             net_argsort(k, a, n);
-        } else {
-            rank_argsort(k, a, n);
+        } else {   // numpy's quicksort tie order is not restated for n > 256
+            rank_argsort(kk, a, n);
+            if (threadIdx.x == 0) *st |= LQ_ST_TIE_UNPINNED;
         }
-        if (threadIdx.x == 0) {
-            int m = diff > 0 ? diff : -diff;
-            if (n > 256 && (m % n) != 0) {   // a tie across the cut makes numpy's choice matter
-                int c = m % n;
-                if (k[a[c - 1]] == k[a[c]]) *st |= LQ_ST_TIE_UNPINNED;
-            }
-            if (diff > 0) {
-                for (int j = 0; j < m; j++) freqs[a[j % n]] += 1;
-            } else {
-                for (int j = 0; j < m; j++) {
-                    int idx = a[j % n];
-                    if (freqs[idx] > 1) freqs[idx] -= 1;
-                }
-            }
-        }
+        for (int p = threadIdx.x; p < n; p += blockDim.x) inset[a[p]] = p < rem ? 1 : 0;
         __syncthreads();
     }
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const int v = full + (inset[i] == 1 ? 1 : 0);
+        const int f = freqs[i];
+        freqs[i] = diff > 0 ? f + v : (f - v > 1 ? f - v : 1);
+    }
+    __syncthreads();
+}
+
+// build_rans_table normalisation (core/gpu_ans.py:62-86) on LDS arrays:
+// counts[n] (int64) in, freqs[n] (int32) out; k, a: network scratch (256),
+// kk, inset: n entries.  Status bits (LQ_ST_TIE_UNPINNED) go to *st.
+//
+// An increment pass always reaches sum == L.  In the decrement branch the
+// excess is below n (only the max(., 1) bumps exceed L), so a pass whose
+// excess covers all G entries with f > 1 decrements exactly those, whatever
+// the order; such passes are counted in closed form and only the last,
+// partial pass (excess < G) goes through adjust_pass.
+__device__ void normalise(const int64_t* counts, int n, int32_t* freqs, int64_t* k, int16_t* a, int64_t* kk,
+                          int8_t* inset, int* st) {
+    int64_t tl = 0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) tl += counts[i];
+    const int64_t total = block_sum(tl);
+    int64_t fl = 0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        int32_t f = 1;
+        if (total != 0) {
+            double q = (double)counts[i] / (double)total * (double)kL;   // (counts / total * L)
+            int32_t t = (int32_t)q;                                       // .astype(int32)
+            f = t < 1 ? 1 : t;
+        }
+        freqs[i] = f;
+        fl += f;
+    }
+    const int diff = (int)(kL - block_sum(fl));
+    if (diff > 0) {
+        adjust_pass(counts, n, freqs, diff, k, a, kk, inset, st);
+    } else if (diff < 0) {
+        int excess = -diff, t = 0;
+        for (;;) {
+            int64_t g = 0;
+            for (int i = threadIdx.x; i < n; i += blockDim.x) g += freqs[i] - t > 1;
+            const int G = (int)block_sum(g);
+            if (G == 0 || excess < G) break;
+            excess -= G;
+            t++;
+        }
+        for (int i = threadIdx.x; i < n; i += blockDim.x) freqs[i] = freqs[i] - t > 1 ? freqs[i] - t : 1;
+        __syncthreads();
+        if (excess > 0) adjust_pass(counts, n, freqs, -excess, k, a, kk, inset, st);
+    }
+}
+
+// Inclusive scan of v over the block (blockDim.x <= 1024, multiple of 64).
+__device__ int block_incl_scan(int v) {
+    __shared__ int wsum[16];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    for (int o = 1; o < 64; o <<= 1) {
+        int t = __shfl_up(v, o, 64);
+        if (lane >= o) v += t;
+    }
+    __syncthreads();
+    if (lane == 63) wsum[w] = v;
+    __syncthreads();
+    for (int i = 0; i < w; i++) v += wsum[i];
+    return v;
+}
+
+// out[i] = in[0] + .. + in[i-1] for i <= n (block-cooperative, any n).
+__device__ void exclusive_scan_array(const int32_t* in, int n, int32_t* out) {
+    __shared__ int carry;
+    if (threadIdx.x == 0) carry = 0;
+    __syncthreads();
+    for (int b = 0; b < n; b += blockDim.x) {
+        int i = b + threadIdx.x;
+        int v = i < n ? in[i] : 0;
+        int incl = block_incl_scan(v);
+        int c = carry;
+        if (i < n) out[i] = c + incl - v;
+        __syncthreads();
+        if (threadIdx.x == blockDim.x - 1) carry = c + incl;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[n] = carry;
+    __syncthreads();
 }
 
 // ------------------------------------------------------------ chunk tables --
@@ -188,15 +262,14 @@ __global__ __launch_bounds__(256) void k_chunk_tables(const uint32_t* __restrict
         counts[i] = (b >= 0 && b < 256) ? (int64_t)h[b] : 0;
     }
     __syncthreads();
-    // n <= 260; arrays for the network hold 256 keys, so n in 257..260 takes the rank path
-    __shared__ int64_t kbig[LQ_MAXSYM];
-    normalise(counts, n, freqs, n <= 256 ? keys : kbig, perm, &s_st);
+    // n <= 260; the network holds 256 keys (n in 257..260 takes the rank path)
+    __shared__ int64_t kk[LQ_MAXSYM];
+    __shared__ int8_t inset[LQ_MAXSYM];
+    normalise(counts, n, freqs, keys, perm, kk, inset, &s_st);
+    __shared__ int32_t cum[LQ_MAXSYM + 1];
+    exclusive_scan_array(freqs, n, cum);
+    for (int i = tid; i < n; i += 256) T->enc[i] = enc_pack((uint32_t)freqs[i], (uint32_t)cum[i]);
     if (tid == 0) {
-        uint32_t cum = 0;
-        for (int i = 0; i < n; i++) {
-            T->enc[i] = enc_pack((uint32_t)freqs[i], cum);
-            cum += (uint32_t)freqs[i];
-        }
         T->lo = lo;
         T->n_sym = n;
         T->n_symbols = (int32_t)s_tot;
@@ -227,16 +300,25 @@ __device__ __forceinline__ Col column(const int8_t* sym, const uint32_t* blk_n1,
     return col;
 }
 
-// enc entry of symbol value v (int8) in table of stream st
-__device__ __forceinline__ uint32_t enc_of(const uint32_t* enc, int lo, int v) { return enc[v - lo]; }
+// Encoder table entry: f | nb << 11 | base << 15 with nb = 11 - bitlen(f) and
+// base = L + cum - f, so a step is  k = nb - 1 + (x >= f << nb);  x = (x >> k) + base.
+__device__ __forceinline__ uint32_t encx_of(uint32_t e) {
+    uint32_t f = enc_f(e), c = enc_c(e), nb = enc_nb(e);
+    return f | (nb << 11) | (((uint32_t)kL + c - f) << 15);
+}
+__device__ __forceinline__ uint32_t encx_step(uint32_t x, uint32_t e, uint32_t* k_out) {
+    uint32_t f = e & 0x7ffu, nb = (e >> 11) & 0xfu, base = e >> 15;
+    uint32_t k = nb - 1u + (x >= (f << nb) ? 1u : 0u);
+    *k_out = k;
+    return (x >> k) + base;
+}
 
 // Interval step: every state in [lo, hi] encodes the symbol; the image is
 // exact when the interval lies on one side of the renormalisation threshold,
 // otherwise the whole image range of the symbol.
 __device__ __forceinline__ void hull_step(uint32_t& lo, uint32_t& hi, uint32_t e) {
-    uint32_t f = enc_f(e), nb = enc_nb(e);
+    uint32_t f = e & 0x7ffu, nb = (e >> 11) & 0xfu, base = e >> 15;
     uint32_t thr = f << nb;
-    uint32_t base = (uint32_t)kL + enc_c(e) - f;
     if (hi < thr || lo >= thr) {
         uint32_t k = nb - 1u + (lo >= thr ? 1u : 0u);
         lo = (lo >> k) + base;
@@ -244,6 +326,38 @@ __device__ __forceinline__ void hull_step(uint32_t& lo, uint32_t& hi, uint32_t e
     } else {
         lo = f + base;
         hi = 2u * f - 1u + base;
+    }
+}
+
+// f(v, b) for the int8 symbols p[n-1], p[n-2], .., p[0], read with aligned
+// 16-byte loads; the next chunk's load is issued before the current chunk is
+// consumed.  b is the symbol's byte index inside its 16-byte chunk (a
+// compile-time constant after unrolling); only the first and the last chunk
+// of the range can be partial.
+template <typename F>
+__device__ __forceinline__ void for_each_rev(const int8_t* p, int n, F&& f) {
+    if (n <= 0) return;
+    const uintptr_t a0 = (uintptr_t)p, a1 = a0 + (uintptr_t)n;
+    const uintptr_t cfirst = a0 & ~(uintptr_t)15;
+    uintptr_t c = (a1 - 1) & ~(uintptr_t)15;
+    uint4 cur = *reinterpret_cast<const uint4*>(c);
+    uint4 nxt = c > cfirst ? *reinterpret_cast<const uint4*>(c - 16) : make_uint4(0, 0, 0, 0);
+    for (;;) {
+        const uint32_t w[4] = {cur.x, cur.y, cur.z, cur.w};
+        const int lo_b = c >= a0 ? 0 : (int)(a0 - c);
+        const int hi_b = c + 16 <= a1 ? 16 : (int)(a1 - c);
+        if (lo_b == 0 && hi_b == 16) {
+#pragma unroll
+            for (int b = 15; b >= 0; b--) f((int)(int8_t)(w[b >> 2] >> ((b & 3) * 8)), b);
+        } else {
+#pragma unroll
+            for (int b = 15; b >= 0; b--)
+                if (b >= lo_b && b < hi_b) f((int)(int8_t)(w[b >> 2] >> ((b & 3) * 8)), b);
+        }
+        if (c == cfirst) break;
+        c -= 16;
+        cur = nxt;
+        if (c > cfirst) nxt = *reinterpret_cast<const uint4*>(c - 16);
     }
 }
 
@@ -275,7 +389,7 @@ __global__ __launch_bounds__(256) void k_chunk_encode(const int8_t* __restrict__
     const lq_table* T = tables + chunk * LQ_STREAMS;
     for (int i = tid; i < LQ_STREAMS * LQ_MAXSYM; i += 256) {
         int s = i / LQ_MAXSYM, j = i % LQ_MAXSYM;
-        senc[s][j] = j < T[s].n_sym ? T[s].enc[j] : 0u;
+        senc[s][j] = j < T[s].n_sym ? encx_of(T[s].enc[j]) : 0u;
     }
     if (tid < LQ_STREAMS) { slo[tid] = T[tid].lo; snsym[tid] = T[tid].n_sym; }
     __syncthreads();
@@ -287,8 +401,9 @@ __global__ __launch_bounds__(256) void k_chunk_encode(const int8_t* __restrict__
         return;
     }
     const int c = st >> 3, idx = st & 7;
-    const uint32_t* enc = senc[st];
+    const uint32_t* encs = senc[st];
     const int lo_sym = slo[st];
+    auto enc = [&](int v) { return encs[v - lo_sym]; };   // entry of symbol value v
 
     // ---- state entering block g (encode order runs from the stream end down)
     uint32_t x = kL;
@@ -303,19 +418,18 @@ __global__ __launch_bounds__(256) void k_chunk_encode(const int8_t* __restrict__
             need -= nc;
             h++;
         }
-        bool exact = h >= nblk;
+        const bool exact = h >= nblk;
         uint32_t lo = kL, hi = exact ? (uint32_t)kL : 2u * kL - 1u;
-        int64_t hb = exact ? nblk - 1 : h;
-        int jtop = exact ? -1 : need - 1;
+        const int64_t hb = exact ? nblk - 1 : h;
         for (int64_t b = hb; b > g; b--) {
             Col col = column(sym, blk_n1, chunk, nblk, V, b, c, idx);
-            int j0 = (b == hb && !exact) ? jtop : col.n - 1;
+            const int cnt = (b == hb && !exact) ? need : col.n;
             if (lo == hi) {
                 uint32_t xx = lo, k;
-                for (int j = j0; j >= 0; j--) xx = enc_step(xx, enc_of(enc, lo_sym, col.p[j]), &k);
+                for_each_rev(col.p, cnt, [&](int v, int) { xx = encx_step(xx, enc(v), &k); });
                 lo = hi = xx;
             } else {
-                for (int j = j0; j >= 0; j--) hull_step(lo, hi, enc_of(enc, lo_sym, col.p[j]));
+                for_each_rev(col.p, cnt, [&](int v, int) { hull_step(lo, hi, enc(v)); });
             }
         }
         if (lo == hi) { x = lo; break; }
@@ -327,24 +441,25 @@ __global__ __launch_bounds__(256) void k_chunk_encode(const int8_t* __restrict__
     uint32_t* scr = scratch + task * (int64_t)kCapW;
     int wpos = kCapW - 1;
     uint64_t acc = 0;
-    uint32_t nacc = 0, total = 0;
-    for (int j = col.n - 1; j >= 0; j--) {
-        uint32_t k;
-        uint32_t e = enc_of(enc, lo_sym, col.p[j]);
-        uint32_t xin = x;
-        x = enc_step(x, e, &k);
-        // emitted group in final stream order is the k low bits of xin, most significant first
-        uint64_t r = ((uint64_t)__builtin_bitreverse32(xin) << k) >> 32;
-        acc = (acc << k) | r;
+    uint32_t nacc = 0;
+    for_each_rev(col.p, col.n, [&](int v, int b) {
+        uint32_t k, xin = x;
+        x = encx_step(x, enc(v), &k);
+        // emitted group in final stream order: the k low bits of xin, most significant first
+        acc = (acc << k) | (((uint64_t)__builtin_bitreverse32(xin) << k) >> 32);
         nacc += k;
-        total += k;
-        if (nacc >= 32) {
+        // at most 3 symbols (<= 30 bits) since the last check: acc holds <= 61 bits
+        if (b % 3 == 0 && nacc >= 32) {
             nacc -= 32;
             scr[wpos--] = (uint32_t)(acc >> nacc);
         }
+    });
+    if (nacc >= 32) {   // the range may end between check points
+        nacc -= 32;
+        scr[wpos--] = (uint32_t)(acc >> nacc);
     }
     if (nacc) scr[wpos] = (uint32_t)(acc << (32 - nacc));
-    blk_bits[task] = total;
+    blk_bits[task] = (uint32_t)(32 * (kCapW - 1 - wpos) + nacc);
     blk_state[task] = (uint16_t)x;
 }
 
@@ -395,14 +510,14 @@ __global__ void k_chunk_offsets(const int64_t* __restrict__ stream_nbits, const 
     chunk_words[c] = w;
 }
 
-// One wave per task: assemble the stream words whose first bit falls in block g.
+// Sixteen lanes per task: assemble the stream words whose first bit falls in block g.
 __global__ __launch_bounds__(256) void k_chunk_pack(int64_t n_tasks, int64_t nblk, const uint32_t* __restrict__ blk_bits,
                                                     const uint32_t* __restrict__ scratch, const uint32_t* __restrict__ blk_off,
                                                     const int64_t* __restrict__ stream_nbits,
                                                     const int64_t* __restrict__ stream_woff,
                                                     const int64_t* __restrict__ chunk_base, uint32_t* __restrict__ words) {
-    const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
+    const int64_t task = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int lane = threadIdx.x & 15;
     if (task >= n_tasks) return;
     const int64_t sid = task / nblk, g = task % nblk, chunk = sid / LQ_STREAMS;
     const int64_t nbits = stream_nbits[sid];
@@ -410,7 +525,7 @@ __global__ __launch_bounds__(256) void k_chunk_pack(int64_t n_tasks, int64_t nbl
     const int64_t off = blk_off[task];
     uint32_t* out = words + chunk_base[chunk] + stream_woff[sid];
     const int64_t w_first = (off + 31) / 32, w_end = (off + b + 31) / 32;
-    for (int64_t w = w_first + lane; w < w_end; w += 64) {
+    for (int64_t w = w_first + lane; w < w_end; w += 16) {
         int64_t cur = 32 * w;
         const int64_t end = 32 * w + 32 < nbits ? 32 * w + 32 : nbits;
         uint32_t res = 0;
@@ -447,154 +562,138 @@ __global__ void k_chunk_tail(int64_t n_streams, const lq_table* __restrict__ tab
 
 // ------------------------------------------------------------ chunk decode --
 
-// slot -> symbol index LUT of every chunk stream (binary search over cumfreqs)
-__global__ __launch_bounds__(256) void k_chunk_lut(const lq_table* __restrict__ tables, uint16_t* __restrict__ lut) {
-    __shared__ uint32_t cum[LQ_MAXSYM + 1];
+// Decoder LUT of every chunk stream, one u32 per slot:
+// symbol index | f << 9 | (slot - cum) << 20, so a step is x = f * (x >> 10) + bias.
+__global__ __launch_bounds__(256) void k_chunk_lut(const lq_table* __restrict__ tables, uint32_t* __restrict__ lut) {
+    __shared__ int32_t fr[LQ_MAXSYM];
+    __shared__ int32_t cum[LQ_MAXSYM + 1];
     const int64_t sid = blockIdx.x;
     const lq_table* T = tables + sid;
     const int n = T->n_sym;
     if (n == 0) return;
-    if (threadIdx.x == 0) {
-        uint32_t c = 0;
-        for (int i = 0; i < n; i++) { cum[i] = c; c += enc_f(T->enc[i]); }
-        cum[n] = c;
-    }
+    for (int i = threadIdx.x; i < n; i += 256) fr[i] = (int32_t)enc_f(T->enc[i]);
     __syncthreads();
+    exclusive_scan_array(fr, n, cum);
     for (int slot = threadIdx.x; slot < kL; slot += 256) {
         int lo = 0, hi = n - 1;   // largest s with cum[s] <= slot
         while (lo < hi) {
             int mid = (lo + hi + 1) >> 1;
-            if (cum[mid] <= (uint32_t)slot) lo = mid; else hi = mid - 1;
+            if (cum[mid] <= slot) lo = mid; else hi = mid - 1;
         }
-        lut[sid * kL + slot] = (uint16_t)lo;
+        lut[sid * kL + slot] = (uint32_t)lo | ((uint32_t)fr[lo] << 9) | ((uint32_t)(slot - cum[lo]) << 20);
     }
 }
 
 __device__ __forceinline__ int shfl_xor_i(int v, int m) { return __shfl_xor(v, m, 64); }
 
-// Workgroup: 16 blocks x 16 streams of one chunk.  Each lane decodes its
-// stream's symbols of one block from the block checkpoint; the 8 lanes of a
-// (block, coset) run in lockstep, so after step j they hold the 8 symbols of
-// the block's j-th vector of that coset, recover c7's parity with a 3-step
-// xor-shuffle and each store one dequantised coordinate.
+constexpr int kDecBlocks = 32;   // blocks per decode workgroup (x 8 coordinate streams of one coset)
+
+// Workgroup: 32 blocks x the 8 streams of one coset of one chunk.  Each lane
+// decodes its stream's symbols of one block from the block checkpoint; the 8
+// lanes of a block run in lockstep, so after step j they hold the 8 symbols
+// of the block's j-th vector of that coset, recover c7's parity with a 3-step
+// xor-shuffle and each store one dequantised coordinate.  The words buffer
+// needs 2 words of slack after the last stream (one-word read-ahead).
 __global__ __launch_bounds__(256) void k_chunk_decode(const uint32_t* __restrict__ words, const int64_t* __restrict__ chunk_base,
                                                       const int64_t* __restrict__ stream_woff, const uint32_t* __restrict__ blk_off,
                                                       const uint16_t* __restrict__ blk_state, const uint8_t* __restrict__ coset_bits,
                                                       const uint32_t* __restrict__ blk_n1, const lq_table* __restrict__ tables,
-                                                      const uint16_t* __restrict__ scale16, const uint16_t* __restrict__ lutg,
+                                                      const uint16_t* __restrict__ scale16, const uint32_t* __restrict__ lutg,
                                                       int64_t n_heads, int64_t bph, int64_t nblk, void* __restrict__ out,
                                                       int out_dtype) {
-    __shared__ uint16_t lut[LQ_STREAMS][kL];
-    __shared__ uint32_t senc[LQ_STREAMS][LQ_MAXSYM];
-    __shared__ uint16_t list[16][kBlk];
-    __shared__ int slo[LQ_STREAMS], snsym[LQ_STREAMS];
-    __shared__ int sn1[16];
+    __shared__ uint32_t lut[8][kL];
+    __shared__ uint32_t bm[kDecBlocks][kBlk / 32];
     const int tid = threadIdx.x;
     const int64_t V = n_heads * bph;
-    const int64_t groups = (nblk + 15) / 16;
-    const int64_t chunk = blockIdx.x / groups;
-    const int64_t gbase = (blockIdx.x % groups) * 16;
-    const lq_table* T = tables + chunk * LQ_STREAMS;
+    const int64_t groups = (nblk + kDecBlocks - 1) / kDecBlocks;
+    const int64_t chunk = blockIdx.x / (2 * groups);
+    const int64_t rem = blockIdx.x % (2 * groups);
+    const int c = (int)(rem / groups);
+    const int64_t gbase = (rem % groups) * kDecBlocks;
+    const lq_table* T = tables + chunk * LQ_STREAMS + c * 8;
+    if (T[0].n_sym == 0) return;   // the whole coset is empty in this chunk
     {
-        const uint4* src = reinterpret_cast<const uint4*>(lutg + chunk * LQ_STREAMS * kL);
+        const uint4* src = reinterpret_cast<const uint4*>(lutg + (chunk * LQ_STREAMS + c * 8) * kL);
         uint4* dst = reinterpret_cast<uint4*>(&lut[0][0]);
-        for (int i = tid; i < LQ_STREAMS * kL / 8; i += 256) dst[i] = src[i];
-    }
-    for (int i = tid; i < LQ_STREAMS * LQ_MAXSYM; i += 256) {
-        int s = i / LQ_MAXSYM, j = i % LQ_MAXSYM;
-        senc[s][j] = j < T[s].n_sym ? T[s].enc[j] : 0u;
-    }
-    if (tid < LQ_STREAMS) { slo[tid] = T[tid].lo; snsym[tid] = T[tid].n_sym; }
-    // coset index lists: thread (block b, part p) scans 32 vectors
-    {
-        const int b = tid >> 4, p = tid & 15;
-        const int64_t g = gbase + b;
-        uint32_t bits = 0;
-        int valid = 0;
-        if (g < nblk) {
-            bits = reinterpret_cast<const uint32_t*>(coset_bits + (chunk * nblk + g) * (kBlk / 8))[p];
-            int64_t vv = V - g * kBlk;
-            valid = (int)(vv < kBlk ? vv : kBlk);
+        for (int i = tid; i < 8 * kL / 4; i += 256) dst[i] = src[i];
+        for (int i = tid; i < kDecBlocks * (kBlk / 32); i += 256) {
+            const int b = i / (kBlk / 32), w = i % (kBlk / 32);
+            const int64_t g = gbase + b;
+            bm[b][w] = g < nblk ? reinterpret_cast<const uint32_t*>(coset_bits + (chunk * nblk + g) * (kBlk / 8))[w] : 0u;
         }
-        int lo_v = p * 32;
-        int nv = valid - lo_v;
-        nv = nv < 0 ? 0 : (nv > 32 ? 32 : nv);
-        uint32_t vmask = nv == 32 ? 0xffffffffu : ((1u << nv) - 1u);
-        bits &= vmask;
-        int c1 = __popc(bits);
-        // exclusive prefix of coset-1 counts over the 16 parts of this block (lanes tid & ~15 .. )
-        int incl = c1;
-        for (int o = 1; o < 16; o <<= 1) {
-            int t = __shfl_up(incl, o, 16);
-            if (p >= o) incl += t;
-        }
-        int r1 = incl - c1;
-        int total1 = __shfl(incl, 15, 16);
-        int n0 = valid - total1;
-        int r0 = lo_v - r1;
-        for (int i = 0; i < nv; i++) {
-            int vl = lo_v + i;
-            if ((bits >> i) & 1u) list[b][n0 + r1++] = (uint16_t)vl;
-            else list[b][r0++] = (uint16_t)vl;
-        }
-        if (p == 0) sn1[b] = total1;
     }
     __syncthreads();
-
-    const int b = tid >> 4;
-    const int st = tid & 15;
+    const int b = tid >> 3, idx = tid & 7;
     const int64_t g = gbase + b;
-    if (g >= nblk || snsym[st] == 0) return;   // whole (block, coset) groups leave together
-    const int c = st >> 3, idx = st & 7;
-    const int64_t vv = V - g * kBlk;
-    const int valid = (int)(vv < kBlk ? vv : kBlk);
-    const int n1 = sn1[b], n0 = valid - n1;
-    const int ncnt = c ? n1 : n0;
-    const int lbase = c ? n0 : 0;
+    if (g >= nblk) return;   // whole 8-lane groups leave together
+    const int st = c * 8 + idx;
     const int64_t task = (chunk * LQ_STREAMS + st) * nblk + g;
+    const int64_t vfirst = g * kBlk;                 // first vector of the block, within the chunk
+    const int valid = (int)(V - vfirst < kBlk ? V - vfirst : kBlk);
+    const uint32_t n1 = blk_n1[chunk * nblk + g];
+    const int ncnt = c ? (int)n1 : valid - (int)n1;
+    const int lo_sym = T[idx].lo;
     const uint32_t* wb = words + chunk_base[chunk] + stream_woff[chunk * LQ_STREAMS + st];
     uint32_t x = blk_state[task];
     const uint32_t bp = blk_off[task];
     uint32_t nwi = bp >> 5;
     uint64_t buf = 0;
-    uint32_t nbuf = 0;
+    uint32_t nbuf = 0, pre = 0;
     if (ncnt > 0) {
         buf = ((uint64_t)__builtin_bitreverse32(wb[nwi]) << 32) << (bp & 31);
         nbuf = 32 - (bp & 31);
-        nwi++;
+        pre = wb[++nwi];
     }
-    const uint16_t* L = lut[st];
-    const uint32_t* E = senc[st];
-    const int lo_sym = slo[st];
+    const uint32_t* LU = lut[idx];
+    // coset-c vectors of the block in ascending order, from the LDS bitmap
+    int wi = 0;
+    auto word_of = [&](int w) -> uint32_t {
+        uint32_t m = bm[b][w];
+        if (!c) m = ~m;
+        const int lim = valid - 32 * w;
+        return lim >= 32 ? m : (lim <= 0 ? 0u : m & ((1u << lim) - 1u));
+    };
+    uint32_t wv = word_of(0);
+    // per-head scale, refreshed when the vector index crosses a head boundary
+    int64_t head = vfirst / bph;
+    int64_t next_head = (head + 1) * bph;
+    float sc = h2f(scale16[chunk * n_heads + head]);
     const float off = c ? 0.5f : 0.f;
-    const int64_t vbase = chunk * V + g * kBlk;
+    const int64_t vout0 = chunk * V + vfirst;
     for (int j = 0; j < ncnt; j++) {
-        uint32_t slot = x & (kL - 1);
-        uint32_t s = L[slot];
-        uint32_t e = E[s];
-        x = enc_f(e) * (x >> 10) + slot - enc_c(e);
+        const uint32_t slot = x & (kL - 1);
+        const uint32_t e = LU[slot];
+        x = ((e >> 9) & 0x7ffu) * (x >> 10) + (e >> 20);
         if (x < (uint32_t)kL) {
-            uint32_t k = (uint32_t)__clz((int)x) - 21u;
+            const uint32_t k = (uint32_t)__clz((int)x) - 21u;
             if (nbuf < k) {
-                buf |= ((uint64_t)__builtin_bitreverse32(wb[nwi++]) << 32) >> nbuf;
+                buf |= ((uint64_t)__builtin_bitreverse32(pre) << 32) >> nbuf;
                 nbuf += 32;
+                pre = wb[++nwi];
             }
             x = (x << k) | (uint32_t)(buf >> (64 - k));
             buf <<= k;
             nbuf -= k;
         }
-        int val = lo_sym + (int)s;
+        const int val = lo_sym + (int)(e & 511u);
         int contrib = idx < 7 ? val : 0;
         contrib += shfl_xor_i(contrib, 1);
         contrib += shfl_xor_i(contrib, 2);
         contrib += shfl_xor_i(contrib, 4);
-        int coord = idx < 7 ? val : 2 * val + (contrib & 1);
-        int vl = list[b][lbase + j];
-        int64_t v = vbase + vl;
-        float sc = h2f(scale16[chunk * n_heads + (g * kBlk + vl) / bph]);
-        float y = ((float)coord + off) * sc;
-        if (out_dtype == LQ_F32) reinterpret_cast<float*>(out)[v * 8 + idx] = y;
-        else reinterpret_cast<uint16_t*>(out)[v * 8 + idx] = f2dtype(y, out_dtype);
+        const int coord = idx < 7 ? val : 2 * val + (contrib & 1);
+        while (wv == 0) wv = word_of(++wi);
+        const int vl = 32 * wi + __builtin_ctz(wv);
+        wv &= wv - 1u;
+        const int64_t vch = vfirst + vl;
+        if (vch >= next_head) {
+            head = vch / bph;
+            next_head = (head + 1) * bph;
+            sc = h2f(scale16[chunk * n_heads + head]);
+        }
+        const float y = ((float)coord + off) * sc;
+        const int64_t o = (vout0 + vl) * 8 + idx;
+        if (out_dtype == LQ_F32) reinterpret_cast<float*>(out)[o] = y;
+        else reinterpret_cast<uint16_t*>(out)[o] = f2dtype(y, out_dtype);
     }
 }
 
@@ -619,18 +718,22 @@ __global__ __launch_bounds__(256) void k_build_tables(const int64_t* __restrict_
     for (int i = threadIdx.x; i < n; i += 256) cnt[i] = counts[o + i];
     if (threadIdx.x == 0) s_st = 0;
     __syncthreads();
-    normalise(cnt, n, fr, keys, perm, &s_st);
+    __shared__ int64_t kk[kL];
+    __shared__ int8_t inset[kL];
+    normalise(cnt, n, fr, keys, perm, kk, inset, &s_st);
+    __shared__ int32_t cum[kL + 1];
+    exclusive_scan_array(fr, n, cum);
     for (int i = threadIdx.x; i < n; i += 256) freqs_out[o + i] = fr[i];
-    if (threadIdx.x == 0) {
-        int32_t c = 0;
-        for (int i = 0; i < n; i++) {
-            cum_out[o + t + i] = c;
-            for (int j = c; j < c + fr[i]; j++) lookup[(int64_t)t * kL + j] = i;
-            c += fr[i];
+    for (int i = threadIdx.x; i <= n; i += 256) cum_out[o + t + i] = cum[i];
+    for (int slot = threadIdx.x; slot < kL; slot += 256) {   // largest s with cum[s] <= slot
+        int lo = 0, hi = n - 1;
+        while (lo < hi) {
+            int mid = (lo + hi + 1) >> 1;
+            if (cum[mid] <= slot) lo = mid; else hi = mid - 1;
         }
-        cum_out[o + t + n] = c;
-        status[t] = s_st;
+        lookup[(int64_t)t * kL + slot] = lo;
     }
+    if (threadIdx.x == 0) status[t] = s_st;
 }
 
 // ------------------------------------------------------ generic streams --
@@ -769,7 +872,7 @@ int lq_chunk_pack(int64_t n_chunks, int64_t n_vectors, const lq_table* d_tables,
     const uint32_t* bits = reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(d_work) + w.bits);
     const uint32_t* scratch = reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(d_work) + w.scratch);
     const int64_t tasks = n_chunks * LQ_STREAMS * nblk;
-    hipLaunchKernelGGL(k_chunk_pack, dim3((unsigned)((tasks + 3) / 4)), dim3(256), 0, s, tasks, nblk, bits, scratch,
+    hipLaunchKernelGGL(k_chunk_pack, dim3((unsigned)((tasks + 15) / 16)), dim3(256), 0, s, tasks, nblk, bits, scratch,
                        d_blk_off, d_stream_nbits, d_stream_woff, d_chunk_base, d_words);
     const int64_t ns = n_chunks * LQ_STREAMS;
     hipLaunchKernelGGL(k_chunk_tail, dim3((unsigned)((ns + 255) / 256)), dim3(256), 0, s, ns, d_tables,
@@ -780,13 +883,13 @@ int lq_chunk_pack(int64_t n_chunks, int64_t n_vectors, const lq_table* d_tables,
 int lq_chunk_decode(const uint32_t* d_words, const int64_t* d_chunk_base, const int64_t* d_stream_woff,
                     const uint32_t* d_blk_off, const uint16_t* d_blk_state, const uint8_t* d_coset_bits,
                     const uint32_t* d_blk_n1, const lq_table* d_tables, const uint16_t* d_scale16, int64_t n_chunks,
-                    int64_t n_heads, int64_t bph, uint16_t* d_lut_work, void* d_out, int out_dtype, hipStream_t s) {
+                    int64_t n_heads, int64_t bph, uint32_t* d_lut_work, void* d_out, int out_dtype, hipStream_t s) {
     if (n_chunks <= 0 || n_heads <= 0 || bph <= 0 || out_dtype < 0 || out_dtype > 2) return LQ_ERR_ARG;
     const int64_t V = n_heads * bph;
     const int64_t nblk = (V + kBlk - 1) / kBlk;
     hipLaunchKernelGGL(k_chunk_lut, dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, d_tables, d_lut_work);
-    const int64_t groups = (nblk + 15) / 16;
-    hipLaunchKernelGGL(k_chunk_decode, dim3((unsigned)(n_chunks * groups)), dim3(256), 0, s, d_words, d_chunk_base,
+    const int64_t groups = (nblk + kDecBlocks - 1) / kDecBlocks;
+    hipLaunchKernelGGL(k_chunk_decode, dim3((unsigned)(n_chunks * 2 * groups)), dim3(256), 0, s, d_words, d_chunk_base,
                        d_stream_woff, d_blk_off, d_blk_state, d_coset_bits, d_blk_n1, d_tables, d_scale16, d_lut_work,
                        n_heads, bph, nblk, d_out, out_dtype);
     return launch_status();
