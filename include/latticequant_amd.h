@@ -30,6 +30,7 @@ extern "C" {
 
 #define LQ_L 1024          /* rANS precision (reference core/gpu_ans.py:44-45) */
 #define LQ_BLK 512         /* vectors per checkpoint block */
+#define LQ_SYM_STRIDE 4352 /* int8 symbol bytes per block (8 * LQ_BLK + 2 x 128 padding) */
 #define LQ_MAXSYM 264      /* alphabet capacity of a chunk table (int8 symbols + 4 guard entries) */
 #define LQ_STREAMS 16      /* 2 cosets x 8 coordinate streams per chunk */
 
@@ -92,8 +93,9 @@ int lq_scale_fastdiv(const float *d_scale32, int64_t n_heads_total, int dtype, i
                      hipStream_t s);
 
 /* Quantize a batch of chunks: x / scale -> E8 nearest point -> symbols.
- * Writes, per chunk: int8 symbols grouped per LQ_BLK block as coset-0 columns
- * then coset-1 columns (d_sym, n_chunks * nblk * LQ_BLK * 8 bytes), the coset
+ * Writes, per chunk: int8 symbols grouped per LQ_BLK block, coset-0 columns
+ * then coset-1 columns, the 8 columns of a coset interleaved in 16-byte units
+ * (d_sym, n_chunks * nblk * LQ_SYM_STRIDE bytes), the coset
  * bitmap in the reference's LSB-first byte order (d_coset_bits,
  * n_chunks * nblk * LQ_BLK / 8 bytes), the coset-1 count per block (d_blk_n1),
  * the 16 x 256 symbol histograms (d_hist, must be zero on entry) and status

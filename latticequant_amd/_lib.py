@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(_HERE, "liblatticequant_amd.so")
 
 LQ_L = 1024
 LQ_BLK = 512
+LQ_SYM_STRIDE = 4352
 LQ_MAXSYM = 264
 LQ_STREAMS = 16
 LQ_F16, LQ_BF16, LQ_F32 = 0, 1, 2

@@ -144,7 +144,7 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
             raise ValueError("scale32 must hold one scale per head of every chunk")
         scale16 = scale32.to(torch.float16)
         L.check(lib.lq_scale_fastdiv(scale32.data_ptr(), C * nh, dt, fastdiv.data_ptr(), s), "lq_scale_fastdiv")
-    sym = _empty(C * nblk * L.LQ_BLK * 8, torch.int8, dev)
+    sym = _empty(C * nblk * L.LQ_SYM_STRIDE, torch.int8, dev)
     coset_bits = _zeros(C * nblk * L.LQ_BLK // 8, torch.uint8, dev)
     blk_n1 = _empty(C * nblk, torch.int32, dev)
     hist = _zeros(C * L.LQ_STREAMS * 256, torch.int32, dev)

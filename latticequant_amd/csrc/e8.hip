@@ -148,7 +148,7 @@ constexpr int kQBlocksPerWG = 4;
 // One workgroup quantizes kQBlocksPerWG consecutive LQ_BLK-vector blocks of one
 // chunk.  Per block it writes the coset bitmap (wave ballots, i.e. the
 // reference's LSB-first pack_coset_bits layout), the coset-1 count and the int8
-// symbols as coset-0 columns followed by coset-1 columns, staged in LDS so the
+// symbols in the interleaved column layout of sym_pos, staged in LDS so the
 // global stores are 16-byte and contiguous.  Histograms accumulate in LDS and
 // are flushed once per workgroup.
 __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
@@ -157,7 +157,7 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
     uint8_t* __restrict__ coset_bits, uint32_t* __restrict__ blk_n1, uint32_t* __restrict__ hist,
     int32_t* __restrict__ status, void* __restrict__ deq, int deq_dtype) {
     __shared__ uint32_t shist[LQ_STREAMS * 256];
-    __shared__ __align__(16) int8_t stage[kBlk * 8];
+    __shared__ __align__(16) int8_t stage[kSymStride];
     __shared__ unsigned long long masks[kBlk / 64];
     __shared__ int sflag;
 
@@ -232,11 +232,13 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
                 int rank1 = before + below;
                 int rank0 = vl - rank1;
                 const int c = cs[r];
+                const int rk = c ? rank1 : rank0;
+                int8_t* sp = stage + sym_pos(c, 0, rk, n0);   // column i adds 16 * i
+                uint32_t* hp = shist + c * 8 * 256 + 128;
 #pragma unroll
                 for (int i = 0; i < 8; i++) {
-                    int pos = c ? 8 * n0 + i * n1 + rank1 : i * n0 + rank0;
-                    stage[pos] = sy[r][i];
-                    atomicAdd(&shist[(c * 8 + i) * 256 + ((int)sy[r][i] + 128)], 1u);
+                    sp[16 * i] = sy[r][i];
+                    atomicAdd(hp + i * 256 + (int)sy[r][i], 1u);
                 }
             }
         }
@@ -244,8 +246,8 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
         // copy-out: symbols, coset bitmap, block count
         {
             const int64_t gblk = chunk * nblk + blk;
-            const int nbytes = valid * 8;
-            uint4* dst = reinterpret_cast<uint4*>(sym + gblk * (int64_t)kBlk * 8);
+            const int nbytes = sym_region(1, n0) + 128 * ((n1 + 15) >> 4);
+            uint4* dst = reinterpret_cast<uint4*>(sym + gblk * (int64_t)kSymStride);
             const uint4* src = reinterpret_cast<const uint4*>(stage);
             for (int i = tid; i * 16 < nbytes; i += kQThreads) dst[i] = src[i];
             unsigned long long* cb = reinterpret_cast<unsigned long long*>(coset_bits + gblk * (kBlk / 8));

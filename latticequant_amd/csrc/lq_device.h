@@ -9,6 +9,8 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "latticequant_amd.h"
 
 namespace lq {
@@ -16,6 +18,17 @@ namespace lq {
 constexpr int kL = LQ_L;
 constexpr int kBlk = LQ_BLK;
 constexpr int kCapW = (10 * LQ_BLK + 31) / 32;   // scratch words per (stream, block) task
+constexpr int kSymStride = LQ_SYM_STRIDE;        // bytes of int8 symbols per block
+
+// Symbols of one block: the coset-0 region then the coset-1 region, each
+// holding its 8 equal-length coordinate columns interleaved in 16-byte units
+// (chunk k of column i at (8 k + i) * 16), so the 8 lanes that walk the 8
+// columns of a (block, coset) together read one full 128-byte line per step.
+// Byte offset of rank r of column i of coset c, given the block's coset-0 count.
+__device__ __forceinline__ int sym_region(int c, int n0) { return c ? 128 * ((n0 + 15) >> 4) : 0; }
+__device__ __forceinline__ int sym_pos(int c, int i, int r, int n0) {
+    return sym_region(c, n0) + ((((r >> 4) << 3) + i) << 4) + (r & 15);
+}
 
 // torch.arange(8, dtype=f32) * 1e-7  ==  RN32(i * f32(1e-7))   (core/e8_quantizer.py:42-44)
 __device__ __forceinline__ float tiebreak(int i) {

@@ -281,10 +281,12 @@ __global__ __launch_bounds__(256) void k_chunk_tables(const uint32_t* __restrict
 // ------------------------------------------------------------ chunk encode --
 //
 // Task = (chunk, stream st = coset * 8 + coord, block g), one lane each; a
-// 256-thread workgroup holds 16 consecutive blocks x 16 streams of one chunk.
+// 256-thread workgroup holds 16 consecutive blocks x 16 streams of one chunk,
+// so the 8 lanes of a (block, coset) read the 8 interleaved columns of that
+// coset one 128-byte line at a time (sym_pos layout).
 
 struct Col {
-    const int8_t* p;
+    const int8_t* p;   // chunk 0 of the column; chunk k at p + 128 k
     int n;
 };
 
@@ -293,9 +295,8 @@ __device__ __forceinline__ Col column(const int8_t* sym, const uint32_t* blk_n1,
     uint32_t n1 = blk_n1[chunk * nblk + h];
     int64_t valid = V - h * kBlk < kBlk ? V - h * kBlk : kBlk;
     int n0 = (int)valid - (int)n1;
-    const int8_t* base = sym + (chunk * nblk + h) * (int64_t)kBlk * 8;
     Col col;
-    col.p = c ? base + 8 * n0 + idx * (int)n1 : base + idx * n0;
+    col.p = sym + (chunk * nblk + h) * (int64_t)kSymStride + sym_region(c, n0) + 16 * idx;
     col.n = c ? (int)n1 : n0;
     return col;
 }
@@ -329,35 +330,43 @@ __device__ __forceinline__ void hull_step(uint32_t& lo, uint32_t& hi, uint32_t e
     }
 }
 
-// f(v, b) for the int8 symbols p[n-1], p[n-2], .., p[0], read with aligned
-// 16-byte loads; the next chunk's load is issued before the current chunk is
-// consumed.  b is the symbol's byte index inside its 16-byte chunk (a
-// compile-time constant after unrolling); only the first and the last chunk
-// of the range can be partial.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const u32x4_t gconst_u32x4;
+
+// 16-byte load through a global (address space 1) pointer: a global_load, not
+// a flat load, so it does not hold up waits on LDS results.
+__device__ __forceinline__ uint4 gload16(uintptr_t a) {
+    u32x4_t v = *reinterpret_cast<gconst_u32x4*>(a);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// f(v, b, in) for the column symbols of ranks n-1, n-2, .., 0 (the column's
+// 16-symbol chunk k sits at p + 128 k), read with 16-byte loads issued one
+// chunk ahead.  b is the symbol's byte index in its chunk (a compile-time
+// constant after unrolling).  Only a column's top chunk can be partial.
+// Control flow is wave-uniform: the loop runs while any lane has chunks left,
+// takes the unconditional path when every lane holds a full chunk and
+// otherwise passes a per-lane predicate; f must leave its state unchanged
+// when in == false.
 template <typename F>
 __device__ __forceinline__ void for_each_rev(const int8_t* p, int n, F&& f) {
-    if (n <= 0) return;
-    const uintptr_t a0 = (uintptr_t)p, a1 = a0 + (uintptr_t)n;
-    const uintptr_t cfirst = a0 & ~(uintptr_t)15;
-    uintptr_t c = (a1 - 1) & ~(uintptr_t)15;
-    uint4 cur = *reinterpret_cast<const uint4*>(c);
-    uint4 nxt = c > cfirst ? *reinterpret_cast<const uint4*>(c - 16) : make_uint4(0, 0, 0, 0);
-    for (;;) {
+    int k = n > 0 ? (n - 1) >> 4 : -1;   // current chunk
+    const uintptr_t base = (uintptr_t)p;
+    uint4 cur = k >= 0 ? gload16(base + 128 * (uintptr_t)k) : make_uint4(0, 0, 0, 0);
+    uint4 nxt = k >= 1 ? gload16(base + 128 * (uintptr_t)(k - 1)) : make_uint4(0, 0, 0, 0);
+    while (__any(k >= 0)) {
         const uint32_t w[4] = {cur.x, cur.y, cur.z, cur.w};
-        const int lo_b = c >= a0 ? 0 : (int)(a0 - c);
-        const int hi_b = c + 16 <= a1 ? 16 : (int)(a1 - c);
-        if (lo_b == 0 && hi_b == 16) {
+        const int hi_b = k < 0 ? 0 : (n - 16 * k < 16 ? n - 16 * k : 16);
+        if (__all(hi_b == 16)) {
 #pragma unroll
-            for (int b = 15; b >= 0; b--) f((int)(int8_t)(w[b >> 2] >> ((b & 3) * 8)), b);
+            for (int b = 15; b >= 0; b--) f((int)(int8_t)(w[b >> 2] >> ((b & 3) * 8)), b, true);
         } else {
 #pragma unroll
-            for (int b = 15; b >= 0; b--)
-                if (b >= lo_b && b < hi_b) f((int)(int8_t)(w[b >> 2] >> ((b & 3) * 8)), b);
+            for (int b = 15; b >= 0; b--) f((int)(int8_t)(w[b >> 2] >> ((b & 3) * 8)), b, b < hi_b);
         }
-        if (c == cfirst) break;
-        c -= 16;
+        k--;
         cur = nxt;
-        if (c > cfirst) nxt = *reinterpret_cast<const uint4*>(c - 16);
+        if (k >= 1) nxt = gload16(base + 128 * (uintptr_t)(k - 1));
     }
 }
 
@@ -375,16 +384,20 @@ __host__ __device__ inline EncWork enc_layout(int64_t n_chunks, int64_t n_vector
     return w;
 }
 
+constexpr int kEncBlocks = 16;   // blocks per encode workgroup (x 16 streams)
+
+// Grid: (block groups, chunks).  The scratch words of a task are collected in
+// an 8-word register queue and stored as aligned 32-byte pieces.
 __global__ __launch_bounds__(256) void k_chunk_encode(const int8_t* __restrict__ sym, const uint32_t* __restrict__ blk_n1,
                                                       int64_t nblk, int64_t V, const lq_table* __restrict__ tables,
                                                       uint32_t* __restrict__ blk_bits, uint32_t* __restrict__ scratch,
                                                       uint16_t* __restrict__ blk_state) {
-    __shared__ uint32_t senc[LQ_STREAMS][LQ_MAXSYM];
+    // odd row stride: the 16 stream tables start in different LDS banks
+    __shared__ uint32_t senc[LQ_STREAMS][LQ_MAXSYM + 1];
     __shared__ int slo[LQ_STREAMS], snsym[LQ_STREAMS];
     const int tid = threadIdx.x;
-    const int64_t groups = (nblk + 15) / 16;
-    const int64_t chunk = blockIdx.x / groups;
-    const int64_t g = (blockIdx.x % groups) * 16 + (tid >> 4);
+    const int64_t chunk = blockIdx.y;
+    const int64_t g = (int64_t)blockIdx.x * kEncBlocks + (tid >> 4);
     const int st = tid & 15;
     const lq_table* T = tables + chunk * LQ_STREAMS;
     for (int i = tid; i < LQ_STREAMS * LQ_MAXSYM; i += 256) {
@@ -426,10 +439,18 @@ __global__ __launch_bounds__(256) void k_chunk_encode(const int8_t* __restrict__
             const int cnt = (b == hb && !exact) ? need : col.n;
             if (lo == hi) {
                 uint32_t xx = lo, k;
-                for_each_rev(col.p, cnt, [&](int v, int) { xx = encx_step(xx, enc(v), &k); });
+                for_each_rev(col.p, cnt, [&](int v, int, bool in) {
+                    const uint32_t xn = encx_step(xx, enc(in ? v : lo_sym), &k);
+                    xx = in ? xn : xx;
+                });
                 lo = hi = xx;
             } else {
-                for_each_rev(col.p, cnt, [&](int v, int) { hull_step(lo, hi, enc(v)); });
+                for_each_rev(col.p, cnt, [&](int v, int, bool in) {
+                    uint32_t l2 = lo, h2 = hi;
+                    hull_step(l2, h2, enc(in ? v : lo_sym));
+                    lo = in ? l2 : lo;
+                    hi = in ? h2 : hi;
+                });
             }
         }
         if (lo == hi) { x = lo; break; }
@@ -439,27 +460,51 @@ __global__ __launch_bounds__(256) void k_chunk_encode(const int8_t* __restrict__
     // ---- encode block g, bits right-aligned in the task's scratch region
     Col col = column(sym, blk_n1, chunk, nblk, V, g, c, idx);
     uint32_t* scr = scratch + task * (int64_t)kCapW;
-    int wpos = kCapW - 1;
+    // words leave in decreasing address order from kCapW - 1; queue word j of the
+    // current 8-word group at q[j] (newest at q[0]) and store the group when full
+    uint32_t q[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int nq = 0, gbase = kCapW - 8, nwords = 0;
+    auto push = [&](uint32_t word) {
+#pragma unroll
+        for (int j = 7; j > 0; j--) q[j] = q[j - 1];
+        q[0] = word;
+        nwords++;
+        if (++nq == 8) {
+            uint4* d = reinterpret_cast<uint4*>(scr + gbase);
+            d[0] = make_uint4(q[0], q[1], q[2], q[3]);
+            d[1] = make_uint4(q[4], q[5], q[6], q[7]);
+            gbase -= 8;
+            nq = 0;
+        }
+    };
     uint64_t acc = 0;
     uint32_t nacc = 0;
-    for_each_rev(col.p, col.n, [&](int v, int b) {
-        uint32_t k, xin = x;
-        x = encx_step(x, enc(v), &k);
+    for_each_rev(col.p, col.n, [&](int v, int b, bool in) {
+        uint32_t k;
+        const uint32_t xin = x;
+        const uint32_t xn = encx_step(xin, enc(in ? v : lo_sym), &k);
+        k = in ? k : 0u;
+        x = in ? xn : xin;
         // emitted group in final stream order: the k low bits of xin, most significant first
         acc = (acc << k) | (((uint64_t)__builtin_bitreverse32(xin) << k) >> 32);
         nacc += k;
         // at most 3 symbols (<= 30 bits) since the last check: acc holds <= 61 bits
         if (b % 3 == 0 && nacc >= 32) {
             nacc -= 32;
-            scr[wpos--] = (uint32_t)(acc >> nacc);
+            push((uint32_t)(acc >> nacc));
         }
     });
     if (nacc >= 32) {   // the range may end between check points
         nacc -= 32;
-        scr[wpos--] = (uint32_t)(acc >> nacc);
+        push((uint32_t)(acc >> nacc));
     }
-    if (nacc) scr[wpos] = (uint32_t)(acc << (32 - nacc));
-    blk_bits[task] = (uint32_t)(32 * (kCapW - 1 - wpos) + nacc);
+    const uint32_t total = 32u * (uint32_t)nwords + nacc;
+    if (nacc) push((uint32_t)(acc << (32 - nacc)));
+    // complete the last group with filler words below the data (never read)
+#pragma unroll
+    for (int j = 0; j < 7; j++)
+        if (nq != 0) push(0u);
+    blk_bits[task] = total;
     blk_state[task] = (uint16_t)x;
 }
 
@@ -510,45 +555,55 @@ __global__ void k_chunk_offsets(const int64_t* __restrict__ stream_nbits, const 
     chunk_words[c] = w;
 }
 
-// Sixteen lanes per task: assemble the stream words whose first bit falls in block g.
+// Sixteen lanes per task.  A task owns the stream words whose first bit falls
+// in its block.  Words that end inside the block are a funnel shift of its
+// right-aligned scratch by one per-task shift; only the word holding the
+// block's last bit (when that is not word-aligned) reaches into later blocks.
 __global__ __launch_bounds__(256) void k_chunk_pack(int64_t n_tasks, int64_t nblk, const uint32_t* __restrict__ blk_bits,
                                                     const uint32_t* __restrict__ scratch, const uint32_t* __restrict__ blk_off,
                                                     const int64_t* __restrict__ stream_nbits,
                                                     const int64_t* __restrict__ stream_woff,
                                                     const int64_t* __restrict__ chunk_base, uint32_t* __restrict__ words) {
-    const int64_t task = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int64_t g = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);   // grid: (blocks / 16, chunks * 16)
     const int lane = threadIdx.x & 15;
-    if (task >= n_tasks) return;
-    const int64_t sid = task / nblk, g = task % nblk, chunk = sid / LQ_STREAMS;
-    const int64_t nbits = stream_nbits[sid];
+    if (g >= nblk) return;
+    const int64_t sid = blockIdx.y, chunk = sid / LQ_STREAMS;
+    const int64_t task = sid * nblk + g;
     const uint32_t b = blk_bits[task];
+    if (b == 0) return;
     const int64_t off = blk_off[task];
     uint32_t* out = words + chunk_base[chunk] + stream_woff[sid];
-    const int64_t w_first = (off + 31) / 32, w_end = (off + b + 31) / 32;
-    for (int64_t w = w_first + lane; w < w_end; w += 16) {
-        int64_t cur = 32 * w;
-        const int64_t end = 32 * w + 32 < nbits ? 32 * w + 32 : nbits;
-        uint32_t res = 0;
-        int64_t h = g;
-        int64_t ho = off;
-        uint32_t hb = b;
-        while (cur < end) {
-            while (cur >= ho + hb) { h++; ho = blk_off[sid * nblk + h]; hb = blk_bits[sid * nblk + h]; }
-            int64_t lim = end < ho + hb ? end : ho + hb;
-            int take = (int)(lim - cur);
-            int64_t sp = (int64_t)kCapW * 32 - hb + (cur - ho);
-            const uint32_t* scr = scratch + (sid * nblk + h) * (int64_t)kCapW;
-            int64_t wi = sp >> 5;
-            int sh = (int)(sp & 31);
-            uint64_t v = scr[wi];
-            if (sh + take > 32) v |= (uint64_t)scr[wi + 1] << 32;
-            v >>= sh;
-            uint32_t bits = take == 32 ? (uint32_t)v : (uint32_t)v & ((1u << take) - 1u);
-            res |= bits << (int)(cur - 32 * w);
-            cur += take;
-        }
-        out[w] = res;
+    const uint32_t* scr = scratch + task * (int64_t)kCapW;
+    const int64_t w_first = (off + 31) >> 5, w_full = (off + b) >> 5;
+    const int64_t sp0 = (int64_t)kCapW * 32 - b + 32 * w_first - off;   // scratch bit of word w_first
+    const int sh = (int)(sp0 & 31);
+    const int64_t k0 = sp0 >> 5;
+    for (int64_t j = lane; w_first + j < w_full; j += 16) {
+        uint64_t v = scr[k0 + j];
+        if (sh) v |= (uint64_t)scr[k0 + j + 1] << 32;
+        out[w_first + j] = (uint32_t)(v >> sh);
     }
+    const int64_t wl = (off + b) >> 5;
+    if (lane != 0 || ((off + b) & 31) == 0 || 32 * wl < off) return;
+    // word wl: bits [32 wl, off + b) from this block, the rest from the next blocks
+    const int64_t nbits = stream_nbits[sid];
+    const int64_t end = 32 * wl + 32 < nbits ? 32 * wl + 32 : nbits;
+    int64_t cur = 32 * wl, ho = off, t = task;
+    uint32_t hb = b, res = 0;
+    while (cur < end) {
+        while (cur >= ho + hb) { t++; ho = blk_off[t]; hb = blk_bits[t]; }
+        const int64_t lim = end < ho + hb ? end : ho + hb;
+        const int take = (int)(lim - cur);
+        const int64_t sp = (int64_t)kCapW * 32 - hb + (cur - ho);
+        const uint32_t* sc = scratch + t * (int64_t)kCapW;
+        const int s2 = (int)(sp & 31);
+        uint64_t v = sc[sp >> 5];
+        if (s2 + take > 32) v |= (uint64_t)sc[(sp >> 5) + 1] << 32;
+        v >>= s2;
+        res |= (take == 32 ? (uint32_t)v : (uint32_t)v & ((1u << take) - 1u)) << (int)(cur - 32 * wl);
+        cur += take;
+    }
+    out[wl] = res;
 }
 
 // trailing zero word of every present stream
@@ -584,23 +639,23 @@ __global__ __launch_bounds__(256) void k_chunk_lut(const lq_table* __restrict__ 
     }
 }
 
-__device__ __forceinline__ int shfl_xor_i(int v, int m) { return __shfl_xor(v, m, 64); }
-
 constexpr int kDecBlocks = 32;   // blocks per decode workgroup (x 8 coordinate streams of one coset)
 
 // Workgroup: 32 blocks x the 8 streams of one coset of one chunk.  Each lane
 // decodes its stream's symbols of one block from the block checkpoint; the 8
 // lanes of a block run in lockstep, so after step j they hold the 8 symbols
-// of the block's j-th vector of that coset, recover c7's parity with a 3-step
-// xor-shuffle and each store one dequantised coordinate.  The words buffer
-// needs 2 words of slack after the last stream (one-word read-ahead).
+// of the block's j-th vector of that coset, recover c7's parity from one
+// wave ballot of the low bits and each store one dequantised coordinate.
+// HEADS_ALIGNED: bph is a multiple of the block size, so a block lies in one
+// head.  The words buffer needs 2 words of slack after the last stream
+// (one-word read-ahead).
+template <int OUT_DT, bool HEADS_ALIGNED>
 __global__ __launch_bounds__(256) void k_chunk_decode(const uint32_t* __restrict__ words, const int64_t* __restrict__ chunk_base,
                                                       const int64_t* __restrict__ stream_woff, const uint32_t* __restrict__ blk_off,
                                                       const uint16_t* __restrict__ blk_state, const uint8_t* __restrict__ coset_bits,
                                                       const uint32_t* __restrict__ blk_n1, const lq_table* __restrict__ tables,
                                                       const uint16_t* __restrict__ scale16, const uint32_t* __restrict__ lutg,
-                                                      int64_t n_heads, int64_t bph, int64_t nblk, void* __restrict__ out,
-                                                      int out_dtype) {
+                                                      int64_t n_heads, int64_t bph, int64_t nblk, void* __restrict__ out) {
     __shared__ uint32_t lut[8][kL];
     __shared__ uint32_t bm[kDecBlocks][kBlk / 32];
     const int tid = threadIdx.x;
@@ -654,46 +709,48 @@ __global__ __launch_bounds__(256) void k_chunk_decode(const uint32_t* __restrict
         return lim >= 32 ? m : (lim <= 0 ? 0u : m & ((1u << lim) - 1u));
     };
     uint32_t wv = word_of(0);
-    // per-head scale, refreshed when the vector index crosses a head boundary
-    int64_t head = vfirst / bph;
-    int64_t next_head = (head + 1) * bph;
-    float sc = h2f(scale16[chunk * n_heads + head]);
+    // per-head scale; without HEADS_ALIGNED it is refreshed when the vector
+    // index crosses a head boundary (vectors come in ascending order)
+    const int64_t head0 = vfirst / bph;
+    const int64_t nh0 = (head0 + 1) * bph - vfirst;
+    int next_head = HEADS_ALIGNED || nh0 > kBlk ? kBlk : (int)nh0;   // in-block vector index
+    float sc = h2f(scale16[chunk * n_heads + head0]);
     const float off = c ? 0.5f : 0.f;
-    const int64_t vout0 = chunk * V + vfirst;
+    using OutT = typename std::conditional<OUT_DT == LQ_F32, float, uint16_t>::type;
+    OutT* const ob = reinterpret_cast<OutT*>(out) + (chunk * V + vfirst) * 8 + idx;
     for (int j = 0; j < ncnt; j++) {
         const uint32_t slot = x & (kL - 1);
         const uint32_t e = LU[slot];
         x = ((e >> 9) & 0x7ffu) * (x >> 10) + (e >> 20);
-        if (x < (uint32_t)kL) {
-            const uint32_t k = (uint32_t)__clz((int)x) - 21u;
-            if (nbuf < k) {
-                buf |= ((uint64_t)__builtin_bitreverse32(pre) << 32) >> nbuf;
-                nbuf += 32;
-                pre = wb[++nwi];
-            }
-            x = (x << k) | (uint32_t)(buf >> (64 - k));
-            buf <<= k;
-            nbuf -= k;
+        // renormalise: k bits so that x is back in [L, 2L) (k = 0 when it already is)
+        const uint32_t k = x < (uint32_t)kL ? (uint32_t)__clz((int)x) - 21u : 0u;
+        if (nbuf < k) {
+            buf |= ((uint64_t)__builtin_bitreverse32(pre) << 32) >> nbuf;
+            nbuf += 32;
+            pre = wb[++nwi];
         }
+        const uint32_t in = k ? (uint32_t)(buf >> ((64u - k) & 63u)) : 0u;
+        x = (x << k) | in;
+        buf <<= k;
+        nbuf -= k;
         const int val = lo_sym + (int)(e & 511u);
-        int contrib = idx < 7 ? val : 0;
-        contrib += shfl_xor_i(contrib, 1);
-        contrib += shfl_xor_i(contrib, 2);
-        contrib += shfl_xor_i(contrib, 4);
-        const int coord = idx < 7 ? val : 2 * val + (contrib & 1);
+        // parity of c0 + .. + c6: the low bits of lanes idx 0..6 of this 8-lane group
+        const unsigned long long odd = __ballot(val & 1);
+        const int par = __popcll(odd & (0x7full << (threadIdx.x & 56))) & 1;
+        const int coord = idx < 7 ? val : 2 * val + par;
         while (wv == 0) wv = word_of(++wi);
         const int vl = 32 * wi + __builtin_ctz(wv);
         wv &= wv - 1u;
-        const int64_t vch = vfirst + vl;
-        if (vch >= next_head) {
-            head = vch / bph;
-            next_head = (head + 1) * bph;
+        if (!HEADS_ALIGNED && vl >= next_head) {
+            const int64_t head = (vfirst + vl) / bph;
+            const int64_t nh = (head + 1) * bph - vfirst;
+            next_head = nh > kBlk ? kBlk : (int)nh;
             sc = h2f(scale16[chunk * n_heads + head]);
         }
         const float y = ((float)coord + off) * sc;
-        const int64_t o = (vout0 + vl) * 8 + idx;
-        if (out_dtype == LQ_F32) reinterpret_cast<float*>(out)[o] = y;
-        else reinterpret_cast<uint16_t*>(out)[o] = f2dtype(y, out_dtype);
+        if constexpr (OUT_DT == LQ_F32) ob[vl * 8] = y;
+        else if constexpr (OUT_DT == LQ_F16) ob[vl * 8] = f2h(y);
+        else ob[vl * 8] = f2bf(y);
     }
 }
 
@@ -853,9 +910,9 @@ int lq_chunk_encode(const int8_t* d_sym, const uint32_t* d_blk_n1, int64_t n_chu
     EncWork w = enc_layout(n_chunks, n_vectors);
     uint32_t* bits = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(d_work) + w.bits);
     uint32_t* scratch = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(d_work) + w.scratch);
-    const int64_t groups = (nblk + 15) / 16;
-    hipLaunchKernelGGL(k_chunk_encode, dim3((unsigned)(n_chunks * groups)), dim3(256), 0, s, d_sym, d_blk_n1, nblk,
-                       n_vectors, d_tables, bits, scratch, d_blk_state);
+    const int64_t groups = (nblk + kEncBlocks - 1) / kEncBlocks;
+    hipLaunchKernelGGL(k_chunk_encode, dim3((unsigned)groups, (unsigned)n_chunks), dim3(256), 0, s, d_sym, d_blk_n1,
+                       nblk, n_vectors, d_tables, bits, scratch, d_blk_state);
     hipLaunchKernelGGL(k_chunk_scan, dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, bits, d_blk_state, d_tables,
                        nblk, d_blk_off, d_stream_nbits, d_stream_state);
     hipLaunchKernelGGL(k_chunk_offsets, dim3((unsigned)((n_chunks + 63) / 64)), dim3(64), 0, s, d_stream_nbits, d_tables,
@@ -872,8 +929,8 @@ int lq_chunk_pack(int64_t n_chunks, int64_t n_vectors, const lq_table* d_tables,
     const uint32_t* bits = reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(d_work) + w.bits);
     const uint32_t* scratch = reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(d_work) + w.scratch);
     const int64_t tasks = n_chunks * LQ_STREAMS * nblk;
-    hipLaunchKernelGGL(k_chunk_pack, dim3((unsigned)((tasks + 15) / 16)), dim3(256), 0, s, tasks, nblk, bits, scratch,
-                       d_blk_off, d_stream_nbits, d_stream_woff, d_chunk_base, d_words);
+    hipLaunchKernelGGL(k_chunk_pack, dim3((unsigned)((nblk + 15) / 16), (unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s,
+                       tasks, nblk, bits, scratch, d_blk_off, d_stream_nbits, d_stream_woff, d_chunk_base, d_words);
     const int64_t ns = n_chunks * LQ_STREAMS;
     hipLaunchKernelGGL(k_chunk_tail, dim3((unsigned)((ns + 255) / 256)), dim3(256), 0, s, ns, d_tables,
                        d_stream_nbits, d_stream_woff, d_chunk_base, d_words);
@@ -889,9 +946,16 @@ int lq_chunk_decode(const uint32_t* d_words, const int64_t* d_chunk_base, const 
     const int64_t nblk = (V + kBlk - 1) / kBlk;
     hipLaunchKernelGGL(k_chunk_lut, dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, d_tables, d_lut_work);
     const int64_t groups = (nblk + kDecBlocks - 1) / kDecBlocks;
-    hipLaunchKernelGGL(k_chunk_decode, dim3((unsigned)(n_chunks * 2 * groups)), dim3(256), 0, s, d_words, d_chunk_base,
-                       d_stream_woff, d_blk_off, d_blk_state, d_coset_bits, d_blk_n1, d_tables, d_scale16, d_lut_work,
-                       n_heads, bph, nblk, d_out, out_dtype);
+    const dim3 grid((unsigned)(n_chunks * 2 * groups));
+    const bool aligned = bph % kBlk == 0;
+#define LQ_DECODE(DT, AL)                                                                                         \
+    hipLaunchKernelGGL((k_chunk_decode<DT, AL>), grid, dim3(256), 0, s, d_words, d_chunk_base, d_stream_woff,       \
+                       d_blk_off, d_blk_state, d_coset_bits, d_blk_n1, d_tables, d_scale16, d_lut_work, n_heads, bph, \
+                       nblk, d_out)
+    if (out_dtype == LQ_F16) { if (aligned) LQ_DECODE(LQ_F16, true); else LQ_DECODE(LQ_F16, false); }
+    else if (out_dtype == LQ_BF16) { if (aligned) LQ_DECODE(LQ_BF16, true); else LQ_DECODE(LQ_BF16, false); }
+    else { if (aligned) LQ_DECODE(LQ_F32, true); else LQ_DECODE(LQ_F32, false); }
+#undef LQ_DECODE
     return launch_status();
 }
 
