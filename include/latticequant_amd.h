@@ -106,6 +106,12 @@ int lq_chunk_quantize(const void *d_x, int dtype, int64_t n_chunks, int64_t n_he
                       uint8_t *d_coset_bits, uint32_t *d_blk_n1, uint32_t *d_hist, int32_t *d_status,
                       void *d_deq, int deq_dtype, hipStream_t s);
 
+/* x / scale32[head] -> nearest E8 point (fp32 (n_heads * bph, 8)), head = vector / bph,
+ * with the same arithmetic as lq_chunk_quantize.  d_fastdiv from lq_head_scales /
+ * lq_scale_fastdiv.  Replaces llm/compressed_kv_cache.py:199-201 (x_scaled, encode_e8). */
+int lq_e8_quantize_heads(const void *d_x, int dtype, int64_t n_heads, int64_t bph, const float *d_scale32,
+                         const int32_t *d_fastdiv, float *d_q, hipStream_t s);
+
 /* ------------------------------------------------------------------ rANS -- */
 
 /* Chunk tables from the histograms: alphabet range(min-2, max+2) and
@@ -191,6 +197,43 @@ int64_t lq_merge_workspace(int64_t total_blocks);
 int lq_fused_merge(const uint8_t *d_packed, int bits, const uint16_t *d_fallback, const uint8_t *d_mask,
                    const float *d_scales, int64_t total_blocks, int64_t bph, void *d_work, uint16_t *d_out,
                    hipStream_t s);
+
+/* ----------------------------------------------------------- API helpers -- */
+
+/* validate_e8 + check_representable on fp32 points (n, 8): per point
+ * LQ_V_VALID (consistently integer or half-integer, even integer sum, within
+ * atol), LQ_V_HALF (the half-integer coset) and, for bits in {3,4,5},
+ * LQ_V_INRANGE (valid and every integer coordinate in [-2^(b-1), 2^(b-1)-1]).
+ * Replaces core/compact_storage.py:39-80 (validate_e8), :235-249 (check_representable). */
+#define LQ_V_VALID 1
+#define LQ_V_HALF 2
+#define LQ_V_INRANGE 4
+int lq_e8_validate(const float *d_q, int64_t n, float atol, int bits, int32_t *d_flags, hipStream_t s);
+
+/* unpack_e8 to fp32 lattice points (n, 8), b in {3,4,5}, big-endian b-byte words.
+ * Replaces core/compact_storage.py:157-222. */
+int lq_unpack_e8(const uint8_t *d_packed, int bits, int64_t n, float *d_q, hipStream_t s);
+
+/* Symbol values -> table indices with rans_encode's rule: an equal alphabet
+ * entry (the last one), else the first entry at minimal distance.
+ * contiguous != 0 declares alphabet = lo, lo+1, ..  (n_alphabet <= 1024).
+ * Replaces the lookup in core/gpu_ans.py:110-119. */
+int lq_symbol_index(const int64_t *d_sym, int64_t n, const int64_t *d_alphabet, int32_t n_alphabet, int contiguous,
+                    int32_t *d_idx, hipStream_t s);
+
+/* Coset bit packing, LSB-first: bit i -> byte i/8, bit i%8 (d_coset: uint8 0/1).
+ * Replaces llm/compressed_kv_cache.py:46-54 and :57-63. */
+int lq_pack_coset_bits(const uint8_t *d_coset, int64_t n, uint8_t *d_out, hipStream_t s);
+int lq_unpack_coset_bits(const uint8_t *d_packed, int64_t n, uint8_t *d_out, hipStream_t s);
+
+/* Randomized Hadamard transform of n_rows rows of d (power of two, 8..512)
+ * elements: forward FWHT(x * signs) / sqrt(d), inverse FWHT(x) / sqrt(d) * signs,
+ * fp32 arithmetic in the reference's butterfly order.  Row r uses sign row
+ * (r / rows_per_sign) % n_sign of d_signs (n_sign, d) fp32.
+ * Replaces core/pipeline.py:49-118 (fast_hadamard_transform, RHT) and
+ * llm/perplexity_eval.py:35-61 (HeadRHT). */
+int lq_rht(const void *d_x, int in_dtype, int64_t n_rows, int d, const float *d_signs, int64_t rows_per_sign,
+           int n_sign, int inverse, void *d_out, int out_dtype, hipStream_t s);
 
 #ifdef __cplusplus
 }

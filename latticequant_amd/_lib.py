@@ -22,6 +22,7 @@ LQ_MAXSYM = 264
 LQ_STREAMS = 16
 LQ_F16, LQ_BF16, LQ_F32 = 0, 1, 2
 LQ_ST_SYM_OVERFLOW, LQ_ST_ALPHABET, LQ_ST_TIE_UNPINNED = 1, 2, 4
+LQ_V_VALID, LQ_V_HALF, LQ_V_INRANGE = 1, 2, 4
 TABLE_BYTES = 16 + 4 * LQ_MAXSYM   # sizeof(lq_table)
 
 _lib = None
@@ -53,6 +54,13 @@ _SIGS = {
     "lq_pack_compact": ([_P, _INT, _I64, _P, _P, _P], _INT),
     "lq_merge_workspace": ([_I64], _I64),
     "lq_fused_merge": ([_P, _INT, _P, _P, _P, _I64, _I64, _P, _P, _P], _INT),
+    "lq_e8_validate": ([_P, _I64, ctypes.c_float, _INT, _P, _P], _INT),
+    "lq_unpack_e8": ([_P, _INT, _I64, _P, _P], _INT),
+    "lq_symbol_index": ([_P, _I64, _P, _I32, _INT, _P, _P], _INT),
+    "lq_pack_coset_bits": ([_P, _I64, _P, _P], _INT),
+    "lq_unpack_coset_bits": ([_P, _I64, _P, _P], _INT),
+    "lq_e8_quantize_heads": ([_P, _INT, _I64, _I64, _P, _P, _P, _P], _INT),
+    "lq_rht": ([_P, _INT, _I64, _INT, _P, _I64, _INT, _INT, _P, _INT, _P], _INT),
 }
 
 

@@ -66,6 +66,24 @@ class EncodedBatch:
     def nblk(self) -> int:
         return (self.n_vectors + L.LQ_BLK - 1) // L.LQ_BLK
 
+    # ---- views ------------------------------------------------------------
+    def select(self, c: int) -> "EncodedBatch":
+        """Chunk c as a one-chunk batch (views, no copies; words stay shared)."""
+        C, S, nb = self.n_chunks, L.LQ_STREAMS, self.nblk
+        if not 0 <= c < C:
+            raise IndexError(c)
+        tb = L.TABLE_BYTES
+        return EncodedBatch(
+            n_chunks=1, n_heads=self.n_heads, bph=self.bph, shape=self.shape, bits=self.bits[c:c + 1],
+            scale32=self.scale32.view(C, -1)[c], scale16=self.scale16.view(C, -1)[c],
+            sigma2=None if self.sigma2 is None else self.sigma2.view(C, -1)[c],
+            coset_bits=self.coset_bits[c:c + 1], blk_n1=self.blk_n1[c:c + 1],
+            tables=self.tables[c * S * tb:(c + 1) * S * tb], blk_off=self.blk_off[c * S * nb:(c + 1) * S * nb],
+            blk_state=self.blk_state[c * S * nb:(c + 1) * S * nb], stream_nbits=self.stream_nbits[c * S:(c + 1) * S],
+            stream_state=self.stream_state[c * S:(c + 1) * S], stream_woff=self.stream_woff[c * S:(c + 1) * S],
+            chunk_words=self.chunk_words[c:c + 1], chunk_base=self.chunk_base[c:c + 1], words=self.words,
+            status=self.status[c:c + 1], hist=None if self.hist is None else self.hist[c * S * 256:(c + 1) * S * 256])
+
     # ---- byte accounting -------------------------------------------------
     def reference_bytes(self) -> torch.Tensor:
         """Bytes the reference counts per chunk (llm/compressed_kv_cache.py:113-119):
@@ -98,37 +116,26 @@ def _empty(n, dtype, dev):
     return torch.empty(int(n), dtype=dtype, device=dev)
 
 
-def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, deq_out: bool = False,
-                 exact_size: bool = True, words_out: Optional[torch.Tensor] = None):
-    """Compress a batch of chunks.
+def _bits_tensor(bits, C, dev):
+    if isinstance(bits, int):
+        return torch.full((C,), bits, dtype=torch.int32, device=dev)
+    b = torch.as_tensor(list(bits), dtype=torch.int32)
+    if b.numel() != C:
+        raise ValueError("bits must be an int or one value per chunk")
+    return b.to(dev)
 
-    x: (C, B, H, T, hd) fp16 / bf16 / fp32 CUDA tensor, hd % 8 == 0.
-    bits: int or (C,) sequence of bits per dimension per chunk (3, 4, 5, ...).
-    scale32: optional (C*B*H,) fp32 scales (otherwise from sigma^2 on the device).
-    deq_out: also return q * scale32 in x's dtype (what update() hands to attention).
-    exact_size: allocate the bitstream arena at its exact size (one host sync);
-      else at a no-sync upper bound (10 bits per symbol).
-    words_out: caller-provided arena (int32) large enough for the upper bound.
-    Returns (EncodedBatch, deq or None)."""
+
+def _head_scales(x: torch.Tensor, bits, scale32: Optional[torch.Tensor]):
+    """Per-head scales of a (C, B, H, T, hd) batch: from sigma^2 on the device
+    (llm/compressed_kv_cache.py:188-196) or the caller's fp32 scales, plus the
+    fast-division flags of the quantizer."""
     lib = L.lib()
-    if x.dim() != 5:
-        raise ValueError("x must be (n_chunks, B, H, T, hd)")
-    if not x.is_cuda:
-        raise ValueError("x must be a CUDA (ROCm) tensor")
-    x = x.contiguous()
     C, B, H, T, hd = x.shape
-    if hd % 8:
-        raise ValueError("head_dim must be a multiple of 8")
     dev = x.device
     nh, bph = B * H, T * hd // 8
-    V = nh * bph
-    nblk = (V + L.LQ_BLK - 1) // L.LQ_BLK
     dt = L.dtype_code(x.dtype)
     s = L.stream_ptr(dev)
-    if isinstance(bits, int):
-        bits_t = torch.full((C,), bits, dtype=torch.int32, device=dev)
-    else:
-        bits_t = torch.as_tensor(list(bits), dtype=torch.int32).to(dev)
+    bits_t = _bits_tensor(bits, C, dev)
     fastdiv = _empty(C * nh, torch.int32, dev)
     sigma2 = None
     if scale32 is None:
@@ -144,6 +151,81 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
             raise ValueError("scale32 must hold one scale per head of every chunk")
         scale16 = scale32.to(torch.float16)
         L.check(lib.lq_scale_fastdiv(scale32.data_ptr(), C * nh, dt, fastdiv.data_ptr(), s), "lq_scale_fastdiv")
+    return bits_t, scale32, scale16, sigma2, fastdiv
+
+
+def _check_input(x: torch.Tensor) -> torch.Tensor:
+    if x.dim() != 5:
+        raise ValueError("x must be (n_chunks, B, H, T, hd)")
+    if not x.is_cuda:
+        raise ValueError("x must be a CUDA (ROCm) tensor")
+    if x.shape[-1] % 8:
+        raise ValueError("head_dim must be a multiple of 8")
+    if x.numel() == 0:
+        raise ValueError("empty chunk")
+    return x.contiguous()
+
+
+def quantize_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None):
+    """E8-quantize a batch of chunks without entropy coding (the reference's
+    eval_only_no_entropy path, llm/compressed_kv_cache.py:199-221).
+    Returns (scale32, scale16, deq) with deq = q * scale32 in x's dtype."""
+    lib = L.lib()
+    x = _check_input(x)
+    C, B, H, T, hd = x.shape
+    dev = x.device
+    nh, bph = B * H, T * hd // 8
+    nblk = (nh * bph + L.LQ_BLK - 1) // L.LQ_BLK
+    dt = L.dtype_code(x.dtype)
+    _, scale32, scale16, _, fastdiv = _head_scales(x, bits, scale32)
+    sym = _empty(C * nblk * L.LQ_SYM_STRIDE, torch.int8, dev)
+    coset_bits = _empty(C * nblk * L.LQ_BLK // 8, torch.uint8, dev)
+    blk_n1 = _empty(C * nblk, torch.int32, dev)
+    hist = _zeros(C * L.LQ_STREAMS * 256, torch.int32, dev)
+    status = _zeros(C, torch.int32, dev)
+    deq = torch.empty_like(x)
+    L.check(lib.lq_chunk_quantize(x.data_ptr(), dt, C, nh, bph, scale32.data_ptr(), fastdiv.data_ptr(), sym.data_ptr(),
+                                  coset_bits.data_ptr(), blk_n1.data_ptr(), hist.data_ptr(), status.data_ptr(),
+                                  deq.data_ptr(), dt, L.stream_ptr(dev)), "lq_chunk_quantize")
+    return scale32, scale16, deq
+
+
+def quantize_points(t: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None):
+    """Lattice points of one (B, H, T, hd) tensor as _compress_tensor computes
+    them (x / scale[head] -> E8).  Returns (q (B*H*T*hd/8, 8) fp32, scale32, scale16)."""
+    lib = L.lib()
+    x = _check_input(t[None])
+    _, B, H, T, hd = x.shape
+    nh, bph = B * H, T * hd // 8
+    _, scale32, scale16, _, fastdiv = _head_scales(x, bits, scale32)
+    q = torch.empty(nh * bph, 8, dtype=torch.float32, device=x.device)
+    L.check(lib.lq_e8_quantize_heads(x.data_ptr(), L.dtype_code(x.dtype), nh, bph, scale32.data_ptr(), fastdiv.data_ptr(),
+                                     q.data_ptr(), L.stream_ptr(x.device)), "lq_e8_quantize_heads")
+    return q, scale32, scale16
+
+
+def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, deq_out: bool = False,
+                 exact_size: bool = True, words_out: Optional[torch.Tensor] = None):
+    """Compress a batch of chunks.
+
+    x: (C, B, H, T, hd) fp16 / bf16 / fp32 CUDA tensor, hd % 8 == 0.
+    bits: int or (C,) sequence of bits per dimension per chunk (3, 4, 5, ...).
+    scale32: optional (C*B*H,) fp32 scales (otherwise from sigma^2 on the device).
+    deq_out: also return q * scale32 in x's dtype (what update() hands to attention).
+    exact_size: allocate the bitstream arena at its exact size (one host sync);
+      else at a no-sync upper bound (10 bits per symbol).
+    words_out: caller-provided arena (int32) large enough for the upper bound.
+    Returns (EncodedBatch, deq or None)."""
+    lib = L.lib()
+    x = _check_input(x)
+    C, B, H, T, hd = x.shape
+    dev = x.device
+    nh, bph = B * H, T * hd // 8
+    V = nh * bph
+    nblk = (V + L.LQ_BLK - 1) // L.LQ_BLK
+    dt = L.dtype_code(x.dtype)
+    s = L.stream_ptr(dev)
+    bits_t, scale32, scale16, sigma2, fastdiv = _head_scales(x, bits, scale32)
     sym = _empty(C * nblk * L.LQ_SYM_STRIDE, torch.int8, dev)
     coset_bits = _zeros(C * nblk * L.LQ_BLK // 8, torch.uint8, dev)
     blk_n1 = _empty(C * nblk, torch.int32, dev)

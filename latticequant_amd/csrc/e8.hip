@@ -56,6 +56,28 @@ __global__ void k_symbols_to_e8(const int32_t* __restrict__ coset, const int32_t
     store8(q, LQ_F32, v, o);
 }
 
+// x / scale[head] -> nearest E8 point (fp32), head = v / bph; the
+// quantizer of _compress_tensor (llm/compressed_kv_cache.py:199-201) without
+// symbolisation, for the fixed-rate path.
+__global__ void k_quantize_heads(const void* __restrict__ x, int dtype, int64_t n, int64_t bph,
+                                 const float* __restrict__ scale32, const int32_t* __restrict__ fastdiv,
+                                 float* __restrict__ q) {
+    int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (v >= n) return;
+    const int64_t h = v / bph;
+    const float s = scale32[h];
+    const bool fast = fastdiv[h] != 0;
+    const float rs = 1.0f / s;
+    float xv[8], t[8], ic[8];
+    load8(x, dtype, v, xv);
+#pragma unroll
+    for (int i = 0; i < 8; i++) t[i] = div_scaled(xv[i], s, rs, fast);
+    const float off = e8_nearest(t, ic) ? 0.5f : 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) ic[i] = ic[i] + off;
+    store8(q, LQ_F32, v, ic);
+}
+
 // ---------------------------------------------------------- head scales --
 
 // Partial sums of x^2 per head in double: grid (heads, parts).
@@ -309,6 +331,15 @@ int lq_head_scales(const void* d_x, int dtype, int64_t n_chunks, int64_t n_heads
 int lq_scale_fastdiv(const float* d_scale32, int64_t n_heads_total, int dtype, int32_t* d_fastdiv, hipStream_t s) {
     if (n_heads_total <= 0) return LQ_ERR_ARG;
     hipLaunchKernelGGL(k_scale_fastdiv, dim3((unsigned)n_heads_total), dim3(256), 0, s, d_scale32, dtype, d_fastdiv);
+    return launch_status();
+}
+
+int lq_e8_quantize_heads(const void* d_x, int dtype, int64_t n_heads, int64_t bph, const float* d_scale32,
+                         const int32_t* d_fastdiv, float* d_q, hipStream_t s) {
+    if (n_heads <= 0 || bph <= 0 || dtype < 0 || dtype > 2) return LQ_ERR_ARG;
+    const int64_t n = n_heads * bph;
+    hipLaunchKernelGGL(k_quantize_heads, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, d_x, dtype, n, bph,
+                       d_scale32, d_fastdiv, d_q);
     return launch_status();
 }
 

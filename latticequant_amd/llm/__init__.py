@@ -1,1 +1,1 @@
-"""KV-cache integration: CompressedKVCache and the fused merge paths."""
+"""KV-cache integration: CompressedKVCache (HF Cache), fixed-rate merge paths, decode attention."""

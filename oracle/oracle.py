@@ -457,6 +457,30 @@ def fwht(x: np.ndarray) -> np.ndarray:
     return y / np.sqrt(d)
 
 
+def rht_f32(x: np.ndarray, signs: np.ndarray, inverse: bool = False) -> np.ndarray:
+    """RHT.forward / RHT.inverse in float32 (core/pipeline.py:49-69, 100-118):
+    butterflies h = 1, 2, .. with (a, b) -> (a + b, a - b), one IEEE division
+    by f32(sqrt(d)), signs applied before (forward) or after (inverse)."""
+    y = np.array(x, dtype=np.float32, copy=True)
+    sg = np.asarray(signs, dtype=np.float32)
+    d = y.shape[-1]
+    if not inverse:
+        y = (y * sg).astype(np.float32)
+    h = 1
+    while h < d:
+        y = y.reshape(*y.shape[:-1], d // (2 * h), 2, h)
+        a = y[..., 0, :].copy()
+        b = y[..., 1, :].copy()
+        y[..., 0, :] = a + b
+        y[..., 1, :] = a - b
+        y = y.reshape(*y.shape[:-3], d)
+        h *= 2
+    y = (y / np.float32(np.sqrt(d))).astype(np.float32)
+    if inverse:
+        y = (y * sg).astype(np.float32)
+    return y
+
+
 # ------------------------------------------------------------ attention ---
 
 def decode_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray) -> np.ndarray:

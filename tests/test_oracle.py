@@ -249,6 +249,10 @@ def test_rht_golden():
         np.testing.assert_array_equal(O.rht_signs(128, int(s)), sg)
     y = O.fwht(g["x"] * O.rht_signs(128, 7))
     np.testing.assert_allclose(y, g["y"], rtol=0, atol=2e-6)
+    # the fp32 restatement is the reference's RHT.forward bit for bit
+    np.testing.assert_array_equal(O.rht_f32(g["x"], O.rht_signs(128, 7)), g["y"])
+    back = O.rht_f32(g["y"], O.rht_signs(128, 7), inverse=True)
+    np.testing.assert_allclose(back, g["x"], rtol=0, atol=1e-5)
     # self-inverse and orthogonal
     x = g["x"].astype(np.float64)
     np.testing.assert_allclose(O.fwht(O.fwht(x)), x, atol=1e-12)
