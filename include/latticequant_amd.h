@@ -151,6 +151,47 @@ int lq_chunk_decode(const uint32_t *d_words, const int64_t *d_chunk_base, const 
                     int64_t n_chunks, int64_t n_heads, int64_t bph, uint32_t *d_lut_work, void *d_out,
                     int out_dtype, hipStream_t s);
 
+/* Decoder LUTs of every stream of a chunk batch (n_chunks * 16 * 1024 uint32:
+ * symbol index | freq << 9 | (slot - cum) << 20), as lq_chunk_decode builds them
+ * internally.  Part of the table stage of core/gpu_ans.py:88-95 (lookup). */
+int lq_chunk_luts(const lq_table *d_tables, int64_t n_chunks, uint32_t *d_lut, hipStream_t s);
+
+/* ---------------------------------------------------- decode attention --- */
+
+/* Device pointers of a batch of chunks in lq_chunk_encode's format (one
+ * EncodedBatch of the host side), with the per-chunk geometry. */
+typedef struct {
+    const uint32_t *words;
+    const int64_t *chunk_base;
+    const int64_t *stream_woff;
+    const uint32_t *blk_off;
+    const uint16_t *blk_state;
+    const uint8_t *coset_bits;
+    const uint32_t *blk_n1;
+    const lq_table *tables;
+    const uint16_t *scale16;
+    int64_t n_chunks;
+    int64_t n_heads;   /* B * H_kv */
+    int64_t bph;       /* T * hd / 8 vectors per head */
+} lq_chunk_batch;
+
+/* Workspace of lq_decode_attention, in bytes. */
+int64_t lq_attn_workspace(int64_t n_chunks, int64_t n_heads, int64_t bph, int group);
+
+/* One decode step of attention over a compressed prefix + fp16 tail:
+ * out[qh] = softmax(q[qh] . K^T / sqrt(128)) V for every query head qh, with
+ * kv head qh / group.  K, V: chunk batches of the same geometry (head_dim 128,
+ * tokens per chunk a multiple of 32), dequantised as _decompress_chunk does
+ * (lattice point times the fp16-stored scale); chunk c holds tokens
+ * c*T .. c*T+T-1 of the prefix.  Tail: (n_heads, t_tail, 128) fp16 K and V,
+ * t_tail <= 1024, following the prefix.  q, out: (n_heads * group, 128) fp16.
+ * Replaces the decompress -> torch.cat -> SDPA read of
+ * llm/compressed_kv_cache.py:384-395 (and the fused merge of
+ * llm/fused_triton_merge.py:33-130 feeding attention). */
+int lq_decode_attention(const lq_chunk_batch *k, const lq_chunk_batch *v, const uint16_t *d_q, int group,
+                        const uint16_t *d_tail_k, const uint16_t *d_tail_v, int64_t t_tail, void *d_work,
+                        uint16_t *d_out, hipStream_t s);
+
 /* Generic tables (build_rans_table API): n_tables histograms of n_sym[t] <= 1024
  * counts at d_counts + d_count_off[t].  Outputs freqs / cumfreqs (n_sym+1) at the
  * same offsets (+t for cum), lookup (1024 per table) and status per table.

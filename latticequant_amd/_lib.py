@@ -60,12 +60,22 @@ _SIGS = {
     "lq_pack_coset_bits": ([_P, _I64, _P, _P], _INT),
     "lq_unpack_coset_bits": ([_P, _I64, _P, _P], _INT),
     "lq_e8_quantize_heads": ([_P, _INT, _I64, _I64, _P, _P, _P, _P], _INT),
+    "lq_chunk_luts": ([_P, _I64, _P, _P], _INT),
+    "lq_attn_workspace": ([_I64, _I64, _I64, _INT], _I64),
+    "lq_decode_attention": ([_P, _P, _P, _INT, _P, _P, _I64, _P, _P, _P], _INT),
     "lq_rht": ([_P, _INT, _I64, _INT, _P, _I64, _INT, _INT, _P, _INT, _P], _INT),
 }
 
 
 class LQError(RuntimeError):
     pass
+
+
+class ChunkBatch(ctypes.Structure):
+    """lq_chunk_batch: device pointers + geometry of one chunk batch."""
+    _fields_ = [("words", _P), ("chunk_base", _P), ("stream_woff", _P), ("blk_off", _P), ("blk_state", _P),
+                ("coset_bits", _P), ("blk_n1", _P), ("tables", _P), ("scale16", _P),
+                ("n_chunks", _I64), ("n_heads", _I64), ("bph", _I64)]
 
 
 def exported_symbols():

@@ -44,6 +44,10 @@ class RANSTable:
     cumfreqs: np.ndarray    # (n_symbols + 1,) int32
     alphabet: List[int]
     n_symbols: int
+    # LQ_ST_TIE_UNPINNED when an alphabet above 256 symbols hit an argsort tie
+    # at the adjustment cut: numpy's tie order there is not restated, a stable
+    # (count, index) order is used instead
+    status: int = 0
 
 
 def build_rans_tables(counts_list, alphabets, device=None) -> List[RANSTable]:
@@ -85,7 +89,7 @@ def build_rans_tables(counts_list, alphabets, device=None) -> List[RANSTable]:
             raise ValueError("alphabet exceeds L")
         a, b = int(off[t]), int(off[t + 1])
         out.append(RANSTable(lookup=lookup[t].copy(), freqs=freqs[a:b].copy(), cumfreqs=cum[a + t:b + t + 1].copy(),
-                             alphabet=list(alphabets[t]), n_symbols=sizes[t]))
+                             alphabet=list(alphabets[t]), n_symbols=sizes[t], status=int(st[t])))
     return out
 
 

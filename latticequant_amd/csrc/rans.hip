@@ -959,6 +959,12 @@ int lq_chunk_decode(const uint32_t* d_words, const int64_t* d_chunk_base, const 
     return launch_status();
 }
 
+int lq_chunk_luts(const lq_table* d_tables, int64_t n_chunks, uint32_t* d_lut, hipStream_t s) {
+    if (n_chunks <= 0 || !d_tables || !d_lut) return LQ_ERR_ARG;
+    hipLaunchKernelGGL(k_chunk_lut, dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, d_tables, d_lut);
+    return launch_status();
+}
+
 int lq_build_tables(const int64_t* d_counts, const int64_t* d_count_off, const int32_t* d_n_sym, int32_t n_tables,
                     int32_t* d_freqs, int32_t* d_cum, int32_t* d_lookup, int32_t* d_status, hipStream_t s) {
     if (n_tables <= 0) return LQ_ERR_ARG;
