@@ -63,6 +63,47 @@ def cpu_baseline(x_host_chunks, bits, scale_rows):
     return nbytes / dt / 1e9, dt
 
 
+def bench_decode_step(dev, iters=30, prefix=32768, tail=128):
+    """C3: one decode step of Llama-3.1-8B GQA attention
+    (32 q heads, 8 kv heads, head_dim 128) over a 32768-token E8+rANS prefix at
+    4 bits/dim plus a 128-token fp16 tail.  Per iteration a 512 MiB write evicts
+    the prefix from L2 / MALL first, so the kernels read it from HBM.
+    Returns dict with the median step time and the roofline figures."""
+    from latticequant_amd import codec
+    from latticequant_amd.llm.decode_attention import attn_workspace, decode_attention
+    g = torch.Generator(device=dev).manual_seed(3)
+    k = torch.randn(1, 1, HEADS, prefix, HD, generator=g, device=dev).to(torch.float16)
+    v = torch.randn(1, 1, HEADS, prefix, HD, generator=g, device=dev).to(torch.float16)
+    q = torch.randn(1, 32, 1, HD, generator=g, device=dev).to(torch.float16)
+    tk = torch.randn(1, HEADS, tail, HD, generator=g, device=dev).to(torch.float16)
+    tv = torch.randn(1, HEADS, tail, HD, generator=g, device=dev).to(torch.float16)
+    ek, _ = codec.encode_batch(k, BITS)
+    ev, _ = codec.encode_batch(v, BITS)
+    work = attn_workspace(ek, 4)
+    out = decode_attention(ek, ev, q, tk, tv, work=work)
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    ts = []
+    for i in range(iters):
+        flush.fill_(i & 0xff)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        decode_attention(ek, ev, q, tk, tv, work=work, out=out)
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1e3)
+    ts.sort()
+    us = ts[len(ts) // 2]
+    cb = int(ek.reference_bytes().sum() + ek.side_bytes().sum() + ev.reference_bytes().sum() + ev.side_bytes().sum())
+    nbytes = cb + tk.numel() * 2 + tv.numel() * 2 + q.numel() * 2 + out.numel() * 2
+    return {"decode_step_us": round(us, 2), "decode_step_bytes": nbytes,
+            "decode_step_GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "decode_step_roofline_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "decode_tokens_per_s_32_layers": round(1e6 / (32 * us), 2),
+            "decode_step_workload": f"C3: q [1,32,1,128], prefix K,V [1,8,{prefix},128] E8+rANS {BITS} b/d, "
+                                    f"tail [1,8,{tail},128] fp16, L2/MALL flushed before each step"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -71,6 +112,7 @@ def main():
     ap.add_argument("--group", type=int, default=64, help="chunks per kernel launch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-chunks", type=int, default=2)
+    ap.add_argument("--no-decode-step", action="store_true", help="skip the C3 decode-step measurement")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for {args.gpus}); "
@@ -155,6 +197,8 @@ def main():
     avg_ms = float(np.mean(dec_ms))
     achieved = float(np.mean(grp_bytes)) / (avg_ms * 1e-3) / 1e9
 
+    step = {} if args.no_decode_step else bench_decode_step(dev)
+
     cpu = None
     if not args.no_cpu_baseline:
         v, dt = cpu_baseline(xs, BITS, scs)
@@ -180,7 +224,8 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "k_chunk_decode (+k_chunk_lut), per 8-chunk launch"},
         "cpu_baseline": cpu,
-        "decode_step_us": None,
+        "decode_step_us": step.get("decode_step_us"),
+        "decode_step": step or None,
         "wall_s": round(wall, 3),
     }
     print(json.dumps(res))

@@ -13,5 +13,6 @@ merge / decode-attention step, as hand-written HIP kernels behind a C ABI
   latticequant_amd.llm.compressed_kv_cache (llm/compressed_kv_cache.py)
   latticequant_amd.llm.fused_triton_merge  (llm/fused_triton_merge.py)
   latticequant_amd.llm.triton_kv_integration (llm/triton_kv_integration.py)
+  latticequant_amd.llm.decode_attention     (decode step over the compressed prefix)
 """
 __version__ = "0.1.0"
