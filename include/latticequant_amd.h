@@ -146,14 +146,15 @@ int lq_chunk_pack(int64_t n_chunks, int64_t n_vectors, const lq_table *d_tables,
  * d_words must have 2 readable words after the last chunk's last stream.
  * Replaces llm/compressed_kv_cache.py:289-332 (_decompress_chunk). */
 int lq_chunk_decode(const uint32_t *d_words, const int64_t *d_chunk_base, const int64_t *d_stream_woff,
-                    const uint32_t *d_blk_off, const uint16_t *d_blk_state, const uint8_t *d_coset_bits,
+                    const uint32_t *d_blk_off, const int64_t *d_stream_nbits, const uint16_t *d_blk_state, const uint8_t *d_coset_bits,
                     const uint32_t *d_blk_n1, const lq_table *d_tables, const uint16_t *d_scale16,
                     int64_t n_chunks, int64_t n_heads, int64_t bph, uint32_t *d_lut_work, void *d_out,
                     int out_dtype, hipStream_t s);
 
 /* Decoder LUTs of every stream of a chunk batch (n_chunks * 16 * 1024 uint32:
- * symbol index | freq << 9 | (slot - cum) << 20), as lq_chunk_decode builds them
- * internally.  Part of the table stage of core/gpu_ans.py:88-95 (lookup). */
+ * per slot: 31 - k | k << 5 | symbol index << 9 | (row * 1024 + (x' << k) - 1024) << 19,
+ * with x' = freq + slot - cum, k its renormalisation bits and row = stream & 7),
+ * as lq_chunk_decode builds them internally.  Part of the table stage of core/gpu_ans.py:88-95 (lookup). */
 int lq_chunk_luts(const lq_table *d_tables, int64_t n_chunks, uint32_t *d_lut, hipStream_t s);
 
 /* ---------------------------------------------------- decode attention --- */

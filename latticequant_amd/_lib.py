@@ -46,7 +46,7 @@ _SIGS = {
     "lq_chunk_encode_workspace": ([_I64, _I64], _I64),
     "lq_chunk_encode": ([_P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P], _INT),
     "lq_chunk_pack": ([_I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P], _INT),
-    "lq_chunk_decode": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _INT, _P], _INT),
+    "lq_chunk_decode": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _INT, _P], _INT),
     "lq_build_tables": ([_P, _P, _P, _I32, _P, _P, _P, _P, _P], _INT),
     "lq_rans_encode_streams": ([_P, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _P], _INT),
     "lq_rans_decode_streams": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _I32, _P, _P], _INT),

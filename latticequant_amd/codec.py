@@ -283,7 +283,8 @@ def decode_batch(enc: EncodedBatch, out_dtype: torch.dtype = torch.float16, out:
     if lut_work is None:
         lut_work = _empty(C * L.LQ_STREAMS * L.LQ_L, torch.int32, dev)
     L.check(lib.lq_chunk_decode(enc.words.data_ptr(), enc.chunk_base.data_ptr(), enc.stream_woff.data_ptr(),
-                                enc.blk_off.data_ptr(), enc.blk_state.data_ptr(), enc.coset_bits.data_ptr(),
+                                enc.blk_off.data_ptr(), enc.stream_nbits.data_ptr(), enc.blk_state.data_ptr(),
+                                enc.coset_bits.data_ptr(),
                                 enc.blk_n1.data_ptr(), enc.tables.data_ptr(), enc.scale16.data_ptr(), C, enc.n_heads,
                                 enc.bph, lut_work.data_ptr(), out.data_ptr(), L.dtype_code(out.dtype),
                                 L.stream_ptr(dev)), "lq_chunk_decode")

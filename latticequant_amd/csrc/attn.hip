@@ -21,7 +21,7 @@
 // multiple of 32 so that blocks hold whole tokens of one head.
 #include <cmath>
 
-#include "lq_device.h"
+#include "lq_decode.h"
 
 using namespace lq;
 
@@ -70,13 +70,13 @@ __device__ __forceinline__ WgPos wg_pos(const BatchArgs& a) {
     return p;
 }
 
-// One lane's decoder of stream (coset c, coordinate idx) inside block g.
+// One lane's decoder of stream (coset c, coordinate idx) inside block g:
+// StreamDec (lq_decode.h) plus the walk over the block's coset bitmap that
+// yields each symbol's vector index.
 struct LaneDecoder {
-    const uint32_t* wb;
-    const uint32_t* LU;
-    uint64_t buf;
-    uint32_t x, nbuf, pre, nwi;
-    int lo_sym, ncnt;
+    StreamDec d;
+    const uint32_t* LU;   // the LDS block of the coset's 8 LUTs
+    int lo_sym, ncnt, steps;
     // coset-c vectors of the block, ascending, from the LDS bitmap
     const uint32_t* bm;
     int c, wi;
@@ -96,42 +96,25 @@ struct LaneDecoder {
         const uint32_t n1 = a.blk_n1[chunk * a.nblk + g];
         ncnt = c ? (int)n1 : kBlk - (int)n1;
         lo_sym = a.tables[chunk * LQ_STREAMS + st].lo;
-        wb = a.words + a.chunk_base[chunk] + a.stream_woff[chunk * LQ_STREAMS + st];
         LU = lut_lds;
-        x = a.blk_state[task];
-        const uint32_t bp = a.blk_off[task];
-        nwi = bp >> 5;
-        buf = 0;
-        nbuf = 0;
-        pre = 0;
-        if (ncnt > 0) {
-            buf = ((uint64_t)__builtin_bitreverse32(wb[nwi]) << 32) << (bp & 31);
-            nbuf = 32 - (bp & 31);
-            pre = wb[++nwi];
-        }
+        steps = 0;
+        if (ncnt > 0)
+            d.init(a.words + a.chunk_base[chunk] + a.stream_woff[chunk * LQ_STREAMS + st], a.blk_off[task],
+                   a.blk_state[task], LU, idx);
         wi = 0;
         wv = word_of(0);
     }
 
     // Next symbol value (alphabet value, before parity) and its vector index.
     __device__ __forceinline__ int next(int* vl) {
-        const uint32_t slot = x & (kL - 1);
-        const uint32_t e = LU[slot];
-        x = ((e >> 9) & 0x7ffu) * (x >> 10) + (e >> 20);
-        const uint32_t k = x < (uint32_t)kL ? (uint32_t)__clz((int)x) - 21u : 0u;
-        if (nbuf < k) {
-            buf |= ((uint64_t)__builtin_bitreverse32(pre) << 32) >> nbuf;
-            nbuf += 32;
-            pre = wb[++nwi];
-        }
-        const uint32_t in = k ? (uint32_t)(buf >> ((64u - k) & 63u)) : 0u;
-        x = (x << k) | in;
-        buf <<= k;
-        nbuf -= k;
+        if (steps % 3 == 0) d.refill();
+        steps++;
+        const int val = lo_sym + (int)d.sym();
+        d.step(LU);
         while (wv == 0) wv = word_of(++wi);
         *vl = 32 * wi + __builtin_ctz(wv);
         wv &= wv - 1u;
-        return lo_sym + (int)(e & 511u);
+        return val;
     }
 };
 
@@ -185,7 +168,7 @@ __global__ __launch_bounds__(256) void k_attn_qk(BatchArgs a, const uint16_t* __
     const float sc = h2f(a.scale16[p.chunk * a.n_heads + p.head]);
     if (present) {
         LaneDecoder dec;
-        if (live) dec.init(a, p.chunk, p.g0 + b, p.c, idx, lut[idx], bm[b]);
+        if (live) dec.init(a, p.chunk, p.g0 + b, p.c, idx, &lut[0][0], bm[b]);
         const int n = live ? dec.ncnt : 0;
         // the 8 lanes of a block share n; loop to the wave's max so ballots see every lane
         int nmax = n;
@@ -307,7 +290,7 @@ __global__ __launch_bounds__(256) void k_attn_pv(BatchArgs a, const float* __res
         for (int m = 0; m < kVpt; m++) o[j][m] = 0.f;
     if (present) {
         LaneDecoder dec;
-        if (live) dec.init(a, p.chunk, p.g0 + b, p.c, idx, lut[idx], bm[b]);
+        if (live) dec.init(a, p.chunk, p.g0 + b, p.c, idx, &lut[0][0], bm[b]);
         const int n = live ? dec.ncnt : 0;
         int nmax = n;
         for (int s = 8; s < 64; s <<= 1) nmax = max(nmax, __shfl_xor(nmax, s, 64));

@@ -288,7 +288,20 @@ def gen_rht(pl):
                         x=x.numpy(), y=y.numpy())
 
 
+def gen_allocation():
+    """The reference's published Qwen2.5-7B 4-bit allocation (results/*.json,
+    data only): the per-layer fields allocation_to_schedule reads."""
+    src = os.path.join(REF, "results", "allocation_Qwen2.5-7B_4b.json")
+    with open(src) as f:
+        d = json.load(f)
+    keep = {"model": d["model"], "n_layers": d["n_layers"], "budget_discrete": d["budget_discrete"],
+            "layers": [{k: lr[k] for k in ("layer", "b_K", "b_V", "b_K_disc", "b_V_disc")} for lr in d["layers"]]}
+    with open(os.path.join(HERE, "allocation_Qwen2.5-7B_4b.json"), "w") as f:
+        json.dump(keep, f, indent=0)
+
+
 def main():
+    gen_allocation()
     e8q, ec, cs, ga, ckv, pl = _import_reference()
     rng = np.random.default_rng(20261201)
     gen_e8(rng, e8q, ec)
