@@ -166,6 +166,7 @@ typedef struct {
     const int64_t *chunk_base;
     const int64_t *stream_woff;
     const uint32_t *blk_off;
+    const int64_t *stream_nbits;
     const uint16_t *blk_state;
     const uint8_t *coset_bits;
     const uint32_t *blk_n1;

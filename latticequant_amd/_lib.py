@@ -73,7 +73,7 @@ class LQError(RuntimeError):
 
 class ChunkBatch(ctypes.Structure):
     """lq_chunk_batch: device pointers + geometry of one chunk batch."""
-    _fields_ = [("words", _P), ("chunk_base", _P), ("stream_woff", _P), ("blk_off", _P), ("blk_state", _P),
+    _fields_ = [("words", _P), ("chunk_base", _P), ("stream_woff", _P), ("blk_off", _P), ("stream_nbits", _P), ("blk_state", _P),
                 ("coset_bits", _P), ("blk_n1", _P), ("tables", _P), ("scale16", _P),
                 ("n_chunks", _I64), ("n_heads", _I64), ("bph", _I64)]
 

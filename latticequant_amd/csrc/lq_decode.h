@@ -83,4 +83,226 @@ struct StreamDec {
     }
 };
 
+// ---------------------------------------------------------------------------
+// Block-phase decoding of one (stream, checkpoint block) task per lane.
+//
+// A workgroup holds the 8 coordinate streams of one coset for a run of
+// blocks; lane (block b, coordinate idx) owns stream idx of block b.  The
+// lane decodes in phases of 8 steps:
+//   * its bitstream words reach the decoder through a 16-word ring in LDS
+//     (column `tid` of ring[kRing][lanes]); 4-word top-ups are loaded at one
+//     phase boundary and written to the ring at the next, so the decode steps
+//     never wait on global memory;
+//   * each step stages the symbol index in LDS (row b of the staging, 8 u16
+//     per step) and walks the block's coset bitmap (words already restricted
+//     to the coset's vectors) to find the vector the 8 lanes just decoded;
+//   * after the phase, lane idx owns the vector of step idx: its 8 symbol
+//     indices are row idx of the staging and its block position is returned.
+// Loads stay within two words after the block's last bit (the stream needs 2
+// words of slack after its n_words + 1).
+constexpr int kPhase = 8;    // decode steps per phase
+constexpr int kRing = 16;    // bitstream words per lane in the LDS ring
+
+struct PhaseLane {
+    const uint32_t* sw;     // stream words from the block's first word
+    uint32_t* rcol;         // this lane's ring column
+    int lanes;              // ring row stride (lanes of the workgroup)
+    int wlim;               // last readable word, relative to sw
+    int ld, rd;             // next word to load into the ring / to move into pre
+    uint64_t buf;
+    uint32_t nbuf, pre, e;
+    uint32_t q0, q1, q2, q3;
+    bool inflight;
+    const uint32_t* bmr;    // the block's coset bitmap row (kBlk / 32 + 1 words, last one zero)
+    int wi;
+    uint32_t wv, wn;
+
+    __device__ __forceinline__ uint32_t gword(int i) const { return sw[i < wlim ? i : wlim]; }
+
+    // stream_words: the stream; bit_off / end_bit: the block's first bit and
+    // the next block's first bit (or the stream's n_bits); state: checkpoint
+    // state; lut: LDS LUT block, row: this stream's row in it.
+    __device__ __forceinline__ void init(const uint32_t* stream_words, uint32_t bit_off, int64_t end_bit, uint32_t state,
+                                         const uint32_t* lut, int row, uint32_t* ring_col, int n_lanes,
+                                         const uint32_t* bm_row) {
+        sw = stream_words + (bit_off >> 5);
+        wlim = (int)((end_bit >> 5) + 2 - (int64_t)(bit_off >> 5));
+        rcol = ring_col;
+        lanes = n_lanes;
+#pragma unroll
+        for (int i = 0; i < 8; i++) rcol[i * lanes] = gword(i);
+        ld = 8;
+        rd = 2;
+        buf = ((uint64_t)__builtin_bitreverse32(rcol[0]) << 32) << (bit_off & 31u);
+        nbuf = 32u - (bit_off & 31u);
+        pre = rcol[lanes];
+        refill();
+        e = lut[row * kL + (int)state - kL];
+        q0 = q1 = q2 = q3 = 0;
+        inflight = false;
+        bmr = bm_row;
+        wi = 0;
+        wv = bmr[0];
+        wn = bmr[1];
+    }
+
+    __device__ __forceinline__ void refill() {
+        if (nbuf < 32u) {
+            buf |= (uint64_t)__builtin_bitreverse32(pre) << (32u - nbuf);
+            nbuf += 32u;
+            pre = rcol[(rd & (kRing - 1)) * lanes];
+            rd++;
+        }
+    }
+
+    // Phase boundary: land the previous top-up, issue the next one.  A phase
+    // moves at most 3 words out of the ring; a top-up is issued only if 4
+    // more words fit even when none is consumed, so the ring always holds the
+    // next phase's words.
+    __device__ __forceinline__ void boundary() {
+        if (inflight) {
+            rcol[(ld & (kRing - 1)) * lanes] = q0;
+            rcol[((ld + 1) & (kRing - 1)) * lanes] = q1;
+            rcol[((ld + 2) & (kRing - 1)) * lanes] = q2;
+            rcol[((ld + 3) & (kRing - 1)) * lanes] = q3;
+            ld += 4;
+            inflight = false;
+        }
+        if (ld - rd <= kRing - 4) {
+            q0 = gword(ld); q1 = gword(ld + 1); q2 = gword(ld + 2); q3 = gword(ld + 3);
+            inflight = true;
+        }
+    }
+
+    // One decode step: stage the current symbol index at stg_j, find its
+    // vector, move to the next symbol.  Returns the vector's block position.
+    __device__ __forceinline__ int step(uint16_t* stg_j, const char* lutb) {
+        *stg_j = (uint16_t)__builtin_amdgcn_ubfe(e, 9, 10);
+        if (wv == 0) {
+            wi++;
+            wv = wn;
+            wn = bmr[wi + 1 <= kBlk / 32 ? wi + 1 : kBlk / 32];
+            while (wv == 0) {   // a word with no vector of this coset
+                wi++;
+                wv = wn;
+                wn = bmr[wi + 1 <= kBlk / 32 ? wi + 1 : kBlk / 32];
+            }
+        }
+        const int vl = (wi << 5) | __builtin_ctz(wv);
+        wv &= wv - 1u;
+        const uint32_t bits = (uint32_t)(buf >> 33) >> (e & 31u);
+        const uint32_t k = __builtin_amdgcn_ubfe(e, 5, 4);
+        const uint32_t addr = ((e >> 19) + bits) << 2;
+        buf <<= k;
+        nbuf -= k;
+        e = *reinterpret_cast<const uint32_t*>(lutb + addr);
+        return vl;
+    }
+
+    // Steps of one phase (m <= kPhase of them); my_stg: this lane's column of
+    // the block's staging (step j at my_stg[8 j]).  Returns the block position
+    // of the vector of step idx (the one this lane rebuilds).
+    __device__ __forceinline__ int phase(int m, int idx, uint16_t* my_stg, const char* lutb) {
+        int vsv = 0;
+        if (m == kPhase) {
+#pragma unroll
+            for (int j = 0; j < kPhase; j++) {
+                if (j % 3 == 0) refill();
+                const int vl = step(my_stg + 8 * j, lutb);
+                vsv = idx == j ? vl : vsv;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kPhase; j++) {
+                if (j < m) {
+                    if (j % 3 == 0) refill();
+                    const int vl = step(my_stg + 8 * j, lutb);
+                    vsv = idx == j ? vl : vsv;
+                }
+            }
+        }
+        return vsv;
+    }
+};
+
+// c7 parity of a staged vector: parity of the seven free coordinates, i.e.
+// of their indices and of the alphabet lows (lpar).
+__device__ __forceinline__ uint32_t staged_parity(const uint4& r, uint32_t lpar) {
+    const uint32_t px = r.x ^ r.y ^ r.z ^ (r.w & 0xffffu);
+    return (px ^ (px >> 16) ^ lpar) & 1u;
+}
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+// Two dequantised fp16 values (q + lo + off) * scale from a pair of 16-bit
+// symbol indices (< 1024), in packed fp16 arithmetic.  (1024 + i) has the bit
+// pattern 0x6400 | i in fp16, so OR + subtract gives i exactly; adding the
+// half-integer lo + off is exact for |value| < 1024, and the product rounds
+// once, to the fp16 nearest to the exact product, which is what rounding the
+// (exact) fp32 product q * scale to fp16 gives.
+__device__ __forceinline__ uint32_t deq_pair_f16(uint32_t idx2, half2_t lo_off, half2_t sc2) {
+    const uint32_t b = idx2 | 0x64006400u;
+    half2_t v = __builtin_bit_cast(half2_t, b);
+    const half2_t k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    v = (v - k1024) + lo_off;
+    return __builtin_bit_cast(uint32_t, v * sc2);
+}
+
+// Per-workgroup dequantisation constants of one coset of one chunk: the
+// 8 alphabet lows, their parity, and the packed (lo + off) pairs; `small`
+// says every value fits the packed fp16 path (alphabet within [-500, 500)).
+struct CosetConsts {
+    int lo[8];
+    uint32_t lpar;
+    half2_t lo2[4];
+    float off;
+    bool small;
+
+    __device__ __forceinline__ void init(const lq_table* T, int c) {
+        int losum = 0;
+        small = true;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            lo[j] = T[j].lo;
+            if (j < 7) losum += lo[j];
+            small = small && lo[j] >= -500 && lo[j] + T[j].n_sym <= 500;
+        }
+        lpar = (uint32_t)losum & 1u;
+        off = c ? 0.5f : 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float a = (float)lo[2 * j] + off;
+            const float b = j < 3 ? (float)lo[2 * j + 1] + off : (float)(2 * lo[7]) + off;
+            lo2[j] = half2_t{(_Float16)a, (_Float16)b};
+        }
+    }
+
+    // The staged vector r (8 symbol indices) dequantised to 8 fp16 values,
+    // packed in pairs; needs small.
+    __device__ __forceinline__ uint4 deq_f16(const uint4& r, half2_t sc2) const {
+        const uint32_t par = staged_parity(r, lpar);
+        const uint32_t w3 = (r.w & 0xffffu) | (((r.w >> 16) * 2u + par) << 16);   // c7 index doubled + parity
+        uint4 o;
+        o.x = deq_pair_f16(r.x, lo2[0], sc2);
+        o.y = deq_pair_f16(r.y, lo2[1], sc2);
+        o.z = deq_pair_f16(r.z, lo2[2], sc2);
+        o.w = deq_pair_f16(w3, lo2[3], sc2);
+        return o;
+    }
+
+    // The same values in fp32 (exact products, before any fp16 rounding):
+    // fma(index, scale, (lo + off) * scale).
+    __device__ __forceinline__ void deq_f32(const uint4& r, float sc, float y[8]) const {
+        const uint32_t par = staged_parity(r, lpar);
+        const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            uint32_t v = (j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu);
+            if (j == 7) v = 2u * v + par;
+            const float cst = ((float)(j < 7 ? lo[j] : 2 * lo[j]) + off) * sc;
+            y[j] = __builtin_fmaf((float)v, sc, cst);
+        }
+    }
+};
+
 }  // namespace lq

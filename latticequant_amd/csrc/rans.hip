@@ -642,41 +642,41 @@ __global__ __launch_bounds__(256) void k_chunk_lut(const lq_table* __restrict__ 
 }
 
 constexpr int kDecBlocks = 64;   // blocks per decode workgroup (x 8 coordinate streams of one coset)
-constexpr int kDecPhase = 8;     // decode steps per phase (one output flush, one bitstream top-up)
-constexpr int kRing = 16;        // bitstream words staged in LDS per lane
 constexpr int kStgRow = 72;      // u16 per block of the output staging (8 x 8 + 8 padding: no bank conflicts)
 constexpr int kDecLanes = kDecBlocks * 8;
 
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-
-// Two dequantised fp16 values (q + lo + off) * scale from a pair of 16-bit
-// symbol indices (< 1024), in packed fp16 arithmetic.  (1024 + i) has the bit
-// pattern 0x6400 | i in fp16, so OR + subtract gives i exactly; adding the
-// half-integer lo + off is exact for |value| < 1024, and the product rounds
-// once, to the fp16 nearest to the exact product, which is what rounding the
-// (exact) fp32 product q * scale to fp16 gives.
-__device__ __forceinline__ uint32_t deq_pair_f16(uint32_t idx2, half2_t lo_off, half2_t sc2) {
-    const uint32_t b = idx2 | 0x64006400u;
-    half2_t v = __builtin_bit_cast(half2_t, b);
-    const half2_t k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
-    v = (v - k1024) + lo_off;
-    return __builtin_bit_cast(uint32_t, v * sc2);
+// Stage the 8 coset LUTs of (chunk, coset) and the coset-c membership bits of
+// blocks gbase .. gbase + nb - 1 (tail vectors cleared, one zero word after
+// each row) in LDS.  Cooperative over the workgroup; the caller syncs.
+template <int NB, int LANES>
+__device__ __forceinline__ void stage_coset(const uint32_t* __restrict__ lutg, const uint8_t* __restrict__ coset_bits,
+                                            int64_t chunk, int c, int64_t gbase, int64_t nblk, int64_t V,
+                                            uint32_t* lut, uint32_t (*bm)[kBlk / 32 + 1]) {
+    const int tid = threadIdx.x;
+    const uint4* src = reinterpret_cast<const uint4*>(lutg + (chunk * LQ_STREAMS + c * 8) * kL);
+    uint4* dst = reinterpret_cast<uint4*>(lut);
+    for (int i = tid; i < 8 * kL / 4; i += LANES) dst[i] = src[i];
+    for (int i = tid; i < NB * (kBlk / 32); i += LANES) {
+        const int b = i / (kBlk / 32), w = i % (kBlk / 32);
+        const int64_t g = gbase + b;
+        uint32_t m = 0;
+        if (g < nblk) {
+            m = reinterpret_cast<const uint32_t*>(coset_bits + (chunk * nblk + g) * (kBlk / 8))[w];
+            if (!c) m = ~m;
+            const int64_t lim = V - g * kBlk - 32 * w;
+            m = lim >= 32 ? m : (lim <= 0 ? 0u : m & ((1u << lim) - 1u));
+        }
+        bm[b][w] = m;
+    }
+    for (int i = tid; i < NB; i += LANES) bm[i][kBlk / 32] = 0u;
 }
 
-// Workgroup: 64 blocks x the 8 streams of one coset of one chunk (512 lanes).
-// Lane (block b, coordinate idx) decodes its stream's symbols of block b from
-// the block checkpoint, in phases of 8 steps:
-//   * the lane's bitstream words reach the decoder through a 16-word LDS ring;
-//     4-word top-ups are loaded at a phase boundary and written to the ring at
-//     the next one, so the only wait on global memory is at phase boundaries,
-//     for loads and stores issued a whole phase earlier;
-//   * each step stages its symbol index in LDS; at the boundary lane idx of
-//     the block rebuilds the phase's vector idx (alphabet lo, c7 = 2 floor(c7/2)
-//     + parity of c0..c6, coset offset, times the fp16 scale) and writes it as
-//     one 16-byte store at the position found by walking the coset bitmap.
-// HEADS_ALIGNED: bph is a multiple of the block size, so a block lies in one
-// head.  Loads stay within two words after the block's last bit, so the words
-// buffer needs 2 words of slack after the last stream.
+// Workgroup: 64 blocks x the 8 streams of one coset of one chunk (512 lanes),
+// decoded by PhaseLane (lq_decode.h).  After each 8-step phase lane idx of a
+// block rebuilds the phase's vector idx (alphabet lo, c7 = 2 floor(c7/2) +
+// parity of c0..c6, coset offset, times the fp16 scale) and writes it as one
+// 16-byte store.  HEADS_ALIGNED: bph is a multiple of the block size, so a
+// block lies in one head.
 template <int OUT_DT, bool HEADS_ALIGNED>
 __global__ __launch_bounds__(512) void k_chunk_decode(const uint32_t* __restrict__ words, const int64_t* __restrict__ chunk_base,
                                                       const int64_t* __restrict__ stream_woff, const uint32_t* __restrict__ blk_off,
@@ -698,25 +698,7 @@ __global__ __launch_bounds__(512) void k_chunk_decode(const uint32_t* __restrict
     const int64_t gbase = (rem % groups) * kDecBlocks;
     const lq_table* T = tables + chunk * LQ_STREAMS + c * 8;
     if (T[0].n_sym == 0) return;   // the whole coset is empty in this chunk
-    {
-        const uint4* src = reinterpret_cast<const uint4*>(lutg + (chunk * LQ_STREAMS + c * 8) * kL);
-        uint4* dst = reinterpret_cast<uint4*>(lut);
-        for (int i = tid; i < 8 * kL / 4; i += kDecLanes) dst[i] = src[i];
-        // coset-c membership bits of the group's blocks (tail vectors cleared)
-        for (int i = tid; i < kDecBlocks * (kBlk / 32); i += kDecLanes) {
-            const int b = i / (kBlk / 32), w = i % (kBlk / 32);
-            const int64_t g = gbase + b;
-            uint32_t m = 0;
-            if (g < nblk) {
-                m = reinterpret_cast<const uint32_t*>(coset_bits + (chunk * nblk + g) * (kBlk / 8))[w];
-                if (!c) m = ~m;
-                const int64_t lim = V - g * kBlk - 32 * w;
-                m = lim >= 32 ? m : (lim <= 0 ? 0u : m & ((1u << lim) - 1u));
-            }
-            bm[b][w] = m;
-        }
-        if (tid < kDecBlocks) bm[tid][kBlk / 32] = 0u;
-    }
+    stage_coset<kDecBlocks, kDecLanes>(lutg, coset_bits, chunk, c, gbase, nblk, V, lut, bm);
     __syncthreads();
     const int b = tid >> 3, idx = tid & 7;
     const int64_t g = gbase + b;
@@ -729,157 +711,45 @@ __global__ __launch_bounds__(512) void k_chunk_decode(const uint32_t* __restrict
     const uint32_t n1 = blk_n1[chunk * nblk + g];
     const int n = c ? (int)n1 : valid - (int)n1;
     if (n == 0) return;
-    // alphabet lows of the coset's 8 streams (uniform over the workgroup)
-    int lo[8];
-    int losum = 0;
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        lo[j] = T[j].lo;
-        if (j < 7) losum += lo[j];
-    }
-    const uint32_t lpar = (uint32_t)losum & 1u;
-    const float off = c ? 0.5f : 0.f;
-    // fp32 path: value = fma(index, scale, cst[j]) with cst[j] = (lo + off) * scale, exact
-    // fp16 path: packed (index + lo + off) * scale, see deq_pair_f16
-    float sc, cst[8];
-    half2_t lo2[4], sc2;
+    CosetConsts cc;
+    cc.init(T, c);
+    float sc;
+    half2_t sc2;
     auto set_scale = [&](int64_t head) {
         const uint16_t s16 = scale16[chunk * n_heads + head];
         sc = h2f(s16);
         const _Float16 sh = __builtin_bit_cast(_Float16, s16);
         sc2 = half2_t{sh, sh};
-#pragma unroll
-        for (int j = 0; j < 8; j++) cst[j] = ((float)(j < 7 ? lo[j] : 2 * lo[j]) + off) * sc;
     };
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const float a = (float)lo[2 * j] + off;
-        const float bb = j < 3 ? (float)lo[2 * j + 1] + off : (float)(2 * lo[7]) + off;
-        lo2[j] = half2_t{(_Float16)a, (_Float16)bb};
-    }
-    // the fp16 path needs every index (c7: 2 index + 1) below 1024 and every
-    // value (c7: 2 value + 1) plus the coset offset exact in fp16, |.| < 1024:
-    // alphabet values within [-500, 500) cover both
-    bool small = true;
-#pragma unroll
-    for (int j = 0; j < 8; j++) small = small && lo[j] >= -500 && lo[j] + T[j].n_sym <= 500;
     const int64_t head0 = vfirst / bph;
     set_scale(head0);
     int64_t head_end = (head0 + 1) * bph;            // first chunk vector of the next head
 
-    // ---- bitstream: words w0 .. wlim of the stream may be read
-    const uint32_t bp = blk_off[task];
+    PhaseLane d;
     const int64_t end_bit = g + 1 < nblk ? (int64_t)blk_off[task + 1] : stream_nbits[sid];
-    const uint32_t* const sw = words + chunk_base[chunk] + stream_woff[sid] + (bp >> 5);
-    const int wlim = (int)((end_bit >> 5) + 2 - (bp >> 5));          // last readable word, relative to sw
-    auto gword = [&](int i) { return sw[i < wlim ? i : wlim]; };
-    uint32_t* const rcol = &ring[0][tid];
-    // ring slot of relative word i is i % kRing; ld = next word to load, rd = next word into `pre`
-    int ld = 8, rd = 2;
-#pragma unroll
-    for (int i = 0; i < 8; i++) rcol[i * kDecLanes] = gword(i);
-    uint64_t buf = ((uint64_t)__builtin_bitreverse32(rcol[0]) << 32) << (bp & 31u);
-    uint32_t nbuf = 32u - (bp & 31u);
-    uint32_t pre = rcol[kDecLanes];
-    auto refill = [&]() {
-        if (nbuf < 32u) {
-            buf |= (uint64_t)__builtin_bitreverse32(pre) << (32u - nbuf);
-            nbuf += 32u;
-            pre = rcol[(rd & (kRing - 1)) * kDecLanes];
-            rd++;
-        }
-    };
-    refill();
+    d.init(words + chunk_base[chunk] + stream_woff[sid], blk_off[task], end_bit, blk_state[task], lut, idx,
+           &ring[0][tid], kDecLanes, bm[b]);
     const char* const lutb = reinterpret_cast<const char*>(lut);
-    uint32_t e = lut[idx * kL + (int)blk_state[task] - kL];
-    uint32_t q0 = 0, q1 = 0, q2 = 0, q3 = 0;   // top-up in flight (loaded at the previous boundary)
-    bool inflight = false;
-
-    // coset-c vectors of the block in ascending order: current word wv (bits
-    // not yet taken), its index wi, and the next word wn
-    int wi = 0;
-    uint32_t wv = bm[b][0], wn = bm[b][1];
-
     using OutT = typename std::conditional<OUT_DT == LQ_F32, float, uint16_t>::type;
     OutT* const ob = reinterpret_cast<OutT*>(out) + (chunk * V + vfirst) * 8;
     uint16_t* const my_stg = &stg[b * kStgRow + idx];
 
-    for (int s0 = 0; s0 < n; s0 += kDecPhase) {
-        // ---- boundary: land the previous top-up, issue the next one
-        if (inflight) {
-            rcol[(ld & (kRing - 1)) * kDecLanes] = q0;
-            rcol[((ld + 1) & (kRing - 1)) * kDecLanes] = q1;
-            rcol[((ld + 2) & (kRing - 1)) * kDecLanes] = q2;
-            rcol[((ld + 3) & (kRing - 1)) * kDecLanes] = q3;
-            ld += 4;
-            inflight = false;
-        }
-        if (ld - rd <= kRing - 4) {   // room for 4 more words even if nothing is consumed
-            q0 = gword(ld); q1 = gword(ld + 1); q2 = gword(ld + 2); q3 = gword(ld + 3);
-            inflight = true;
-        }
-        const int m = n - s0 < kDecPhase ? n - s0 : kDecPhase;
-        int vsv = 0;   // block position of this lane's vector of the phase
-        auto one = [&](int j) {
-            if (j % 3 == 0) refill();
-            my_stg[j * 8] = (uint16_t)__builtin_amdgcn_ubfe(e, 9, 10);
-            if (wv == 0) {
-                wi++;
-                wv = wn;
-                wn = bm[b][wi + 1 <= kBlk / 32 ? wi + 1 : kBlk / 32];
-                while (wv == 0) {   // a word with no coset-c vector
-                    wi++;
-                    wv = wn;
-                    wn = bm[b][wi + 1 <= kBlk / 32 ? wi + 1 : kBlk / 32];
-                }
-            }
-            const int vl = (wi << 5) | __builtin_ctz(wv);
-            wv &= wv - 1u;
-            vsv = idx == j ? vl : vsv;
-            const uint32_t bits = (uint32_t)(buf >> 33) >> (e & 31u);
-            const uint32_t k = __builtin_amdgcn_ubfe(e, 5, 4);
-            const uint32_t addr = ((e >> 19) + bits) << 2;
-            buf <<= k;
-            nbuf -= k;
-            e = *reinterpret_cast<const uint32_t*>(lutb + addr);
-        };
-        if (m == kDecPhase) {
-#pragma unroll
-            for (int j = 0; j < kDecPhase; j++) one(j);
-        } else {
-#pragma unroll
-            for (int j = 0; j < kDecPhase; j++)
-                if (j < m) one(j);
-        }
-        // ---- flush: lane idx rebuilds the vector of step idx
-        if (idx < m) {
+    for (int s0 = 0; s0 < n; s0 += kPhase) {
+        d.boundary();
+        const int m = n - s0 < kPhase ? n - s0 : kPhase;
+        const int vl = d.phase(m, idx, my_stg, lutb);
+        if (idx < m) {   // lane idx rebuilds the vector of step idx
             const uint4 r = *reinterpret_cast<const uint4*>(&stg[b * kStgRow + idx * 8]);
-            const int vl = vsv;
             if (!HEADS_ALIGNED && vfirst + vl >= head_end) {
                 const int64_t head = (vfirst + vl) / bph;
                 head_end = (head + 1) * bph;
                 set_scale(head);
             }
-            const uint32_t px = r.x ^ r.y ^ r.z ^ (r.w & 0xffffu);
-            const uint32_t par = (px ^ (px >> 16) ^ lpar) & 1u;
-            if (OUT_DT == LQ_F16 && small) {
-                // c7 index doubled plus the parity, in the high half of r.w
-                const uint32_t w3 = (r.w & 0xffffu) | (((r.w >> 16) * 2u + par) << 16);
-                uint4 o;
-                o.x = deq_pair_f16(r.x, lo2[0], sc2);
-                o.y = deq_pair_f16(r.y, lo2[1], sc2);
-                o.z = deq_pair_f16(r.z, lo2[2], sc2);
-                o.w = deq_pair_f16(w3, lo2[3], sc2);
-                reinterpret_cast<uint4*>(ob)[vl] = o;
+            if (OUT_DT == LQ_F16 && cc.small) {
+                reinterpret_cast<uint4*>(ob)[vl] = cc.deq_f16(r, sc2);
             } else {
-                const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
                 float y[8];
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    uint32_t v = (j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu);
-                    if (j == 7) v = 2u * v + par;
-                    y[j] = __builtin_fmaf((float)v, sc, cst[j]);
-                }
+                cc.deq_f32(r, sc, y);
                 store8(ob, OUT_DT, vl, y);
             }
         }

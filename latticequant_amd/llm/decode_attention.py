@@ -4,9 +4,10 @@ out = softmax(q K^T / sqrt(128)) V over a prefix held as E8 + rANS chunks
 (the reference's bitstreams, llm/compressed_kv_cache.py:176-287) followed by
 an fp16 residual tail.  K and V are dequantised the way _decompress_chunk
 does (lattice point times the fp16-stored scale,
-llm/compressed_kv_cache.py:289-332), inside the kernels: the prefix is never
-materialised in fp16.  The kernels are lq_decode_attention's three launches
-(scores, weighted values, log-sum-exp combine with the tail).
+llm/compressed_kv_cache.py:289-332).  The scores are computed straight from
+K's bitstreams (K is never materialised); V is decoded to fp16 in workspace
+by the chunk decoder and consumed by a split-token softmax . V pass, whose
+records are merged with the tail's by log-sum-exp (lq_decode_attention).
 """
 from __future__ import annotations
 
@@ -23,7 +24,7 @@ def chunk_batch(enc: EncodedBatch) -> L.ChunkBatch:
     """lq_chunk_batch view of an EncodedBatch (device pointers, no copies)."""
     return L.ChunkBatch(words=enc.words.data_ptr(), chunk_base=enc.chunk_base.data_ptr(),
                         stream_woff=enc.stream_woff.data_ptr(), blk_off=enc.blk_off.data_ptr(),
-                        blk_state=enc.blk_state.data_ptr(), coset_bits=enc.coset_bits.data_ptr(),
+                        stream_nbits=enc.stream_nbits.data_ptr(), blk_state=enc.blk_state.data_ptr(), coset_bits=enc.coset_bits.data_ptr(),
                         blk_n1=enc.blk_n1.data_ptr(), tables=enc.tables.data_ptr(), scale16=enc.scale16.data_ptr(),
                         n_chunks=enc.n_chunks, n_heads=enc.n_heads, bph=enc.bph)
 
