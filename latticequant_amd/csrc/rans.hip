@@ -555,55 +555,97 @@ __global__ void k_chunk_offsets(const int64_t* __restrict__ stream_nbits, const 
     chunk_words[c] = w;
 }
 
-// Sixteen lanes per task.  A task owns the stream words whose first bit falls
-// in its block.  Words that end inside the block are a funnel shift of its
-// right-aligned scratch by one per-task shift; only the word holding the
-// block's last bit (when that is not word-aligned) reaches into later blocks.
-__global__ __launch_bounds__(256) void k_chunk_pack(int64_t n_tasks, int64_t nblk, const uint32_t* __restrict__ blk_bits,
-                                                    const uint32_t* __restrict__ scratch, const uint32_t* __restrict__ blk_off,
+// One wave per (stream, group of 32 blocks).  The group owns the stream
+// words whose first bit lies in its blocks' bit range; lane l assembles words
+// W0 + l + 64 k, four per round with all their scratch loads in flight
+// (256-byte coalesced stores).  A word's first bits come from the
+// right-aligned scratch of the block holding its first bit (binary search over
+// the group's offsets, staged in LDS); the rare word that runs past that
+// block's end continues block by block.  Stream bit positions are 32-bit
+// (blk_off is uint32).
+constexpr int kPackBlocks = 32;
+
+__global__ __launch_bounds__(256) void k_chunk_pack(int64_t n_streams_total, int64_t nblk, const uint32_t* __restrict__ scratch,
+                                                    const uint32_t* __restrict__ blk_off,
                                                     const int64_t* __restrict__ stream_nbits,
                                                     const int64_t* __restrict__ stream_woff,
-                                                    const int64_t* __restrict__ chunk_base, uint32_t* __restrict__ words) {
-    const int64_t g = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);   // grid: (blocks / 16, chunks * 16)
-    const int lane = threadIdx.x & 15;
-    if (g >= nblk) return;
-    const int64_t sid = blockIdx.y, chunk = sid / LQ_STREAMS;
-    const int64_t task = sid * nblk + g;
-    const uint32_t b = blk_bits[task];
-    if (b == 0) return;
-    const int64_t off = blk_off[task];
-    uint32_t* out = words + chunk_base[chunk] + stream_woff[sid];
-    const uint32_t* scr = scratch + task * (int64_t)kCapW;
-    const int64_t w_first = (off + 31) >> 5, w_full = (off + b) >> 5;
-    const int64_t sp0 = (int64_t)kCapW * 32 - b + 32 * w_first - off;   // scratch bit of word w_first
-    const int sh = (int)(sp0 & 31);
-    const int64_t k0 = sp0 >> 5;
-    for (int64_t j = lane; w_first + j < w_full; j += 16) {
-        uint64_t v = scr[k0 + j];
-        if (sh) v |= (uint64_t)scr[k0 + j + 1] << 32;
-        out[w_first + j] = (uint32_t)(v >> sh);
+                                                    const int64_t* __restrict__ chunk_base,
+                                                    const lq_table* __restrict__ tables, uint32_t* __restrict__ words) {
+    __shared__ uint32_t offs[4][kPackBlocks + 1];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t gps = (nblk + kPackBlocks - 1) / kPackBlocks;   // groups per stream
+    const int64_t job = (int64_t)blockIdx.x * 4 + wave;
+    const int64_t sid = job / gps;
+    const int64_t g0 = (job % gps) * kPackBlocks;
+    if (sid >= n_streams_total || tables[sid].n_sym == 0) return;   // wave-uniform; no barrier follows
+    const uint32_t nbits = (uint32_t)stream_nbits[sid];
+    const int nb = (int)(nblk - g0 < kPackBlocks ? nblk - g0 : kPackBlocks);
+    const uint32_t* bo = blk_off + sid * nblk;
+    // offset of block g0 + i (the stream end past the last block)
+    auto off_mem = [&](int i) -> uint32_t { return g0 + i < nblk ? bo[g0 + i] : nbits; };
+    uint32_t* of = offs[wave];
+    if (lane <= nb) of[lane] = off_mem(lane);
+    __builtin_amdgcn_wave_barrier();
+    const uint32_t W0 = (of[0] + 31u) >> 5, W1 = (of[nb] + 31u) >> 5;
+    uint32_t* out = words + chunk_base[sid / LQ_STREAMS] + stream_woff[sid];
+    const uint32_t* scr0 = scratch + (sid * nblk + g0) * (int64_t)kCapW;
+    constexpr uint32_t kCapBits = (uint32_t)kCapW * 32u;
+    for (uint32_t wb = W0 + lane; wb < W1; wb += 256) {
+        uint32_t lo[4], hi[4], res[4];
+        int blk[4], take[4], s2[4];
+        uint32_t pe[4];   // bit after the word's first segment
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint32_t w = wb + 64u * u;
+            const bool ok = w < W1;
+            const uint32_t p = 32u * (ok ? w : W0);
+            // block holding bit p: largest b < nb with of[b] <= p
+            int b = 0;
+#pragma unroll
+            for (int step = kPackBlocks / 2; step > 0; step >>= 1)
+                if (b + step < nb && of[b + step] <= p) b += step;
+            const uint32_t ob = of[b], oe = of[b + 1];
+            const uint32_t end = p + 32u < nbits ? p + 32u : nbits;
+            const uint32_t e1 = end < oe ? end : oe;
+            const uint32_t sp = kCapBits - (oe - ob) + (p - ob);   // scratch bit of p
+            const uint32_t* sc = scr0 + (int64_t)b * kCapW;
+            const uint32_t k0 = sp >> 5;
+            lo[u] = sc[k0];
+            hi[u] = sc[k0 + 1 < (uint32_t)kCapW ? k0 + 1 : k0];
+            blk[u] = b;
+            take[u] = (int)(e1 - p);
+            s2[u] = (int)(sp & 31u);
+            pe[u] = e1;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint32_t w = wb + 64u * u;
+            if (w >= W1) continue;
+            uint64_t v = ((uint64_t)hi[u] << 32 | lo[u]) >> s2[u];
+            int got = take[u];
+            res[u] = got == 32 ? (uint32_t)v : (uint32_t)v & ((1u << got) - 1u);
+            uint32_t p = pe[u];
+            const uint32_t end = 32u * w + 32u < nbits ? 32u * w + 32u : nbits;
+            int b = blk[u] + 1;
+            while (p < end) {   // the word continues in the following block(s)
+                const uint32_t ob = off_mem(b), oe = off_mem(b + 1);
+                if (oe > ob) {
+                    const uint32_t e1 = end < oe ? end : oe;
+                    const int tk = (int)(e1 - p);
+                    const uint32_t sp = kCapBits - (oe - ob) + (p - ob);
+                    const uint32_t* sc = scr0 + (int64_t)b * kCapW;
+                    uint64_t x = sc[sp >> 5];
+                    if ((int)(sp & 31u) + tk > 32) x |= (uint64_t)sc[(sp >> 5) + 1] << 32;
+                    x >>= (sp & 31u);
+                    res[u] |= (tk == 32 ? (uint32_t)x : (uint32_t)x & ((1u << tk) - 1u)) << got;
+                    got += tk;
+                    p = e1;
+                }
+                b++;
+            }
+            out[w] = res[u];
+        }
     }
-    const int64_t wl = (off + b) >> 5;
-    if (lane != 0 || ((off + b) & 31) == 0 || 32 * wl < off) return;
-    // word wl: bits [32 wl, off + b) from this block, the rest from the next blocks
-    const int64_t nbits = stream_nbits[sid];
-    const int64_t end = 32 * wl + 32 < nbits ? 32 * wl + 32 : nbits;
-    int64_t cur = 32 * wl, ho = off, t = task;
-    uint32_t hb = b, res = 0;
-    while (cur < end) {
-        while (cur >= ho + hb) { t++; ho = blk_off[t]; hb = blk_bits[t]; }
-        const int64_t lim = end < ho + hb ? end : ho + hb;
-        const int take = (int)(lim - cur);
-        const int64_t sp = (int64_t)kCapW * 32 - hb + (cur - ho);
-        const uint32_t* sc = scratch + t * (int64_t)kCapW;
-        const int s2 = (int)(sp & 31);
-        uint64_t v = sc[sp >> 5];
-        if (s2 + take > 32) v |= (uint64_t)sc[(sp >> 5) + 1] << 32;
-        v >>= s2;
-        res |= (take == 32 ? (uint32_t)v : (uint32_t)v & ((1u << take) - 1u)) << (int)(cur - 32 * wl);
-        cur += take;
-    }
-    out[wl] = res;
 }
 
 // trailing zero word of every present stream
@@ -928,11 +970,11 @@ int lq_chunk_pack(int64_t n_chunks, int64_t n_vectors, const lq_table* d_tables,
     if (n_chunks <= 0 || n_vectors <= 0) return LQ_ERR_ARG;
     const int64_t nblk = (n_vectors + kBlk - 1) / kBlk;
     EncWork w = enc_layout(n_chunks, n_vectors);
-    const uint32_t* bits = reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(d_work) + w.bits);
     const uint32_t* scratch = reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(d_work) + w.scratch);
-    const int64_t tasks = n_chunks * LQ_STREAMS * nblk;
-    hipLaunchKernelGGL(k_chunk_pack, dim3((unsigned)((nblk + 15) / 16), (unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s,
-                       tasks, nblk, bits, scratch, d_blk_off, d_stream_nbits, d_stream_woff, d_chunk_base, d_words);
+    const int64_t ns_total = n_chunks * LQ_STREAMS;
+    const int64_t jobs = ns_total * ((nblk + kPackBlocks - 1) / kPackBlocks);
+    hipLaunchKernelGGL(k_chunk_pack, dim3((unsigned)((jobs + 3) / 4)), dim3(256), 0, s, ns_total, nblk, scratch,
+                       d_blk_off, d_stream_nbits, d_stream_woff, d_chunk_base, d_tables, d_words);
     const int64_t ns = n_chunks * LQ_STREAMS;
     hipLaunchKernelGGL(k_chunk_tail, dim3((unsigned)((ns + 255) / 256)), dim3(256), 0, s, ns, d_tables,
                        d_stream_nbits, d_stream_woff, d_chunk_base, d_words);
