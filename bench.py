@@ -139,7 +139,7 @@ def main():
 
     def write():
         for gi, (a, b) in enumerate(groups):
-            encs[gi], _ = codec.encode_batch(x[a:b], BITS, exact_size=False, words_out=arenas[gi])
+            encs[gi], _ = codec.encode_batch(x[a:b], BITS, exact_size=False, words_out=arenas[gi], wide=False)
 
     def read():
         for gi, (a, b) in enumerate(groups):

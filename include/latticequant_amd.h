@@ -30,8 +30,9 @@ extern "C" {
 
 #define LQ_L 1024          /* rANS precision (reference core/gpu_ans.py:44-45) */
 #define LQ_BLK 512         /* vectors per checkpoint block */
-#define LQ_SYM_STRIDE 4352 /* int8 symbol bytes per block (8 * LQ_BLK + 2 x 128 padding) */
-#define LQ_MAXSYM 264      /* alphabet capacity of a chunk table (int8 symbols + 4 guard entries) */
+#define LQ_SYM_STRIDE 4352 /* symbols per block in the staging layout (8 * LQ_BLK + 2 x 128 padding);
+                              bytes: x 1 for int8 symbols, x 2 for the wide (int16) path */
+#define LQ_MAXSYM 1028     /* alphabet capacity of a table: the reference's L = 1024 + 4 guard entries */
 #define LQ_STREAMS 16      /* 2 cosets x 8 coordinate streams per chunk */
 
 /* status codes */
@@ -42,7 +43,7 @@ extern "C" {
 #define LQ_ERR_RANGE -4        /* lattice symbol outside int8 */
 
 /* per-chunk status bits written by the device */
-#define LQ_ST_SYM_OVERFLOW 1   /* a lattice symbol did not fit int8 */
+#define LQ_ST_SYM_OVERFLOW 1   /* a lattice symbol did not fit the staging type (int8: use the wide path) */
 #define LQ_ST_ALPHABET 2       /* a stream alphabet exceeded L */
 #define LQ_ST_TIE_UNPINNED 4   /* table of > 256 symbols hit an argsort tie at a cut */
 
@@ -106,6 +107,25 @@ int lq_chunk_quantize(const void *d_x, int dtype, int64_t n_chunks, int64_t n_he
                       uint8_t *d_coset_bits, uint32_t *d_blk_n1, uint32_t *d_hist, int32_t *d_status,
                       void *d_deq, int deq_dtype, hipStream_t s);
 
+/* Wide path (alphabets up to L = 1024 symbols, e.g. heavy-tailed K at low
+ * rates): as lq_chunk_quantize with int16 symbols (n_chunks * nblk *
+ * LQ_SYM_STRIDE int16) and, instead of histograms, per-stream min / max in
+ * d_minmax (n_chunks * 16 * 2 int32, initialised to INT_MAX / INT_MIN).  A
+ * symbol outside int16 sets LQ_ST_SYM_OVERFLOW.  Followed by
+ * lq_chunk_hist_wide, lq_chunk_tables_wide, lq_chunk_encode_wide and the
+ * shared lq_chunk_pack / lq_chunk_decode.  Replaces the same reference lines
+ * as lq_chunk_quantize (llm/compressed_kv_cache.py:199-231,270). */
+int lq_chunk_quantize_wide(const void *d_x, int dtype, int64_t n_chunks, int64_t n_heads, int64_t bph,
+                           const float *d_scale32, const int32_t *d_fastdiv, int16_t *d_sym, uint8_t *d_coset_bits,
+                           uint32_t *d_blk_n1, int32_t *d_minmax, int32_t *d_status, void *d_deq, int deq_dtype,
+                           hipStream_t s);
+
+/* Wide path: per-stream histograms (n_chunks * 16 * 1024 uint32, zero on
+ * entry) of the int16 symbols in the window [min, min + 1023].
+ * Replaces the np.unique counting of llm/compressed_kv_cache.py:242-246. */
+int lq_chunk_hist_wide(const int16_t *d_sym, const uint32_t *d_blk_n1, int64_t n_chunks, int64_t n_vectors,
+                       const int32_t *d_minmax, uint32_t *d_hist, hipStream_t s);
+
 /* x / scale32[head] -> nearest E8 point (fp32 (n_heads * bph, 8)), head = vector / bph,
  * with the same arithmetic as lq_chunk_quantize.  d_fastdiv from lq_head_scales /
  * lq_scale_fastdiv.  Replaces llm/compressed_kv_cache.py:199-201 (x_scaled, encode_e8). */
@@ -120,6 +140,14 @@ int lq_e8_quantize_heads(const void *d_x, int dtype, int64_t n_heads, int64_t bp
 int lq_chunk_tables(const uint32_t *d_hist, int64_t n_chunks, lq_table *d_tables, int32_t *d_status,
                     hipStream_t s);
 
+/* Wide-path tables: alphabet range(min-2, max+2) from d_minmax, counts from
+ * lq_chunk_hist_wide; an alphabet above L = 1024 symbols (where the
+ * reference's normalisation loop never ends) sets LQ_ST_ALPHABET in the
+ * table and the chunk status and leaves the stream empty.
+ * Replaces llm/compressed_kv_cache.py:242-250 + core/gpu_ans.py:62-98. */
+int lq_chunk_tables_wide(const uint32_t *d_hist, const int32_t *d_minmax, int64_t n_chunks, lq_table *d_tables,
+                         int32_t *d_status, hipStream_t s);
+
 /* Workspace of the chunk encoder, in bytes. */
 int64_t lq_chunk_encode_workspace(int64_t n_chunks, int64_t n_vectors);
 
@@ -133,6 +161,12 @@ int lq_chunk_encode(const int8_t *d_sym, const uint32_t *d_blk_n1, int64_t n_chu
                     const lq_table *d_tables, void *d_work, uint32_t *d_blk_off, uint16_t *d_blk_state,
                     int64_t *d_stream_nbits, int32_t *d_stream_state, int64_t *d_stream_woff,
                     int64_t *d_chunk_words, hipStream_t s);
+
+/* lq_chunk_encode on the wide path's int16 symbols (same outputs). */
+int lq_chunk_encode_wide(const int16_t *d_sym, const uint32_t *d_blk_n1, int64_t n_chunks, int64_t n_vectors,
+                         const lq_table *d_tables, void *d_work, uint32_t *d_blk_off, uint16_t *d_blk_state,
+                         int64_t *d_stream_nbits, int32_t *d_stream_state, int64_t *d_stream_woff,
+                         int64_t *d_chunk_words, hipStream_t s);
 
 /* Write the merged bitstreams: chunk c's words start at d_words + d_chunk_base[c]
  * (caller-chosen, e.g. an exclusive prefix of d_chunk_words).  Each stream is

@@ -18,7 +18,7 @@ LIB_PATH = os.path.join(_HERE, "liblatticequant_amd.so")
 LQ_L = 1024
 LQ_BLK = 512
 LQ_SYM_STRIDE = 4352
-LQ_MAXSYM = 264
+LQ_MAXSYM = 1028
 LQ_STREAMS = 16
 LQ_F16, LQ_BF16, LQ_F32 = 0, 1, 2
 LQ_ST_SYM_OVERFLOW, LQ_ST_ALPHABET, LQ_ST_TIE_UNPINNED = 1, 2, 4
@@ -43,6 +43,10 @@ _SIGS = {
     "lq_scale_fastdiv": ([_P, _I64, _INT, _P, _P], _INT),
     "lq_chunk_quantize": ([_P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _INT, _P], _INT),
     "lq_chunk_tables": ([_P, _I64, _P, _P, _P], _INT),
+    "lq_chunk_quantize_wide": ([_P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _INT, _P], _INT),
+    "lq_chunk_hist_wide": ([_P, _P, _I64, _I64, _P, _P, _P], _INT),
+    "lq_chunk_tables_wide": ([_P, _P, _I64, _P, _P, _P], _INT),
+    "lq_chunk_encode_wide": ([_P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P], _INT),
     "lq_chunk_encode_workspace": ([_I64, _I64], _I64),
     "lq_chunk_encode": ([_P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P], _INT),
     "lq_chunk_pack": ([_I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P], _INT),

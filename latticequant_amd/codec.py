@@ -82,7 +82,8 @@ class EncodedBatch:
             blk_state=self.blk_state[c * S * nb:(c + 1) * S * nb], stream_nbits=self.stream_nbits[c * S:(c + 1) * S],
             stream_state=self.stream_state[c * S:(c + 1) * S], stream_woff=self.stream_woff[c * S:(c + 1) * S],
             chunk_words=self.chunk_words[c:c + 1], chunk_base=self.chunk_base[c:c + 1], words=self.words,
-            status=self.status[c:c + 1], hist=None if self.hist is None else self.hist[c * S * 256:(c + 1) * S * 256])
+            status=self.status[c:c + 1],
+            hist=None if self.hist is None else self.hist.view(C, -1)[c], extra=dict(self.extra))
 
     # ---- byte accounting -------------------------------------------------
     def reference_bytes(self) -> torch.Tensor:
@@ -204,8 +205,21 @@ def quantize_points(t: torch.Tensor, bits, scale32: Optional[torch.Tensor] = Non
     return q, scale32, scale16
 
 
+def _status_or(status: torch.Tensor) -> int:
+    """OR of the per-chunk LQ_ST_* bits (one device-to-host copy)."""
+    st = 0
+    for v in status.cpu().tolist():
+        st |= int(v)
+    return st
+
+
+class AlphabetError(ValueError):
+    """A stream's alphabet range(min-2, max+2) exceeds L = 1024 symbols: the
+    reference's build_rans_table never terminates there (core/gpu_ans.py:73-84)."""
+
+
 def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, deq_out: bool = False,
-                 exact_size: bool = True, words_out: Optional[torch.Tensor] = None):
+                 exact_size: bool = True, words_out: Optional[torch.Tensor] = None, wide="auto"):
     """Compress a batch of chunks.
 
     x: (C, B, H, T, hd) fp16 / bf16 / fp32 CUDA tensor, hd % 8 == 0.
@@ -215,6 +229,12 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
     exact_size: allocate the bitstream arena at its exact size (one host sync);
       else at a no-sync upper bound (10 bits per symbol).
     words_out: caller-provided arena (int32) large enough for the upper bound.
+    wide: symbol staging width.  False: int8 (lattice symbols within int8; a
+      chunk beyond sets LQ_ST_SYM_OVERFLOW in enc.status).  True: int16, for
+      alphabets up to 1024 symbols.  "auto": int8 first, and if a chunk
+      overflowed (one status read-back) the batch is redone on the wide path.
+    An alphabet above 1024 symbols raises AlphabetError when the status is read
+    back (wide="auto" or True with exact_size) and is otherwise left in enc.status.
     Returns (EncodedBatch, deq or None)."""
     lib = L.lib()
     x = _check_input(x)
@@ -226,17 +246,43 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
     dt = L.dtype_code(x.dtype)
     s = L.stream_ptr(dev)
     bits_t, scale32, scale16, sigma2, fastdiv = _head_scales(x, bits, scale32)
-    sym = _empty(C * nblk * L.LQ_SYM_STRIDE, torch.int8, dev)
     coset_bits = _zeros(C * nblk * L.LQ_BLK // 8, torch.uint8, dev)
     blk_n1 = _empty(C * nblk, torch.int32, dev)
-    hist = _zeros(C * L.LQ_STREAMS * 256, torch.int32, dev)
     status = _zeros(C, torch.int32, dev)
     deq = torch.empty_like(x) if deq_out else None
-    L.check(lib.lq_chunk_quantize(x.data_ptr(), dt, C, nh, bph, scale32.data_ptr(), fastdiv.data_ptr(), sym.data_ptr(),
-                                  coset_bits.data_ptr(), blk_n1.data_ptr(), hist.data_ptr(), status.data_ptr(),
-                                  L.ptr(deq), dt, s), "lq_chunk_quantize")
     tables = _empty(C * L.LQ_STREAMS * L.TABLE_BYTES, torch.uint8, dev)
-    L.check(lib.lq_chunk_tables(hist.data_ptr(), C, tables.data_ptr(), status.data_ptr(), s), "lq_chunk_tables")
+    use_wide = wide is True
+    if not use_wide:
+        sym = _empty(C * nblk * L.LQ_SYM_STRIDE, torch.int8, dev)
+        hist = _zeros(C * L.LQ_STREAMS * 256, torch.int32, dev)
+        L.check(lib.lq_chunk_quantize(x.data_ptr(), dt, C, nh, bph, scale32.data_ptr(), fastdiv.data_ptr(),
+                                      sym.data_ptr(), coset_bits.data_ptr(), blk_n1.data_ptr(), hist.data_ptr(),
+                                      status.data_ptr(), L.ptr(deq), dt, s), "lq_chunk_quantize")
+        if wide == "auto" and _status_or(status) & L.LQ_ST_SYM_OVERFLOW:
+            use_wide = True
+            status.zero_()
+        else:
+            L.check(lib.lq_chunk_tables(hist.data_ptr(), C, tables.data_ptr(), status.data_ptr(), s), "lq_chunk_tables")
+    if use_wide:
+        sym = _empty(C * nblk * L.LQ_SYM_STRIDE, torch.int16, dev)
+        minmax = torch.empty(C * L.LQ_STREAMS, 2, dtype=torch.int32, device=dev)
+        minmax[:, 0] = 2 ** 31 - 1
+        minmax[:, 1] = -2 ** 31
+        hist = _zeros(C * L.LQ_STREAMS * L.LQ_L, torch.int32, dev)
+        L.check(lib.lq_chunk_quantize_wide(x.data_ptr(), dt, C, nh, bph, scale32.data_ptr(), fastdiv.data_ptr(),
+                                           sym.data_ptr(), coset_bits.data_ptr(), blk_n1.data_ptr(), minmax.data_ptr(),
+                                           status.data_ptr(), L.ptr(deq), dt, s), "lq_chunk_quantize_wide")
+        L.check(lib.lq_chunk_hist_wide(sym.data_ptr(), blk_n1.data_ptr(), C, V, minmax.data_ptr(), hist.data_ptr(), s),
+                "lq_chunk_hist_wide")
+        L.check(lib.lq_chunk_tables_wide(hist.data_ptr(), minmax.data_ptr(), C, tables.data_ptr(), status.data_ptr(), s),
+                "lq_chunk_tables_wide")
+        if wide == "auto" or exact_size:
+            st = _status_or(status)
+            if st & L.LQ_ST_ALPHABET:
+                raise AlphabetError("a stream's alphabet exceeds L = 1024 symbols (the reference's table "
+                                    "normalisation never terminates there); use more bits or smaller chunks")
+            if st & L.LQ_ST_SYM_OVERFLOW:
+                raise AlphabetError("a lattice symbol does not fit int16")
     ws = lib.lq_chunk_encode_workspace(C, V)
     work = _empty(ws, torch.uint8, dev)
     ntask = C * L.LQ_STREAMS * nblk
@@ -246,10 +292,11 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
     stream_state = _empty(C * L.LQ_STREAMS, torch.int32, dev)
     stream_woff = _empty(C * L.LQ_STREAMS, torch.int64, dev)
     chunk_words = _empty(C, torch.int64, dev)
-    L.check(lib.lq_chunk_encode(sym.data_ptr(), blk_n1.data_ptr(), C, V, tables.data_ptr(), work.data_ptr(),
-                                blk_off.data_ptr(), blk_state.data_ptr(), stream_nbits.data_ptr(),
-                                stream_state.data_ptr(), stream_woff.data_ptr(), chunk_words.data_ptr(), s),
-            "lq_chunk_encode")
+    enc_fn = lib.lq_chunk_encode_wide if use_wide else lib.lq_chunk_encode
+    L.check(enc_fn(sym.data_ptr(), blk_n1.data_ptr(), C, V, tables.data_ptr(), work.data_ptr(),
+                   blk_off.data_ptr(), blk_state.data_ptr(), stream_nbits.data_ptr(),
+                   stream_state.data_ptr(), stream_woff.data_ptr(), chunk_words.data_ptr(), s),
+            "lq_chunk_encode_wide" if use_wide else "lq_chunk_encode")
     chunk_base = torch.cumsum(chunk_words, 0) - chunk_words
     bound = words_bound(C, V)
     if words_out is not None:
@@ -266,7 +313,7 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
                        scale16=scale16, sigma2=sigma2, coset_bits=coset_bits.view(C, -1), blk_n1=blk_n1.view(C, -1),
                        tables=tables, blk_off=blk_off, blk_state=blk_state, stream_nbits=stream_nbits,
                        stream_state=stream_state, stream_woff=stream_woff, chunk_words=chunk_words,
-                       chunk_base=chunk_base, words=words, status=status, hist=hist)
+                       chunk_base=chunk_base, words=words, status=status, hist=hist, extra={"wide": use_wide})
     return enc, deq
 
 

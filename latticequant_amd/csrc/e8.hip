@@ -1,5 +1,7 @@
 // E8 lattice kernels for gfx950: nearest-point search, symbolisation,
 // per-head scales and the chunk quantizer of the compressed-KV write path.
+#include <climits>
+
 #include "lq_device.h"
 
 using namespace lq;
@@ -169,17 +171,25 @@ constexpr int kQBlocksPerWG = 4;
 
 // One workgroup quantizes kQBlocksPerWG consecutive LQ_BLK-vector blocks of one
 // chunk.  Per block it writes the coset bitmap (wave ballots, i.e. the
-// reference's LSB-first pack_coset_bits layout), the coset-1 count and the int8
-// symbols in the interleaved column layout of sym_pos, staged in LDS so the
-// global stores are 16-byte and contiguous.  Histograms accumulate in LDS and
-// are flushed once per workgroup.
+// reference's LSB-first pack_coset_bits layout), the coset-1 count and the
+// symbols in the interleaved column layout of sym_pos (element index; int8
+// symbols, or int16 for the wide path), staged in LDS so the global stores are
+// 16-byte and contiguous.  int8: the 16 x 256 symbol histograms accumulate in
+// LDS and are flushed once per workgroup; a symbol outside int8 sets
+// LQ_ST_SYM_OVERFLOW (the chunk then needs the wide path).  int16: per-stream
+// min / max instead (the histogram of the wide path is a second pass over the
+// symbols, in the window the min fixes).
+template <typename SymT>
 __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
     const void* __restrict__ x, int dtype, int64_t n_heads, int64_t bph, int64_t nblk,
-    const float* __restrict__ scale32, const int32_t* __restrict__ fastdiv, int8_t* __restrict__ sym,
+    const float* __restrict__ scale32, const int32_t* __restrict__ fastdiv, SymT* __restrict__ sym,
     uint8_t* __restrict__ coset_bits, uint32_t* __restrict__ blk_n1, uint32_t* __restrict__ hist,
-    int32_t* __restrict__ status, void* __restrict__ deq, int deq_dtype) {
-    __shared__ uint32_t shist[LQ_STREAMS * 256];
-    __shared__ __align__(16) int8_t stage[kSymStride];
+    int32_t* __restrict__ minmax, int32_t* __restrict__ status, void* __restrict__ deq, int deq_dtype) {
+    constexpr bool kWide = sizeof(SymT) == 2;
+    constexpr int kSymMin = kWide ? -32768 : -128, kSymMax = kWide ? 32767 : 127;
+    __shared__ uint32_t shist[kWide ? 1 : LQ_STREAMS * 256];
+    __shared__ int smin[LQ_STREAMS], smax[LQ_STREAMS];
+    __shared__ __align__(16) SymT stage[kSymStride];
     __shared__ unsigned long long masks[kBlk / 64];
     __shared__ int sflag;
 
@@ -191,9 +201,18 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
     const int64_t b0 = (blockIdx.x % wg_per_chunk) * kQBlocksPerWG;
     const int64_t V = n_heads * bph;
 
-    for (int i = tid; i < LQ_STREAMS * 256; i += kQThreads) shist[i] = 0;
+    if constexpr (!kWide) {
+        for (int i = tid; i < LQ_STREAMS * 256; i += kQThreads) shist[i] = 0;
+    }
+    if (tid < LQ_STREAMS) { smin[tid] = INT_MAX; smax[tid] = INT_MIN; }
     if (tid == 0) sflag = 0;
     __syncthreads();
+    // wide path: this thread's running min / max per stream
+    int tmin[kWide ? LQ_STREAMS : 1], tmax[kWide ? LQ_STREAMS : 1];
+    if constexpr (kWide) {
+#pragma unroll
+        for (int i = 0; i < LQ_STREAMS; i++) { tmin[i] = INT_MAX; tmax[i] = INT_MIN; }
+    }
 
     int flag = 0;
     for (int bi = 0; bi < kQBlocksPerWG; bi++) {
@@ -201,7 +220,7 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
         if (blk >= nblk) break;
         const int64_t vbase = blk * kBlk;
         const int valid = (int)((V - vbase) < kBlk ? (V - vbase) : kBlk);
-        int8_t sy[2][8];
+        int32_t sy[2][8];
         int cs[2];
         // pass 1: quantize two vectors per thread
 #pragma unroll
@@ -224,8 +243,8 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
                 for (int i = 0; i < 8; i++) {
                     int32_t iv = (int32_t)ic[i];
                     int32_t sv = i < 7 ? iv : (iv >> 1);
-                    if (sv < -128 || sv > 127) { flag = 1; sv = sv < -128 ? -128 : 127; }
-                    sy[r][i] = (int8_t)sv;
+                    if (sv < kSymMin || sv > kSymMax) { flag = 1; sv = sv < kSymMin ? kSymMin : kSymMax; }
+                    sy[r][i] = sv;
                 }
                 if (deq) {
                     float off = c ? 0.5f : 0.f, y[8];
@@ -255,12 +274,26 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
                 int rank0 = vl - rank1;
                 const int c = cs[r];
                 const int rk = c ? rank1 : rank0;
-                int8_t* sp = stage + sym_pos(c, 0, rk, n0);   // column i adds 16 * i
-                uint32_t* hp = shist + c * 8 * 256 + 128;
+                SymT* sp = stage + sym_pos(c, 0, rk, n0);   // column i adds 16 * i
+                if constexpr (!kWide) {
+                    uint32_t* hp = shist + c * 8 * 256 + 128;
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    sp[16 * i] = sy[r][i];
-                    atomicAdd(hp + i * 256 + (int)sy[r][i], 1u);
+                    for (int i = 0; i < 8; i++) {
+                        sp[16 * i] = (SymT)sy[r][i];
+                        atomicAdd(hp + i * 256 + sy[r][i], 1u);
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        sp[16 * i] = (SymT)sy[r][i];
+                        // c is 0 or 1: update both halves with selects (registers stay static)
+#pragma unroll
+                        for (int cc = 0; cc < 2; cc++) {
+                            const int st = cc * 8 + i;
+                            tmin[st] = c == cc ? min(tmin[st], sy[r][i]) : tmin[st];
+                            tmax[st] = c == cc ? max(tmax[st], sy[r][i]) : tmax[st];
+                        }
+                    }
                 }
             }
         }
@@ -268,7 +301,7 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
         // copy-out: symbols, coset bitmap, block count
         {
             const int64_t gblk = chunk * nblk + blk;
-            const int nbytes = sym_region(1, n0) + 128 * ((n1 + 15) >> 4);
+            const int nbytes = (sym_region(1, n0) + 128 * ((n1 + 15) >> 4)) * (int)sizeof(SymT);
             uint4* dst = reinterpret_cast<uint4*>(sym + gblk * (int64_t)kSymStride);
             const uint4* src = reinterpret_cast<const uint4*>(stage);
             for (int i = tid; i * 16 < nbytes; i += kQThreads) dst[i] = src[i];
@@ -279,13 +312,66 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
         __syncthreads();
     }
     if (flag) atomicOr(&sflag, 1);
+    if constexpr (kWide) {
+#pragma unroll
+        for (int i = 0; i < LQ_STREAMS; i++) {
+            if (tmin[i] != INT_MAX) atomicMin(&smin[i], tmin[i]);
+            if (tmax[i] != INT_MIN) atomicMax(&smax[i], tmax[i]);
+        }
+    }
     __syncthreads();
-    uint32_t* gh = hist + chunk * (LQ_STREAMS * 256);
-    for (int i = tid; i < LQ_STREAMS * 256; i += kQThreads) {
-        uint32_t c = shist[i];
-        if (c) atomicAdd(gh + i, c);
+    if constexpr (!kWide) {
+        uint32_t* gh = hist + chunk * (LQ_STREAMS * 256);
+        for (int i = tid; i < LQ_STREAMS * 256; i += kQThreads) {
+            uint32_t c = shist[i];
+            if (c) atomicAdd(gh + i, c);
+        }
+    } else {
+        if (tid < LQ_STREAMS && smax[tid] != INT_MIN) {
+            atomicMin(minmax + (chunk * LQ_STREAMS + tid) * 2, smin[tid]);
+            atomicMax(minmax + (chunk * LQ_STREAMS + tid) * 2 + 1, smax[tid]);
+        }
     }
     if (tid == 0 && sflag) atomicOr(status + chunk, LQ_ST_SYM_OVERFLOW);
+}
+
+// Wide path, second pass: histograms of the int16 symbols in the window
+// [min, min + 1023] of each stream (a stream whose max exceeds the window has
+// an alphabet beyond L and is flagged by the table stage).  Workgroup: 16
+// blocks x 16 streams of one chunk, one lane per (block, stream) column;
+// counts accumulate in LDS (16 x 1024) and are added to hist once.
+constexpr int kHBlocks = 16;
+
+__global__ __launch_bounds__(256) void k_chunk_hist_wide(const int16_t* __restrict__ sym, const uint32_t* __restrict__ blk_n1,
+                                                         int64_t nblk, int64_t V, const int32_t* __restrict__ minmax,
+                                                         uint32_t* __restrict__ hist) {
+    __shared__ uint32_t sh[LQ_STREAMS * LQ_L];
+    const int tid = threadIdx.x;
+    const int64_t chunk = blockIdx.y;
+    for (int i = tid; i < LQ_STREAMS * LQ_L; i += 256) sh[i] = 0;
+    __syncthreads();
+    const int64_t g = (int64_t)blockIdx.x * kHBlocks + (tid >> 4);
+    const int st = tid & 15;
+    if (g < nblk) {
+        const int c = st >> 3, idx = st & 7;
+        const int64_t valid = V - g * kBlk < kBlk ? V - g * kBlk : kBlk;
+        const int n1 = (int)blk_n1[chunk * nblk + g];
+        const int n0 = (int)valid - n1;
+        const int n = c ? n1 : n0;
+        const int lo = minmax[(chunk * LQ_STREAMS + st) * 2];
+        const int16_t* col = sym + (chunk * nblk + g) * (int64_t)kSymStride + sym_region(c, n0) + 16 * idx;
+        uint32_t* hs = sh + st * LQ_L;
+        for (int r = 0; r < n; r++) {
+            const int v = col[((r >> 4) << 7) + (r & 15)] - lo;
+            if (v < LQ_L) atomicAdd(hs + v, 1u);
+        }
+    }
+    __syncthreads();
+    uint32_t* gh = hist + chunk * (LQ_STREAMS * LQ_L);
+    for (int i = tid; i < LQ_STREAMS * LQ_L; i += 256) {
+        const uint32_t cnt = sh[i];
+        if (cnt) atomicAdd(gh + i, cnt);
+    }
 }
 
 inline int launch_status() { return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_LAUNCH; }
@@ -351,8 +437,32 @@ int lq_chunk_quantize(const void* d_x, int dtype, int64_t n_chunks, int64_t n_he
     const int64_t V = n_heads * bph;
     const int64_t nblk = (V + kBlk - 1) / kBlk;
     const int64_t wg = n_chunks * ((nblk + kQBlocksPerWG - 1) / kQBlocksPerWG);
-    hipLaunchKernelGGL(k_chunk_quantize, dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x, dtype, n_heads, bph, nblk,
-                       d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, d_hist, d_status, d_deq, deq_dtype);
+    hipLaunchKernelGGL((k_chunk_quantize<int8_t>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x, dtype, n_heads, bph,
+                       nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, d_hist, nullptr, d_status, d_deq,
+                       deq_dtype);
+    return launch_status();
+}
+
+int lq_chunk_quantize_wide(const void* d_x, int dtype, int64_t n_chunks, int64_t n_heads, int64_t bph,
+                           const float* d_scale32, const int32_t* d_fastdiv, int16_t* d_sym, uint8_t* d_coset_bits,
+                           uint32_t* d_blk_n1, int32_t* d_minmax, int32_t* d_status, void* d_deq, int deq_dtype,
+                           hipStream_t s) {
+    if (n_chunks <= 0 || n_heads <= 0 || bph <= 0 || dtype < 0 || dtype > 2 || !d_minmax) return LQ_ERR_ARG;
+    const int64_t V = n_heads * bph;
+    const int64_t nblk = (V + kBlk - 1) / kBlk;
+    const int64_t wg = n_chunks * ((nblk + kQBlocksPerWG - 1) / kQBlocksPerWG);
+    hipLaunchKernelGGL((k_chunk_quantize<int16_t>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x, dtype, n_heads,
+                       bph, nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, nullptr, d_minmax, d_status,
+                       d_deq, deq_dtype);
+    return launch_status();
+}
+
+int lq_chunk_hist_wide(const int16_t* d_sym, const uint32_t* d_blk_n1, int64_t n_chunks, int64_t n_vectors,
+                       const int32_t* d_minmax, uint32_t* d_hist, hipStream_t s) {
+    if (n_chunks <= 0 || n_vectors <= 0 || !d_sym || !d_minmax || !d_hist) return LQ_ERR_ARG;
+    const int64_t nblk = (n_vectors + kBlk - 1) / kBlk;
+    hipLaunchKernelGGL(k_chunk_hist_wide, dim3((unsigned)((nblk + kHBlocks - 1) / kHBlocks), (unsigned)n_chunks),
+                       dim3(256), 0, s, d_sym, d_blk_n1, nblk, n_vectors, d_minmax, d_hist);
     return launch_status();
 }
 

@@ -14,6 +14,8 @@
 // the true history.  If the interval has not collapsed the window grows, up to
 // the end of the stream where the state is exactly L.  Results are therefore
 // exact, and identical to a serial encode.
+#include <climits>
+
 #include "lq_decode.h"
 
 using namespace lq;
@@ -234,8 +236,11 @@ __device__ void exclusive_scan_array(const int32_t* in, int n, int32_t* out) {
 
 // ------------------------------------------------------------ chunk tables --
 
-__global__ __launch_bounds__(256) void k_chunk_tables(const uint32_t* __restrict__ hist, lq_table* __restrict__ tables,
-                                                      int32_t* __restrict__ status) {
+// WIDE = false: hist holds 16 x 256 int8-symbol bins (value + 128).
+// WIDE = true:  hist holds 16 x 1024 bins from the stream's min (minmax).
+template <bool WIDE>
+__global__ __launch_bounds__(256) void k_chunk_tables(const uint32_t* __restrict__ hist, const int32_t* __restrict__ minmax,
+                                                      lq_table* __restrict__ tables, int32_t* __restrict__ status) {
     __shared__ int64_t counts[LQ_MAXSYM];
     __shared__ int32_t freqs[LQ_MAXSYM];
     __shared__ int64_t keys[256];
@@ -245,24 +250,51 @@ __global__ __launch_bounds__(256) void k_chunk_tables(const uint32_t* __restrict
     __shared__ uint32_t s_tot;
     const int64_t sid = blockIdx.x;   // chunk * 16 + stream
     const int tid = threadIdx.x;
-    h[tid] = hist[sid * 256 + tid];
-    if (tid == 0) { s_min = 256; s_max = -1; s_tot = 0; s_st = 0; }
-    __syncthreads();
-    if (h[tid]) { atomicMin(&s_min, tid); atomicMax(&s_max, tid); atomicAdd(&s_tot, h[tid]); }
-    __syncthreads();
     lq_table* T = tables + sid;
-    if (s_max < 0) {
-        if (tid == 0) { T->lo = 0; T->n_sym = 0; T->n_symbols = 0; T->status = 0; }
-        return;
-    }
-    const int lo = s_min - 128 - 2;
-    const int n = s_max - s_min + 5;
-    for (int i = tid; i < n; i += 256) {
-        int b = lo + i + 128;
-        counts[i] = (b >= 0 && b < 256) ? (int64_t)h[b] : 0;
+    int lo, n;
+    if constexpr (!WIDE) {
+        h[tid] = hist[sid * 256 + tid];
+        if (tid == 0) { s_min = 256; s_max = -1; s_tot = 0; s_st = 0; }
+        __syncthreads();
+        if (h[tid]) { atomicMin(&s_min, tid); atomicMax(&s_max, tid); atomicAdd(&s_tot, h[tid]); }
+        __syncthreads();
+        if (s_max < 0) {
+            if (tid == 0) { T->lo = 0; T->n_sym = 0; T->n_symbols = 0; T->status = 0; }
+            return;
+        }
+        lo = s_min - 128 - 2;
+        n = s_max - s_min + 5;
+        for (int i = tid; i < n; i += 256) {
+            int b = lo + i + 128;
+            counts[i] = (b >= 0 && b < 256) ? (int64_t)h[b] : 0;
+        }
+    } else {
+        const int mn = minmax[sid * 2], mx = minmax[sid * 2 + 1];
+        if (mx == INT_MIN) {   // absent stream (empty coset)
+            if (tid == 0) { T->lo = 0; T->n_sym = 0; T->n_symbols = 0; T->status = 0; }
+            return;
+        }
+        lo = mn - 2;
+        n = mx - mn + 5;
+        if (n > kL) {   // the reference's normalisation never terminates here
+            if (tid == 0) {
+                T->lo = lo; T->n_sym = 0; T->n_symbols = 0; T->status = LQ_ST_ALPHABET;
+                atomicOr(status + sid / LQ_STREAMS, LQ_ST_ALPHABET);
+            }
+            return;
+        }
+        if (tid == 0) { s_tot = 0; s_st = 0; }
+        __syncthreads();
+        uint32_t tl = 0;
+        for (int i = tid; i < n; i += 256) {
+            const uint32_t c = (i >= 2 && i - 2 < kL) ? hist[sid * kL + i - 2] : 0u;
+            counts[i] = c;
+            tl += c;
+        }
+        atomicAdd(&s_tot, tl);
     }
     __syncthreads();
-    // n <= 260; the network holds 256 keys (n in 257..260 takes the rank path)
+    // n <= 1028; the network holds 256 keys (larger alphabets take the rank path)
     __shared__ int64_t kk[LQ_MAXSYM];
     __shared__ int8_t inset[LQ_MAXSYM];
     normalise(counts, n, freqs, keys, perm, kk, inset, &s_st);
@@ -285,17 +317,19 @@ __global__ __launch_bounds__(256) void k_chunk_tables(const uint32_t* __restrict
 // so the 8 lanes of a (block, coset) read the 8 interleaved columns of that
 // coset one 128-byte line at a time (sym_pos layout).
 
+template <typename SymT>
 struct Col {
-    const int8_t* p;   // chunk 0 of the column; chunk k at p + 128 k
+    const SymT* p;   // chunk 0 of the column; chunk k at p + 128 k (elements)
     int n;
 };
 
-__device__ __forceinline__ Col column(const int8_t* sym, const uint32_t* blk_n1, int64_t chunk, int64_t nblk,
-                                      int64_t V, int64_t h, int c, int idx) {
+template <typename SymT>
+__device__ __forceinline__ Col<SymT> column(const SymT* sym, const uint32_t* blk_n1, int64_t chunk, int64_t nblk,
+                                            int64_t V, int64_t h, int c, int idx) {
     uint32_t n1 = blk_n1[chunk * nblk + h];
     int64_t valid = V - h * kBlk < kBlk ? V - h * kBlk : kBlk;
     int n0 = (int)valid - (int)n1;
-    Col col;
+    Col<SymT> col;
     col.p = sym + (chunk * nblk + h) * (int64_t)kSymStride + sym_region(c, n0) + 16 * idx;
     col.n = c ? (int)n1 : n0;
     return col;
@@ -340,33 +374,57 @@ __device__ __forceinline__ uint4 gload16(uintptr_t a) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// 16 symbols of one column chunk (int8: one 16-byte load, int16: two).
+template <typename SymT>
+struct Chunk16 {
+    uint4 a, b;
+    __device__ __forceinline__ int get(int i) const {
+        if constexpr (sizeof(SymT) == 1) {
+            const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+            return (int)(int8_t)(w[i >> 2] >> ((i & 3) * 8));
+        } else {
+            const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            return (int)(int16_t)(w[i >> 1] >> ((i & 1) * 16));
+        }
+    }
+};
+
+template <typename SymT>
+__device__ __forceinline__ Chunk16<SymT> gload_chunk(const SymT* p) {
+    Chunk16<SymT> c;
+    const uintptr_t a = (uintptr_t)p;
+    c.a = gload16(a);
+    if constexpr (sizeof(SymT) == 2) c.b = gload16(a + 16);
+    else c.b = make_uint4(0, 0, 0, 0);
+    return c;
+}
+
 // f(v, b, in) for the column symbols of ranks n-1, n-2, .., 0 (the column's
 // 16-symbol chunk k sits at p + 128 k), read with 16-byte loads issued one
-// chunk ahead.  b is the symbol's byte index in its chunk (a compile-time
+// chunk ahead.  b is the symbol's index in its chunk (a compile-time
 // constant after unrolling).  Only a column's top chunk can be partial.
 // Control flow is wave-uniform: the loop runs while any lane has chunks left,
 // takes the unconditional path when every lane holds a full chunk and
 // otherwise passes a per-lane predicate; f must leave its state unchanged
 // when in == false.
-template <typename F>
-__device__ __forceinline__ void for_each_rev(const int8_t* p, int n, F&& f) {
+template <typename SymT, typename F>
+__device__ __forceinline__ void for_each_rev(const SymT* p, int n, F&& f) {
     int k = n > 0 ? (n - 1) >> 4 : -1;   // current chunk
-    const uintptr_t base = (uintptr_t)p;
-    uint4 cur = k >= 0 ? gload16(base + 128 * (uintptr_t)k) : make_uint4(0, 0, 0, 0);
-    uint4 nxt = k >= 1 ? gload16(base + 128 * (uintptr_t)(k - 1)) : make_uint4(0, 0, 0, 0);
+    Chunk16<SymT> cur = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)}, nxt = cur;
+    if (k >= 0) cur = gload_chunk(p + 128 * (int64_t)k);
+    if (k >= 1) nxt = gload_chunk(p + 128 * (int64_t)(k - 1));
     while (__any(k >= 0)) {
-        const uint32_t w[4] = {cur.x, cur.y, cur.z, cur.w};
         const int hi_b = k < 0 ? 0 : (n - 16 * k < 16 ? n - 16 * k : 16);
         if (__all(hi_b == 16)) {
 #pragma unroll
-            for (int b = 15; b >= 0; b--) f((int)(int8_t)(w[b >> 2] >> ((b & 3) * 8)), b, true);
+            for (int b = 15; b >= 0; b--) f(cur.get(b), b, true);
         } else {
 #pragma unroll
-            for (int b = 15; b >= 0; b--) f((int)(int8_t)(w[b >> 2] >> ((b & 3) * 8)), b, b < hi_b);
+            for (int b = 15; b >= 0; b--) f(cur.get(b), b, b < hi_b);
         }
         k--;
         cur = nxt;
-        if (k >= 1) nxt = gload16(base + 128 * (uintptr_t)(k - 1));
+        if (k >= 1) nxt = gload_chunk(p + 128 * (int64_t)(k - 1));
     }
 }
 
@@ -388,20 +446,23 @@ constexpr int kEncBlocks = 16;   // blocks per encode workgroup (x 16 streams)
 
 // Grid: (block groups, chunks).  The scratch words of a task are collected in
 // an 8-word register queue and stored as aligned 32-byte pieces.
-__global__ __launch_bounds__(256) void k_chunk_encode(const int8_t* __restrict__ sym, const uint32_t* __restrict__ blk_n1,
+template <typename SymT>
+__global__ __launch_bounds__(256) void k_chunk_encode(const SymT* __restrict__ sym, const uint32_t* __restrict__ blk_n1,
                                                       int64_t nblk, int64_t V, const lq_table* __restrict__ tables,
                                                       uint32_t* __restrict__ blk_bits, uint32_t* __restrict__ scratch,
                                                       uint16_t* __restrict__ blk_state) {
     // odd row stride: the 16 stream tables start in different LDS banks
-    __shared__ uint32_t senc[LQ_STREAMS][LQ_MAXSYM + 1];
+    // alphabet capacity: int8 symbols fit 260 entries, wide streams up to L + 4
+    constexpr int kCap = sizeof(SymT) == 1 ? 264 : LQ_MAXSYM;
+    __shared__ uint32_t senc[LQ_STREAMS][kCap + 1];
     __shared__ int slo[LQ_STREAMS], snsym[LQ_STREAMS];
     const int tid = threadIdx.x;
     const int64_t chunk = blockIdx.y;
     const int64_t g = (int64_t)blockIdx.x * kEncBlocks + (tid >> 4);
     const int st = tid & 15;
     const lq_table* T = tables + chunk * LQ_STREAMS;
-    for (int i = tid; i < LQ_STREAMS * LQ_MAXSYM; i += 256) {
-        int s = i / LQ_MAXSYM, j = i % LQ_MAXSYM;
+    for (int i = tid; i < LQ_STREAMS * kCap; i += 256) {
+        int s = i / kCap, j = i % kCap;
         senc[s][j] = j < T[s].n_sym ? encx_of(T[s].enc[j]) : 0u;
     }
     if (tid < LQ_STREAMS) { slo[tid] = T[tid].lo; snsym[tid] = T[tid].n_sym; }
@@ -435,7 +496,7 @@ __global__ __launch_bounds__(256) void k_chunk_encode(const int8_t* __restrict__
         uint32_t lo = kL, hi = exact ? (uint32_t)kL : 2u * kL - 1u;
         const int64_t hb = exact ? nblk - 1 : h;
         for (int64_t b = hb; b > g; b--) {
-            Col col = column(sym, blk_n1, chunk, nblk, V, b, c, idx);
+            Col<SymT> col = column(sym, blk_n1, chunk, nblk, V, b, c, idx);
             const int cnt = (b == hb && !exact) ? need : col.n;
             if (lo == hi) {
                 uint32_t xx = lo, k;
@@ -458,7 +519,7 @@ __global__ __launch_bounds__(256) void k_chunk_encode(const int8_t* __restrict__
     }
 
     // ---- encode block g, bits right-aligned in the task's scratch region
-    Col col = column(sym, blk_n1, chunk, nblk, V, g, c, idx);
+    Col<SymT> col = column(sym, blk_n1, chunk, nblk, V, g, c, idx);
     uint32_t* scr = scratch + task * (int64_t)kCapW;
     // words leave in decreasing address order from kCapW - 1; queue word j of the
     // current 8-word group at q[j] (newest at q[0]) and store the group when full
@@ -930,13 +991,34 @@ __global__ void k_decode_streams(const int32_t* __restrict__ bits, const int32_t
     }
 }
 
+template <typename SymT>
+int encode_launch(const SymT* d_sym, const uint32_t* d_blk_n1, int64_t n_chunks, int64_t n_vectors,
+                  const lq_table* d_tables, void* d_work, uint32_t* d_blk_off, uint16_t* d_blk_state,
+                  int64_t* d_stream_nbits, int32_t* d_stream_state, int64_t* d_stream_woff, int64_t* d_chunk_words,
+                  hipStream_t s) {
+    if (n_chunks <= 0 || n_vectors <= 0) return LQ_ERR_ARG;
+    const int64_t nblk = (n_vectors + kBlk - 1) / kBlk;
+    EncWork w = enc_layout(n_chunks, n_vectors);
+    uint32_t* bits = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(d_work) + w.bits);
+    uint32_t* scratch = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(d_work) + w.scratch);
+    const int64_t groups = (nblk + kEncBlocks - 1) / kEncBlocks;
+    hipLaunchKernelGGL((k_chunk_encode<SymT>), dim3((unsigned)groups, (unsigned)n_chunks), dim3(256), 0, s, d_sym,
+                       d_blk_n1, nblk, n_vectors, d_tables, bits, scratch, d_blk_state);
+    hipLaunchKernelGGL(k_chunk_scan, dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, bits, d_blk_state, d_tables,
+                       nblk, d_blk_off, d_stream_nbits, d_stream_state);
+    hipLaunchKernelGGL(k_chunk_offsets, dim3((unsigned)((n_chunks + 63) / 64)), dim3(64), 0, s, d_stream_nbits, d_tables,
+                       n_chunks, d_stream_woff, d_chunk_words);
+    return launch_status();
+}
+
 }  // namespace
 
 extern "C" {
 
 int lq_chunk_tables(const uint32_t* d_hist, int64_t n_chunks, lq_table* d_tables, int32_t* d_status, hipStream_t s) {
     if (n_chunks <= 0) return LQ_ERR_ARG;
-    hipLaunchKernelGGL(k_chunk_tables, dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, d_hist, d_tables, d_status);
+    hipLaunchKernelGGL((k_chunk_tables<false>), dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, d_hist, nullptr,
+                       d_tables, d_status);
     return launch_status();
 }
 
@@ -949,18 +1031,23 @@ int lq_chunk_encode(const int8_t* d_sym, const uint32_t* d_blk_n1, int64_t n_chu
                     const lq_table* d_tables, void* d_work, uint32_t* d_blk_off, uint16_t* d_blk_state,
                     int64_t* d_stream_nbits, int32_t* d_stream_state, int64_t* d_stream_woff, int64_t* d_chunk_words,
                     hipStream_t s) {
-    if (n_chunks <= 0 || n_vectors <= 0) return LQ_ERR_ARG;
-    const int64_t nblk = (n_vectors + kBlk - 1) / kBlk;
-    EncWork w = enc_layout(n_chunks, n_vectors);
-    uint32_t* bits = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(d_work) + w.bits);
-    uint32_t* scratch = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(d_work) + w.scratch);
-    const int64_t groups = (nblk + kEncBlocks - 1) / kEncBlocks;
-    hipLaunchKernelGGL(k_chunk_encode, dim3((unsigned)groups, (unsigned)n_chunks), dim3(256), 0, s, d_sym, d_blk_n1,
-                       nblk, n_vectors, d_tables, bits, scratch, d_blk_state);
-    hipLaunchKernelGGL(k_chunk_scan, dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, bits, d_blk_state, d_tables,
-                       nblk, d_blk_off, d_stream_nbits, d_stream_state);
-    hipLaunchKernelGGL(k_chunk_offsets, dim3((unsigned)((n_chunks + 63) / 64)), dim3(64), 0, s, d_stream_nbits, d_tables,
-                       n_chunks, d_stream_woff, d_chunk_words);
+    return encode_launch(d_sym, d_blk_n1, n_chunks, n_vectors, d_tables, d_work, d_blk_off, d_blk_state, d_stream_nbits,
+                         d_stream_state, d_stream_woff, d_chunk_words, s);
+}
+
+int lq_chunk_encode_wide(const int16_t* d_sym, const uint32_t* d_blk_n1, int64_t n_chunks, int64_t n_vectors,
+                         const lq_table* d_tables, void* d_work, uint32_t* d_blk_off, uint16_t* d_blk_state,
+                         int64_t* d_stream_nbits, int32_t* d_stream_state, int64_t* d_stream_woff, int64_t* d_chunk_words,
+                         hipStream_t s) {
+    return encode_launch(d_sym, d_blk_n1, n_chunks, n_vectors, d_tables, d_work, d_blk_off, d_blk_state, d_stream_nbits,
+                         d_stream_state, d_stream_woff, d_chunk_words, s);
+}
+
+int lq_chunk_tables_wide(const uint32_t* d_hist, const int32_t* d_minmax, int64_t n_chunks, lq_table* d_tables,
+                         int32_t* d_status, hipStream_t s) {
+    if (n_chunks <= 0 || !d_hist || !d_minmax) return LQ_ERR_ARG;
+    hipLaunchKernelGGL((k_chunk_tables<true>), dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, d_hist, d_minmax,
+                       d_tables, d_status);
     return launch_status();
 }
 
