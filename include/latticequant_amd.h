@@ -101,11 +101,15 @@ int lq_scale_fastdiv(const float *d_scale32, int64_t n_heads_total, int dtype, i
  * n_chunks * nblk * LQ_BLK / 8 bytes), the coset-1 count per block (d_blk_n1),
  * the 16 x 256 symbol histograms (d_hist, must be zero on entry) and status
  * bits.  d_deq (nullable) receives q * scale32 in deq_dtype, the value
- * update() returns.  Replaces llm/compressed_kv_cache.py:199-231,270. */
+ * update() returns.  d_dither_seed (nullable, one int64 per chunk) turns on the
+ * subtractive dither of the rotated path: d in [-1, 1)^8 per vector from
+ * SplitMix64 of (seed, vector index) is added to x / scale before the search
+ * and removed in d_deq ((q - d) * scale32); no counterpart in the reference.
+ * Replaces llm/compressed_kv_cache.py:199-231,270. */
 int lq_chunk_quantize(const void *d_x, int dtype, int64_t n_chunks, int64_t n_heads, int64_t bph,
                       const float *d_scale32, const int32_t *d_fastdiv, int8_t *d_sym,
                       uint8_t *d_coset_bits, uint32_t *d_blk_n1, uint32_t *d_hist, int32_t *d_status,
-                      void *d_deq, int deq_dtype, hipStream_t s);
+                      void *d_deq, int deq_dtype, const int64_t *d_dither_seed, hipStream_t s);
 
 /* Wide path (alphabets up to L = 1024 symbols, e.g. heavy-tailed K at low
  * rates): as lq_chunk_quantize with int16 symbols (n_chunks * nblk *
@@ -118,7 +122,7 @@ int lq_chunk_quantize(const void *d_x, int dtype, int64_t n_chunks, int64_t n_he
 int lq_chunk_quantize_wide(const void *d_x, int dtype, int64_t n_chunks, int64_t n_heads, int64_t bph,
                            const float *d_scale32, const int32_t *d_fastdiv, int16_t *d_sym, uint8_t *d_coset_bits,
                            uint32_t *d_blk_n1, int32_t *d_minmax, int32_t *d_status, void *d_deq, int deq_dtype,
-                           hipStream_t s);
+                           const int64_t *d_dither_seed, hipStream_t s);
 
 /* Wide path: per-stream histograms (n_chunks * 16 * 1024 uint32, zero on
  * entry) of the int16 symbols in the window [min, min + 1023].
@@ -178,12 +182,14 @@ int lq_chunk_pack(int64_t n_chunks, int64_t n_vectors, const lq_table *d_tables,
 /* Decode + dequantize a batch of chunks to (B, H, T, hd) in out_dtype:
  * fp16(q * float(scale16[head])).  d_lut_work: n_chunks * 16 * 1024 uint32.
  * d_words must have 2 readable words after the last chunk's last stream.
+ * d_dither_seed (nullable): the seeds the chunks were quantized with; the
+ * output is then (q - d) * scale16 (fp32 arithmetic, then out_dtype).
  * Replaces llm/compressed_kv_cache.py:289-332 (_decompress_chunk). */
 int lq_chunk_decode(const uint32_t *d_words, const int64_t *d_chunk_base, const int64_t *d_stream_woff,
                     const uint32_t *d_blk_off, const int64_t *d_stream_nbits, const uint16_t *d_blk_state, const uint8_t *d_coset_bits,
                     const uint32_t *d_blk_n1, const lq_table *d_tables, const uint16_t *d_scale16,
                     int64_t n_chunks, int64_t n_heads, int64_t bph, uint32_t *d_lut_work, void *d_out,
-                    int out_dtype, hipStream_t s);
+                    int out_dtype, const int64_t *d_dither_seed, hipStream_t s);
 
 /* Decoder LUTs of every stream of a chunk batch (n_chunks * 16 * 1024 uint32:
  * per slot: 31 - k | k << 5 | symbol index << 9 | (row * 1024 + (x' << k) - 1024) << 19,

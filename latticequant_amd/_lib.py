@@ -41,16 +41,16 @@ _SIGS = {
     "lq_symbols_to_e8": ([_P, _P, _I64, _P, _P], _INT),
     "lq_head_scales": ([_P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P], _INT),
     "lq_scale_fastdiv": ([_P, _I64, _INT, _P, _P], _INT),
-    "lq_chunk_quantize": ([_P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _INT, _P], _INT),
+    "lq_chunk_quantize": ([_P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _INT, _P, _P], _INT),
     "lq_chunk_tables": ([_P, _I64, _P, _P, _P], _INT),
-    "lq_chunk_quantize_wide": ([_P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _INT, _P], _INT),
+    "lq_chunk_quantize_wide": ([_P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _INT, _P, _P], _INT),
     "lq_chunk_hist_wide": ([_P, _P, _I64, _I64, _P, _P, _P], _INT),
     "lq_chunk_tables_wide": ([_P, _P, _I64, _P, _P, _P], _INT),
     "lq_chunk_encode_wide": ([_P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P], _INT),
     "lq_chunk_encode_workspace": ([_I64, _I64], _I64),
     "lq_chunk_encode": ([_P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P], _INT),
     "lq_chunk_pack": ([_I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P], _INT),
-    "lq_chunk_decode": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _INT, _P], _INT),
+    "lq_chunk_decode": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _INT, _P, _P], _INT),
     "lq_build_tables": ([_P, _P, _P, _I32, _P, _P, _P, _P, _P], _INT),
     "lq_rans_encode_streams": ([_P, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _P], _INT),
     "lq_rans_decode_streams": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _I32, _P, _P], _INT),

@@ -83,7 +83,9 @@ class EncodedBatch:
             stream_state=self.stream_state[c * S:(c + 1) * S], stream_woff=self.stream_woff[c * S:(c + 1) * S],
             chunk_words=self.chunk_words[c:c + 1], chunk_base=self.chunk_base[c:c + 1], words=self.words,
             status=self.status[c:c + 1],
-            hist=None if self.hist is None else self.hist.view(C, -1)[c], extra=dict(self.extra))
+            hist=None if self.hist is None else self.hist.view(C, -1)[c],
+            extra={**self.extra, "dither_seed": None if self.extra.get("dither_seed") is None
+                   else self.extra["dither_seed"][c:c + 1]})
 
     # ---- byte accounting -------------------------------------------------
     def reference_bytes(self) -> torch.Tensor:
@@ -187,7 +189,7 @@ def quantize_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None
     deq = torch.empty_like(x)
     L.check(lib.lq_chunk_quantize(x.data_ptr(), dt, C, nh, bph, scale32.data_ptr(), fastdiv.data_ptr(), sym.data_ptr(),
                                   coset_bits.data_ptr(), blk_n1.data_ptr(), hist.data_ptr(), status.data_ptr(),
-                                  deq.data_ptr(), dt, L.stream_ptr(dev)), "lq_chunk_quantize")
+                                  deq.data_ptr(), dt, None, L.stream_ptr(dev)), "lq_chunk_quantize")
     return scale32, scale16, deq
 
 
@@ -219,7 +221,8 @@ class AlphabetError(ValueError):
 
 
 def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, deq_out: bool = False,
-                 exact_size: bool = True, words_out: Optional[torch.Tensor] = None, wide="auto"):
+                 exact_size: bool = True, words_out: Optional[torch.Tensor] = None, wide="auto",
+                 dither_seed=None):
     """Compress a batch of chunks.
 
     x: (C, B, H, T, hd) fp16 / bf16 / fp32 CUDA tensor, hd % 8 == 0.
@@ -235,6 +238,8 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
       overflowed (one status read-back) the batch is redone on the wide path.
     An alphabet above 1024 symbols raises AlphabetError when the status is read
     back (wide="auto" or True with exact_size) and is otherwise left in enc.status.
+    dither_seed: int or (C,) ints: subtractive dither per chunk (the rotated
+      path; the seeds are kept in enc.extra and decode_batch removes the dither).
     Returns (EncodedBatch, deq or None)."""
     lib = L.lib()
     x = _check_input(x)
@@ -251,13 +256,19 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
     status = _zeros(C, torch.int32, dev)
     deq = torch.empty_like(x) if deq_out else None
     tables = _empty(C * L.LQ_STREAMS * L.TABLE_BYTES, torch.uint8, dev)
+    dseed = None
+    if dither_seed is not None:
+        ds = [int(dither_seed)] * C if isinstance(dither_seed, int) else [int(v) for v in dither_seed]
+        if len(ds) != C:
+            raise ValueError("dither_seed must be an int or one seed per chunk")
+        dseed = torch.tensor(ds, dtype=torch.int64).to(dev)
     use_wide = wide is True
     if not use_wide:
         sym = _empty(C * nblk * L.LQ_SYM_STRIDE, torch.int8, dev)
         hist = _zeros(C * L.LQ_STREAMS * 256, torch.int32, dev)
         L.check(lib.lq_chunk_quantize(x.data_ptr(), dt, C, nh, bph, scale32.data_ptr(), fastdiv.data_ptr(),
                                       sym.data_ptr(), coset_bits.data_ptr(), blk_n1.data_ptr(), hist.data_ptr(),
-                                      status.data_ptr(), L.ptr(deq), dt, s), "lq_chunk_quantize")
+                                      status.data_ptr(), L.ptr(deq), dt, L.ptr(dseed), s), "lq_chunk_quantize")
         if wide == "auto" and _status_or(status) & L.LQ_ST_SYM_OVERFLOW:
             use_wide = True
             status.zero_()
@@ -271,7 +282,8 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
         hist = _zeros(C * L.LQ_STREAMS * L.LQ_L, torch.int32, dev)
         L.check(lib.lq_chunk_quantize_wide(x.data_ptr(), dt, C, nh, bph, scale32.data_ptr(), fastdiv.data_ptr(),
                                            sym.data_ptr(), coset_bits.data_ptr(), blk_n1.data_ptr(), minmax.data_ptr(),
-                                           status.data_ptr(), L.ptr(deq), dt, s), "lq_chunk_quantize_wide")
+                                           status.data_ptr(), L.ptr(deq), dt, L.ptr(dseed), s),
+                "lq_chunk_quantize_wide")
         L.check(lib.lq_chunk_hist_wide(sym.data_ptr(), blk_n1.data_ptr(), C, V, minmax.data_ptr(), hist.data_ptr(), s),
                 "lq_chunk_hist_wide")
         L.check(lib.lq_chunk_tables_wide(hist.data_ptr(), minmax.data_ptr(), C, tables.data_ptr(), status.data_ptr(), s),
@@ -313,7 +325,8 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
                        scale16=scale16, sigma2=sigma2, coset_bits=coset_bits.view(C, -1), blk_n1=blk_n1.view(C, -1),
                        tables=tables, blk_off=blk_off, blk_state=blk_state, stream_nbits=stream_nbits,
                        stream_state=stream_state, stream_woff=stream_woff, chunk_words=chunk_words,
-                       chunk_base=chunk_base, words=words, status=status, hist=hist, extra={"wide": use_wide})
+                       chunk_base=chunk_base, words=words, status=status, hist=hist,
+                       extra={"wide": use_wide, "dither_seed": dseed})
     return enc, deq
 
 
@@ -334,7 +347,7 @@ def decode_batch(enc: EncodedBatch, out_dtype: torch.dtype = torch.float16, out:
                                 enc.coset_bits.data_ptr(),
                                 enc.blk_n1.data_ptr(), enc.tables.data_ptr(), enc.scale16.data_ptr(), C, enc.n_heads,
                                 enc.bph, lut_work.data_ptr(), out.data_ptr(), L.dtype_code(out.dtype),
-                                L.stream_ptr(dev)), "lq_chunk_decode")
+                                L.ptr(enc.extra.get("dither_seed")), L.stream_ptr(dev)), "lq_chunk_decode")
     return out
 
 

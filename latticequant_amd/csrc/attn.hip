@@ -507,7 +507,7 @@ int lq_decode_attention(const lq_chunk_batch* k, const lq_chunk_batch* v, const 
     // V: decode + dequantise to fp16 (n_chunks, n_heads, T, 128)
     rc = lq_chunk_decode(v->words, v->chunk_base, v->stream_woff, v->blk_off, v->stream_nbits, v->blk_state,
                          v->coset_bits, v->blk_n1, v->tables, v->scale16, v->n_chunks, v->n_heads, v->bph, lut_v, vdec,
-                         LQ_F16, s);
+                         LQ_F16, nullptr, s);
     if (rc) return rc;
     const BatchArgs ak = to_args(k, lut_k);
     const int64_t gph = ((k->bph / kBlk) + kSB - 1) / kSB;

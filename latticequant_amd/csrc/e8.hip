@@ -179,12 +179,15 @@ constexpr int kQBlocksPerWG = 4;
 // LQ_ST_SYM_OVERFLOW (the chunk then needs the wide path).  int16: per-stream
 // min / max instead (the histogram of the wide path is a second pass over the
 // symbols, in the window the min fixes).
-template <typename SymT>
+// DITHER: the chunk's dither (dither8, seed dseed[chunk]) is added to x / scale
+// before the nearest-point search and taken off again in the dequantised output.
+template <typename SymT, bool DITHER>
 __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
     const void* __restrict__ x, int dtype, int64_t n_heads, int64_t bph, int64_t nblk,
     const float* __restrict__ scale32, const int32_t* __restrict__ fastdiv, SymT* __restrict__ sym,
     uint8_t* __restrict__ coset_bits, uint32_t* __restrict__ blk_n1, uint32_t* __restrict__ hist,
-    int32_t* __restrict__ minmax, int32_t* __restrict__ status, void* __restrict__ deq, int deq_dtype) {
+    int32_t* __restrict__ minmax, int32_t* __restrict__ status, void* __restrict__ deq, int deq_dtype,
+    const int64_t* __restrict__ dseed) {
     constexpr bool kWide = sizeof(SymT) == 2;
     constexpr int kSymMin = kWide ? -32768 : -128, kSymMax = kWide ? 32767 : 127;
     __shared__ uint32_t shist[kWide ? 1 : LQ_STREAMS * 256];
@@ -233,10 +236,15 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
                 const float s = scale32[h];
                 const bool fast = fastdiv[h] != 0;
                 const float rs = 1.0f / s;
-                float xv[8], t[8], ic[8];
+                float xv[8], t[8], ic[8], dd[8];
                 load8(x, dtype, chunk * V + v, xv);
 #pragma unroll
                 for (int i = 0; i < 8; i++) t[i] = div_scaled(xv[i], s, rs, fast);
+                if constexpr (DITHER) {
+                    dither8(mix64((uint64_t)dseed[chunk]), v, dd);
+#pragma unroll
+                    for (int i = 0; i < 8; i++) t[i] = t[i] + dd[i];
+                }
                 int c = e8_nearest(t, ic);
                 cs[r] = c;
 #pragma unroll
@@ -249,7 +257,10 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
                 if (deq) {
                     float off = c ? 0.5f : 0.f, y[8];
 #pragma unroll
-                    for (int i = 0; i < 8; i++) y[i] = (ic[i] + off) * s;
+                    for (int i = 0; i < 8; i++) {
+                        if constexpr (DITHER) y[i] = ((ic[i] + off) - dd[i]) * s;
+                        else y[i] = (ic[i] + off) * s;
+                    }
                     store8(deq, deq_dtype, chunk * V + v, y);
                 }
             }
@@ -432,28 +443,38 @@ int lq_e8_quantize_heads(const void* d_x, int dtype, int64_t n_heads, int64_t bp
 int lq_chunk_quantize(const void* d_x, int dtype, int64_t n_chunks, int64_t n_heads, int64_t bph,
                       const float* d_scale32, const int32_t* d_fastdiv, int8_t* d_sym, uint8_t* d_coset_bits,
                       uint32_t* d_blk_n1, uint32_t* d_hist, int32_t* d_status, void* d_deq, int deq_dtype,
-                      hipStream_t s) {
+                      const int64_t* d_dither_seed, hipStream_t s) {
     if (n_chunks <= 0 || n_heads <= 0 || bph <= 0 || dtype < 0 || dtype > 2) return LQ_ERR_ARG;
     const int64_t V = n_heads * bph;
     const int64_t nblk = (V + kBlk - 1) / kBlk;
     const int64_t wg = n_chunks * ((nblk + kQBlocksPerWG - 1) / kQBlocksPerWG);
-    hipLaunchKernelGGL((k_chunk_quantize<int8_t>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x, dtype, n_heads, bph,
-                       nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, d_hist, nullptr, d_status, d_deq,
-                       deq_dtype);
+    if (d_dither_seed)
+        hipLaunchKernelGGL((k_chunk_quantize<int8_t, true>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x, dtype,
+                           n_heads, bph, nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, d_hist, nullptr,
+                           d_status, d_deq, deq_dtype, d_dither_seed);
+    else
+        hipLaunchKernelGGL((k_chunk_quantize<int8_t, false>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x, dtype,
+                           n_heads, bph, nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, d_hist, nullptr,
+                           d_status, d_deq, deq_dtype, nullptr);
     return launch_status();
 }
 
 int lq_chunk_quantize_wide(const void* d_x, int dtype, int64_t n_chunks, int64_t n_heads, int64_t bph,
                            const float* d_scale32, const int32_t* d_fastdiv, int16_t* d_sym, uint8_t* d_coset_bits,
                            uint32_t* d_blk_n1, int32_t* d_minmax, int32_t* d_status, void* d_deq, int deq_dtype,
-                           hipStream_t s) {
+                           const int64_t* d_dither_seed, hipStream_t s) {
     if (n_chunks <= 0 || n_heads <= 0 || bph <= 0 || dtype < 0 || dtype > 2 || !d_minmax) return LQ_ERR_ARG;
     const int64_t V = n_heads * bph;
     const int64_t nblk = (V + kBlk - 1) / kBlk;
     const int64_t wg = n_chunks * ((nblk + kQBlocksPerWG - 1) / kQBlocksPerWG);
-    hipLaunchKernelGGL((k_chunk_quantize<int16_t>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x, dtype, n_heads,
-                       bph, nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, nullptr, d_minmax, d_status,
-                       d_deq, deq_dtype);
+    if (d_dither_seed)
+        hipLaunchKernelGGL((k_chunk_quantize<int16_t, true>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x, dtype,
+                           n_heads, bph, nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, nullptr, d_minmax,
+                           d_status, d_deq, deq_dtype, d_dither_seed);
+    else
+        hipLaunchKernelGGL((k_chunk_quantize<int16_t, false>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x, dtype,
+                           n_heads, bph, nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, nullptr, d_minmax,
+                           d_status, d_deq, deq_dtype, nullptr);
     return launch_status();
 }
 

@@ -150,6 +150,33 @@ __device__ __forceinline__ float div_scaled(float x, float s, float r, bool fast
     return x / s;
 }
 
+// -------------------------------------------------------------- dither ---
+//
+// Subtractive dither of the rotated path (build-defined: the reference has no
+// E8 dither).  Vector v of a chunk with seed s gets d in [-1, 1)^8, uniform on
+// a 2^-23 grid: a fundamental domain of 2Z^8, a sublattice of E8, so modulo E8
+// the dither is uniform on the Voronoi cell and the error Q(t + d) - d - t is
+// uniform on the cell and independent of t.  Coordinates 2p, 2p + 1 come from
+// 24-bit fields of h = mix64(mix64(s) + 4 v + p), mix64 the SplitMix64 output
+// function (Steele, Lea, Flood 2014).  The quantizer adds d to x / scale; the
+// decoder subtracts it from the lattice point before scaling.
+__host__ __device__ inline uint64_t mix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// key = mix64(seed); d = dither of vector v (exact in fp32)
+__device__ __forceinline__ void dither8(uint64_t key, int64_t v, float d[8]) {
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const uint64_t h = mix64(key + (uint64_t)v * 4u + (uint64_t)p);
+        d[2 * p] = (float)((int32_t)((h >> 40) & 0xFFFFFFu) - (1 << 23)) * 0x1p-23f;
+        d[2 * p + 1] = (float)((int32_t)((h >> 16) & 0xFFFFFFu) - (1 << 23)) * 0x1p-23f;
+    }
+}
+
 // ---------------------------------------------------------------- rANS ---
 
 __device__ __forceinline__ uint32_t enc_pack(uint32_t f, uint32_t cum) {

@@ -779,15 +779,17 @@ __device__ __forceinline__ void stage_coset(const uint32_t* __restrict__ lutg, c
 // block rebuilds the phase's vector idx (alphabet lo, c7 = 2 floor(c7/2) +
 // parity of c0..c6, coset offset, times the fp16 scale) and writes it as one
 // 16-byte store.  HEADS_ALIGNED: bph is a multiple of the block size, so a
-// block lies in one head.
-template <int OUT_DT, bool HEADS_ALIGNED>
+// block lies in one head.  DITHER: the chunk's dither (dither8, seed
+// dseed[chunk]) is subtracted from each lattice point before scaling.
+template <int OUT_DT, bool HEADS_ALIGNED, bool DITHER>
 __global__ __launch_bounds__(512) void k_chunk_decode(const uint32_t* __restrict__ words, const int64_t* __restrict__ chunk_base,
                                                       const int64_t* __restrict__ stream_woff, const uint32_t* __restrict__ blk_off,
                                                       const int64_t* __restrict__ stream_nbits,
                                                       const uint16_t* __restrict__ blk_state, const uint8_t* __restrict__ coset_bits,
                                                       const uint32_t* __restrict__ blk_n1, const lq_table* __restrict__ tables,
                                                       const uint16_t* __restrict__ scale16, const uint32_t* __restrict__ lutg,
-                                                      int64_t n_heads, int64_t bph, int64_t nblk, void* __restrict__ out) {
+                                                      int64_t n_heads, int64_t bph, int64_t nblk, void* __restrict__ out,
+                                                      const int64_t* __restrict__ dseed) {
     __shared__ uint32_t lut[8 * kL];
     __shared__ uint32_t ring[kRing][kDecLanes];
     __shared__ __align__(16) uint16_t stg[kDecBlocks * kStgRow];
@@ -836,6 +838,7 @@ __global__ __launch_bounds__(512) void k_chunk_decode(const uint32_t* __restrict
     using OutT = typename std::conditional<OUT_DT == LQ_F32, float, uint16_t>::type;
     OutT* const ob = reinterpret_cast<OutT*>(out) + (chunk * V + vfirst) * 8;
     uint16_t* const my_stg = &stg[b * kStgRow + idx];
+    const uint64_t dkey = DITHER ? mix64((uint64_t)dseed[chunk]) : 0u;
 
     for (int s0 = 0; s0 < n; s0 += kPhase) {
         d.boundary();
@@ -848,7 +851,14 @@ __global__ __launch_bounds__(512) void k_chunk_decode(const uint32_t* __restrict
                 head_end = (head + 1) * bph;
                 set_scale(head);
             }
-            if (OUT_DT == LQ_F16 && cc.small) {
+            if constexpr (DITHER) {
+                float y[8], dd[8];
+                cc.deq_f32(r, 1.0f, y);   // the lattice point itself (exact)
+                dither8(dkey, vfirst + vl, dd);
+#pragma unroll
+                for (int j = 0; j < 8; j++) y[j] = (y[j] - dd[j]) * sc;
+                store8(ob, OUT_DT, vl, y);
+            } else if (OUT_DT == LQ_F16 && cc.small) {
                 reinterpret_cast<uint4*>(ob)[vl] = cc.deq_f16(r, sc2);
             } else {
                 float y[8];
@@ -1069,9 +1079,10 @@ int lq_chunk_pack(int64_t n_chunks, int64_t n_vectors, const lq_table* d_tables,
 }
 
 int lq_chunk_decode(const uint32_t* d_words, const int64_t* d_chunk_base, const int64_t* d_stream_woff,
-                    const uint32_t* d_blk_off, const int64_t* d_stream_nbits, const uint16_t* d_blk_state, const uint8_t* d_coset_bits,
-                    const uint32_t* d_blk_n1, const lq_table* d_tables, const uint16_t* d_scale16, int64_t n_chunks,
-                    int64_t n_heads, int64_t bph, uint32_t* d_lut_work, void* d_out, int out_dtype, hipStream_t s) {
+                    const uint32_t* d_blk_off, const int64_t* d_stream_nbits, const uint16_t* d_blk_state,
+                    const uint8_t* d_coset_bits, const uint32_t* d_blk_n1, const lq_table* d_tables,
+                    const uint16_t* d_scale16, int64_t n_chunks, int64_t n_heads, int64_t bph, uint32_t* d_lut_work,
+                    void* d_out, int out_dtype, const int64_t* d_dither_seed, hipStream_t s) {
     if (n_chunks <= 0 || n_heads <= 0 || bph <= 0 || out_dtype < 0 || out_dtype > 2) return LQ_ERR_ARG;
     const int64_t V = n_heads * bph;
     const int64_t nblk = (V + kBlk - 1) / kBlk;
@@ -1079,13 +1090,19 @@ int lq_chunk_decode(const uint32_t* d_words, const int64_t* d_chunk_base, const 
     const int64_t groups = (nblk + kDecBlocks - 1) / kDecBlocks;
     const dim3 grid((unsigned)(n_chunks * 2 * groups));
     const bool aligned = bph % kBlk == 0;
-#define LQ_DECODE(DT, AL)                                                                                         \
-    hipLaunchKernelGGL((k_chunk_decode<DT, AL>), grid, dim3(512), 0, s, d_words, d_chunk_base, d_stream_woff,       \
-                       d_blk_off, d_stream_nbits, d_blk_state, d_coset_bits, d_blk_n1, d_tables, d_scale16, d_lut_work, n_heads, bph, \
-                       nblk, d_out)
-    if (out_dtype == LQ_F16) { if (aligned) LQ_DECODE(LQ_F16, true); else LQ_DECODE(LQ_F16, false); }
-    else if (out_dtype == LQ_BF16) { if (aligned) LQ_DECODE(LQ_BF16, true); else LQ_DECODE(LQ_BF16, false); }
-    else { if (aligned) LQ_DECODE(LQ_F32, true); else LQ_DECODE(LQ_F32, false); }
+#define LQ_DECODE(DT, AL, DI)                                                                                     \
+    hipLaunchKernelGGL((k_chunk_decode<DT, AL, DI>), grid, dim3(512), 0, s, d_words, d_chunk_base, d_stream_woff,   \
+                       d_blk_off, d_stream_nbits, d_blk_state, d_coset_bits, d_blk_n1, d_tables, d_scale16, d_lut_work, \
+                       n_heads, bph, nblk, d_out, d_dither_seed)
+#define LQ_DECODE_DT(DT)                                                                                          \
+    do {                                                                                                          \
+        if (d_dither_seed) { if (aligned) LQ_DECODE(DT, true, true); else LQ_DECODE(DT, false, true); }           \
+        else { if (aligned) LQ_DECODE(DT, true, false); else LQ_DECODE(DT, false, false); }                       \
+    } while (0)
+    if (out_dtype == LQ_F16) LQ_DECODE_DT(LQ_F16);
+    else if (out_dtype == LQ_BF16) LQ_DECODE_DT(LQ_BF16);
+    else LQ_DECODE_DT(LQ_F32);
+#undef LQ_DECODE_DT
 #undef LQ_DECODE
     return launch_status();
 }

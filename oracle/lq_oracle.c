@@ -17,6 +17,11 @@
  *   lqo_build_table     sum == L, freqs >= 1, golden tables
  *   lqo_rans_encode     decode(encode(s)) == s, golden bitstreams
  *   lqo_pack/unpack     known-answer points of the reference test, round trip
+ *   lqo_dither          build-defined (the reference has no E8 dither):
+ *                       SplitMix64 known-answer values, range [-1, 1), mean
+ *                       and variance 1/3 per coordinate, and the subtractive-
+ *                       dither error being uniform on the E8 Voronoi cell
+ *                       (per-dimension MSE G(E8) = 0.07168, zero mean)
  */
 #include <math.h>
 #include <stdint.h>
@@ -94,6 +99,46 @@ void lqo_quantize_heads(const float *x, const float *scale, int64_t n_heads, int
         for (int64_t v = 0; v < bph; v++) {
             const float *xv = x + 8 * (h * bph + v);
             for (int i = 0; i < 8; i++) t[i] = xv[i] / s;
+            e8_one(t, q + 8 * (h * bph + v));
+        }
+    }
+}
+
+/* ------------------------------------------------------------- dither --- */
+
+/* SplitMix64 output function (Steele, Lea, Flood, "Fast splittable
+ * pseudorandom number generators", OOPSLA 2014). */
+uint64_t lqo_mix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+/* Dither of vectors v0 .. v0 + n - 1 of a chunk with seed `seed`: coordinates
+ * 2p, 2p + 1 from bits 40..63 and 16..39 of mix64(mix64(seed) + 4 v + p),
+ * each (k - 2^23) * 2^-23 in [-1, 1). */
+void lqo_dither(int64_t seed, int64_t v0, int64_t n, float *d) {
+    const uint64_t key = lqo_mix64((uint64_t)seed);
+    for (int64_t v = 0; v < n; v++) {
+        for (int p = 0; p < 4; p++) {
+            const uint64_t h = lqo_mix64(key + (uint64_t)(v0 + v) * 4u + (uint64_t)p);
+            d[8 * v + 2 * p] = (float)((int32_t)((h >> 40) & 0xFFFFFFu) - (1 << 23)) * 0x1p-23f;
+            d[8 * v + 2 * p + 1] = (float)((int32_t)((h >> 16) & 0xFFFFFFu) - (1 << 23)) * 0x1p-23f;
+        }
+    }
+}
+
+/* lqo_quantize_heads with the subtractive dither added to x / scale. */
+void lqo_quantize_heads_dither(const float *x, const float *scale, int64_t n_heads, int64_t bph, int64_t seed,
+                               float *q) {
+    float t[8], d[8];
+    for (int64_t h = 0; h < n_heads; h++) {
+        float s = scale[h];
+        for (int64_t v = 0; v < bph; v++) {
+            const float *xv = x + 8 * (h * bph + v);
+            lqo_dither(seed, h * bph + v, 1, d);
+            for (int i = 0; i < 8; i++) t[i] = xv[i] / s + d[i];
             e8_one(t, q + 8 * (h * bph + v));
         }
     }

@@ -57,6 +57,9 @@ def lib():
             ("lqo_encode_d8", [f32p, f32p, i64], None),
             ("lqo_encode_e8", [f32p, f32p, i64], None),
             ("lqo_quantize_heads", [f32p, f32p, i64, i64, f32p], None),
+            ("lqo_quantize_heads_dither", [f32p, f32p, i64, i64, i64, f32p], None),
+            ("lqo_dither", [i64, i64, i64, f32p], None),
+            ("lqo_mix64", [ctypes.c_uint64], ctypes.c_uint64),
             ("lqo_e8_to_symbols", [f32p, i64, f32p, f32p], None),
             ("lqo_symbols_to_e8", [f32p, f32p, i64, f32p], None),
             ("lqo_pack_coset_bits", [f32p, i64, f32p], None),
@@ -122,15 +125,27 @@ def head_sigma2(t: np.ndarray) -> np.ndarray:
     return (th * th).mean(axis=1).astype(np.float32)
 
 
-def quantize_heads(t32: np.ndarray, scales: np.ndarray) -> np.ndarray:
-    """x / scale[head] then encode_e8 (llm/compressed_kv_cache.py:199-201)."""
+def quantize_heads(t32: np.ndarray, scales: np.ndarray, dither_seed: Optional[int] = None) -> np.ndarray:
+    """x / scale[head] then encode_e8 (llm/compressed_kv_cache.py:199-201);
+    with dither_seed, x / scale + dither (build-defined, see dither())."""
     t32 = _c(t32, np.float32)
     nh = scales.shape[0]
     bph = t32.size // (8 * nh)
     sc = _c(scales, np.float32)
     q = np.empty((nh * bph, 8), dtype=np.float32)
-    lib().lqo_quantize_heads(_p(t32), _p(sc), nh, bph, _p(q))
+    if dither_seed is None:
+        lib().lqo_quantize_heads(_p(t32), _p(sc), nh, bph, _p(q))
+    else:
+        lib().lqo_quantize_heads_dither(_p(t32), _p(sc), nh, bph, int(dither_seed), _p(q))
     return q
+
+
+def dither(seed: int, n_vectors: int, v0: int = 0) -> np.ndarray:
+    """Subtractive dither of vectors v0 .. v0+n-1 of a chunk: (n, 8) float32 in
+    [-1, 1) (build-defined; lq_oracle.c lqo_dither)."""
+    d = np.empty((n_vectors, 8), dtype=np.float32)
+    lib().lqo_dither(int(seed), int(v0), int(n_vectors), _p(d))
+    return d
 
 
 def e8_to_symbols(q: np.ndarray):
@@ -337,6 +352,7 @@ class Chunk:
     bitstream: np.ndarray = None  # merged uint32 words
     word_offsets: List[int] = field(default_factory=list)
     decompressed: np.ndarray = None
+    dither_seed: Optional[int] = None
 
     @property
     def n_vectors(self):
@@ -359,7 +375,7 @@ def column_table(col: np.ndarray):
 
 
 def compress_chunk(t: np.ndarray, bits: int, scales_f32: Optional[np.ndarray] = None,
-                   entropy: bool = True) -> Chunk:
+                   entropy: bool = True, dither_seed: Optional[int] = None) -> Chunk:
     """CompressedKVCache._compress_tensor (llm/compressed_kv_cache.py:176-287).
 
     t: (B, H, T, hd) array in the model dtype.  scales_f32 injects the per-head
@@ -373,15 +389,17 @@ def compress_chunk(t: np.ndarray, bits: int, scales_f32: Optional[np.ndarray] = 
     else:
         sc32 = _c(scales_f32, np.float32)
         sc16 = sc32.astype(np.float16)
-    q = quantize_heads(t32, sc32)
+    q = quantize_heads(t32, sc32, dither_seed)
     bph = q.shape[0] // nh
-    dec = (q.reshape(nh, bph, 8) * sc32[:, None, None]).astype(np.float32)
+    qd = q if dither_seed is None else (q - dither(dither_seed, q.shape[0])).astype(np.float32)
+    dec = (qd.reshape(nh, bph, 8) * sc32[:, None, None]).astype(np.float32)
     dec = dec.reshape(t.shape).astype(np.asarray(t).dtype if np.asarray(t).dtype != np.float64 else np.float32)
     coset, free, c8h = e8_to_symbols(q)
     syms = np.concatenate([free, c8h[:, None]], 1)
     ch = Chunk(shape=t.shape, bits=bits, scales_f32=sc32, scales=sc16,
                coset_packed=pack_coset_bits(coset),
-               coset_counts=(int((coset == 0).sum()), int((coset == 1).sum())), decompressed=dec)
+               coset_counts=(int((coset == 0).sum()), int((coset == 1).sum())), decompressed=dec,
+               dither_seed=dither_seed)
     if not entropy:
         return ch
     all_words = []
@@ -401,9 +419,10 @@ def compress_chunk(t: np.ndarray, bits: int, scales_f32: Optional[np.ndarray] = 
     return ch
 
 
-def decompress_chunk(ch: Chunk) -> np.ndarray:
+def decompress_chunk(ch: Chunk, out_dtype=np.float16) -> np.ndarray:
     """CompressedKVCache._decompress_chunk (llm/compressed_kv_cache.py:289-332):
-    decode streams, scatter columns by coset, symbols_to_e8, times the fp16 scale."""
+    decode streams, scatter columns by coset, symbols_to_e8, times the fp16 scale
+    (with a dither seed: the dither is subtracted first, fp32 arithmetic)."""
     n = ch.n_vectors
     cos = unpack_coset_bits(ch.coset_packed, n).astype(np.int64)
     syms = np.zeros((n, 8), dtype=np.int64)
@@ -411,10 +430,12 @@ def decompress_chunk(ch: Chunk) -> np.ndarray:
         rows = np.where(cos == s.coset)[0]
         syms[rows, s.idx] = rans_decode(s.words, s.n_bits, s.state, s.table, s.n_symbols)
     q = symbols_to_e8(cos, syms[:, :7], syms[:, 7])
+    if ch.dither_seed is not None:
+        q = (q - dither(ch.dither_seed, n)).astype(np.float32)
     nh = ch.scales.shape[0]
     sc = ch.scales.astype(np.float32)
     out = (q.reshape(nh, -1, 8) * sc[:, None, None]).astype(np.float32)
-    return out.reshape(ch.shape).astype(np.float16)
+    return out.reshape(ch.shape).astype(out_dtype)
 
 
 def dequant_compact(packed: np.ndarray, bits: int, scales: np.ndarray, head_idx: np.ndarray) -> np.ndarray:
