@@ -104,6 +104,113 @@ def bench_decode_step(dev, iters=30, prefix=32768, tail=128):
                                     f"tail [1,8,{tail},128] fp16, L2/MALL flushed before each step"}
 
 
+def time_quantize(x, enc, reps=3):
+    """Average duration (ms) of the k_chunk_quantize launch over the batch x
+    (the launch encode_batch makes), with the scales enc holds, timed with
+    events on the stream the kernel runs on; the histogram is cleared between
+    launches, outside the events."""
+    from latticequant_amd import _lib as L
+    lib = L.lib()
+    dev = x.device
+    C = x.shape[0]
+    nh, bph = HEADS, TOKENS * HD // 8
+    nblk = (nh * bph + L.LQ_BLK - 1) // L.LQ_BLK
+    s = L.stream_ptr(dev)
+    fastdiv = torch.empty(C * nh, dtype=torch.int32, device=dev)
+    L.check(lib.lq_scale_fastdiv(enc.scale32.data_ptr(), C * nh, L.dtype_code(x.dtype), fastdiv.data_ptr(), s),
+            "lq_scale_fastdiv")
+    sym = torch.empty(C * nblk * L.LQ_SYM_STRIDE, dtype=torch.int8, device=dev)
+    coset = torch.empty(C * nblk * L.LQ_BLK // 8, dtype=torch.uint8, device=dev)
+    n1 = torch.empty(C * nblk, dtype=torch.int32, device=dev)
+    hist = torch.empty(C * L.LQ_STREAMS * 256, dtype=torch.int32, device=dev)
+    status = torch.zeros(C, dtype=torch.int32, device=dev)
+    ms = []
+    for _ in range(reps):
+        hist.zero_()
+        e0 = torch.cuda.Event(enable_timing=True); e1 = torch.cuda.Event(enable_timing=True)
+        gpu_busy()
+        e0.record()
+        L.check(lib.lq_chunk_quantize(x.data_ptr(), L.dtype_code(x.dtype), C, nh, bph, enc.scale32.data_ptr(),
+                                      fastdiv.data_ptr(), sym.data_ptr(), coset.data_ptr(), n1.data_ptr(),
+                                      hist.data_ptr(), status.data_ptr(), None, 0, None, s), "lq_chunk_quantize")
+        e1.record()
+        torch.cuda.synchronize()
+        ms.append(e0.elapsed_time(e1))
+    return float(np.mean(ms))
+
+
+def gpu_busy():
+    """Queue a short spin on the stream so that the host has submitted the
+    launches that follow before the start event is reached: the events then
+    bracket GPU time only, not the host's submission latency."""
+    torch.cuda._sleep(10_000_000)
+
+
+
+def load_traffic():
+    """HBM bytes per launch per kernel, from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter on a copy of known
+    size); {} when absent."""
+    p = os.path.join(ROOT, "profiles", "roofline_traffic.json")
+    if not os.path.exists(p):
+        return {}
+    with open(p) as f:
+        return json.load(f).get("bytes_per_launch", {})
+
+
+def copy_calibration(dev, nbytes=1 << 30):
+    """One plain device copy of nbytes (the PMC calibration kernel)."""
+    a = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    a.fill_(1)
+    b.copy_(a)
+    torch.cuda.synchronize()
+
+
+def summarize_pmc(fetch_csv, write_csv, out_path, calib_bytes=1 << 30):
+    """Turn two rocprofv3 --pmc counter_collection.csv files (FETCH_SIZE, then
+    WRITE_SIZE, KiB per dispatch) of a `bench.py --copy-calib` run into HBM
+    bytes per launch: each counter is scaled by what it reads for the 1 GiB
+    copy (the largest __amd_rocclr_copyBuffer dispatch).  Per kernel the
+    dispatches with the largest grid (the full-batch launches) are averaged."""
+    import pandas as pd
+    vals, factors = {}, {}
+    for ctr, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        df = pd.read_csv(path)
+        df = df[df["Counter_Name"] == ctr]
+        cp = df[df["Kernel_Name"].str.contains("copyBuffer")]
+        factors[ctr] = float(cp["Counter_Value"].max()) * 1024.0 / calib_bytes
+        for name in ("k_chunk_quantize", "k_chunk_decode"):
+            d = df[df["Kernel_Name"].str.contains(name)]
+            if len(d) == 0:
+                continue
+            d = d[d["Grid_Size"] == d["Grid_Size"].max()]
+            vals.setdefault(name, {})[ctr] = float(d["Counter_Value"].mean()) * 1024.0
+    res = {"bytes_per_launch": {n: round(v["FETCH_SIZE"] / factors["FETCH_SIZE"] + v["WRITE_SIZE"] / factors["WRITE_SIZE"])
+                                for n, v in vals.items() if len(v) == 2},
+           "raw_bytes": vals, "copy_factor": factors, "calib_bytes": calib_bytes}
+    with open(out_path, "w") as f:
+        json.dump(res, f, indent=1)
+    print(json.dumps(res))
+
+
+def summarize_trace(trace_csv, top=16):
+    """Per (kernel, grid size) launch counts and durations from a rocprofv3
+    --kernel-trace kernel_trace.csv, as a markdown table (longest total first)."""
+    import pandas as pd
+    df = pd.read_csv(trace_csv)
+    df["us"] = (df["End_Timestamp"] - df["Start_Timestamp"]) / 1e3
+    df["kernel"] = df["Kernel_Name"].str.replace("(anonymous namespace)::", "", regex=False).str.slice(0, 60)
+    df["Grid_Size"] = df["Grid_Size_X"] * df["Grid_Size_Y"] * df["Grid_Size_Z"]
+    g = df.groupby(["kernel", "Grid_Size"])["us"].agg(["count", "sum", "mean", "min", "max"]).reset_index()
+    g = g.sort_values("sum", ascending=False).head(top)
+    print("| kernel | grid | launches | total us | avg us | min us | max us |")
+    print("|---|---:|---:|---:|---:|---:|---:|")
+    for _, r in g.iterrows():
+        print(f"| {r['kernel']} | {r['Grid_Size']} | {r['count']} | {r['sum']:.1f} | {r['mean']:.1f} | "
+              f"{r['min']:.1f} | {r['max']:.1f} |")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -111,9 +218,21 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--group", type=int, default=64, help="chunks per kernel launch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-chunks", type=int, default=2)
+    ap.add_argument("--cpu-chunks", type=int, default=8)
     ap.add_argument("--no-decode-step", action="store_true", help="skip the C3 decode-step measurement")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="also run one 1 GiB device copy (the HBM-counter calibration kernel under rocprofv3 --pmc)")
+    ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "OUT_JSON"),
+                    help="only summarise two rocprofv3 --pmc runs into per-launch HBM traffic and exit")
+    ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
+                    help="only print per-(kernel, grid) launch durations of a rocprofv3 --kernel-trace run and exit")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        summarize_pmc(*args.summarize_pmc)
+        return
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for {args.gpus}); "
               "the per-chunk work is independent and would shard by layer / K-V with no communication.",
@@ -185,19 +304,43 @@ def main():
     bit_exact = bool(np.array_equal(encs[0].words[base:base + nw].cpu().numpy().view(np.uint32), ch0.bitstream)
                      and np.array_equal(out[0].cpu().numpy(), O.decompress_chunk(ch0)))
 
-    # dominant-kernel roofline: the decode kernel (read path), timed per launch with events
-    dec_ms = []
+    # rooflines of the two largest kernels, each timed per launch with events on
+    # its own stream: k_chunk_quantize (write) and k_chunk_decode (read, with
+    # its k_chunk_lut table build); the longer one is the headline roofline
+    dec_ms, q_ms = [], []
     for gi, (a, b) in enumerate(groups):
         s0 = torch.cuda.Event(enable_timing=True); s1 = torch.cuda.Event(enable_timing=True)
+        gpu_busy()
         s0.record(); codec.decode_batch(encs[gi], out=out[a:b], lut_work=luts); s1.record()
         torch.cuda.synchronize()
         dec_ms.append(s0.elapsed_time(s1))
-    grp_bytes = [2 * (b - a) * V * 8 + int(encs[gi].reference_bytes().sum() + encs[gi].side_bytes().sum())
-                 for gi, (a, b) in enumerate(groups)]
-    avg_ms = float(np.mean(dec_ms))
-    achieved = float(np.mean(grp_bytes)) / (avg_ms * 1e-3) / 1e9
+        q_ms.append(time_quantize(x[a:b], encs[gi]))
+    # algorithmic bytes: decode reads the stored chunk and writes 16 B of fp16 per
+    # vector; the quantizer reads 16 B of fp16 and writes 8 B of int8 symbols and
+    # one coset bit per vector
+    dec_bytes = float(np.mean([2 * (b - a) * V * 8 + int(encs[gi].reference_bytes().sum() + encs[gi].side_bytes().sum())
+                               for gi, (a, b) in enumerate(groups)]))
+    q_bytes = float(np.mean([(b - a) * V * (16 + 8) + (b - a) * V // 8 for a, b in groups]))
+    traffic = load_traffic()
+    kern = {
+        "k_chunk_decode": {"ms": float(np.mean(dec_ms)), "bytes": dec_bytes,
+                           "desc": f"k_chunk_decode (+k_chunk_lut), {G}-chunk launch, algorithmic bytes = stored chunk + 16 B fp16 out per vector"},
+        "k_chunk_quantize": {"ms": float(np.mean(q_ms)), "bytes": q_bytes,
+                             "desc": f"k_chunk_quantize, {G}-chunk launch, algorithmic bytes = 16 B fp16 in + 8 B int8 symbols + 1 coset bit per vector"},
+    }
+    roof = {}
+    for name, k in kern.items():
+        ach = k["bytes"] / (k["ms"] * 1e-3) / 1e9
+        tr = traffic.get(name)
+        roof[name] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": int(tr) if tr is not None else None,
+                      "kernel": k["desc"], "avg_launch_us": round(k["ms"] * 1e3, 1),
+                      "algorithmic_bytes": int(k["bytes"])}
+    dominant = max(kern, key=lambda n: kern[n]["ms"])
 
     step = {} if args.no_decode_step else bench_decode_step(dev)
+    if args.copy_calib:
+        copy_calibration(dev)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -220,9 +363,8 @@ def main():
         "effective_bits_per_dim": round(8 * Cb / D, 4),
         "reference_bits_per_dim": round(8 * ref_bytes / D, 4),
         "status_flags": int(np.bitwise_or.reduce(status)), "bit_exact_chunk0": bit_exact,
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_chunk_decode (+k_chunk_lut), per 8-chunk launch"},
+        "roofline": roof[dominant],
+        "roofline_other": {n: r for n, r in roof.items() if n != dominant},
         "cpu_baseline": cpu,
         "decode_step_us": step.get("decode_step_us"),
         "decode_step": step or None,

@@ -105,6 +105,7 @@ int lq_scale_fastdiv(const float *d_scale32, int64_t n_heads_total, int dtype, i
  * subtractive dither of the rotated path: d in [-1, 1)^8 per vector from
  * SplitMix64 of (seed, vector index) is added to x / scale before the search
  * and removed in d_deq ((q - d) * scale32); no counterpart in the reference.
+ * bph must not exceed 2^30 (LQ_ERR_ARG).
  * Replaces llm/compressed_kv_cache.py:199-231,270. */
 int lq_chunk_quantize(const void *d_x, int dtype, int64_t n_chunks, int64_t n_heads, int64_t bph,
                       const float *d_scale32, const int32_t *d_fastdiv, int8_t *d_sym,

@@ -167,7 +167,8 @@ __global__ void k_scale_fastdiv(const float* __restrict__ scale32, int dtype, in
 // -------------------------------------------------------- chunk quantize --
 
 constexpr int kQThreads = 256;
-constexpr int kQBlocksPerWG = 4;
+constexpr int kQBlocksPerWG = 8;
+constexpr int64_t kMaxBph = 1 << 30;   // vectors per head (2^27 tokens of 128 dims): in-head offsets stay int32
 
 // One workgroup quantizes kQBlocksPerWG consecutive LQ_BLK-vector blocks of one
 // chunk.  Per block it writes the coset bitmap (wave ballots, i.e. the
@@ -223,6 +224,22 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
         if (blk >= nblk) break;
         const int64_t vbase = blk * kBlk;
         const int valid = (int)((V - vbase) < kBlk ? (V - vbase) : kBlk);
+        // head of the block's first vector and its offset in that head (uniform);
+        // a lane steps over the head boundaries its vector lies past
+        const int64_t hblk = vbase / bph;
+        const int rblk = (int)(vbase - hblk * bph);
+        // with bph >= kBlk a block spans at most two heads: their scale,
+        // reciprocal and fast-division flag are read once per block
+        const bool two_heads = bph >= kBlk;
+        const int64_t hq0 = chunk * n_heads + hblk;
+        const int64_t hq1 = hblk + 1 < n_heads ? hq0 + 1 : hq0;
+        float s0 = 1.f, s1 = 1.f, rs0 = 1.f, rs1 = 1.f;
+        bool f0 = false, f1 = false;
+        if (two_heads) {
+            s0 = scale32[hq0]; s1 = scale32[hq1];
+            rs0 = 1.0f / s0; rs1 = 1.0f / s1;
+            f0 = fastdiv[hq0] != 0; f1 = fastdiv[hq1] != 0;
+        }
         int32_t sy[2][8];
         int cs[2];
         // pass 1: quantize two vectors per thread
@@ -232,14 +249,30 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
             cs[r] = 0;
             if (vl < valid) {
                 const int64_t v = vbase + vl;
-                const int64_t h = chunk * n_heads + v / bph;
-                const float s = scale32[h];
-                const bool fast = fastdiv[h] != 0;
-                const float rs = 1.0f / s;
+                float s, rs;
+                bool fast;
+                if (two_heads) {
+                    const bool nxt = rblk + vl >= (int)bph;
+                    s = nxt ? s1 : s0;
+                    rs = nxt ? rs1 : rs0;
+                    fast = nxt ? f1 : f0;
+                } else {
+                    int rr = rblk + vl;
+                    int64_t h = hq0;
+                    while (rr >= (int)bph) { rr -= (int)bph; h++; }
+                    s = scale32[h];
+                    rs = 1.0f / s;
+                    fast = fastdiv[h] != 0;
+                }
                 float xv[8], t[8], ic[8], dd[8];
                 load8(x, dtype, chunk * V + v, xv);
+                if (fast) {
 #pragma unroll
-                for (int i = 0; i < 8; i++) t[i] = div_scaled(xv[i], s, rs, fast);
+                    for (int i = 0; i < 8; i++) t[i] = div_scaled(xv[i], s, rs, true);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) t[i] = div_scaled(xv[i], s, rs, false);
+                }
                 if constexpr (DITHER) {
                     dither8(mix64((uint64_t)dseed[chunk]), v, dd);
 #pragma unroll
@@ -247,12 +280,19 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
                 }
                 int c = e8_nearest(t, ic);
                 cs[r] = c;
+                int32_t lo = INT_MAX, hi = INT_MIN;
 #pragma unroll
                 for (int i = 0; i < 8; i++) {
-                    int32_t iv = (int32_t)ic[i];
-                    int32_t sv = i < 7 ? iv : (iv >> 1);
-                    if (sv < kSymMin || sv > kSymMax) { flag = 1; sv = sv < kSymMin ? kSymMin : kSymMax; }
-                    sy[r][i] = sv;
+                    const int32_t iv = (int32_t)ic[i];
+                    sy[r][i] = i < 7 ? iv : (iv >> 1);
+                    lo = min(lo, sy[r][i]);
+                    hi = max(hi, sy[r][i]);
+                }
+                // out-of-range symbols are flagged and clamped (histogram indices stay in range)
+                if (lo < kSymMin || hi > kSymMax) {
+                    flag = 1;
+#pragma unroll
+                    for (int i = 0; i < 8; i++) sy[r][i] = min(max(sy[r][i], kSymMin), kSymMax);
                 }
                 if (deq) {
                     float off = c ? 0.5f : 0.f, y[8];
@@ -444,7 +484,7 @@ int lq_chunk_quantize(const void* d_x, int dtype, int64_t n_chunks, int64_t n_he
                       const float* d_scale32, const int32_t* d_fastdiv, int8_t* d_sym, uint8_t* d_coset_bits,
                       uint32_t* d_blk_n1, uint32_t* d_hist, int32_t* d_status, void* d_deq, int deq_dtype,
                       const int64_t* d_dither_seed, hipStream_t s) {
-    if (n_chunks <= 0 || n_heads <= 0 || bph <= 0 || dtype < 0 || dtype > 2) return LQ_ERR_ARG;
+    if (n_chunks <= 0 || n_heads <= 0 || bph <= 0 || bph > kMaxBph || dtype < 0 || dtype > 2) return LQ_ERR_ARG;
     const int64_t V = n_heads * bph;
     const int64_t nblk = (V + kBlk - 1) / kBlk;
     const int64_t wg = n_chunks * ((nblk + kQBlocksPerWG - 1) / kQBlocksPerWG);
@@ -463,7 +503,8 @@ int lq_chunk_quantize_wide(const void* d_x, int dtype, int64_t n_chunks, int64_t
                            const float* d_scale32, const int32_t* d_fastdiv, int16_t* d_sym, uint8_t* d_coset_bits,
                            uint32_t* d_blk_n1, int32_t* d_minmax, int32_t* d_status, void* d_deq, int deq_dtype,
                            const int64_t* d_dither_seed, hipStream_t s) {
-    if (n_chunks <= 0 || n_heads <= 0 || bph <= 0 || dtype < 0 || dtype > 2 || !d_minmax) return LQ_ERR_ARG;
+    if (n_chunks <= 0 || n_heads <= 0 || bph <= 0 || bph > kMaxBph || dtype < 0 || dtype > 2 || !d_minmax)
+        return LQ_ERR_ARG;
     const int64_t V = n_heads * bph;
     const int64_t nblk = (V + kBlk - 1) / kBlk;
     const int64_t wg = n_chunks * ((nblk + kQBlocksPerWG - 1) / kQBlocksPerWG);

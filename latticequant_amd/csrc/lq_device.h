@@ -57,10 +57,18 @@ __device__ __forceinline__ void load8(const void* base, int dtype, int64_t v, fl
     } else {
         uint4 r = reinterpret_cast<const uint4*>(base)[v];
         uint32_t w[4] = {r.x, r.y, r.z, r.w};
-        for (int i = 0; i < 4; i++) {
-            uint16_t lo = (uint16_t)(w[i] & 0xffffu), hi = (uint16_t)(w[i] >> 16);
-            x[2 * i] = dtype == LQ_F16 ? h2f(lo) : bf2f(lo);
-            x[2 * i + 1] = dtype == LQ_F16 ? h2f(hi) : bf2f(hi);
+        if (dtype == LQ_F16) {   // dtype is uniform: one branch, not a select per element
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                x[2 * i] = h2f((uint16_t)(w[i] & 0xffffu));
+                x[2 * i + 1] = h2f((uint16_t)(w[i] >> 16));
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                x[2 * i] = __uint_as_float(w[i] << 16);
+                x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+            }
         }
     }
 }
@@ -98,12 +106,15 @@ __device__ __forceinline__ void d8_round(const float x[8], float r[8]) {
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         res[i] = x[i] - r[i];
-        float two = 2.0f * fabsf(res[i]);
-        float fc = 1.0f - two;
-        float adj = fc + tiebreak(i);
+        // RN(1 - 2|res|): 2|res| is exact, so one fused op rounds the same way
+        const float fc = __builtin_fmaf(-2.0f, fabsf(res[i]), 1.0f);
+        const float adj = i == 0 ? fc : fc + tiebreak(i);   // tiebreak(0) = 0 and fc is never -0
         if (i == 0 || adj < best) { best = adj; idx = i; }
     }
-    if (((int64_t)s) & 1) {
+    // parity of the fp32 sum (torch: r.sum(-1) % 2): every fp32 value of
+    // magnitude >= 2^24 is even, below that the int32 conversion is exact
+    const bool odd = fabsf(s) < 16777216.0f && (((int32_t)s) & 1);
+    if (odd) {
         float rv = res[0];
 #pragma unroll
         for (int i = 1; i < 8; i++) rv = (idx == i) ? res[i] : rv;
