@@ -242,6 +242,7 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
         }
         int32_t sy[2][8];
         int cs[2];
+        unsigned long long bal[2];
         // pass 1: quantize two vectors per thread
 #pragma unroll
         for (int r = 0; r < 2; r++) {
@@ -304,23 +305,34 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
                     store8(deq, deq_dtype, chunk * V + v, y);
                 }
             }
-            unsigned long long m = __ballot(cs[r]);
-            if (lane == 0) masks[r * 4 + wave] = m;
+            bal[r] = __ballot(cs[r]);
+            if (lane == 0) masks[r * 4 + wave] = bal[r];
         }
         __syncthreads();
+        // coset-1 counts of the block's 8 ballot words: the words are the same
+        // for every lane, so they are made wave-uniform and counted on the
+        // scalar unit
+        int pc[kBlk / 64];
         int n1 = 0;
 #pragma unroll
-        for (int k = 0; k < kBlk / 64; k++) n1 += __popcll(masks[k]);
+        for (int k = 0; k < kBlk / 64; k++) {
+            const unsigned long long mk = masks[k];
+            const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)mk);
+            const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(mk >> 32));
+            pc[k] = __builtin_popcount(lo) + __builtin_popcount(hi);
+            n1 += pc[k];
+        }
         const int n0 = valid - n1;
 #pragma unroll
         for (int r = 0; r < 2; r++) {
             const int vl = r * kQThreads + tid;
             if (vl < valid) {
-                const int word = r * 4 + wave;
-                int before = 0;
-                for (int k = 0; k < word; k++) before += __popcll(masks[k]);
-                unsigned long long m = masks[word];
-                int below = __popcll(m & ((1ull << lane) - 1ull));
+                int before = 0;   // coset-1 vectors of the earlier words (wave-uniform)
+#pragma unroll
+                for (int k = 0; k < kBlk / 64; k++) before += k < r * 4 + wave ? pc[k] : 0;
+                const unsigned long long m = bal[r];
+                const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
                 int rank1 = before + below;
                 int rank0 = vl - rank1;
                 const int c = cs[r];

@@ -101,15 +101,26 @@ __device__ __forceinline__ void d8_round(const float x[8], float r[8]) {
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; i++) { r[i] = rintf(x[i]); s += r[i]; }
+    // first-index argmin of RN(RN(1 - 2|res_i|) + tiebreak_i): upd[i] says the
+    // running minimum moved to i, so the argmin is the last i with upd[i]
+    // (the per-lane flags stay lane masks; no index is materialised)
     float best = 0.f;
-    int idx = 0;
+    bool upd[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         res[i] = x[i] - r[i];
         // RN(1 - 2|res|): 2|res| is exact, so one fused op rounds the same way
         const float fc = __builtin_fmaf(-2.0f, fabsf(res[i]), 1.0f);
         const float adj = i == 0 ? fc : fc + tiebreak(i);   // tiebreak(0) = 0 and fc is never -0
-        if (i == 0 || adj < best) { best = adj; idx = i; }
+        upd[i] = i == 0 || adj < best;
+        best = upd[i] ? adj : best;
+    }
+    bool sel[8];
+    bool later = false;
+#pragma unroll
+    for (int i = 7; i >= 0; i--) {
+        sel[i] = upd[i] && !later;
+        later = later || upd[i];
     }
     // parity of the fp32 sum (torch: r.sum(-1) % 2): every fp32 value of
     // magnitude >= 2^24 is even, below that the int32 conversion is exact
@@ -117,10 +128,10 @@ __device__ __forceinline__ void d8_round(const float x[8], float r[8]) {
     if (odd) {
         float rv = res[0];
 #pragma unroll
-        for (int i = 1; i < 8; i++) rv = (idx == i) ? res[i] : rv;
-        float sg = rv > 0.f ? 1.f : (rv < 0.f ? -1.f : 1.f);
+        for (int i = 1; i < 8; i++) rv = sel[i] ? res[i] : rv;
+        const float sg = rv < 0.f ? -1.f : 1.f;   // sign(res), 0 -> +1
 #pragma unroll
-        for (int i = 0; i < 8; i++) r[i] = (idx == i) ? r[i] + sg : r[i];
+        for (int i = 0; i < 8; i++) r[i] = sel[i] ? r[i] + sg : r[i];
     }
 }
 
