@@ -319,6 +319,80 @@ int lq_unpack_coset_bits(const uint8_t *d_packed, int64_t n, uint8_t *d_out, hip
 int lq_rht(const void *d_x, int in_dtype, int64_t n_rows, int d, const float *d_signs, int64_t rows_per_sign,
            int n_sign, int inverse, void *d_out, int out_dtype, hipStream_t s);
 
+/* ------------------------------------------------------ resident form --- */
+
+/* Fixed-width resident form of a compressed KV prefix (head_dim 128), read by
+ * lq_resident_attention.  Per kv head, tokens in blocks of 16; per block 256
+ * vector records laid out [slot 0..63][group 0..3] (record (slot, group) is
+ * vector 4*group + slot/16 of token 16*block + slot%16).  A record is the
+ * reference's b = 5 fixed-rate code word of the lattice point
+ * (core/compact_storage.py:87-154: coset, c0..c6 + 16 in 5 bits, (c7 + 16) >> 1
+ * in 4 bits, c7's low bit = parity of c0..c6), its 40 bits split as
+ *   a (uint32): coset @0, u0 @1, u2 @6, u4 @11, bit 3 of c7h @16, u1 @17, u3 @22, u5 @27
+ *   b (uint8):  u6 @0, bits 0..2 of c7h @5
+ * (u_i = c_i + 16, c7h = u7 >> 1).  Vectors with a coordinate outside [-16, 15]
+ * are exceptions (bit slot of mask[block][group]); their lattice point is kept
+ * as 8 int16 values 2c in exc[], block entries from meta[block].base on, in
+ * (group, slot) order -- the representable-or-fallback split of
+ * llm/fused_triton_merge.py:33-130 with lattice values as the fallback.
+ * meta[block] = {header low, header high, base, count}: the 64-bit header
+ * repeats the first seven exceptions for the attention kernel (byte 0 = count
+ * saturated at 255, byte 1 + k = slot | group << 6 of exception k), base is
+ * the index of the block's first entry in exc[].  scale[token] is the fp16
+ * scale the token's chunk stores. */
+typedef struct {
+    uint32_t *a;             /* [n_heads][cap_blocks][64][4] */
+    uint8_t *b;              /* [n_heads][cap_blocks][64][4] */
+    uint64_t *mask;          /* [n_heads][cap_blocks][4] */
+    uint32_t *meta;          /* [n_heads][cap_blocks][4] */
+    int16_t *exc;            /* [exc_cap][8] */
+    uint16_t *scale;         /* [n_heads][cap_blocks * 16] fp16 */
+    int32_t *n_exc;          /* device counter: exception entries in use */
+    int32_t *status;         /* device flags: LQ_RES_ST_* */
+    int64_t n_heads;
+    int64_t cap_blocks;
+    int64_t exc_cap;
+} lq_resident;
+
+#define LQ_RES_ST_EXC_OVERFLOW 1  /* more exceptions than exc_cap: entries beyond it were dropped */
+
+/* Workspace (bytes) of lq_resident_quantize for n_heads x t_tokens. */
+int64_t lq_resident_workspace(int64_t n_heads, int64_t t_tokens);
+
+/* Quantize x (n_heads, t_tokens, 128) of dtype into blocks blk0 .. blk0 + t_tokens/16
+ * of resident heads h0 .. h0 + n_heads (t_tokens a multiple of 16): the lattice
+ * point of every vector is encode_e8(x / scale32[head]) (core/e8_quantizer.py:61-83,
+ * the division and decisions of llm/compressed_kv_cache.py:197-201), so it is the
+ * point the chunk codec codes with the same scales; scale16[head] is stored per
+ * token.  Exception entries are appended at *n_exc (capacity exc_cap; overflow
+ * sets LQ_RES_ST_EXC_OVERFLOW).  Stream-ordered, no host sync. */
+int lq_resident_quantize(const void *d_x, int dtype, int64_t n_heads, int64_t t_tokens, const float *d_scale32,
+                         const uint16_t *d_scale16, const lq_resident *r, int64_t h0, int64_t blk0, void *d_work,
+                         hipStream_t s);
+
+/* Dequantise resident blocks back to (n_heads, n_blocks*16, 128) fp16 / bf16 / fp32:
+ * lattice point times the stored fp16 scale, rounded once, as _decompress_chunk
+ * writes it (llm/compressed_kv_cache.py:289-332). */
+int lq_resident_dequant(const lq_resident *r, int64_t h0, int64_t n_heads, int64_t blk0, int64_t n_blocks,
+                        void *d_out, int out_dtype, hipStream_t s);
+
+/* Workspace (bytes) of lq_resident_attention; its first n_heads uint32 are
+ * completion counters that must be zero before the first call (each call leaves
+ * them zero). */
+int64_t lq_resident_attn_workspace(int64_t n_heads, int group, int64_t t_prefix, int64_t t_tail);
+
+/* One decode step of attention over resident prefixes + fp16 tail:
+ * out[qh] = softmax(q[qh] . K^T / sqrt(128)) V, kv head qh / group, over the
+ * first t_prefix tokens (a multiple of 16) of resident heads 0 .. n_heads of k
+ * and v, then t_tail tokens of tail_k / tail_v (n_heads, t_tail, 128) fp16.
+ * q, out: (n_heads * group, 128) fp16; group 1..16.  Replaces the fp16-resident
+ * read of llm/compressed_kv_cache.py:384-395 + HF attention, and the fused
+ * merge of llm/fused_triton_merge.py:33-130 that joins packed vectors with
+ * their fallback before attention. */
+int lq_resident_attention(const lq_resident *k, const lq_resident *v, int64_t t_prefix, const uint16_t *d_q,
+                          int group, const uint16_t *d_tail_k, const uint16_t *d_tail_v, int64_t t_tail,
+                          void *d_work, uint16_t *d_out, hipStream_t s);
+
 #ifdef __cplusplus
 }
 #endif

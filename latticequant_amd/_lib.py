@@ -68,6 +68,11 @@ _SIGS = {
     "lq_attn_workspace": ([_I64, _I64, _I64, _INT], _I64),
     "lq_decode_attention": ([_P, _P, _P, _INT, _P, _P, _I64, _P, _P, _P], _INT),
     "lq_rht": ([_P, _INT, _I64, _INT, _P, _I64, _INT, _INT, _P, _INT, _P], _INT),
+    "lq_resident_workspace": ([_I64, _I64], _I64),
+    "lq_resident_quantize": ([_P, _INT, _I64, _I64, _P, _P, _P, _I64, _I64, _P, _P], _INT),
+    "lq_resident_dequant": ([_P, _I64, _I64, _I64, _I64, _P, _INT, _P], _INT),
+    "lq_resident_attn_workspace": ([_I64, _INT, _I64, _I64], _I64),
+    "lq_resident_attention": ([_P, _P, _I64, _P, _INT, _P, _P, _I64, _P, _P, _P], _INT),
 }
 
 
@@ -80,6 +85,15 @@ class ChunkBatch(ctypes.Structure):
     _fields_ = [("words", _P), ("chunk_base", _P), ("stream_woff", _P), ("blk_off", _P), ("stream_nbits", _P), ("blk_state", _P),
                 ("coset_bits", _P), ("blk_n1", _P), ("tables", _P), ("scale16", _P),
                 ("n_chunks", _I64), ("n_heads", _I64), ("bph", _I64)]
+
+
+class Resident(ctypes.Structure):
+    """lq_resident: device pointers + geometry of a resident (fixed-width) KV prefix."""
+    _fields_ = [("a", _P), ("b", _P), ("mask", _P), ("meta", _P), ("exc", _P), ("scale", _P), ("n_exc", _P),
+                ("status", _P), ("n_heads", _I64), ("cap_blocks", _I64), ("exc_cap", _I64)]
+
+
+LQ_RES_ST_EXC_OVERFLOW = 1
 
 
 def exported_symbols():

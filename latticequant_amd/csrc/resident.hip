@@ -1,0 +1,959 @@
+// Resident (working) form of a compressed KV prefix and the decode-attention
+// kernel that reads it, for gfx950.
+//
+// The rANS streams are the at-rest form of the cache (bit-exact with the
+// reference).  A decode step cannot re-run rANS over a 32k-token prefix, so
+// the cache also keeps the same lattice points in a fixed-width form: one
+// b = 5 compact code word per vector (core/compact_storage.py:87-154), 40 bits
+// split into a uint32 and a uint8 plane (layout in latticequant_amd.h), plus
+// int16 exception entries for the rare vectors outside the 5-bit range.  A
+// 16-token block of one kv head is 256 records stored [slot][group]: record
+// (slot, group) is vector 4*group + slot/16 of token slot%16, which is the B
+// operand layout of v_mfma_f32_16x16x32_f16 for q . k^T (lane = slot, its 8
+// halves = the 8 dimensions of one vector).
+//
+// Decoding a record to fp16 is bit arithmetic: a 5-bit field u placed at bit
+// 1 of a half whose high bits are 0x64 gives the fp16 number 1024 + 2u + coset
+// (the coset bit sits at bit 0), so one AND-OR turns two fields into a packed
+// pair; subtracting 1056 leaves 2c exactly (c the lattice coordinate), and a
+// packed multiply by s / 2 gives fp16(c * s), the value _decompress_chunk
+// writes for the token's fp16 scale s.  The MFMA operands are therefore the
+// fp16 K / V the reference's attention reads.
+//
+// lq_resident_attention: per (kv head, 512-token split) one workgroup of four
+// waves; a wave takes 32-token tiles:
+//   S = Q K^T        8 MFMA 16x16x32 (rows: the group's query heads, spread so
+//                    that query head h sits in row 4 (h % 4) + h / 4)
+//   online softmax   exp2, row max by DPP within 16 lanes
+//   O += P V         P (fp16) and V go through LDS: V is decoded two tokens
+//                    per lane into (token t, token t+1) pairs and stored
+//                    dimension-major, so each MFMA B operand is two 8-byte reads
+// then the four waves merge their (m, l, O) in LDS, each workgroup writes one
+// record per query head, and the last workgroup of a kv head (device-scope
+// counter) merges the records and writes the output.
+#include <climits>
+#include <cmath>
+
+#include "lq_device.h"
+
+using namespace lq;
+
+namespace {
+
+inline int launch_status() { return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_LAUNCH; }
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kHd = 128;
+constexpr int kRB = 16;                       // tokens per resident block
+constexpr uint32_t kPairBias = 0x64206420u;   // fp16 pair (1056, 1056)
+constexpr uint32_t kFieldMask = 0x003E003Eu;  // bits 1..5 of both halves
+constexpr uint32_t kLsbMask = 0x08420842u;    // low bits of u0..u5 in the a word
+
+__device__ __forceinline__ uint32_t unbias(uint32_t v) {
+    const h2_t r = __builtin_bit_cast(h2_t, v) - __builtin_bit_cast(h2_t, kPairBias);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// One record -> four fp16 pairs 1056 + 2c of coordinates (0,1) (2,3) (4,5) (6,7).
+__device__ __forceinline__ void rec_pairs(uint32_t a, uint32_t b, uint32_t p[4]) {
+    const uint32_t kc = 0x64006400u | ((a & 1u) * 0x00010001u);
+    p[0] = (a & kFieldMask) | kc;
+    p[1] = ((a >> 5) & kFieldMask) | kc;
+    p[2] = ((a >> 10) & kFieldMask) | kc;
+    const uint32_t c7h = ((b >> 5) & 7u) | ((a >> 13) & 8u);
+    const uint32_t par = ((uint32_t)__builtin_popcount(a & kLsbMask) + b) & 1u;
+    const uint32_t u7 = (c7h << 1) | par;
+    p[3] = kc | ((b & 31u) << 1) | (u7 << 17);
+}
+
+// Records of tokens t and t+1 (same vector) -> eight fp16 pairs
+// (coordinate i of t, coordinate i of t+1), values 1056 + 2c.
+__device__ __forceinline__ void rec_pairs_tok(uint32_t a0, uint32_t b0, uint32_t a1, uint32_t b1, uint32_t p[8]) {
+    const uint32_t lo = __builtin_amdgcn_perm(a1, a0, 0x05040100u);   // a0[15:0] | a1[15:0] << 16
+    const uint32_t hi = __builtin_amdgcn_perm(a1, a0, 0x07060302u);   // a0[31:16] | a1[31:16] << 16
+    const uint32_t kc = 0x64006400u | (lo & 0x00010001u);             // coset of t at bit 0, of t+1 at bit 16
+    p[0] = (lo & kFieldMask) | kc;
+    p[2] = ((lo >> 5) & kFieldMask) | kc;
+    p[4] = ((lo >> 10) & kFieldMask) | kc;
+    p[1] = (hi & kFieldMask) | kc;
+    p[3] = ((hi >> 5) & kFieldMask) | kc;
+    p[5] = ((hi >> 10) & kFieldMask) | kc;
+    const uint32_t h0 = ((b0 >> 5) & 7u) | ((a0 >> 13) & 8u);
+    const uint32_t h1 = ((b1 >> 5) & 7u) | ((a1 >> 13) & 8u);
+    const uint32_t q0 = ((uint32_t)__builtin_popcount(a0 & kLsbMask) + b0) & 1u;
+    const uint32_t q1 = ((uint32_t)__builtin_popcount(a1 & kLsbMask) + b1) & 1u;
+    p[6] = kc | ((b0 & 31u) << 1) | ((b1 & 31u) << 17);
+    p[7] = kc | (((h0 << 1) | q0) << 1) | (((h1 << 1) | q1) << 17);
+}
+
+// int16 lattice values 2c -> fp16 pair
+__device__ __forceinline__ uint32_t pair_from_i16(int a, int b) {
+    const h2_t r = {(_Float16)(float)a, (_Float16)(float)b};
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// fp16 pairs of exact lattice values 2c -> the pairs fp16(c * s) with s the
+// fp16 scale of the low / high element, rounded once as _decompress_chunk
+// rounds (llm/compressed_kv_cache.py:330).  c * s is exact in fp32, so one
+// packed fp16 multiply by s / 2 rounds it the same way whenever s / 2 is a
+// normal fp16 number (s >= 2^-13); smaller scales take the fp32 route.
+template <int N>
+__device__ __forceinline__ void dequant_pairs(uint32_t p[N], uint16_t s_lo, uint16_t s_hi) {
+    const float flo = h2f(s_lo), fhi = h2f(s_hi);
+    if (fminf(flo, fhi) >= 0x1p-13f) {
+        const h2_t m = {(_Float16)(0.5f * flo), (_Float16)(0.5f * fhi)};
+#pragma unroll
+        for (int i = 0; i < N; i++) p[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, p[i]) * m);
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            const h2_t h = __builtin_bit_cast(h2_t, p[i]);
+            const h2_t r = {(_Float16)(((float)h[0] * 0.5f) * flo), (_Float16)(((float)h[1] * 0.5f) * fhi)};
+            p[i] = __builtin_bit_cast(uint32_t, r);
+        }
+    }
+}
+
+// The pair (s_lo / 2, s_hi / 2) for dequant_pairs' fast path and whether it
+// applies (both scales >= 2^-13, so that the halves are exact).
+__device__ __forceinline__ uint32_t half_scales(uint32_t s_pair, bool* exact) {
+    const h2_t sp = __builtin_bit_cast(h2_t, s_pair);
+    *exact = (float)sp[0] >= 0x1p-13f && (float)sp[1] >= 0x1p-13f;
+    const h2_t half = {(_Float16)0.5f, (_Float16)0.5f};
+    return __builtin_bit_cast(uint32_t, sp * half);
+}
+template <int N>
+__device__ __forceinline__ void mul_pairs(uint32_t p[N], uint32_t m) {
+#pragma unroll
+    for (int i = 0; i < N; i++)
+        p[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, p[i]) * __builtin_bit_cast(h2_t, m));
+}
+
+__device__ __forceinline__ h8_t as_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    const uint4 u = make_uint4(a, b, c, d);
+    return __builtin_bit_cast(h8_t, u);
+}
+
+// ------------------------------------------------------------ producer --
+
+// encode one lattice point (integer coordinates ic of the coset
+// representative, coset bit cs) as a record; false when out of range
+__device__ __forceinline__ bool rec_encode(const float ic[8], int cs, uint32_t* a, uint32_t* b) {
+    int u[8];
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float f = ic[i] + 16.0f;
+        ok = ok && f >= 0.0f && f <= 31.0f;
+        u[i] = ok ? (int)f : 0;
+    }
+    if (!ok) { *a = 0u; *b = 0u; return false; }
+    const uint32_t c7h = (uint32_t)u[7] >> 1;
+    *a = (uint32_t)cs | ((uint32_t)u[0] << 1) | ((uint32_t)u[2] << 6) | ((uint32_t)u[4] << 11) |
+         ((c7h >> 3) << 16) | ((uint32_t)u[1] << 17) | ((uint32_t)u[3] << 22) | ((uint32_t)u[5] << 27);
+    *b = (uint32_t)u[6] | ((c7h & 7u) << 5);
+    return true;
+}
+
+// lattice point of vector (head hh, token t, vector g) of x with IEEE x / s
+__device__ __forceinline__ int res_point(const void* x, int dtype, int64_t T, int64_t hh, int64_t t, int g, float s,
+                                         float ic[8]) {
+    float xv[8], tv[8];
+    load8(x, dtype, (hh * T + t) * (kHd / 8) + g, xv);
+#pragma unroll
+    for (int i = 0; i < 8; i++) tv[i] = xv[i] / s;
+    return e8_nearest(tv, ic);
+}
+
+// grid (t_tokens / 16, n_heads), 256 threads: wave = group, lane = slot
+__global__ __launch_bounds__(256) void k_res_quant(const void* __restrict__ x, int dtype, int64_t T,
+                                                   const float* __restrict__ scale32,
+                                                   const uint16_t* __restrict__ scale16, lq_resident r, int64_t h0,
+                                                   int64_t blk0, uint32_t* __restrict__ cnt) {
+    __shared__ unsigned long long wm[4];
+    const int tid = threadIdx.x, grp = tid >> 6, slot = tid & 63;
+    const int64_t bb = blockIdx.x, hh = blockIdx.y;
+    const int64_t t = bb * kRB + (slot & 15);
+    const int g = 4 * grp + (slot >> 4);
+    float ic[8];
+    const int cs = res_point(x, dtype, T, hh, t, g, scale32[hh], ic);
+    uint32_t a, b;
+    const bool ok = rec_encode(ic, cs, &a, &b);
+    const int64_t rb = (h0 + hh) * r.cap_blocks + blk0 + bb;
+    r.a[(rb * 64 + slot) * 4 + grp] = a;
+    r.b[(rb * 64 + slot) * 4 + grp] = (uint8_t)b;
+    const unsigned long long m = __ballot(!ok);
+    if (slot == 0) {
+        r.mask[rb * 4 + grp] = m;
+        wm[grp] = m;
+    }
+    if (grp == 0 && slot < kRB) r.scale[(h0 + hh) * r.cap_blocks * kRB + (blk0 + bb) * kRB + slot] = scale16[hh];
+    __syncthreads();
+    if (tid == 0) {
+        // header: count and the first seven exceptions in (group, slot) order
+        uint64_t hdr = 0;
+        int n = 0;
+        for (int c = 0; c < 4; c++) {
+            unsigned long long mm = wm[c];
+            while (mm) {
+                const int sl = __ffsll((long long)mm) - 1;
+                mm &= mm - 1ull;
+                if (n < 7) hdr |= (uint64_t)(sl | (c << 6)) << (8 * (n + 1));
+                n++;
+            }
+        }
+        hdr |= (uint64_t)(n < 255 ? n : 255);
+        r.meta[rb * 4 + 0] = (uint32_t)hdr;
+        r.meta[rb * 4 + 1] = (uint32_t)(hdr >> 32);
+        r.meta[rb * 4 + 3] = (uint32_t)n;
+        cnt[hh * gridDim.x + bb] = (uint32_t)n;
+    }
+}
+
+// exclusive scan of the per-block exception counts (one workgroup) -> base,
+// starting at *n_exc, which advances by the total
+__global__ __launch_bounds__(256) void k_res_scan(const uint32_t* __restrict__ cnt, int64_t nblk_call,
+                                                  int64_t n_heads_call, lq_resident r, int64_t h0, int64_t blk0) {
+    __shared__ uint32_t part[256];
+    const int tid = threadIdx.x;
+    const int64_t n = nblk_call * n_heads_call;
+    const int64_t per = (n + 255) / 256;
+    const int64_t lo = tid * per, hi = lo + per < n ? lo + per : n;
+    uint32_t s = 0;
+    for (int64_t i = lo; i < hi; i++) s += cnt[i];
+    part[tid] = s;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {
+        const uint32_t v = tid >= off ? part[tid - off] : 0u;
+        __syncthreads();
+        part[tid] += v;
+        __syncthreads();
+    }
+    const uint32_t start = (uint32_t)*r.n_exc;
+    uint32_t run = start + (tid ? part[tid - 1] : 0u);
+    for (int64_t i = lo; i < hi; i++) {
+        const int64_t hh = i / nblk_call, bb = i % nblk_call;
+        r.meta[((h0 + hh) * r.cap_blocks + blk0 + bb) * 4 + 2] = run;
+        run += cnt[i];
+    }
+    __syncthreads();
+    if (tid == 255) *r.n_exc = (int32_t)(start + part[255]);
+}
+
+// exception entries: the vectors flagged by k_res_quant, recomputed
+__global__ __launch_bounds__(256) void k_res_fill(const void* __restrict__ x, int dtype, int64_t T,
+                                                  const float* __restrict__ scale32, lq_resident r, int64_t h0,
+                                                  int64_t blk0) {
+    const int tid = threadIdx.x, grp = tid >> 6, slot = tid & 63;
+    const int64_t bb = blockIdx.x, hh = blockIdx.y;
+    const int64_t rb = (h0 + hh) * r.cap_blocks + blk0 + bb;
+    const unsigned long long m0 = r.mask[rb * 4 + 0], m1 = r.mask[rb * 4 + 1], m2 = r.mask[rb * 4 + 2],
+                             m3 = r.mask[rb * 4 + 3];
+    if ((m0 | m1 | m2 | m3) == 0ull) return;
+    const unsigned long long m = grp == 0 ? m0 : grp == 1 ? m1 : grp == 2 ? m2 : m3;
+    if (!((m >> slot) & 1ull)) return;
+    int before = 0;
+    if (grp > 0) before += __popcll(m0);
+    if (grp > 1) before += __popcll(m1);
+    if (grp > 2) before += __popcll(m2);
+    before += __popcll(m & ((1ull << slot) - 1ull));
+    const int64_t idx = (int64_t)r.meta[rb * 4 + 2] + before;
+    if (idx >= r.exc_cap) {
+        atomicOr(r.status, LQ_RES_ST_EXC_OVERFLOW);
+        return;
+    }
+    float ic[8];
+    const int cs = res_point(x, dtype, T, hh, bb * kRB + (slot & 15), 4 * grp + (slot >> 4), scale32[hh], ic);
+    int16_t e[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float v = fminf(fmaxf(2.0f * ic[i] + (float)cs, -32768.0f), 32767.0f);
+        e[i] = (int16_t)v;
+    }
+    uint4 w;
+    w.x = (uint16_t)e[0] | ((uint32_t)(uint16_t)e[1] << 16);
+    w.y = (uint16_t)e[2] | ((uint32_t)(uint16_t)e[3] << 16);
+    w.z = (uint16_t)e[4] | ((uint32_t)(uint16_t)e[5] << 16);
+    w.w = (uint16_t)e[6] | ((uint32_t)(uint16_t)e[7] << 16);
+    reinterpret_cast<uint4*>(r.exc)[idx] = w;
+}
+
+// exception entry idx -> 8 lattice values 2c
+__device__ __forceinline__ void exc_load(const int16_t* exc, int64_t idx, int v[8]) {
+    const uint4 w = reinterpret_cast<const uint4*>(exc)[idx];
+    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        v[2 * i] = (int)(int16_t)(ww[i] & 0xffffu);
+        v[2 * i + 1] = (int)(int16_t)(ww[i] >> 16);
+    }
+}
+
+// grid (n_blocks, n_heads), 256 threads: one record per thread
+__global__ __launch_bounds__(256) void k_res_dequant(lq_resident r, int64_t h0, int64_t blk0, int64_t nblk_call,
+                                                     void* __restrict__ out, int out_dtype) {
+    const int tid = threadIdx.x, grp = tid >> 6, slot = tid & 63;
+    const int64_t bb = blockIdx.x, hh = blockIdx.y;
+    const int64_t rb = (h0 + hh) * r.cap_blocks + blk0 + bb;
+    const int64_t tok = bb * kRB + (slot & 15);
+    const int g = 4 * grp + (slot >> 4);
+    const unsigned long long m = r.mask[rb * 4 + grp];
+    int v2[8];
+    if ((m >> slot) & 1ull) {
+        int before = 0;
+        for (int c = 0; c < grp; c++) before += __popcll(r.mask[rb * 4 + c]);
+        before += __popcll(m & ((1ull << slot) - 1ull));
+        const int64_t idx = (int64_t)r.meta[rb * 4 + 2] + before;
+        if (idx < r.exc_cap) {
+            exc_load(r.exc, idx, v2);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) v2[i] = 0;
+        }
+    } else {
+        uint32_t p[4];
+        rec_pairs(r.a[(rb * 64 + slot) * 4 + grp], r.b[(rb * 64 + slot) * 4 + grp], p);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const h2_t h = __builtin_bit_cast(h2_t, p[i]);
+            v2[2 * i] = (int)(float)h[0] - 1056;
+            v2[2 * i + 1] = (int)(float)h[1] - 1056;
+        }
+    }
+    const float s = h2f(r.scale[(h0 + hh) * r.cap_blocks * kRB + (blk0 + bb) * kRB + (slot & 15)]);
+    float y[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) y[i] = ((float)v2[i] * 0.5f) * s;
+    store8(out, out_dtype, (hh * nblk_call * kRB + tok) * (kHd / 8) + g, y);
+}
+
+// ----------------------------------------------------------- attention --
+
+constexpr int kAW = 8;                          // waves per workgroup
+constexpr int kTile = 32;                       // tokens per tile (two blocks)
+constexpr int kWaveTiles = 4;
+constexpr int kVtRow = 18;                      // uint32 per LDS V row (32 tokens fp16 + 8 B pad)
+constexpr int kPtRow = 20;                      // uint32 per LDS P row (32 tokens fp16 + 16 B pad)
+constexpr int kRecF = 4 + kHd;                  // floats per split record (m, l, 2 pad, o[128])
+constexpr int kMaxRec = 2048;                   // (split, head) records one merge can take
+constexpr int kCtrStride = 64;                  // uint32 per completion counter (one per 256-byte line)
+
+struct AttnArgs {
+    lq_resident k, v;
+    int64_t t_prefix, t_tail;
+    const uint16_t* q;
+    const uint16_t* tail_k;
+    const uint16_t* tail_v;
+    int group, nsp;
+    float* rec;
+    uint32_t* counter;
+    uint16_t* out;
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+// max / sum over the 16 lanes of a DPP row
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp<0xB1>(v));    // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp<0x4E>(v));    // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp<0x141>(v));   // row_half_mirror
+    v = fmaxf(v, dpp<0x140>(v));   // row_mirror
+    return v;
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp<0xB1>(v);
+    v += dpp<0x4E>(v);
+    v += dpp<0x141>(v);
+    v += dpp<0x140>(v);
+    return v;
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// ---- prefix tiles: records loaded one tile ahead into registers
+//
+// K lane layout: block x (0, 1), slot = lane: token 16 x + lane % 16, vectors
+// 4 c + lane / 16 (c = 0..3).  V lane layout: group j = lane / 16, block
+// xb = (lane / 8) % 2, token pair u = lane % 8: tokens 16 xb + 2 u, + 1 of
+// vectors 4 c + j.
+struct TileRaw {
+    uint4 ka[2];            // K records (c = 0..3) of blocks 0, 1
+    uint32_t kb[2];
+    uint32_t ks;            // fp16 scale of the K token of block 0 (low) and 1 (high)
+    uint4 va0, va1;         // V records of tokens ta, ta + 1
+    uint2 vb;
+    uint32_t vs;            // fp16 scales of tokens ta, ta + 1
+    uint4 meta;             // lanes 0..3: block metadata of K block 0, 1, V block 0, 1
+};
+
+// a block's exception header and base from the tile's meta registers
+// (i = 0, 1: K blocks, 2, 3: V blocks); wave-uniform
+__device__ __forceinline__ uint64_t meta_hdr(const TileRaw& d, int i) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)d.meta.x, i);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)d.meta.y, i);
+    return (uint64_t)lo | ((uint64_t)hi << 32);
+}
+__device__ __forceinline__ uint32_t meta_base(const TileRaw& d, int i) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)d.meta.z, i);
+}
+
+__device__ __forceinline__ void tile_load(const AttnArgs& A, int64_t kvh, int64_t t0, int64_t T, int lane,
+                                          TileRaw& d) {
+    // Blocks past the prefix (only block 1 of the last tile, T being a
+    // multiple of 16) read the last block instead: every address is valid and
+    // no branch waits on the loads; their tokens are masked out of the scores
+    // and carry p = 0 into P V.
+    const int64_t hb = kvh * A.k.cap_blocks;
+    const int64_t last = T - kRB;
+    uint32_t ks[2];
+#pragma unroll
+    for (int x = 0; x < 2; x++) {
+        const int64_t tb = min(t0 + 16 * x, last);
+        const int64_t rb = hb + tb / kRB;
+        d.ka[x] = reinterpret_cast<const uint4*>(A.k.a)[rb * 64 + lane];
+        d.kb[x] = reinterpret_cast<const uint32_t*>(A.k.b)[rb * 64 + lane];
+        ks[x] = A.k.scale[hb * kRB + tb + (lane & 15)];
+    }
+    d.ks = ks[0] | (ks[1] << 16);
+    {   // lanes 0..3 (and their copies): meta of K block 0, 1 and V block 0, 1.
+        // A per-lane address keeps this a vector load: scalar loads share the
+        // LDS wait counter and would stall every tile's LDS traffic.
+        const int i = lane & 3;
+        const int64_t tb = min(t0 + 16 * (i & 1), last);
+        const uint32_t* mp = ((i & 2) ? A.v.meta : A.k.meta) + (hb + tb / kRB) * 4;
+        d.meta = *reinterpret_cast<const uint4*>(mp);
+    }
+    const int j = lane >> 4, xb = (lane >> 3) & 1, u = lane & 7;
+    const int64_t tb = min(t0 + 16 * xb, last);
+    const int64_t rb = hb + tb / kRB;
+    const int s0 = 16 * j + 2 * u;
+    const uint4* ap = reinterpret_cast<const uint4*>(A.v.a) + rb * 64 + s0;
+    d.va0 = ap[0];
+    d.va1 = ap[1];
+    d.vb = reinterpret_cast<const uint2*>(A.v.b)[(rb * 64 + s0) >> 1];
+    d.vs = *reinterpret_cast<const uint32_t*>(A.v.scale + hb * kRB + tb + 2 * u);
+}
+
+// exception k of a block (0 <= k < count): slot | group << 6 from the header,
+// or, past the header's seven entries, from the block's masks; -1 past the end
+__device__ __forceinline__ int exc_code(const lq_resident& r, int64_t rb, uint64_t hdr, int k) {
+    if (k < 7) return (int)((hdr >> (8 * (k + 1))) & 0xffu);
+    int before = 0;
+    for (int c = 0; c < 4; c++) {
+        unsigned long long m = r.mask[rb * 4 + c];
+        const int pc = __popcll(m);
+        if (k < before + pc) {
+            for (int q = before; q < k; q++) m &= m - 1ull;
+            return (__ffsll((long long)m) - 1) | (c << 6);
+        }
+        before += pc;
+    }
+    return -1;
+}
+
+// K operands of block x from the tile registers
+__device__ __forceinline__ void tile_k(const AttnArgs& A, const TileRaw& d, int64_t rb, int x, int lane, bool fast,
+                                       uint32_t mk, h8_t kb[4]) {
+    const uint32_t aa[4] = {d.ka[x].x, d.ka[x].y, d.ka[x].z, d.ka[x].w};
+    uint32_t p[4][4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        rec_pairs(aa[c], d.kb[x] >> (8 * c), p[c]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) p[c][i] = unbias(p[c][i]);
+    }
+    const uint64_t hdr = meta_hdr(d, x);
+    const int n = (int)(hdr & 0xffu);
+    if (n) {   // rare: exception entries replace records (uniform loop)
+        const int64_t base = meta_base(d, x);
+        const int cnt = n < 255 ? n : 4 * 64;
+        for (int e = 0; e < cnt; e++) {
+            const int code = exc_code(A.k, rb, hdr, e);
+            if (code < 0) break;
+            const int64_t idx = base + e;
+            if ((code & 63) == lane && idx < A.k.exc_cap) {
+                int v[8];
+                exc_load(A.k.exc, idx, v);
+                const int g = code >> 6;
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) p[c][i] = g == c ? pair_from_i16(v[2 * i], v[2 * i + 1]) : p[c][i];
+            }
+        }
+    }
+    if (fast) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) mul_pairs<4>(p[c], mk);
+    } else {
+        const uint16_t sk = (uint16_t)(x ? d.ks >> 16 : d.ks & 0xffffu);
+#pragma unroll
+        for (int c = 0; c < 4; c++) dequant_pairs<4>(p[c], sk, sk);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) kb[c] = as_h8(p[c][0], p[c][1], p[c][2], p[c][3]);
+}
+
+// V of the tile into LDS, dimension-major: vt[d * kVtRow + token / 2] holds
+// (token, token + 1) of dimension d
+__device__ __forceinline__ void tile_v(const AttnArgs& A, const TileRaw& d, int64_t rb0, int lane, bool fast,
+                                       uint32_t mv, uint32_t* vt) {
+    const int j = lane >> 4, xb = (lane >> 3) & 1, u = lane & 7;
+    const int s0 = 16 * j + 2 * u;
+    const uint32_t x0[4] = {d.va0.x, d.va0.y, d.va0.z, d.va0.w}, x1[4] = {d.va1.x, d.va1.y, d.va1.z, d.va1.w};
+    uint32_t pr[4][8];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        rec_pairs_tok(x0[c], d.vb.x >> (8 * c), x1[c], d.vb.y >> (8 * c), pr[c]);
+#pragma unroll
+        for (int i = 0; i < 8; i++) pr[c][i] = unbias(pr[c][i]);
+    }
+    const uint64_t h0 = meta_hdr(d, 2), h1 = meta_hdr(d, 3);
+    if ((h0 | h1) & 0xffull) {   // rare: exception entries replace records
+        const uint64_t hdr = xb ? h1 : h0;
+        const int64_t base = xb ? meta_base(d, 3) : meta_base(d, 2);
+        const int n = (int)(hdr & 0xffu);
+        const int cnt = n < 255 ? n : 4 * 64;
+        for (int e = 0; e < cnt; e++) {
+            const int code = exc_code(A.v, rb0 + xb, hdr, e);
+            if (code < 0) break;
+            const int sl = code & 63;
+            const int64_t idx = base + e;
+            if ((sl == s0 || sl == s0 + 1) && idx < A.v.exc_cap) {
+                int v[8];
+                exc_load(A.v.exc, idx, v);
+                const int g = code >> 6, hi = sl - s0;
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        h2_t h = __builtin_bit_cast(h2_t, pr[c][i]);
+                        if (g == c) {
+                            if (hi) h[1] = (_Float16)(float)v[i];
+                            else h[0] = (_Float16)(float)v[i];
+                        }
+                        pr[c][i] = __builtin_bit_cast(uint32_t, h);
+                    }
+            }
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        if (fast) mul_pairs<8>(pr[c], mv);
+        else dequant_pairs<8>(pr[c], (uint16_t)(d.vs & 0xffffu), (uint16_t)(d.vs >> 16));
+#pragma unroll
+        for (int i = 0; i < 8; i++) vt[(8 * (4 * c + j) + i) * kVtRow + 8 * xb + u] = pr[c][i];
+    }
+}
+
+// ---- tail tiles (fp16 K / V, t_tail tokens, no prefetch)
+__device__ __forceinline__ void tail_k(const AttnArgs& A, int64_t kvh, int64_t tb, int64_t T, int lane, h8_t kb[4]) {
+    const int64_t t = tb + (lane & 15);
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        uint4 w = make_uint4(0u, 0u, 0u, 0u);
+        if (t < T) w = *reinterpret_cast<const uint4*>(A.tail_k + (kvh * T + t) * kHd + 32 * c + 8 * (lane >> 4));
+        kb[c] = __builtin_bit_cast(h8_t, w);
+    }
+}
+
+__device__ __forceinline__ void tail_v(const AttnArgs& A, int64_t kvh, int64_t t0, int64_t T, int lane, uint32_t* vt) {
+    const int j = lane >> 4, xb = (lane >> 3) & 1, u = lane & 7;
+    const int64_t ta = t0 + 16 * xb + 2 * u;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        uint4 w0 = make_uint4(0u, 0u, 0u, 0u), w1 = w0;
+        const int64_t off = 32 * c + 8 * j;
+        if (ta < T) w0 = *reinterpret_cast<const uint4*>(A.tail_v + (kvh * T + ta) * kHd + off);
+        if (ta + 1 < T) w1 = *reinterpret_cast<const uint4*>(A.tail_v + (kvh * T + ta + 1) * kHd + off);
+        const uint32_t x0[4] = {w0.x, w0.y, w0.z, w0.w}, x1[4] = {w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            vt[(8 * (4 * c + j) + 2 * i) * kVtRow + 8 * xb + u] = __builtin_amdgcn_perm(x1[i], x0[i], 0x05040100u);
+            vt[(8 * (4 * c + j) + 2 * i + 1) * kVtRow + 8 * xb + u] = __builtin_amdgcn_perm(x1[i], x0[i], 0x07060302u);
+        }
+    }
+}
+
+// Online softmax of one tile's scores, P into LDS, O += P V (V already in LDS).
+template <int HPL>
+__device__ __forceinline__ void tile_softmax_pv(int G, const f4_t s[2], const bool valid[2], int lane,
+                                                const uint32_t* vt, uint32_t* pt, float m_run[HPL], float l_run[HPL],
+                                                f4_t o[8]) {
+    const float c0 = 1.4426950408889634f / 11.313708498984761f;   // log2(e) / sqrt(128)
+    _Float16* ph = reinterpret_cast<_Float16*>(pt);
+#pragma unroll
+    for (int i = 0; i < HPL; i++) {
+        const int h = (lane >> 4) + 4 * i;
+        const float z0 = valid[0] ? s[0][i] * c0 : -INFINITY;
+        const float z1 = valid[1] ? s[1][i] * c0 : -INFINITY;
+        const float mn = fmaxf(m_run[i], row16_max(fmaxf(z0, z1)));
+        const float al = __builtin_amdgcn_exp2f(m_run[i] - mn);
+        const float p0 = __builtin_amdgcn_exp2f(z0 - mn), p1 = __builtin_amdgcn_exp2f(z1 - mn);
+        l_run[i] = l_run[i] * al + (p0 + p1);
+        m_run[i] = mn;
+#pragma unroll
+        for (int mm = 0; mm < 8; mm++) o[mm][i] *= al;
+        const bool hv = h < G;
+        const int row = 4 * (lane >> 4) + i;
+        ph[row * (2 * kPtRow) + (lane & 15)] = hv ? (_Float16)p0 : (_Float16)0.f;
+        ph[row * (2 * kPtRow) + 16 + (lane & 15)] = hv ? (_Float16)p1 : (_Float16)0.f;
+    }
+    wave_lds_sync();
+    // A = P rows (query heads) x 32 tokens, B = V 32 tokens x 16 dims
+    const uint4 pa = *reinterpret_cast<const uint4*>(pt + (lane & 15) * kPtRow + 4 * (lane >> 4));
+    const h8_t pA = __builtin_bit_cast(h8_t, pa);
+#pragma unroll
+    for (int mm = 0; mm < 8; mm++) {
+        const uint32_t* vr = vt + (16 * mm + (lane & 15)) * kVtRow + 4 * (lane >> 4);
+        const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+        const uint2 hi = *reinterpret_cast<const uint2*>(vr + 2);
+        o[mm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pA, as_h8(lo.x, lo.y, hi.x, hi.y), o[mm], 0, 0, 0);
+    }
+    wave_lds_sync();
+}
+
+// one prefix tile from its registers (rb0: resident block of the tile's first token)
+template <int HPL>
+__device__ __forceinline__ void prefix_tile(const AttnArgs& A, const TileRaw& d, int64_t rb0, int64_t t0, int64_t T,
+                                            int lane, const h8_t qa[4], uint32_t* vt, uint32_t* pt,
+                                            float m_run[HPL], float l_run[HPL], f4_t o[8]) {
+    // dequant multipliers (s / 2 per token); the packed-multiply path is
+    // taken when every scale of the tile allows it (wave-uniform)
+    bool e0, e1, e2;
+    const uint32_t mk0 = half_scales((d.ks & 0xffffu) * 0x10001u, &e0);
+    const uint32_t mk1 = half_scales((d.ks >> 16) * 0x10001u, &e1);
+    const uint32_t mv = half_scales(d.vs, &e2);
+    const bool fast = __all(e0 && e1 && e2);
+    f4_t s[2];
+    bool valid[2];
+#pragma unroll
+    for (int x = 0; x < 2; x++) {
+        s[x] = f4_t{0.f, 0.f, 0.f, 0.f};
+        valid[x] = t0 + 16 * x + (lane & 15) < T;
+        if (t0 + 16 * x < T) {   // wave-uniform
+            h8_t kb[4];
+            tile_k(A, d, rb0 + x, x, lane, fast, x ? mk1 : mk0, kb);
+#pragma unroll
+            for (int c = 0; c < 4; c++) s[x] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], kb[c], s[x], 0, 0, 0);
+        }
+    }
+    tile_v(A, d, rb0, lane, fast, mv, vt);
+    tile_softmax_pv<HPL>(A.group, s, valid, lane, vt, pt, m_run, l_run, o);
+}
+
+// The wave's prefix tiles, records loaded one tile ahead (two register sets,
+// no copies).  Tiles are dealt round-robin over all waves of the kv head (wave
+// gw of W takes tiles gw, gw + W, ...): the waves in flight read one
+// contiguous stretch of the prefix at a time instead of W strided ones.
+template <int HPL>
+__device__ __forceinline__ void prefix_tiles(const AttnArgs& A, int64_t kvh, int64_t gw, int64_t W, int64_t T,
+                                             int lane, const h8_t qa[4], uint32_t* vt, uint32_t* pt, float m_run[HPL],
+                                             float l_run[HPL], f4_t o[8]) {
+    const int64_t step = W * kTile;
+    int64_t ta = gw * kTile;
+    if (ta >= T) return;
+    const int64_t hb = kvh * A.k.cap_blocks;
+    TileRaw d0, d1;
+    tile_load(A, kvh, ta, T, lane, d0);
+    while (true) {
+        const int64_t tb = ta + step;
+        if (tb < T) tile_load(A, kvh, tb, T, lane, d1);
+        prefix_tile<HPL>(A, d0, hb + ta / kRB, ta, T, lane, qa, vt, pt, m_run, l_run, o);
+        if (tb >= T) break;
+        const int64_t tc = tb + step;
+        if (tc < T) tile_load(A, kvh, tc, T, lane, d0);
+        prefix_tile<HPL>(A, d1, hb + tb / kRB, tb, T, lane, qa, vt, pt, m_run, l_run, o);
+        if (tc >= T) break;
+        ta = tc;
+    }
+}
+
+// The tail tiles of this wave: tile indices continue after the prefix's in
+// the same round-robin (g = prefix tiles + tail tile), fp16 K / V read directly.
+template <int HPL>
+__device__ __forceinline__ void tail_tiles(const AttnArgs& A, int64_t kvh, int64_t gw, int64_t W, int64_t npt,
+                                           int64_t T, int lane, const h8_t qa[4], uint32_t* vt, uint32_t* pt,
+                                           float m_run[HPL], float l_run[HPL], f4_t o[8]) {
+    int64_t g = gw;
+    if (g < npt) g += (npt - g + W - 1) / W * W;   // first index of this wave past the prefix
+    for (; (g - npt) * kTile < T; g += W) {
+        const int64_t t0 = (g - npt) * kTile;
+        f4_t s[2];
+        bool valid[2];
+#pragma unroll
+        for (int x = 0; x < 2; x++) {
+            s[x] = f4_t{0.f, 0.f, 0.f, 0.f};
+            valid[x] = t0 + 16 * x + (lane & 15) < T;
+            if (t0 + 16 * x < T) {
+                h8_t kb[4];
+                tail_k(A, kvh, t0 + 16 * x, T, lane, kb);
+#pragma unroll
+                for (int c = 0; c < 4; c++) s[x] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], kb[c], s[x], 0, 0, 0);
+            }
+        }
+        tail_v(A, kvh, t0, T, lane, vt);
+        tile_softmax_pv<HPL>(A.group, s, valid, lane, vt, pt, m_run, l_run, o);
+    }
+}
+
+template <int HPL>
+__global__ __launch_bounds__(kAW * 64) void k_res_attn(AttnArgs A) {
+    __shared__ __align__(16) uint32_t s_vt[kAW][kHd * kVtRow];
+    __shared__ __align__(16) uint32_t s_pt[kAW][16 * kPtRow];
+    __shared__ float s_m[kAW][16], s_l[kAW][16];
+    __shared__ float s_L[16];
+    __shared__ int s_last;
+    // the wave index is made wave-uniform explicitly so that all tile control
+    // flow stays scalar (no exec-masked paths around in-flight loads)
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int G = A.group;
+    // one split = kAW waves; the kv head's waves share its prefix tiles and
+    // then its tail tiles round-robin
+    const int nsp = A.nsp;
+    const int64_t kvh = (int64_t)blockIdx.x / nsp;
+    const int sp = (int)((int64_t)blockIdx.x % nsp);
+    const int64_t gw = (int64_t)sp * kAW + wave, W = (int64_t)nsp * kAW;
+    const int64_t npt = (A.t_prefix + kTile - 1) / kTile;
+
+    // Q fragments: row m of the A operand is query head 4 (m % 4) + m / 4
+    h8_t qa[4];
+    {
+        const int m = lane & 15, h = 4 * (m & 3) + (m >> 2);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            uint4 w = make_uint4(0u, 0u, 0u, 0u);
+            if (h < G) w = *reinterpret_cast<const uint4*>(A.q + (kvh * G + h) * kHd + 32 * c + 8 * (lane >> 4));
+            qa[c] = __builtin_bit_cast(h8_t, w);
+        }
+    }
+    uint32_t* vt = s_vt[wave];
+    uint32_t* pt = s_pt[wave];
+    for (int i = lane; i < 16 * kPtRow; i += 64) pt[i] = 0u;
+    wave_lds_sync();
+    float m_run[HPL], l_run[HPL];
+    f4_t o[8];
+#pragma unroll
+    for (int i = 0; i < HPL; i++) { m_run[i] = -INFINITY; l_run[i] = 0.f; }
+#pragma unroll
+    for (int mm = 0; mm < 8; mm++) o[mm] = f4_t{0.f, 0.f, 0.f, 0.f};
+    if (A.t_prefix > 0) prefix_tiles<HPL>(A, kvh, gw, W, A.t_prefix, lane, qa, vt, pt, m_run, l_run, o);
+    if (A.t_tail > 0) tail_tiles<HPL>(A, kvh, gw, W, npt, A.t_tail, lane, qa, vt, pt, m_run, l_run, o);
+
+    // ---- merge the four waves (LDS), one record per query head
+    __syncthreads();
+    float* wo = reinterpret_cast<float*>(&s_vt[0][0]);   // [wave][16 heads][128]
+#pragma unroll
+    for (int i = 0; i < HPL; i++) {
+        const int h = (lane >> 4) + 4 * i;
+        const float l = row16_sum(l_run[i]);
+        if (h < G) {
+            if ((lane & 15) == 0) { s_m[wave][h] = m_run[i]; s_l[wave][h] = l; }
+#pragma unroll
+            for (int mm = 0; mm < 8; mm++) wo[(wave * 16 + h) * kHd + 16 * mm + (lane & 15)] = o[mm][i];
+        }
+    }
+    __syncthreads();
+    // Records cross workgroups (and the XCDs' separate L2s): they are written
+    // with device-scope stores (written through to the coherent level), which
+    // complete before the counter increment, and read back with device-scope
+    // loads.  No device-wide fence (an L2 write-back per workgroup) is needed.
+    float* rec = A.rec + ((int64_t)kvh * nsp + sp) * G * kRecF;
+    for (int idx = tid; idx < G * kHd; idx += kAW * 64) {
+        const int h = idx / kHd, d = idx % kHd;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kAW; w++) M = fmaxf(M, s_m[w][h]);
+        float L = 0.f, Ov = 0.f;
+#pragma unroll
+        for (int w = 0; w < kAW; w++) {
+            const float f = s_m[w][h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s_m[w][h] - M);
+            L += s_l[w][h] * f;
+            Ov += wo[(w * 16 + h) * kHd + d] * f;
+        }
+        __hip_atomic_store(rec + h * kRecF + 4 + d, Ov, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (d == 0) {
+            __hip_atomic_store(rec + h * kRecF, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(rec + h * kRecF + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // this thread's record stores have completed
+    __syncthreads();
+    uint32_t* ctr = A.counter + kvh * kCtrStride;
+    if (tid == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = old == (uint32_t)(nsp - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    // ---- the last workgroup of this kv head merges every split: each thread
+    // issues all its loads in one batch (latency, not bandwidth, bounds this)
+    const float* r0 = A.rec + (int64_t)kvh * nsp * G * kRecF;
+    float* s_cm = reinterpret_cast<float*>(&s_vt[0][0]);
+    float* s_cf = s_cm + kMaxRec;
+    float* s_cl = s_cf + kMaxRec;
+    const int ne = nsp * G;
+    constexpr int kMU = 40;                   // o values in flight per thread
+    float ov[kMU];
+    const int h0 = tid / kHd, d0 = tid % kHd;   // first output of this thread
+    for (int i = tid; i < ne; i += kAW * 64) {
+        s_cm[i] = __hip_atomic_load(r0 + (int64_t)i * kRecF, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_cl[i] = __hip_atomic_load(r0 + (int64_t)i * kRecF + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (h0 < G) {
+#pragma unroll
+        for (int k = 0; k < kMU; k++)
+            ov[k] = k < nsp ? __hip_atomic_load(r0 + (int64_t)(k * G + h0) * kRecF + 4 + d0, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT)
+                            : 0.f;
+    }
+    __syncthreads();
+    for (int h = wave; h < G; h += kAW) {
+        float M = -INFINITY;
+        for (int p = lane; p < nsp; p += 64) M = fmaxf(M, s_cm[p * G + h]);
+        for (int o2 = 32; o2 > 0; o2 >>= 1) M = fmaxf(M, __shfl_xor(M, o2, 64));
+        float L = 0.f;
+        for (int p = lane; p < nsp; p += 64) {
+            const float mp = s_cm[p * G + h];
+            const float f = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - M);
+            s_cf[p * G + h] = f;
+            L += f * s_cl[p * G + h];
+        }
+        for (int o2 = 32; o2 > 0; o2 >>= 1) L += __shfl_xor(L, o2, 64);
+        if (lane == 0) s_L[h] = L;
+    }
+    __syncthreads();
+    for (int idx = tid; idx < G * kHd; idx += kAW * 64) {
+        const int h = idx / kHd, d = idx % kHd;
+        float acc = 0.f;
+        if (idx == tid) {   // first output: its first kMU splits are in registers
+#pragma unroll
+            for (int k = 0; k < kMU; k++) acc += k < nsp ? ov[k] * s_cf[k * G + h] : 0.f;
+        } else {
+            for (int k = 0; k < kMU && k < nsp; k++)
+                acc += __hip_atomic_load(r0 + (int64_t)(k * G + h) * kRecF + 4 + d, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT) * s_cf[k * G + h];
+        }
+        for (int k = kMU; k < nsp; k++)
+            acc += __hip_atomic_load(r0 + (int64_t)(k * G + h) * kRecF + 4 + d, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT) * s_cf[k * G + h];
+        A.out[(kvh * G + h) * kHd + d] = f2h(acc / s_L[h]);
+    }
+    if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Splits (workgroups) per kv head: enough for the prefix at kWaveTiles tiles
+// per wave, more when that leaves the 256 CUs idle (down to one tile per
+// wave); the tail's tiles ride along (a wave may take a few more).
+int64_t n_splits(int64_t n_heads, int group, int64_t t_prefix, int64_t t_tail) {
+    const int64_t np = (t_prefix + kTile - 1) / kTile, nt = (t_tail + kTile - 1) / kTile;
+    const int64_t tiles = np > 0 ? np : nt;
+    int64_t n = (tiles + (int64_t)kAW * kWaveTiles - 1) / ((int64_t)kAW * kWaveTiles);
+    int64_t fill = (256 + n_heads - 1) / n_heads;
+    const int64_t most = (tiles + kAW - 1) / kAW;
+    if (fill > kMaxRec / group) fill = kMaxRec / group;   // the merge stages nsp * group records
+    if (n < fill) n = fill < most ? fill : most;
+    return n > 0 ? n : 1;
+}
+
+bool res_ok(const lq_resident* r) {
+    return r && r->a && r->b && r->mask && r->meta && r->scale && r->n_exc && r->status && r->n_heads > 0 &&
+           r->cap_blocks > 0 && r->exc_cap >= 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t lq_resident_workspace(int64_t n_heads, int64_t t_tokens) {
+    if (n_heads <= 0 || t_tokens <= 0 || t_tokens % kRB) return -1;
+    return n_heads * (t_tokens / kRB) * (int64_t)sizeof(uint32_t);
+}
+
+int lq_resident_quantize(const void* d_x, int dtype, int64_t n_heads, int64_t t_tokens, const float* d_scale32,
+                         const uint16_t* d_scale16, const lq_resident* r, int64_t h0, int64_t blk0, void* d_work,
+                         hipStream_t s) {
+    if (!d_x || !d_scale32 || !d_scale16 || !res_ok(r) || !d_work || dtype < 0 || dtype > 2 || n_heads <= 0 ||
+        t_tokens <= 0 || t_tokens % kRB || h0 < 0 || blk0 < 0)
+        return LQ_ERR_ARG;
+    const int64_t nb = t_tokens / kRB;
+    if (h0 + n_heads > r->n_heads || blk0 + nb > r->cap_blocks || nb > INT_MAX || n_heads > 65535) return LQ_ERR_ARG;
+    uint32_t* cnt = static_cast<uint32_t*>(d_work);
+    const dim3 grid((unsigned)nb, (unsigned)n_heads);
+    hipLaunchKernelGGL(k_res_quant, grid, dim3(256), 0, s, d_x, dtype, t_tokens, d_scale32, d_scale16, *r, h0, blk0,
+                       cnt);
+    hipLaunchKernelGGL(k_res_scan, dim3(1), dim3(256), 0, s, cnt, nb, n_heads, *r, h0, blk0);
+    hipLaunchKernelGGL(k_res_fill, grid, dim3(256), 0, s, d_x, dtype, t_tokens, d_scale32, *r, h0, blk0);
+    return launch_status();
+}
+
+int lq_resident_dequant(const lq_resident* r, int64_t h0, int64_t n_heads, int64_t blk0, int64_t n_blocks,
+                        void* d_out, int out_dtype, hipStream_t s) {
+    if (!res_ok(r) || !d_out || out_dtype < 0 || out_dtype > 2 || h0 < 0 || n_heads <= 0 || blk0 < 0 ||
+        n_blocks <= 0 || h0 + n_heads > r->n_heads || blk0 + n_blocks > r->cap_blocks || n_heads > 65535 ||
+        n_blocks > INT_MAX)
+        return LQ_ERR_ARG;
+    hipLaunchKernelGGL(k_res_dequant, dim3((unsigned)n_blocks, (unsigned)n_heads), dim3(256), 0, s, *r, h0, blk0,
+                       n_blocks, d_out, out_dtype);
+    return launch_status();
+}
+
+int64_t lq_resident_attn_workspace(int64_t n_heads, int group, int64_t t_prefix, int64_t t_tail) {
+    if (n_heads <= 0 || group < 1 || group > 16 || t_prefix < 0 || t_tail < 0 || t_prefix + t_tail <= 0) return -1;
+    const int64_t nsp = n_splits(n_heads, group, t_prefix, t_tail);
+    if (nsp * group > kMaxRec) return -1;
+    const int64_t counters = n_heads * kCtrStride * 4;
+    return counters + n_heads * nsp * group * kRecF * (int64_t)sizeof(float);
+}
+
+int lq_resident_attention(const lq_resident* k, const lq_resident* v, int64_t t_prefix, const uint16_t* d_q,
+                          int group, const uint16_t* d_tail_k, const uint16_t* d_tail_v, int64_t t_tail,
+                          void* d_work, uint16_t* d_out, hipStream_t s) {
+    if (!d_q || !d_out || !d_work || group < 1 || group > 16 || t_prefix < 0 || t_tail < 0 ||
+        t_prefix + t_tail <= 0 || t_prefix % kRB)
+        return LQ_ERR_ARG;
+    if (t_tail > 0 && (!d_tail_k || !d_tail_v)) return LQ_ERR_ARG;
+    if (t_prefix > 0 && (!res_ok(k) || !res_ok(v) || k->n_heads != v->n_heads || k->cap_blocks != v->cap_blocks ||
+                         t_prefix / kRB > k->cap_blocks ||
+                         t_prefix / kRB > v->cap_blocks))
+        return LQ_ERR_ARG;
+    int64_t n_heads = t_prefix > 0 ? k->n_heads : -1;
+    if (n_heads <= 0) {
+        if (!k || k->n_heads <= 0) return LQ_ERR_ARG;
+        n_heads = k->n_heads;
+    }
+    AttnArgs A{};
+    if (t_prefix > 0) { A.k = *k; A.v = *v; }
+    A.t_prefix = t_prefix;
+    A.t_tail = t_tail;
+    A.q = d_q;
+    A.tail_k = d_tail_k;
+    A.tail_v = d_tail_v;
+    A.group = group;
+    A.nsp = (int)n_splits(n_heads, group, t_prefix, t_tail);
+    const int64_t counters = n_heads * kCtrStride * 4;
+    A.counter = static_cast<uint32_t*>(d_work);
+    A.rec = reinterpret_cast<float*>(static_cast<char*>(d_work) + counters);
+    A.out = d_out;
+    const int64_t grid = n_heads * A.nsp;
+    if (grid > INT_MAX || (int64_t)A.nsp * group > kMaxRec) return LQ_ERR_ARG;
+    const int hpl = (group + 3) / 4;
+    switch (hpl) {
+        case 1: hipLaunchKernelGGL(k_res_attn<1>, dim3((unsigned)grid), dim3(kAW * 64), 0, s, A); break;
+        case 2: hipLaunchKernelGGL(k_res_attn<2>, dim3((unsigned)grid), dim3(kAW * 64), 0, s, A); break;
+        case 3: hipLaunchKernelGGL(k_res_attn<3>, dim3((unsigned)grid), dim3(kAW * 64), 0, s, A); break;
+        default: hipLaunchKernelGGL(k_res_attn<4>, dim3((unsigned)grid), dim3(kAW * 64), 0, s, A); break;
+    }
+    return launch_status();
+}
+
+}  // extern "C"
