@@ -239,7 +239,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--group", type=int, default=64, help="chunks per kernel launch")
+    ap.add_argument("--group", type=int, default=32, help="chunks per kernel launch in the timed step")
+    ap.add_argument("--streams", type=int, default=2,
+                    help="streams the chunk groups of a step are dealt to (their kernels overlap on the GPU)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-chunks", type=int, default=8)
     ap.add_argument("--no-decode-step", action="store_true", help="skip the C3 decode-step measurement")
@@ -276,7 +278,9 @@ def main():
     bound = codec.words_bound(G, V)
     arenas = [torch.empty(bound, dtype=torch.int32, device=dev) for _ in groups]
     out = torch.empty_like(x)
-    luts = torch.empty(G * L.LQ_STREAMS * L.LQ_L, dtype=torch.int32, device=dev)
+    NS = max(1, args.streams)
+    streams = [torch.cuda.Stream(device=dev) for _ in range(NS)]   # default priority
+    luts = [torch.empty(G * L.LQ_STREAMS * L.LQ_L, dtype=torch.int32, device=dev) for _ in range(NS)]
     encs = [None] * len(groups)
 
     def write():
@@ -285,11 +289,24 @@ def main():
 
     def read():
         for gi, (a, b) in enumerate(groups):
-            codec.decode_batch(encs[gi], out=out[a:b], lut_work=luts)
+            codec.decode_batch(encs[gi], out=out[a:b], lut_work=luts[0])
+
+    def step():
+        """Write then read every chunk group; group gi runs on stream gi % NS, so
+        one group's memory-bound kernels (scales, bitstream assembly) overlap
+        another's instruction-bound ones (quantizer, encoder, decoder)."""
+        cur = torch.cuda.current_stream(dev)
+        for st in streams:
+            st.wait_stream(cur)
+        for gi, (a, b) in enumerate(groups):
+            with torch.cuda.stream(streams[gi % NS]):
+                encs[gi], _ = codec.encode_batch(x[a:b], BITS, exact_size=False, words_out=arenas[gi], wide=False)
+                codec.decode_batch(encs[gi], out=out[a:b], lut_work=luts[gi % NS])
+        for st in streams:
+            cur.wait_stream(st)
 
     for _ in range(args.warmup):
-        write()
-        read()
+        step()
     torch.cuda.synchronize()
     # separate write / read timing (outside the headline loop)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
@@ -302,8 +319,7 @@ def main():
     e0 = torch.cuda.Event(enable_timing=True); e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(args.steps):
-        write()
-        read()
+        step()
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -330,26 +346,30 @@ def main():
     # rooflines of the two largest kernels, each timed per launch with events on
     # its own stream: k_chunk_quantize (write) and k_chunk_decode (read, with
     # its k_chunk_lut table build); the longer one is the headline roofline
+    # (measured on single launches over all 64 chunks, outside the step)
+    rgroups = [(0, C)]
+    renc = [codec.encode_batch(x, BITS, exact_size=False, wide=False)[0]]
+    rluts = torch.empty(C * L.LQ_STREAMS * L.LQ_L, dtype=torch.int32, device=dev)
     dec_ms, q_ms = [], []
-    for gi, (a, b) in enumerate(groups):
+    for gi, (a, b) in enumerate(rgroups):
         s0 = torch.cuda.Event(enable_timing=True); s1 = torch.cuda.Event(enable_timing=True)
         gpu_busy()
-        s0.record(); codec.decode_batch(encs[gi], out=out[a:b], lut_work=luts); s1.record()
+        s0.record(); codec.decode_batch(renc[gi], out=out[a:b], lut_work=rluts); s1.record()
         torch.cuda.synchronize()
         dec_ms.append(s0.elapsed_time(s1))
-        q_ms.append(time_quantize(x[a:b], encs[gi]))
+        q_ms.append(time_quantize(x[a:b], renc[gi]))
     # algorithmic bytes: decode reads the stored chunk and writes 16 B of fp16 per
     # vector; the quantizer reads 16 B of fp16 and writes 8 B of int8 symbols and
     # one coset bit per vector
-    dec_bytes = float(np.mean([2 * (b - a) * V * 8 + int(encs[gi].reference_bytes().sum() + encs[gi].side_bytes().sum())
-                               for gi, (a, b) in enumerate(groups)]))
-    q_bytes = float(np.mean([(b - a) * V * (16 + 8) + (b - a) * V // 8 for a, b in groups]))
+    dec_bytes = float(np.mean([2 * (b - a) * V * 8 + int(renc[gi].reference_bytes().sum() + renc[gi].side_bytes().sum())
+                               for gi, (a, b) in enumerate(rgroups)]))
+    q_bytes = float(np.mean([(b - a) * V * (16 + 8) + (b - a) * V // 8 for a, b in rgroups]))
     traffic = load_traffic()
     kern = {
         "k_chunk_decode": {"ms": float(np.mean(dec_ms)), "bytes": dec_bytes,
-                           "desc": f"k_chunk_decode (+k_chunk_lut), {G}-chunk launch, algorithmic bytes = stored chunk + 16 B fp16 out per vector"},
+                           "desc": f"k_chunk_decode (+k_chunk_lut), {C}-chunk launch, algorithmic bytes = stored chunk + 16 B fp16 out per vector"},
         "k_chunk_quantize": {"ms": float(np.mean(q_ms)), "bytes": q_bytes,
-                             "desc": f"k_chunk_quantize, {G}-chunk launch, algorithmic bytes = 16 B fp16 in + 8 B int8 symbols + 1 coset bit per vector"},
+                             "desc": f"k_chunk_quantize, {C}-chunk launch, algorithmic bytes = 16 B fp16 in + 8 B int8 symbols + 1 coset bit per vector"},
     }
     roof = {}
     for name, k in kern.items():
@@ -378,7 +398,7 @@ def main():
         "vs_baseline": None, "dtype": "f32 quantize / u32 rANS (fp16 in, fp16 out)", "data": "synthetic",
         "config": {"workload": "C2: Llama-3.1-8B KV cache write+read, 32 layers x K,V x [1,8,8192,128] fp16, "
                                "N(0,1) + 4 outlier channels x10 per head, 4 bits/dim, one chunk per layer/K-V",
-                   "chunks": C, "group": G, "bits_per_dim": BITS},
+                   "chunks": C, "group": G, "streams": NS, "bits_per_dim": BITS},
         "write_ms": round(t_write_ms, 4), "read_ms": round(t_read_ms, 4),
         "write_GBps": round((2 * D + Cb) / (t_write_ms * 1e-3) / 1e9, 2),
         "read_GBps": round((2 * D + Cb) / (t_read_ms * 1e-3) / 1e9, 2),

@@ -89,13 +89,40 @@ __global__ void k_head_sumsq(const void* __restrict__ x, int dtype, int64_t vec_
     int p = blockIdx.y;
     int64_t per = (vec_per_head + parts - 1) / parts;
     int64_t v0 = (int64_t)p * per, v1 = v0 + per < vec_per_head ? v0 + per : vec_per_head;
-    double acc = 0.0;
-    for (int64_t v = v0 + threadIdx.x; v < v1; v += blockDim.x) {
-        float xv[8];
-        load8(x, dtype, h * vec_per_head + v, xv);
+    // Per vector: the 8 squares (exact in fp32 for fp16 / bf16 inputs) summed
+    // in fp32 by a chain of FMAs, then accumulated in fp64; four independent
+    // loads in flight per thread per step, four accumulators.
+    double acc4[4] = {0.0, 0.0, 0.0, 0.0};
+    const int64_t bd = blockDim.x;
+    int64_t v = v0 + threadIdx.x;
+    auto sq8 = [](const float xv[8]) {
+        float a = xv[0] * xv[0];
 #pragma unroll
-        for (int i = 0; i < 8; i++) acc += (double)xv[i] * (double)xv[i];
+        for (int i = 1; i < 8; i++) a = __builtin_fmaf(xv[i], xv[i], a);
+        return (double)a;
+    };
+    if (dtype == LQ_F32) {   // fp32 squares are not exact: keep every product in fp64
+        for (; v < v1; v += bd) {
+            float xv[8];
+            load8(x, dtype, h * vec_per_head + v, xv);
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc4[0] += (double)xv[i] * (double)xv[i];
+        }
+    } else {
+        for (; v + 3 * bd < v1; v += 4 * bd) {
+            float xv[4][8];
+#pragma unroll
+            for (int u = 0; u < 4; u++) load8(x, dtype, h * vec_per_head + v + u * bd, xv[u]);
+#pragma unroll
+            for (int u = 0; u < 4; u++) acc4[u] += sq8(xv[u]);
+        }
+        for (; v < v1; v += bd) {
+            float xv[8];
+            load8(x, dtype, h * vec_per_head + v, xv);
+            acc4[0] += sq8(xv);
+        }
     }
+    const double acc = (acc4[0] + acc4[1]) + (acc4[2] + acc4[3]);
     __shared__ double red[256];
     red[threadIdx.x] = acc;
     __syncthreads();
