@@ -385,3 +385,198 @@ def chunk_streams_host(enc: EncodedBatch, c: int):
                         words=words[w0:w0 + (nb + 31) // 32 + 1].copy(), state=int(state[sid]), n_bits=nb,
                         word_offset=w0, status=stt))
     return res
+
+
+# ------------------------------------------------------------ wire format --
+#
+# A self-describing, versioned byte form of an EncodedBatch for offload and
+# restore (the reference has no serialisation of its chunks).  Layout, all
+# little-endian:
+#
+#   b"LQE8RANS" | u32 version | u32 header bytes | header (UTF-8 JSON) |
+#   payload (the fields in header order, each padded to 8 bytes) | u32 CRC-32
+#
+# The CRC covers every byte before it.  Per chunk the payload holds what
+# decoding needs and nothing of the write path: the reference's merged
+# bitstream words, coset bitmap and fp16 scales (its accounting,
+# llm/compressed_kv_cache.py:113-119), then the compact tables (lo, n_sym,
+# n_symbols, status + one uint16 frequency per symbol; cumulative
+# frequencies and renormalisation shifts are rebuilt on load), the block
+# checkpoints of present streams (uint32 bit offset + uint16 state), the
+# per-block coset-1 counts (uint16) and the stream metadata.
+
+WIRE_MAGIC = b"LQE8RANS"
+WIRE_VERSION = 1
+
+
+class WireFormatError(ValueError):
+    """A byte string that is not a valid serialised EncodedBatch."""
+
+
+def _table_heads(enc: EncodedBatch) -> np.ndarray:
+    t = enc.tables.view(torch.int32).view(-1, L.TABLE_BYTES // 4).cpu().numpy()
+    return t
+
+
+def to_bytes(enc: EncodedBatch) -> bytes:
+    """Serialise an EncodedBatch (one device-to-host copy per field)."""
+    import json
+    import zlib
+    C, S, nb = enc.n_chunks, L.LQ_STREAMS, enc.nblk
+    t = _table_heads(enc)
+    heads = np.ascontiguousarray(t[:, :4]).astype(np.int32)
+    nsym = heads[:, 1].astype(np.int64)
+    present = nsym > 0
+    freqs = np.concatenate([(t[i, 4:4 + nsym[i]].view(np.uint32) & 0x7FF).astype(np.uint16) for i in range(C * S)]
+                           or [np.zeros(0, np.uint16)])
+    cw = enc.chunk_words.cpu().numpy().astype(np.int64)
+    cb = enc.chunk_base.cpu().numpy().astype(np.int64)
+    wall = enc.words.cpu().numpy().view(np.uint32)
+    words = np.concatenate([wall[cb[c]:cb[c] + cw[c]] for c in range(C)] or [np.zeros(0, np.uint32)])
+    off = enc.blk_off.cpu().numpy().view(np.uint32).reshape(C * S, nb)[present]
+    st = enc.blk_state.cpu().numpy().view(np.uint16).reshape(C * S, nb)[present]
+    fields = [
+        ("bits", enc.bits.cpu().numpy().astype(np.int32)),
+        ("status", enc.status.cpu().numpy().astype(np.int32)),
+        ("scale32", enc.scale32.cpu().numpy().astype(np.float32)),
+        ("scale16", enc.scale16.cpu().numpy().astype(np.float16)),
+        ("chunk_words", cw),
+        ("words", words),
+        ("stream_nbits", enc.stream_nbits.cpu().numpy().astype(np.int64)),
+        ("stream_state", enc.stream_state.cpu().numpy().astype(np.int32)),
+        ("stream_woff", enc.stream_woff.cpu().numpy().astype(np.int64)),
+        ("table_heads", heads.reshape(-1)),
+        ("table_freqs", freqs),
+        ("coset_bits", enc.coset_bits.cpu().numpy().astype(np.uint8).reshape(-1)),
+        ("blk_n1", enc.blk_n1.cpu().numpy().astype(np.uint16).reshape(-1)),
+        ("blk_off", off.reshape(-1)),
+        ("blk_state", st.reshape(-1)),
+    ]
+    if enc.sigma2 is not None:
+        fields.append(("sigma2", enc.sigma2.cpu().numpy().astype(np.float32)))
+    extra = {}
+    ds = enc.extra.get("dither_seed")
+    if ds is not None:
+        fields.append(("dither_seed", ds.cpu().numpy().astype(np.int64)))
+    if "rht" in enc.extra:
+        layers, kvs = enc.extra["rht"]
+        extra["rht"] = [[int(v) for v in layers], [int(v) for v in kvs]]
+    header = {"n_chunks": C, "n_heads": enc.n_heads, "bph": enc.bph, "shape": [int(v) for v in enc.shape],
+              "fields": [[n, a.dtype.str, int(a.size)] for n, a in fields], "extra": extra}
+    hb = json.dumps(header, separators=(",", ":")).encode()
+    parts = [WIRE_MAGIC, np.uint32(WIRE_VERSION).tobytes(), np.uint32(len(hb)).tobytes(), hb]
+    pos = sum(len(p) for p in parts)
+    for _, a in fields:
+        pad = (-pos) % 8
+        parts.append(b"\0" * pad)
+        b = np.ascontiguousarray(a).tobytes()
+        parts.append(b)
+        pos += pad + len(b)
+    body = b"".join(parts)
+    return body + np.uint32(zlib.crc32(body) & 0xFFFFFFFF).tobytes()
+
+
+def from_bytes(buf, device=None) -> EncodedBatch:
+    """Restore an EncodedBatch on `device` (default: the current CUDA device).
+    Raises WireFormatError on a bad magic, version, checksum or layout."""
+    import json
+    import zlib
+    mv = memoryview(buf)
+    if len(mv) < 20 or bytes(mv[:8]) != WIRE_MAGIC:
+        raise WireFormatError("not an LQE8RANS chunk batch")
+    version = int(np.frombuffer(mv[8:12], np.uint32)[0])
+    if version != WIRE_VERSION:
+        raise WireFormatError(f"unsupported wire format version {version} (this build reads {WIRE_VERSION})")
+    crc = int(np.frombuffer(mv[len(mv) - 4:], np.uint32)[0])
+    if zlib.crc32(mv[:len(mv) - 4]) & 0xFFFFFFFF != crc:
+        raise WireFormatError("checksum mismatch: the chunk batch is corrupted")
+    hl = int(np.frombuffer(mv[12:16], np.uint32)[0])
+    try:
+        header = json.loads(bytes(mv[16:16 + hl]).decode())
+        C, nh, bph = int(header["n_chunks"]), int(header["n_heads"]), int(header["bph"])
+        shape = tuple(int(v) for v in header["shape"])
+    except (ValueError, KeyError, TypeError) as e:
+        raise WireFormatError(f"bad header: {e}") from None
+    pos = 16 + hl
+    end = len(mv) - 4
+    arrs = {}
+    for name, dts, n in header["fields"]:
+        pos += (-pos) % 8
+        dt = np.dtype(dts)
+        nbytes = dt.itemsize * int(n)
+        if pos + nbytes > end:
+            raise WireFormatError(f"truncated field {name}")
+        arrs[name] = np.frombuffer(mv[pos:pos + nbytes], dt).copy()
+        pos += nbytes
+    S = L.LQ_STREAMS
+    nv = nh * bph
+    nb = (nv + L.LQ_BLK - 1) // L.LQ_BLK
+    heads = arrs["table_heads"].reshape(C * S, 4)
+    nsym = heads[:, 1].astype(np.int64)
+    if heads.shape[0] != C * S or arrs["table_freqs"].size != int(nsym.sum()) or np.any(nsym > L.LQ_MAXSYM):
+        raise WireFormatError("inconsistent tables")
+    # rebuild the device tables: enc[j] = f | cum << 11 | (11 - bitlen(f)) << 21
+    tab = np.zeros((C * S, L.TABLE_BYTES // 4), np.uint32)
+    tab[:, :4] = heads.view(np.uint32)
+    f_all = arrs["table_freqs"].astype(np.uint32)
+    o = 0
+    for i in range(C * S):
+        k = int(nsym[i])
+        if k:
+            f = f_all[o:o + k]
+            if np.any(f == 0) or int(f.sum()) != L.LQ_L:
+                raise WireFormatError("table frequencies do not sum to L")
+            cum = np.cumsum(f) - f
+            bl = np.frexp(f.astype(np.float64))[1].astype(np.uint32)   # bit length of f
+            tab[i, 4:4 + k] = f | (cum.astype(np.uint32) << 11) | ((11 - bl) << 21)
+        o += k
+    present = nsym > 0
+    npres = int(present.sum())
+    off = np.zeros((C * S, nb), np.uint32)
+    st = np.full((C * S, nb), L.LQ_L, np.uint16)
+    if arrs["blk_off"].size != npres * nb or arrs["blk_state"].size != npres * nb:
+        raise WireFormatError("inconsistent checkpoints")
+    off[present] = arrs["blk_off"].reshape(npres, nb)
+    st[present] = arrs["blk_state"].reshape(npres, nb)
+    cw = arrs["chunk_words"].astype(np.int64)
+    if arrs["words"].size != int(cw.sum()):
+        raise WireFormatError("inconsistent bitstream length")
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+
+    def T(a, dt):
+        return torch.from_numpy(np.ascontiguousarray(a)).to(dt).to(dev)
+
+    words = np.concatenate([arrs["words"], np.zeros(2, np.uint32)])   # decoder read-ahead slack
+    enc = EncodedBatch(
+        n_chunks=C, n_heads=nh, bph=bph, shape=shape, bits=T(arrs["bits"], torch.int32),
+        scale32=T(arrs["scale32"], torch.float32), scale16=T(arrs["scale16"], torch.float16),
+        sigma2=T(arrs["sigma2"], torch.float32) if "sigma2" in arrs else None,
+        coset_bits=T(arrs["coset_bits"].reshape(C, -1), torch.uint8),
+        blk_n1=T(arrs["blk_n1"].astype(np.int32).reshape(C, nb), torch.int32),
+        tables=torch.from_numpy(tab.view(np.uint8).reshape(-1).copy()).to(dev),
+        blk_off=torch.from_numpy(off.view(np.int32).reshape(-1).copy()).to(dev),
+        blk_state=torch.from_numpy(st.view(np.int16).reshape(-1).copy()).to(dev),
+        stream_nbits=T(arrs["stream_nbits"], torch.int64), stream_state=T(arrs["stream_state"], torch.int32),
+        stream_woff=T(arrs["stream_woff"], torch.int64), chunk_words=T(cw, torch.int64),
+        chunk_base=T(np.cumsum(cw) - cw, torch.int64),
+        words=torch.from_numpy(words.view(np.int32).copy()).to(dev), status=T(arrs["status"], torch.int32))
+    if "dither_seed" in arrs:
+        enc.extra["dither_seed"] = T(arrs["dither_seed"], torch.int64)
+    if "rht" in header.get("extra", {}):
+        layers, kvs = header["extra"]["rht"]
+        enc.extra["rht"] = (list(layers), list(kvs))
+    return enc
+
+
+def save_batch(path, enc: EncodedBatch) -> int:
+    """Write an EncodedBatch to `path`; returns the bytes written."""
+    b = to_bytes(enc)
+    with open(path, "wb") as f:
+        f.write(b)
+    return len(b)
+
+
+def load_batch(path, device=None) -> EncodedBatch:
+    """Read an EncodedBatch written by save_batch."""
+    with open(path, "rb") as f:
+        return from_bytes(f.read(), device)

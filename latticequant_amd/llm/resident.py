@@ -68,6 +68,25 @@ class ResidentKV:
         per_blk = 64 * 4 * 4 + 64 * 4 + 16 + RB * 2   # records, meta, scales
         return self.n_heads * nb * per_blk + int(self.n_exc.item()) * 16
 
+    def reserve(self, cap_tokens: int) -> None:
+        """Grow the capacity to at least cap_tokens tokens per head (copies the blocks in use)."""
+        nb = (cap_tokens + RB - 1) // RB
+        if nb <= self.cap_blocks:
+            return
+        H, ob = self.n_heads, self.cap_blocks
+        used = (self.n_tokens + RB - 1) // RB
+
+        def grow(t, per_blk):
+            n = torch.zeros(H * nb * per_blk, dtype=t.dtype, device=t.device)
+            n.view(H, nb, per_blk)[:, :used].copy_(t.view(H, ob, per_blk)[:, :used])
+            return n
+        self.a = grow(self.a, 64 * 4)
+        self.b = grow(self.b, 64 * 4)
+        self.mask = grow(self.mask, 4)
+        self.meta = grow(self.meta, 4)
+        self.scale = grow(self.scale, RB)
+        self.cap_blocks = nb
+
     def append(self, x: torch.Tensor, scale32: torch.Tensor, scale16: torch.Tensor) -> None:
         """Quantize x (B, H, T, 128) with the per-head scales of its chunk
         (B*H of each; the points are those the chunk codec codes with the same

@@ -1,0 +1,200 @@
+"""HF cache whose decode steps attend straight over the compressed prefix.
+
+The reference's ``CompressedKVCache.update`` (llm/compressed_kv_cache.py:342-395)
+compresses every update and hands HF attention fully decompressed fp16 K / V
+(kept resident beside the chunks and ``torch.cat``-ed each step).  Here:
+
+* every layer keeps its newest tokens (up to ``tail_tokens`` + 15) as an fp16
+  residual tail; older tokens are flushed in blocks of 16 into
+  - E8 + rANS chunks (:func:`codec.encode_batch`, the reference's bitstream
+    format: the at-rest form, what ``compressed_bytes`` counts), and
+  - the resident fixed-width form of the same lattice points
+    (:class:`ResidentKV`) that decode attention reads;
+* ``update`` returns, for a one-token step, marker views that carry the cache
+  and layer, and the registered attention ``"lq_resident"`` runs
+  ``lq_resident_attention`` over resident prefix + tail (no fp16 prefix is
+  ever materialised); for a prompt (several query tokens) it returns the
+  materialised K / V (resident prefix dequantised as ``_decompress_chunk``
+  writes it, then the tail) for HF's causal SDPA.
+
+Use::
+
+    from latticequant_amd.llm.resident_cache import ResidentKVCache, register
+    register()                                   # adds attn_implementation "lq_resident"
+    model = AutoModelForCausalLM.from_config(cfg, attn_implementation="lq_resident")
+    out = model.generate(ids, past_key_values=ResidentKVCache(bits_per_dim=4), ...)
+"""
+from __future__ import annotations
+
+from typing import List, Optional
+
+import torch
+from transformers.cache_utils import DynamicCache
+
+from .. import codec
+from .resident import RB, ResidentKV, attn_workspace, resident_decode_attention
+
+ATTN_NAME = "lq_resident"
+
+
+class ResidentKVCache(DynamicCache):
+    """HF cache: rANS chunks at rest + resident b=5 prefix + fp16 residual tail."""
+
+    def __init__(self, bits_per_dim: int = 4, tail_tokens: int = 128):
+        super().__init__()
+        if bits_per_dim not in (3, 4, 5):
+            raise ValueError("bits_per_dim must be 3, 4 or 5")
+        if tail_tokens < 0 or tail_tokens % RB:
+            raise ValueError(f"tail_tokens must be a non-negative multiple of {RB}")
+        self.bits = bits_per_dim
+        self.tail_tokens = tail_tokens
+        self.res_k: List[Optional[ResidentKV]] = []
+        self.res_v: List[Optional[ResidentKV]] = []
+        self.tail_k: List[Optional[torch.Tensor]] = []
+        self.tail_v: List[Optional[torch.Tensor]] = []
+        self.chunks: List[list] = []          # per layer: [(EncodedBatch K, EncodedBatch V)]
+        self._work = None
+
+    # -- storage ----------------------------------------------------------
+    def _ensure(self, layer_idx: int):
+        while len(self.res_k) <= layer_idx:
+            self.res_k.append(None)
+            self.res_v.append(None)
+            self.tail_k.append(None)
+            self.tail_v.append(None)
+            self.chunks.append([])
+
+    def _flush(self, layer_idx: int, n: int):
+        """Compress the oldest n (a multiple of 16) tail tokens of the layer."""
+        tk, tv = self.tail_k[layer_idx], self.tail_v[layer_idx]
+        B, H, _, hd = tk.shape
+        xk, xv = tk[:, :, :n].contiguous(), tv[:, :, :n].contiguous()
+        enc, _ = codec.encode_batch(torch.stack([xk, xv]), self.bits)
+        ek, ev = enc.select(0), enc.select(1)
+        for i, (res, x, e) in enumerate(((self.res_k, xk, ek), (self.res_v, xv, ev))):
+            r = res[layer_idx]
+            if r is None:
+                r = ResidentKV(B * H, max(4 * n, 1024), device=x.device)
+                res[layer_idx] = r
+            elif r.n_tokens + n > r.cap_blocks * RB:
+                r.reserve(max(2 * r.cap_blocks * RB, r.n_tokens + n))
+            r.append(x, e.scale32, e.scale16)
+        self.chunks[layer_idx].append((ek, ev))
+        self.tail_k[layer_idx] = tk[:, :, n:].contiguous()
+        self.tail_v[layer_idx] = tv[:, :, n:].contiguous()
+
+    # -- HF Cache interface ----------------------------------------------
+    def update(self, key_states, value_states, layer_idx, cache_kwargs=None, *args, **kwargs):
+        if key_states.shape[-1] != 128:
+            raise ValueError("ResidentKVCache needs head_dim 128")
+        self._ensure(layer_idx)
+        if self.tail_k[layer_idx] is None:
+            self.tail_k[layer_idx] = key_states.contiguous()
+            self.tail_v[layer_idx] = value_states.contiguous()
+        else:
+            self.tail_k[layer_idx] = torch.cat([self.tail_k[layer_idx], key_states], 2)
+            self.tail_v[layer_idx] = torch.cat([self.tail_v[layer_idx], value_states], 2)
+        over = self.tail_k[layer_idx].shape[2] - self.tail_tokens
+        if over >= RB:
+            self._flush(layer_idx, over // RB * RB)
+        if key_states.shape[2] == 1:
+            # decode step: marker views carrying the cache; the attention reads
+            # the resident prefix and the tail itself
+            mk, mv = key_states.view_as(key_states), value_states.view_as(value_states)
+            mk._lq_cache = mv._lq_cache = self
+            mk._lq_layer = mv._lq_layer = layer_idx
+            return mk, mv
+        return self.materialise(layer_idx)
+
+    def materialise(self, layer_idx: int):
+        """Full (B, H, T, hd) K / V of the layer: the resident prefix dequantised
+        (lattice point x fp16 scale, rounded once) followed by the tail."""
+        tk, tv = self.tail_k[layer_idx], self.tail_v[layer_idx]
+        rk, rv = self.res_k[layer_idx], self.res_v[layer_idx]
+        if rk is None or rk.n_tokens == 0:
+            return tk, tv
+        B, H = tk.shape[:2]
+        pk = rk.dequant(tk.dtype).view(B, H, -1, 128)
+        pv = rv.dequant(tv.dtype).view(B, H, -1, 128)
+        return torch.cat([pk, tk], 2), torch.cat([pv, tv], 2)
+
+    def attend(self, layer_idx: int, query: torch.Tensor) -> torch.Tensor:
+        """One decode step of the layer: query (B, Hq, 1, 128) -> (B, Hq, 1, 128)."""
+        tk, tv = self.tail_k[layer_idx], self.tail_v[layer_idx]
+        B, H = tk.shape[:2]
+        rk, rv = self.res_k[layer_idx], self.res_v[layer_idx]
+        if rk is None:   # nothing flushed yet: an empty prefix
+            rk = self.res_k[layer_idx] = ResidentKV(B * H, 1024, device=tk.device)
+            rv = self.res_v[layer_idx] = ResidentKV(B * H, 1024, device=tk.device)
+        group = query.shape[1] // H
+        n = attn_workspace_size(B * H, group, rk.n_tokens, tk.shape[2])
+        if self._work is None or self._work.numel() < n or self._work.device != tk.device:
+            self._work = attn_workspace(B * H, group, rk.n_tokens, tk.shape[2], device=tk.device)
+        out = resident_decode_attention(rk, rv, query.to(torch.float16), tk.to(torch.float16),
+                                        tv.to(torch.float16), work=self._work)
+        return out.to(query.dtype)
+
+    def get_seq_length(self, layer_idx=0):
+        if layer_idx >= len(self.tail_k) or self.tail_k[layer_idx] is None:
+            return 0
+        r = self.res_k[layer_idx]
+        return (r.n_tokens if r is not None else 0) + self.tail_k[layer_idx].shape[2]
+
+    def get_mask_sizes(self, query_length: int, layer_idx: int = 0) -> tuple:
+        """(kv_length, kv_offset): past tokens + the new query."""
+        return self.get_seq_length(layer_idx) + query_length, 0
+
+    def get_max_length(self, layer_idx=None) -> int:
+        return -1
+
+    def __len__(self):
+        return len(self.tail_k)
+
+    @property
+    def is_compileable(self) -> bool:
+        return False
+
+    # -- reporting --------------------------------------------------------
+    def compressed_bytes(self) -> int:
+        """Bytes of the at-rest chunks as the reference counts them
+        (bitstream + coset bits + fp16 scales, llm/compressed_kv_cache.py:113-119)."""
+        return sum(int(e.reference_bytes().sum()) for ch in self.chunks for pair in ch for e in pair)
+
+    def resident_bytes(self) -> int:
+        """Bytes of the resident decode form (records, meta, scales, exceptions)."""
+        return sum(r.nbytes() for r in self.res_k + self.res_v if r is not None)
+
+    def tail_bytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in self.tail_k + self.tail_v if t is not None)
+
+
+def attn_workspace_size(n_heads: int, group: int, t_prefix: int, t_tail: int) -> int:
+    from .. import _lib as L
+    n = L.lib().lq_resident_attn_workspace(n_heads, group, t_prefix, t_tail)
+    if n < 0:
+        raise ValueError("bad attention geometry")
+    return int(n)
+
+
+def resident_attention(module, query, key, value, attention_mask, dropout: float = 0.0, scaling=None, **kwargs):
+    """HF attention function "lq_resident": one-token decode steps over a
+    ResidentKVCache run lq_resident_attention; everything else (prompts,
+    plain tensors) goes to HF's SDPA over the materialised K / V."""
+    cache = getattr(key, "_lq_cache", None)
+    if cache is None or query.shape[2] != 1:
+        from transformers.integrations.sdpa_attention import sdpa_attention_forward
+        return sdpa_attention_forward(module, query, key, value, attention_mask, dropout=dropout, scaling=scaling,
+                                      **kwargs)
+    if scaling is not None and abs(scaling - 128 ** -0.5) > 1e-12:
+        raise ValueError("lq_resident attention uses softmax scale 1/sqrt(128)")
+    out = cache.attend(key._lq_layer, query)            # (B, Hq, 1, hd)
+    return out.transpose(1, 2).contiguous(), None        # HF layout (B, q_len, Hq, hd)
+
+
+def register(name: str = ATTN_NAME) -> str:
+    """Register the attention function (and SDPA's mask builder) under `name`."""
+    from transformers import AttentionInterface
+    from transformers.masking_utils import AttentionMaskInterface, sdpa_mask
+    AttentionInterface.register(name, resident_attention)
+    AttentionMaskInterface.register(name, sdpa_mask)
+    return name

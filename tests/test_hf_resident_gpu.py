@@ -1,0 +1,79 @@
+"""End-to-end HF decode over the resident compressed prefix (ResidentKVCache +
+the "lq_resident" attention), on a random-init Llama-architecture model.
+
+Each decode step of the model runs lq_resident_attention over the compressed
+prefix + fp16 tail.  The reference for the same cache contents is HF's SDPA
+over the materialised K / V (prefix dequantised as _decompress_chunk writes
+it, then the tail): the same model, teacher-forced with the same tokens, must
+give the same next-token logits up to the attention tolerance."""
+import pytest
+import torch
+
+
+def _model(seed=0, layers=2, heads=4, kv_heads=2, vocab=512):
+    from transformers import LlamaConfig, LlamaForCausalLM
+    from latticequant_amd.llm.resident_cache import register
+    name = register()
+    cfg = LlamaConfig(vocab_size=vocab, hidden_size=heads * 128, intermediate_size=1024, num_hidden_layers=layers,
+                      num_attention_heads=heads, num_key_value_heads=kv_heads, head_dim=128,
+                      max_position_embeddings=4096, attn_implementation=name)
+    torch.manual_seed(seed)
+    return LlamaForCausalLM(cfg).to(device="cuda", dtype=torch.float16).eval(), cfg
+
+
+def test_register_and_cache_bookkeeping_cpu():
+    from latticequant_amd.llm.resident_cache import ResidentKVCache, register
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+    name = register()
+    assert name in ALL_ATTENTION_FUNCTIONS.valid_keys()
+    c = ResidentKVCache(bits_per_dim=4, tail_tokens=32)
+    assert c.get_seq_length() == 0 and c.get_mask_sizes(5) == (5, 0)
+    with pytest.raises(ValueError):
+        ResidentKVCache(bits_per_dim=6)
+    with pytest.raises(ValueError):
+        ResidentKVCache(tail_tokens=20)
+
+
+class _Materialising:
+    """Same cache contents, but every update hands HF the materialised K / V."""
+
+    def __init__(self, **kw):
+        from latticequant_amd.llm.resident_cache import ResidentKVCache
+
+        class C(ResidentKVCache):
+            def update(self, k, v, layer_idx, *a, **kw2):
+                super().update(k, v, layer_idx, *a, **kw2)
+                return self.materialise(layer_idx)
+        self.cache = C(**kw)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("prompt,steps,tail,heads,kv", [(100, 60, 32, 4, 2), (40, 30, 0, 8, 2), (70, 25, 128, 4, 4)])
+def test_hf_decode_over_resident_prefix_gpu(prompt, steps, tail, heads, kv):
+    from latticequant_amd.llm.resident_cache import ResidentKVCache
+    model, cfg = _model(heads=heads, kv_heads=kv)
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, cfg.vocab_size, (1, prompt), generator=g).cuda()
+    a = ResidentKVCache(bits_per_dim=4, tail_tokens=tail)
+    b = _Materialising(bits_per_dim=4, tail_tokens=tail).cache
+    with torch.no_grad():
+        la = model(ids, past_key_values=a, use_cache=True).logits[:, -1].float()
+        lb = model(ids, past_key_values=b, use_cache=True).logits[:, -1].float()
+        assert torch.allclose(la, lb)                       # prompt: both take the SDPA path
+        agree = 0
+        for _ in range(steps):
+            nxt = la.argmax(-1, keepdim=True)
+            la = model(nxt, past_key_values=a, use_cache=True).logits[:, -1].float()
+            lb = model(nxt, past_key_values=b, use_cache=True).logits[:, -1].float()
+            # attention agrees to <= 1e-3 relative; two fp16 layers, MLPs and the
+            # head carry that into the logits
+            err = ((la - lb).abs().max() / lb.abs().max()).item()
+            assert err < 5e-3, err
+            agree += int(la.argmax() == lb.argmax())
+    assert agree >= steps - 1
+    n = prompt + steps
+    assert a.get_seq_length() == n == b.get_seq_length()
+    flushed = a.res_k[0].n_tokens
+    assert flushed % 16 == 0 and n - flushed == a.tail_k[0].shape[2] and a.tail_k[0].shape[2] < tail + 16
+    if flushed:
+        assert a.compressed_bytes() > 0 and a.resident_bytes() > 0

@@ -1,0 +1,125 @@
+"""Wire / on-disk format of a compressed chunk batch (codec.to_bytes / from_bytes).
+
+CPU tests exercise the container on a synthetic batch (field round trip,
+table rebuild, corruption and version checks); the GPU tests round-trip real
+encoded batches and check that the restored batch decodes bit-exactly."""
+import io
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from latticequant_amd import codec
+from latticequant_amd import _lib as L
+
+
+def _fake_batch(C=2, nh=2, bph=1024, seed=0):
+    """A structurally valid EncodedBatch on the CPU (random contents)."""
+    rng = np.random.default_rng(seed)
+    S, nb = L.LQ_STREAMS, (nh * bph + L.LQ_BLK - 1) // L.LQ_BLK
+    tab = np.zeros((C * S, L.TABLE_BYTES // 4), np.uint32)
+    for i in range(C * S):
+        if i % 5 == 3:
+            continue                                   # an absent stream
+        n = int(rng.integers(3, 40))
+        # every symbol at least once, the rest at random: sums to L, every f >= 1
+        f = np.bincount(np.concatenate([np.arange(n), rng.integers(0, n, L.LQ_L - n)]), minlength=n)
+        cum = np.cumsum(f) - f
+        bl = np.array([int(v).bit_length() for v in f], np.uint32)
+        tab[i, :4] = np.array([-(n // 2), n, int(rng.integers(1, 999)), 0], np.int32).view(np.uint32)
+        tab[i, 4:4 + n] = f.astype(np.uint32) | (cum.astype(np.uint32) << 11) | ((11 - bl) << 21)
+    cw = rng.integers(10, 50, C)
+    words = rng.integers(0, 2 ** 32, int(cw.sum()) + 7, dtype=np.uint64).astype(np.uint32)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a))
+    return codec.EncodedBatch(
+        n_chunks=C, n_heads=nh, bph=bph, shape=(1, nh, bph * 8 // 128, 128), bits=T(np.full(C, 4, np.int32)),
+        scale32=T(rng.random(C * nh).astype(np.float32)), scale16=T(rng.random(C * nh).astype(np.float16)),
+        sigma2=T(rng.random(C * nh).astype(np.float32)),
+        coset_bits=T(rng.integers(0, 256, (C, nb * L.LQ_BLK // 8)).astype(np.uint8)),
+        blk_n1=T(rng.integers(0, 513, (C, nb)).astype(np.int32)),
+        tables=T(tab.view(np.uint8).reshape(-1)),
+        blk_off=T(rng.integers(0, 2 ** 31, C * S * nb).astype(np.int32)),
+        blk_state=T(rng.integers(1024, 2048, C * S * nb).astype(np.int16)),
+        stream_nbits=T(rng.integers(0, 10 ** 6, C * S)), stream_state=T(rng.integers(1024, 2048, C * S).astype(np.int32)),
+        stream_woff=T(rng.integers(0, 10 ** 5, C * S)), chunk_words=T(cw.astype(np.int64)),
+        chunk_base=T((np.cumsum(cw) - cw + 3).astype(np.int64)), words=T(words.view(np.int32)),
+        status=T(np.zeros(C, np.int32)))
+
+
+def _meaningful_tables(enc):
+    t = enc.tables.view(torch.int32).view(-1, L.TABLE_BYTES // 4).cpu().numpy()
+    return [t[i, :4 + t[i, 1]].copy() for i in range(t.shape[0])]
+
+
+def test_wire_round_trip_fields_cpu():
+    e = _fake_batch()
+    b = codec.to_bytes(e)
+    r = codec.from_bytes(b, device="cpu")
+    C, S, nb = e.n_chunks, L.LQ_STREAMS, e.nblk
+    for name in ("bits", "status", "scale32", "scale16", "sigma2", "coset_bits", "blk_n1", "stream_nbits",
+                 "stream_state", "stream_woff", "chunk_words"):
+        assert torch.equal(getattr(r, name).cpu().view(-1), getattr(e, name).view(-1)), name
+    for a, b2 in zip(_meaningful_tables(e), _meaningful_tables(r)):
+        assert np.array_equal(a, b2)
+    ew = e.words.numpy().view(np.uint32)
+    rw = r.words.numpy().view(np.uint32)
+    for c in range(C):
+        b0, n = int(e.chunk_base[c]), int(e.chunk_words[c])
+        r0 = int(r.chunk_base[c])
+        assert np.array_equal(ew[b0:b0 + n], rw[r0:r0 + n])
+    # checkpoints of present streams survive; absent streams read as empty
+    nsym = e.tables.view(torch.int32).view(-1, L.TABLE_BYTES // 4)[:, 1].numpy()
+    eo = e.blk_off.numpy().reshape(C * S, nb)
+    ro = r.blk_off.numpy().reshape(C * S, nb)
+    assert np.array_equal(eo[nsym > 0], ro[nsym > 0])
+    assert (ro[nsym == 0] == 0).all()
+
+
+def test_wire_rejects_corruption_and_versions_cpu(tmp_path):
+    e = _fake_batch(seed=1)
+    b = bytearray(codec.to_bytes(e))
+    p = tmp_path / "batch.lq"
+    assert codec.save_batch(p, e) == len(b)
+    assert codec.load_batch(p, device="cpu").n_chunks == e.n_chunks
+    bad = bytearray(b)
+    bad[len(bad) // 2] ^= 0x40
+    with pytest.raises(codec.WireFormatError, match="checksum"):
+        codec.from_bytes(bytes(bad), device="cpu")
+    with pytest.raises(codec.WireFormatError):
+        codec.from_bytes(bytes(b[:100]), device="cpu")
+    with pytest.raises(codec.WireFormatError, match="not an"):
+        codec.from_bytes(b"XXXXXXXX" + bytes(b[8:]), device="cpu")
+    v2 = bytearray(b)
+    v2[8:12] = np.uint32(99).tobytes()
+    with pytest.raises(codec.WireFormatError, match="version"):
+        codec.from_bytes(bytes(v2), device="cpu")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind", ["normal", "outliers", "rotated"])
+def test_wire_round_trip_decodes_bit_exact_gpu(kind):
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(3, 1, 4, 256, 128, generator=g)
+    if kind == "outliers":
+        x[..., :4] *= 10
+    x = x.half().cuda()
+    if kind == "rotated":
+        from latticequant_amd.llm.rotated import decode_rotated, encode_rotated
+        enc, _ = encode_rotated(x, 4, [0, 1, 2], [0, 1, 0])
+        ref = decode_rotated(enc)
+    else:
+        enc, _ = codec.encode_batch(x, 4)
+        ref = codec.decode_batch(enc)
+    b = codec.to_bytes(enc)
+    r = codec.from_bytes(b)
+    for a, b2 in zip(_meaningful_tables(enc), _meaningful_tables(r)):
+        assert np.array_equal(a, b2)      # rebuilt tables equal the encoder's
+    if kind == "rotated":
+        from latticequant_amd.llm.rotated import decode_rotated
+        got = decode_rotated(r)
+    else:
+        got = codec.decode_batch(r)
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    # the reference-accounted bytes are what the payload carries for them
+    assert int(r.reference_bytes().sum()) == int(enc.reference_bytes().sum())
