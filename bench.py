@@ -127,6 +127,66 @@ def bench_decode_step(dev, iters=30, prefix=32768, tail=128):
                                     f"L2/MALL flushed before each step"}
 
 
+def e2e_decode_throughput(dev, prefills=(128, 8192), decode_tokens=64, warmup=2, repeats=3):
+    """F1: model decode throughput through the HF cache interface, measured the
+    way the reference measures it (llm/e2e_eval.py:285-362: prefill, then
+    decode_tokens one-token forwards, tok/s over the decode phase), on a
+    random-initialised model of the Llama-3.1-8B architecture (no weights are
+    downloadable here), fp16.  Caches compared per prefill length:
+      fp16      HF DynamicCache, SDPA over fp16 K / V (the reference's attention input)
+      rans      CompressedKVCache (the reference's semantics: every update E8+rANS
+                coded, decompressed fp16 K / V kept resident for SDPA)
+      resident  ResidentKVCache: rANS chunks at rest + resident b=5 prefix +
+                128-token fp16 tail; decode steps run lq_resident_attention"""
+    from transformers import LlamaConfig, LlamaForCausalLM
+    from transformers.cache_utils import DynamicCache
+    from latticequant_amd.llm.compressed_kv_cache import CompressedKVCache
+    from latticequant_amd.llm.resident_cache import ResidentKVCache, register
+    name = register()
+    cfg = LlamaConfig(vocab_size=128256, hidden_size=4096, intermediate_size=14336, num_hidden_layers=32,
+                      num_attention_heads=32, num_key_value_heads=8, head_dim=128, rope_theta=500000.0,
+                      max_position_embeddings=131072, attn_implementation=name)
+    with torch.device("meta"):
+        model = LlamaForCausalLM(cfg)
+    model = model.to_empty(device=dev).to(torch.float16).eval()
+    g = torch.Generator(device=dev).manual_seed(0)
+    with torch.no_grad():
+        for p_ in model.parameters():
+            p_.normal_(0.0, 0.02, generator=g)
+    for m in model.modules():   # RMSNorm weights to 1
+        if hasattr(m, "variance_epsilon"):
+            m.weight.data.fill_(1.0)
+    from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding
+    model.model.rotary_emb = LlamaRotaryEmbedding(cfg, device=dev)   # buffers were left empty on meta
+    caches = {"fp16": lambda: DynamicCache(), "rans": lambda: CompressedKVCache(bits_per_dim=BITS),
+              "resident": lambda: ResidentKVCache(bits_per_dim=BITS, tail_tokens=128)}
+    res = {}
+    for pre in prefills:
+        ids = torch.randint(0, cfg.vocab_size, (1, pre), generator=g, device=dev)
+        for label, mk in caches.items():
+            ts = []
+            for trial in range(warmup + repeats):
+                cache = mk()
+                with torch.no_grad():
+                    out = model(ids, past_key_values=cache, use_cache=True)
+                nxt = out.logits[:, -1:].argmax(-1)
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                with torch.no_grad():
+                    for _ in range(decode_tokens):
+                        out = model(nxt, past_key_values=cache, use_cache=True)
+                        nxt = out.logits[:, -1:].argmax(-1)
+                torch.cuda.synchronize()
+                if trial >= warmup:
+                    ts.append(time.perf_counter() - t0)
+                del cache, out
+            t = float(np.mean(ts))
+            res[f"{label}_prefill{pre}"] = {"tok_per_s": round(decode_tokens / t, 2),
+                                             "ms_per_tok": round(t / decode_tokens * 1e3, 3)}
+            print(f"e2e prefill {pre} {label}: {decode_tokens / t:.1f} tok/s", file=sys.stderr, flush=True)
+    return res
+
+
 def time_quantize(x, enc, reps=3):
     """Average duration (ms) of the k_chunk_quantize launch over the batch x
     (the launch encode_batch makes), with the scales enc holds, timed with
@@ -249,6 +309,9 @@ def main():
                     help="also run one 1 GiB device copy (the HBM-counter calibration kernel under rocprofv3 --pmc)")
     ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "OUT_JSON"),
                     help="only summarise two rocprofv3 --pmc runs into per-launch HBM traffic and exit")
+    ap.add_argument("--e2e", action="store_true",
+                    help="only measure model decode tok/s through the HF cache interface (random-init Llama-3.1-8B "
+                         "architecture; fp16, rANS and resident caches) and print one JSON line")
     ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
                     help="only print per-(kernel, grid) launch durations of a rocprofv3 --kernel-trace run and exit")
     args = ap.parse_args()
@@ -257,6 +320,15 @@ def main():
         return
     if args.summarize_trace:
         summarize_trace(args.summarize_trace)
+        return
+    if args.e2e:
+        dev = torch.device("cuda", 0)
+        torch.cuda.set_device(dev)
+        r = e2e_decode_throughput(dev)
+        print(json.dumps({"metric": "decode tok/s (1 GPU, batch 1, 64 decode tokens after the prefill)",
+                          "unit": "tok/s", "higher_is_better": True, "n_gpus": 1, "data": "synthetic",
+                          "dtype": "fp16", "config": {"model": "Llama-3.1-8B architecture, random weights",
+                                                     "bits_per_dim": BITS}, "results": r}))
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for {args.gpus}); "

@@ -795,26 +795,22 @@ __global__ __launch_bounds__(kAW * 64) void k_res_attn(AttnArgs A) {
     }
     __syncthreads();
     if (!s_last) return;
-    // ---- the last workgroup of this kv head merges every split: each thread
-    // issues all its loads in one batch (latency, not bandwidth, bounds this)
+    // ---- the last workgroup of this kv head merges every split.  One
+    // device-scope acquire (this XCD's L2 drops its non-coherent lines) makes
+    // the other workgroups' write-through records visible to plain loads,
+    // which are issued unconditionally (clamped indices, zero weights past the
+    // end) so that each thread's loads go out as one batch.
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     const float* r0 = A.rec + (int64_t)kvh * nsp * G * kRecF;
     float* s_cm = reinterpret_cast<float*>(&s_vt[0][0]);
     float* s_cf = s_cm + kMaxRec;
     float* s_cl = s_cf + kMaxRec;
+    f4_t* s_part = reinterpret_cast<f4_t*>(s_cl + kMaxRec);
     const int ne = nsp * G;
-    constexpr int kMU = 40;                   // o values in flight per thread
-    float ov[kMU];
-    const int h0 = tid / kHd, d0 = tid % kHd;   // first output of this thread
     for (int i = tid; i < ne; i += kAW * 64) {
-        s_cm[i] = __hip_atomic_load(r0 + (int64_t)i * kRecF, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_cl[i] = __hip_atomic_load(r0 + (int64_t)i * kRecF + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (h0 < G) {
-#pragma unroll
-        for (int k = 0; k < kMU; k++)
-            ov[k] = k < nsp ? __hip_atomic_load(r0 + (int64_t)(k * G + h0) * kRecF + 4 + d0, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT)
-                            : 0.f;
+        const f4_t h4 = *reinterpret_cast<const f4_t*>(r0 + (int64_t)i * kRecF);
+        s_cm[i] = h4[0];
+        s_cl[i] = h4[1];
     }
     __syncthreads();
     for (int h = wave; h < G; h += kAW) {
@@ -832,22 +828,40 @@ __global__ __launch_bounds__(kAW * 64) void k_res_attn(AttnArgs A) {
         if (lane == 0) s_L[h] = L;
     }
     __syncthreads();
-    for (int idx = tid; idx < G * kHd; idx += kAW * 64) {
-        const int h = idx / kHd, d = idx % kHd;
-        float acc = 0.f;
-        if (idx == tid) {   // first output: its first kMU splits are in registers
+    constexpr int kMU = 12;                      // o rows in flight per thread
+    const int ng = G * (kHd / 4);                // float4 groups of the outputs
+    const int tpg = ng >= kAW * 64 ? 1 : kAW * 64 / ng;   // threads per group, each a stride of the splits
+    for (int it = tid; it < ng * tpg; it += kAW * 64) {
+        const int gi = it % ng, sub = it / ng;
+        const int h = gi / (kHd / 4), d4 = gi % (kHd / 4);
+        f4_t acc = f4_t{0.f, 0.f, 0.f, 0.f};
+        for (int p0 = sub; p0 < nsp; p0 += kMU * tpg) {
+            f4_t v[kMU];
+            float f[kMU];
 #pragma unroll
-            for (int k = 0; k < kMU; k++) acc += k < nsp ? ov[k] * s_cf[k * G + h] : 0.f;
-        } else {
-            for (int k = 0; k < kMU && k < nsp; k++)
-                acc += __hip_atomic_load(r0 + (int64_t)(k * G + h) * kRecF + 4 + d, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT) * s_cf[k * G + h];
+            for (int k = 0; k < kMU; k++) {
+                const int p = p0 + k * tpg;
+                const int pc = p < nsp ? p : nsp - 1;
+                v[k] = *reinterpret_cast<const f4_t*>(r0 + (int64_t)(pc * G + h) * kRecF + 4 + 4 * d4);
+                f[k] = p < nsp ? s_cf[pc * G + h] : 0.f;
+            }
+#pragma unroll
+            for (int k = 0; k < kMU; k++) acc += v[k] * f[k];
         }
-        for (int k = kMU; k < nsp; k++)
-            acc += __hip_atomic_load(r0 + (int64_t)(k * G + h) * kRecF + 4 + d, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT) * s_cf[k * G + h];
-        A.out[(kvh * G + h) * kHd + d] = f2h(acc / s_L[h]);
+        s_part[it] = acc;
     }
+    __syncthreads();
+    for (int gi = tid; gi < ng; gi += kAW * 64) {
+        f4_t acc = s_part[gi];
+        for (int sub = 1; sub < tpg; sub++) acc += s_part[gi + sub * ng];
+        const int h = gi / (kHd / 4), d4 = gi % (kHd / 4);
+        const float inv = 1.f / s_L[h];
+        uint16_t* op = A.out + (kvh * G + h) * kHd + 4 * d4;
+        const uint2 w = make_uint2((uint32_t)f2h(acc[0] * inv) | ((uint32_t)f2h(acc[1] * inv) << 16),
+                                   (uint32_t)f2h(acc[2] * inv) | ((uint32_t)f2h(acc[3] * inv) << 16));
+        *reinterpret_cast<uint2*>(op) = w;
+    }
+    __syncthreads();
     if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
