@@ -136,10 +136,10 @@ __global__ __launch_bounds__(256) void k_attn_scores(BatchArgs a, const uint16_t
         const float sc = h2f(s16);
         const _Float16 sh = __builtin_bit_cast(_Float16, s16);
         const half2_t sc2 = half2_t{sh, sh};
-        PhaseLane d;
+        PhaseLane<kSLanes> d;
         const int64_t end_bit = g + 1 < a.nblk ? (int64_t)a.blk_off[task + 1] : a.stream_nbits[sid];
         d.init(a.words + a.chunk_base[chunk] + a.stream_woff[sid], a.blk_off[task], end_bit, a.blk_state[task], lut, idx,
-               &ring[0][tid], kSLanes, bm[b]);
+               &ring[0][tid], bm[b]);
         const char* const lutb = reinterpret_cast<const char*>(lut);
         uint16_t* const my_stg = &stg[b * kStgRowA + idx];
         for (int s0 = 0; s0 < n; s0 += kPhase) {

@@ -90,55 +90,68 @@ struct StreamDec {
 // blocks; lane (block b, coordinate idx) owns stream idx of block b.  The
 // lane decodes in phases of 8 steps:
 //   * its bitstream words reach the decoder through a 16-word ring in LDS
-//     (column `tid` of ring[kRing][lanes]); 4-word top-ups are loaded at one
-//     phase boundary and written to the ring at the next, so the decode steps
-//     never wait on global memory;
+//     (column `tid` of ring[kRing][LANES]) that holds the stream's 16-byte
+//     aligned 4-word groups; a top-up is one aligned 16-byte load, issued at
+//     one phase boundary and written to the ring at the next, so the decode
+//     steps never wait on global memory;
 //   * each step stages the symbol index in LDS (row b of the staging, 8 u16
 //     per step) and walks the block's coset bitmap (words already restricted
 //     to the coset's vectors) to find the vector the 8 lanes just decoded;
 //   * after the phase, lane idx owns the vector of step idx: its 8 symbol
 //     indices are row idx of the staging and its block position is returned.
-// Loads stay within two words after the block's last bit (the stream needs 2
-// words of slack after its n_words + 1).
+// Reads stay inside the aligned 16-byte groups that hold the block's words
+// up to two words after its last bit (the stream needs 2 words of slack after
+// its n_words + 1); such a group never crosses a page.
 constexpr int kPhase = 8;    // decode steps per phase
 constexpr int kRing = 16;    // bitstream words per lane in the LDS ring
 
+template <int LANES>
 struct PhaseLane {
-    const uint32_t* sw;     // stream words from the block's first word
+    const uint32_t* gs;     // the 16-byte aligned group holding the block's first word
     uint32_t* rcol;         // this lane's ring column
-    int lanes;              // ring row stride (lanes of the workgroup)
-    int wlim;               // last readable word, relative to sw
-    int ld, rd;             // next word to load into the ring / to move into pre
+    int glim;               // first word (group index * 4, from gs) of the last readable group
+    int ld, rd;             // next word (from gs) to load into the ring / to move into pre
     uint64_t buf;
     uint32_t nbuf, pre, e;
-    uint32_t q0, q1, q2, q3;
+    uint4 q;
     bool inflight;
     const uint32_t* bmr;    // the block's coset bitmap row (kBlk / 32 + 1 words, last one zero)
     int wi;
     uint32_t wv, wn;
 
-    __device__ __forceinline__ uint32_t gword(int i) const { return sw[i < wlim ? i : wlim]; }
+    __device__ __forceinline__ uint4 group(int i) const {   // i: a multiple of 4
+        return *reinterpret_cast<const uint4*>(gs + (i < glim ? i : glim));
+    }
+    __device__ __forceinline__ void land(int i, const uint4& g) {   // ring slots i .. i + 3 (i % 4 == 0)
+        uint32_t* p = rcol + (i & (kRing - 1)) * LANES;
+        p[0] = g.x;
+        p[LANES] = g.y;
+        p[2 * LANES] = g.z;
+        p[3 * LANES] = g.w;
+    }
 
     // stream_words: the stream; bit_off / end_bit: the block's first bit and
     // the next block's first bit (or the stream's n_bits); state: checkpoint
     // state; lut: LDS LUT block, row: this stream's row in it.
     __device__ __forceinline__ void init(const uint32_t* stream_words, uint32_t bit_off, int64_t end_bit, uint32_t state,
-                                         const uint32_t* lut, int row, uint32_t* ring_col, int n_lanes,
-                                         const uint32_t* bm_row) {
-        sw = stream_words + (bit_off >> 5);
-        wlim = (int)((end_bit >> 5) + 2 - (int64_t)(bit_off >> 5));
+                                         const uint32_t* lut, int row, uint32_t* ring_col, const uint32_t* bm_row) {
+        const uint32_t* sw = stream_words + (bit_off >> 5);
+        const int o = (int)((reinterpret_cast<uintptr_t>(sw) >> 2) & 3u);
+        gs = sw - o;
+        const int wlim = (int)((end_bit >> 5) + 2 - (int64_t)(bit_off >> 5));   // last readable word, from sw
+        glim = (wlim + o) & ~3;
         rcol = ring_col;
-        lanes = n_lanes;
-#pragma unroll
-        for (int i = 0; i < 8; i++) rcol[i * lanes] = gword(i);
-        ld = 8;
-        rd = 2;
-        buf = ((uint64_t)__builtin_bitreverse32(rcol[0]) << 32) << (bit_off & 31u);
+        const uint4 g0 = group(0), g1 = group(4), g2 = group(8);
+        land(0, g0);
+        land(4, g1);
+        land(8, g2);
+        ld = 12;
+        rd = o + 2;
+        buf = ((uint64_t)__builtin_bitreverse32(rcol[o * LANES]) << 32) << (bit_off & 31u);
         nbuf = 32u - (bit_off & 31u);
-        pre = rcol[lanes];
+        pre = rcol[(o + 1) * LANES];
         refill();
         e = lut[row * kL + (int)state - kL];
-        q0 = q1 = q2 = q3 = 0;
         inflight = false;
         bmr = bm_row;
         wi = 0;
@@ -150,26 +163,23 @@ struct PhaseLane {
         if (nbuf < 32u) {
             buf |= (uint64_t)__builtin_bitreverse32(pre) << (32u - nbuf);
             nbuf += 32u;
-            pre = rcol[(rd & (kRing - 1)) * lanes];
+            pre = rcol[(rd & (kRing - 1)) * LANES];
             rd++;
         }
     }
 
     // Phase boundary: land the previous top-up, issue the next one.  A phase
-    // moves at most 3 words out of the ring; a top-up is issued only if 4
-    // more words fit even when none is consumed, so the ring always holds the
-    // next phase's words.
+    // moves at most 3 words out of the ring and a top-up (4 words) is issued
+    // only if it fits even when none is consumed, so every phase starts with
+    // at least 3 words in the ring (at least 6 after init).
     __device__ __forceinline__ void boundary() {
         if (inflight) {
-            rcol[(ld & (kRing - 1)) * lanes] = q0;
-            rcol[((ld + 1) & (kRing - 1)) * lanes] = q1;
-            rcol[((ld + 2) & (kRing - 1)) * lanes] = q2;
-            rcol[((ld + 3) & (kRing - 1)) * lanes] = q3;
+            land(ld, q);
             ld += 4;
             inflight = false;
         }
         if (ld - rd <= kRing - 4) {
-            q0 = gword(ld); q1 = gword(ld + 1); q2 = gword(ld + 2); q3 = gword(ld + 3);
+            q = group(ld);
             inflight = true;
         }
     }

@@ -830,10 +830,10 @@ __global__ __launch_bounds__(512) void k_chunk_decode(const uint32_t* __restrict
     set_scale(head0);
     int64_t head_end = (head0 + 1) * bph;            // first chunk vector of the next head
 
-    PhaseLane d;
+    PhaseLane<kDecLanes> d;
     const int64_t end_bit = g + 1 < nblk ? (int64_t)blk_off[task + 1] : stream_nbits[sid];
     d.init(words + chunk_base[chunk] + stream_woff[sid], blk_off[task], end_bit, blk_state[task], lut, idx,
-           &ring[0][tid], kDecLanes, bm[b]);
+           &ring[0][tid], bm[b]);
     const char* const lutb = reinterpret_cast<const char*>(lut);
     using OutT = typename std::conditional<OUT_DT == LQ_F32, float, uint16_t>::type;
     OutT* const ob = reinterpret_cast<OutT*>(out) + (chunk * V + vfirst) * 8;
