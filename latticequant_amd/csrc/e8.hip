@@ -226,7 +226,7 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t wg_per_chunk = (nblk + kQBlocksPerWG - 1) / kQBlocksPerWG;
     const int64_t chunk = blockIdx.x / wg_per_chunk;
     const int64_t b0 = (blockIdx.x % wg_per_chunk) * kQBlocksPerWG;

@@ -98,9 +98,11 @@ __device__ __forceinline__ uint16_t f2dtype(float f, int dtype) { return dtype =
 // RN(RN(1 - 2|r|) + tiebreak_i) (first index on ties) one step away from x.
 __device__ __forceinline__ void d8_round(const float x[8], float r[8]) {
     float res[8];
-    float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; i++) { r[i] = rintf(x[i]); s += r[i]; }
+    for (int i = 0; i < 8; i++) r[i] = rintf(x[i]);
+    float s = r[0];
+#pragma unroll
+    for (int i = 1; i < 8; i++) s += r[i];
     // first-index argmin of RN(RN(1 - 2|res_i|) + tiebreak_i): upd[i] says the
     // running minimum moved to i, so the argmin is the last i with upd[i]
     // (the per-lane flags stay lane masks; no index is materialised)
