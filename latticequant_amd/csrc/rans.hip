@@ -620,10 +620,14 @@ __global__ void k_chunk_offsets(const int64_t* __restrict__ stream_nbits, const 
 // words whose first bit lies in its blocks' bit range; lane l assembles words
 // W0 + l + 64 k, four per round with all their scratch loads in flight
 // (256-byte coalesced stores).  A word's first bits come from the
-// right-aligned scratch of the block holding its first bit (binary search over
-// the group's offsets, staged in LDS); the rare word that runs past that
-// block's end continues block by block.  Stream bit positions are 32-bit
-// (blk_off is uint32).
+// right-aligned scratch of the block holding its first bit; the rare word
+// that runs past that block's end continues block by block.  The block of
+// each word comes from the blocks' first owned words fw_i = ceil(off_i / 32),
+// held one per lane: within a 64-word slice, the block of word w is the last
+// block with fw_i <= w, i.e. the last block starting at or before the slice
+// (a ballot count) unless one of the few blocks starting inside the slice
+// (another ballot, walked on the scalar unit) has fw_i <= w.  Stream bit
+// positions are 32-bit (blk_off is uint32).
 constexpr int kPackBlocks = 32;
 
 __global__ __launch_bounds__(256) void k_chunk_pack(int64_t n_streams_total, int64_t nblk, const uint32_t* __restrict__ scratch,
@@ -632,8 +636,8 @@ __global__ __launch_bounds__(256) void k_chunk_pack(int64_t n_streams_total, int
                                                     const int64_t* __restrict__ stream_woff,
                                                     const int64_t* __restrict__ chunk_base,
                                                     const lq_table* __restrict__ tables, uint32_t* __restrict__ words) {
-    __shared__ uint32_t offs[4][kPackBlocks + 1];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __shared__ uint32_t offs[4][kPackBlocks + 2];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int64_t gps = (nblk + kPackBlocks - 1) / kPackBlocks;   // groups per stream
     const int64_t job = (int64_t)blockIdx.x * 4 + wave;
     const int64_t sid = job / gps;
@@ -642,30 +646,42 @@ __global__ __launch_bounds__(256) void k_chunk_pack(int64_t n_streams_total, int
     const uint32_t nbits = (uint32_t)stream_nbits[sid];
     const int nb = (int)(nblk - g0 < kPackBlocks ? nblk - g0 : kPackBlocks);
     const uint32_t* bo = blk_off + sid * nblk;
-    // offset of block g0 + i (the stream end past the last block)
-    auto off_mem = [&](int i) -> uint32_t { return g0 + i < nblk ? bo[g0 + i] : nbits; };
+    // offset of block g0 + i (the stream end past the last block); staged for i <= nb + 1
+    auto off_glb = [&](int i) -> uint32_t { return g0 + i < nblk ? bo[g0 + i] : nbits; };
     uint32_t* of = offs[wave];
-    if (lane <= nb) of[lane] = off_mem(lane);
+    const uint32_t myof = lane <= nb + 1 ? off_glb(lane) : 0u;
+    if (lane <= nb + 1) of[lane] = myof;
     __builtin_amdgcn_wave_barrier();
-    const uint32_t W0 = (of[0] + 31u) >> 5, W1 = (of[nb] + 31u) >> 5;
+    auto off_at = [&](int i) -> uint32_t { return i <= nb + 1 ? of[i] : off_glb(i); };
+    // first owned word of block `lane` (blocks 0 .. nb - 1), else past every word
+    const uint32_t myfw = lane < nb ? (myof + 31u) >> 5 : 0xffffffffu;
+    const uint32_t W0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)((myof + 31u) >> 5));
+    const uint32_t W1 = (uint32_t)__builtin_amdgcn_readlane((int)((myof + 31u) >> 5), nb);
     uint32_t* out = words + chunk_base[sid / LQ_STREAMS] + stream_woff[sid];
     const uint32_t* scr0 = scratch + (sid * nblk + g0) * (int64_t)kCapW;
     constexpr uint32_t kCapBits = (uint32_t)kCapW * 32u;
-    for (uint32_t wb = W0 + lane; wb < W1; wb += 256) {
-        uint32_t lo[4], hi[4], res[4];
-        int blk[4], take[4], s2[4];
-        uint32_t pe[4];   // bit after the word's first segment
+    for (uint32_t wr = W0; wr < W1; wr += 256) {
+        uint32_t lo[4], hi[4], clo[4], chi[4];
+        int blk[4], take[4], s2[4], cs[4];
+        uint32_t pe[4], nx[4];   // bit after the word's first segment; end of the next block
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-            const uint32_t w = wb + 64u * u;
+            const uint32_t ws = wr + 64u * u;   // first word of the slice (wave-uniform)
+            const uint32_t w = ws + lane;
             const bool ok = w < W1;
+            // blocks starting at or before the slice, and inside it
+            const uint64_t at = __ballot(myfw <= ws);
+            uint64_t in = __ballot(myfw > ws && myfw <= ws + 63u);
+            int b = __builtin_popcountll(at) - 1;
+            while (in) {
+                const int i = __builtin_ctzll(in);
+                in &= in - 1;
+                const uint32_t fwi = (uint32_t)__builtin_amdgcn_readlane((int)myfw, i);
+                b = w >= fwi ? i : b;
+            }
             const uint32_t p = 32u * (ok ? w : W0);
-            // block holding bit p: largest b < nb with of[b] <= p
-            int b = 0;
-#pragma unroll
-            for (int step = kPackBlocks / 2; step > 0; step >>= 1)
-                if (b + step < nb && of[b + step] <= p) b += step;
-            const uint32_t ob = of[b], oe = of[b + 1];
+            if (!ok) b = 0;
+            const uint32_t ob = of[b], oe = of[b + 1], on = of[b + 2];
             const uint32_t end = p + 32u < nbits ? p + 32u : nbits;
             const uint32_t e1 = end < oe ? end : oe;
             const uint32_t sp = kCapBits - (oe - ob) + (p - ob);   // scratch bit of p
@@ -673,38 +689,60 @@ __global__ __launch_bounds__(256) void k_chunk_pack(int64_t n_streams_total, int
             const uint32_t k0 = sp >> 5;
             lo[u] = sc[k0];
             hi[u] = sc[k0 + 1 < (uint32_t)kCapW ? k0 + 1 : k0];
+            // a word running past its block's end continues with the first bits
+            // of block b + 1: load them now, in the lanes that need them
+            const uint32_t sp1 = kCapBits - (on - oe);            // scratch bit of block b + 1's first bit
+            clo[u] = 0u;
+            chi[u] = 0u;
+            if (ok && e1 < end && on > oe) {
+                const uint32_t* sc1 = sc + kCapW;
+                const uint32_t k1 = sp1 >> 5;
+                clo[u] = sc1[k1];
+                chi[u] = sc1[k1 + 1 < (uint32_t)kCapW ? k1 + 1 : k1];
+            }
             blk[u] = b;
             take[u] = (int)(e1 - p);
             s2[u] = (int)(sp & 31u);
+            cs[u] = (int)(sp1 & 31u);
             pe[u] = e1;
+            nx[u] = on;
         }
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-            const uint32_t w = wb + 64u * u;
+            const uint32_t w = wr + 64u * u + lane;
             if (w >= W1) continue;
             uint64_t v = ((uint64_t)hi[u] << 32 | lo[u]) >> s2[u];
             int got = take[u];
-            res[u] = got == 32 ? (uint32_t)v : (uint32_t)v & ((1u << got) - 1u);
+            uint32_t res = got == 32 ? (uint32_t)v : (uint32_t)v & ((1u << got) - 1u);
             uint32_t p = pe[u];
             const uint32_t end = 32u * w + 32u < nbits ? 32u * w + 32u : nbits;
-            int b = blk[u] + 1;
-            while (p < end) {   // the word continues in the following block(s)
-                const uint32_t ob = off_mem(b), oe = off_mem(b + 1);
-                if (oe > ob) {
-                    const uint32_t e1 = end < oe ? end : oe;
-                    const int tk = (int)(e1 - p);
-                    const uint32_t sp = kCapBits - (oe - ob) + (p - ob);
-                    const uint32_t* sc = scr0 + (int64_t)b * kCapW;
-                    uint64_t x = sc[sp >> 5];
-                    if ((int)(sp & 31u) + tk > 32) x |= (uint64_t)sc[(sp >> 5) + 1] << 32;
-                    x >>= (sp & 31u);
-                    res[u] |= (tk == 32 ? (uint32_t)x : (uint32_t)x & ((1u << tk) - 1u)) << got;
-                    got += tk;
-                    p = e1;
+            if (p < end) {
+                // block b + 1 (its first bits were loaded above when it is not empty)
+                const uint32_t e2 = end < nx[u] ? end : nx[u];
+                const int tk = (int)(e2 - p);
+                const uint64_t x = ((uint64_t)chi[u] << 32 | clo[u]) >> cs[u];
+                res |= (tk == 32 ? (uint32_t)x : (uint32_t)x & ((1u << tk) - 1u)) << got;
+                got += tk;
+                p = e2;
+                int b = blk[u] + 2;
+                while (p < end) {   // rare: block b + 1 ends inside the word too
+                    const uint32_t ob = off_at(b), oe = off_at(b + 1);
+                    if (oe > ob) {
+                        const uint32_t e1 = end < oe ? end : oe;
+                        const int tk2 = (int)(e1 - p);
+                        const uint32_t sp = kCapBits - (oe - ob) + (p - ob);
+                        const uint32_t* sc = scr0 + (int64_t)b * kCapW;
+                        uint64_t y = sc[sp >> 5];
+                        if ((int)(sp & 31u) + tk2 > 32) y |= (uint64_t)sc[(sp >> 5) + 1] << 32;
+                        y >>= (sp & 31u);
+                        res |= (tk2 == 32 ? (uint32_t)y : (uint32_t)y & ((1u << tk2) - 1u)) << got;
+                        got += tk2;
+                        p = e1;
+                    }
+                    b++;
                 }
-                b++;
             }
-            out[w] = res[u];
+            out[w] = res;
         }
     }
 }
