@@ -445,7 +445,7 @@ __host__ __device__ inline EncWork enc_layout(int64_t n_chunks, int64_t n_vector
 constexpr int kEncBlocks = 16;   // blocks per encode workgroup (x 16 streams)
 
 // Grid: (block groups, chunks).  The scratch words of a task are collected in
-// an 8-word register queue and stored as aligned 32-byte pieces.
+// an 8-word LDS queue and stored as aligned 32-byte pieces.
 template <typename SymT>
 __global__ __launch_bounds__(256) void k_chunk_encode(const SymT* __restrict__ sym, const uint32_t* __restrict__ blk_n1,
                                                       int64_t nblk, int64_t V, const lq_table* __restrict__ tables,
@@ -456,6 +456,7 @@ __global__ __launch_bounds__(256) void k_chunk_encode(const SymT* __restrict__ s
     constexpr int kCap = sizeof(SymT) == 1 ? 264 : LQ_MAXSYM;
     __shared__ uint32_t senc[LQ_STREAMS][kCap + 1];
     __shared__ int slo[LQ_STREAMS], snsym[LQ_STREAMS];
+    __shared__ uint32_t sq[8][256];   // per-lane queue of scratch words
     const int tid = threadIdx.x;
     const int64_t chunk = blockIdx.y;
     const int64_t g = (int64_t)blockIdx.x * kEncBlocks + (tid >> 4);
@@ -521,19 +522,19 @@ __global__ __launch_bounds__(256) void k_chunk_encode(const SymT* __restrict__ s
     // ---- encode block g, bits right-aligned in the task's scratch region
     Col<SymT> col = column(sym, blk_n1, chunk, nblk, V, g, c, idx);
     uint32_t* scr = scratch + task * (int64_t)kCapW;
-    // words leave in decreasing address order from kCapW - 1; queue word j of the
-    // current 8-word group at q[j] (newest at q[0]) and store the group when full
-    uint32_t q[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    // words leave in decreasing address order from kCapW - 1; word j of the
+    // current 8-word group waits in LDS at qcol[(7 - j) * 256] (this lane's
+    // column, so a wave's writes are contiguous) and the group leaves as two
+    // 16-byte stores when full
+    uint32_t* const qcol = &sq[0][tid];
     int nq = 0, gbase = kCapW - 8, nwords = 0;
     auto push = [&](uint32_t word) {
-#pragma unroll
-        for (int j = 7; j > 0; j--) q[j] = q[j - 1];
-        q[0] = word;
+        qcol[(7 - nq) * 256] = word;
         nwords++;
         if (++nq == 8) {
             uint4* d = reinterpret_cast<uint4*>(scr + gbase);
-            d[0] = make_uint4(q[0], q[1], q[2], q[3]);
-            d[1] = make_uint4(q[4], q[5], q[6], q[7]);
+            d[0] = make_uint4(qcol[0], qcol[256], qcol[512], qcol[768]);
+            d[1] = make_uint4(qcol[1024], qcol[1280], qcol[1536], qcol[1792]);
             gbase -= 8;
             nq = 0;
         }
@@ -561,10 +562,11 @@ __global__ __launch_bounds__(256) void k_chunk_encode(const SymT* __restrict__ s
     }
     const uint32_t total = 32u * (uint32_t)nwords + nacc;
     if (nacc) push((uint32_t)(acc << (32 - nacc)));
-    // complete the last group with filler words below the data (never read)
-#pragma unroll
-    for (int j = 0; j < 7; j++)
-        if (nq != 0) push(0u);
+    if (nq) {   // the last, partial group: its words sit in the top nq slots
+        uint4* d = reinterpret_cast<uint4*>(scr + gbase);
+        d[0] = make_uint4(qcol[0], qcol[256], qcol[512], qcol[768]);
+        d[1] = make_uint4(qcol[1024], qcol[1280], qcol[1536], qcol[1792]);
+    }
     blk_bits[task] = total;
     blk_state[task] = (uint16_t)x;
 }
