@@ -299,9 +299,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--group", type=int, default=32, help="chunks per kernel launch in the timed step")
-    ap.add_argument("--streams", type=int, default=2,
-                    help="streams the chunk groups of a step are dealt to (their kernels overlap on the GPU)")
+    ap.add_argument("--group", type=int, default=64, help="chunks per kernel launch in the timed step")
+    ap.add_argument("--streams", type=int, default=1,
+                    help="streams the chunk groups of a step are dealt to (measured: one 64-chunk group on one "
+                         "stream is fastest; concurrent groups do not overlap usefully)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-chunks", type=int, default=8)
     ap.add_argument("--no-decode-step", action="store_true", help="skip the C3 decode-step measurement")
@@ -364,9 +365,8 @@ def main():
             codec.decode_batch(encs[gi], out=out[a:b], lut_work=luts[0])
 
     def step():
-        """Write then read every chunk group; group gi runs on stream gi % NS, so
-        one group's memory-bound kernels (scales, bitstream assembly) overlap
-        another's instruction-bound ones (quantizer, encoder, decoder)."""
+        """Write then read every chunk group; group gi runs on stream gi % NS
+        (defaults: one group of all 64 chunks, one stream)."""
         cur = torch.cuda.current_stream(dev)
         for st in streams:
             st.wait_stream(cur)
