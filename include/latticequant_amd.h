@@ -323,7 +323,7 @@ int lq_rht(const void *d_x, int in_dtype, int64_t n_rows, int d, const float *d_
 
 /* Fixed-width resident form of a compressed KV prefix (head_dim 128), read by
  * lq_resident_attention.  Per kv head, tokens in blocks of 16; per block 256
- * vector records laid out [slot 0..63][group 0..3] (record (slot, group) is
+ * vector records laid out [group 0..3][slot 0..63] (record (slot, group) is
  * vector 4*group + slot/16 of token 16*block + slot%16).  A record is the
  * reference's b = 5 fixed-rate code word of the lattice point
  * (core/compact_storage.py:87-154: coset, c0..c6 + 16 in 5 bits, (c7 + 16) >> 1
@@ -341,8 +341,8 @@ int lq_rht(const void *d_x, int in_dtype, int64_t n_rows, int d, const float *d_
  * the index of the block's first entry in exc[].  scale[token] is the fp16
  * scale the token's chunk stores. */
 typedef struct {
-    uint32_t *a;             /* [n_heads][cap_blocks][64][4] */
-    uint8_t *b;              /* [n_heads][cap_blocks][64][4] */
+    uint32_t *a;             /* [n_heads][cap_blocks][4][64] */
+    uint8_t *b;              /* [n_heads][cap_blocks][4][64] */
     uint64_t *mask;          /* [n_heads][cap_blocks][4] */
     uint32_t *meta;          /* [n_heads][cap_blocks][4] */
     int16_t *exc;            /* [exc_cap][8] */

@@ -7,10 +7,9 @@
 // b = 5 compact code word per vector (core/compact_storage.py:87-154), 40 bits
 // split into a uint32 and a uint8 plane (layout in latticequant_amd.h), plus
 // int16 exception entries for the rare vectors outside the 5-bit range.  A
-// 16-token block of one kv head is 256 records stored [slot][group]: record
-// (slot, group) is vector 4*group + slot/16 of token slot%16, which is the B
-// operand layout of v_mfma_f32_16x16x32_f16 for q . k^T (lane = slot, its 8
-// halves = the 8 dimensions of one vector).
+// 16-token block of one kv head is 256 records stored group-major: record
+// (slot, group) is vector 4*group + slot/16 of token slot%16 and sits at
+// group * 64 + slot, so one group of a block is 64 records in a row.
 //
 // Decoding a record to fp16 is bit arithmetic: a 5-bit field u placed at bit
 // 1 of a half whose high bits are 0x64 gives the fp16 number 1024 + 2u + coset
@@ -20,15 +19,17 @@
 // writes for the token's fp16 scale s.  The MFMA operands are therefore the
 // fp16 K / V the reference's attention reads.
 //
-// lq_resident_attention: per (kv head, 512-token split) one workgroup of four
-// waves; a wave takes 32-token tiles:
+// lq_resident_attention: per (kv head, split) one workgroup of eight waves; a
+// wave takes 32-token tiles:
 //   S = Q K^T        8 MFMA 16x16x32 (rows: the group's query heads, spread so
-//                    that query head h sits in row 4 (h % 4) + h / 4)
-//   online softmax   exp2, row max by DPP within 16 lanes
-//   O += P V         P (fp16) and V go through LDS: V is decoded two tokens
-//                    per lane into (token t, token t+1) pairs and stored
-//                    dimension-major, so each MFMA B operand is two 8-byte reads
-// then the four waves merge their (m, l, O) in LDS, each workgroup writes one
+//                    that query head h sits in row 4 (h % 4) + h / 4); lane l
+//                    decodes records (slot l, group c) of each block
+//   online softmax   exp2, row max by DPP within 16 lanes; P (fp16) through
+//                    LDS into the A operand layout
+//   O += P V         lane l decodes vector l % 16 of 8 consecutive tokens, and
+//                    MFMA mm's column n is dimension 8 n + mm, so the V pairs
+//                    become B operands in registers (v_perm), without LDS
+// then the waves merge their (m, l, O) in LDS, each workgroup writes one
 // record per query head, and the last workgroup of a kv head (device-scope
 // counter) merges the records and writes the output.
 #include <climits>
@@ -183,8 +184,8 @@ __global__ __launch_bounds__(256) void k_res_quant(const void* __restrict__ x, i
     uint32_t a, b;
     const bool ok = rec_encode(ic, cs, &a, &b);
     const int64_t rb = (h0 + hh) * r.cap_blocks + blk0 + bb;
-    r.a[(rb * 64 + slot) * 4 + grp] = a;
-    r.b[(rb * 64 + slot) * 4 + grp] = (uint8_t)b;
+    r.a[rb * 256 + grp * 64 + slot] = a;
+    r.b[rb * 256 + grp * 64 + slot] = (uint8_t)b;
     const unsigned long long m = __ballot(!ok);
     if (slot == 0) {
         r.mask[rb * 4 + grp] = m;
@@ -315,7 +316,7 @@ __global__ __launch_bounds__(256) void k_res_dequant(lq_resident r, int64_t h0, 
         }
     } else {
         uint32_t p[4];
-        rec_pairs(r.a[(rb * 64 + slot) * 4 + grp], r.b[(rb * 64 + slot) * 4 + grp], p);
+        rec_pairs(r.a[rb * 256 + grp * 64 + slot], r.b[rb * 256 + grp * 64 + slot], p);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const h2_t h = __builtin_bit_cast(h2_t, p[i]);
@@ -335,10 +336,11 @@ __global__ __launch_bounds__(256) void k_res_dequant(lq_resident r, int64_t h0, 
 constexpr int kAW = 8;                          // waves per workgroup
 constexpr int kTile = 32;                       // tokens per tile (two blocks)
 constexpr int kWaveTiles = 4;
-constexpr int kVtRow = 18;                      // uint32 per LDS V row (32 tokens fp16 + 8 B pad)
 constexpr int kPtRow = 20;                      // uint32 per LDS P row (32 tokens fp16 + 16 B pad)
 constexpr int kRecF = 4 + kHd;                  // floats per split record (m, l, 2 pad, o[128])
 constexpr int kMaxRec = 2048;                   // (split, head) records one merge can take
+constexpr int kMergeF = 4 * kMaxRec;            // floats of the merge buffer (3 record arrays + partial sums)
+constexpr int kMergeH = kMergeF / (kAW * kHd);  // query heads per round of the workgroup merge
 constexpr int kCtrStride = 64;                  // uint32 per completion counter (one per 256-byte line)
 
 struct AttnArgs {
@@ -379,19 +381,23 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// ---- prefix tiles: records loaded one tile ahead into registers
+// ---- prefix tiles
 //
-// K lane layout: block x (0, 1), slot = lane: token 16 x + lane % 16, vectors
-// 4 c + lane / 16 (c = 0..3).  V lane layout: group j = lane / 16, block
-// xb = (lane / 8) % 2, token pair u = lane % 8: tokens 16 xb + 2 u, + 1 of
-// vectors 4 c + j.
+// K lane layout (B operand of S = Q K^T): block x (0, 1), slot = lane: token
+// 16 x + lane % 16, vectors 4 c + lane / 16 = records (slot lane, group c).
+// V lane layout (B operand of O += P V): column n = lane % 16, token octet
+// k8 = lane / 16 (tokens 8 k8 .. 8 k8 + 7 of the tile, block k8 / 2): the
+// lane decodes the 8 records of vector n of those tokens (8 consecutive slots
+// of group n / 4), and MFMA mm of P V takes dimension 8 n + mm of each token
+// for column n, so the output column n of MFMA mm is dimension 8 n + mm and
+// the decoded records feed the MFMAs without a transpose through LDS.
 struct TileRaw {
-    uint4 ka[2];            // K records (c = 0..3) of blocks 0, 1
-    uint32_t kb[2];
+    uint32_t ka[2][4];      // K record words of blocks 0, 1, groups 0..3
+    uint32_t kb[2][4];      // their low bytes
     uint32_t ks;            // fp16 scale of the K token of block 0 (low) and 1 (high)
-    uint4 va0, va1;         // V records of tokens ta, ta + 1
-    uint2 vb;
-    uint32_t vs;            // fp16 scales of tokens ta, ta + 1
+    uint4 va0, va1;         // V records of the lane's 8 tokens (vector lane % 16)
+    uint2 vb;               // their low bytes
+    uint4 vs;               // fp16 scales of those 8 tokens
     uint4 meta;             // lanes 0..3: block metadata of K block 0, 1, V block 0, 1
 };
 
@@ -419,8 +425,11 @@ __device__ __forceinline__ void tile_load(const AttnArgs& A, int64_t kvh, int64_
     for (int x = 0; x < 2; x++) {
         const int64_t tb = min(t0 + 16 * x, last);
         const int64_t rb = hb + tb / kRB;
-        d.ka[x] = reinterpret_cast<const uint4*>(A.k.a)[rb * 64 + lane];
-        d.kb[x] = reinterpret_cast<const uint32_t*>(A.k.b)[rb * 64 + lane];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            d.ka[x][c] = A.k.a[rb * 256 + c * 64 + lane];
+            d.kb[x][c] = A.k.b[rb * 256 + c * 64 + lane];
+        }
         ks[x] = A.k.scale[hb * kRB + tb + (lane & 15)];
     }
     d.ks = ks[0] | (ks[1] << 16);
@@ -432,15 +441,15 @@ __device__ __forceinline__ void tile_load(const AttnArgs& A, int64_t kvh, int64_
         const uint32_t* mp = ((i & 2) ? A.v.meta : A.k.meta) + (hb + tb / kRB) * 4;
         d.meta = *reinterpret_cast<const uint4*>(mp);
     }
-    const int j = lane >> 4, xb = (lane >> 3) & 1, u = lane & 7;
-    const int64_t tb = min(t0 + 16 * xb, last);
+    const int n = lane & 15, k8 = lane >> 4;
+    const int64_t tb = min(t0 + 16 * (k8 >> 1), last);
     const int64_t rb = hb + tb / kRB;
-    const int s0 = 16 * j + 2 * u;
-    const uint4* ap = reinterpret_cast<const uint4*>(A.v.a) + rb * 64 + s0;
+    const int64_t r0 = rb * 256 + (n >> 2) * 64 + 16 * (n & 3) + 8 * (k8 & 1);   // 8 consecutive records
+    const uint4* ap = reinterpret_cast<const uint4*>(A.v.a + r0);
     d.va0 = ap[0];
     d.va1 = ap[1];
-    d.vb = reinterpret_cast<const uint2*>(A.v.b)[(rb * 64 + s0) >> 1];
-    d.vs = *reinterpret_cast<const uint32_t*>(A.v.scale + hb * kRB + tb + 2 * u);
+    d.vb = *reinterpret_cast<const uint2*>(A.v.b + r0);
+    d.vs = *reinterpret_cast<const uint4*>(A.v.scale + hb * kRB + tb + 8 * (k8 & 1));
 }
 
 // exception k of a block (0 <= k < count): slot | group << 6 from the header,
@@ -460,98 +469,89 @@ __device__ __forceinline__ int exc_code(const lq_resident& r, int64_t rb, uint64
     return -1;
 }
 
-// K operands of block x from the tile registers
+// Scores of block x: s += q . k over the four record groups, each group's K
+// operand decoded (and, rarely, patched with exception entries) just before
+// its MFMA, so that only one group's pairs are live at a time.
 __device__ __forceinline__ void tile_k(const AttnArgs& A, const TileRaw& d, int64_t rb, int x, int lane, bool fast,
-                                       uint32_t mk, h8_t kb[4]) {
-    const uint32_t aa[4] = {d.ka[x].x, d.ka[x].y, d.ka[x].z, d.ka[x].w};
-    uint32_t p[4][4];
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        rec_pairs(aa[c], d.kb[x] >> (8 * c), p[c]);
-#pragma unroll
-        for (int i = 0; i < 4; i++) p[c][i] = unbias(p[c][i]);
-    }
+                                       uint32_t mk, const h8_t qa[4], f4_t& s) {
     const uint64_t hdr = meta_hdr(d, x);
     const int n = (int)(hdr & 0xffu);
-    if (n) {   // rare: exception entries replace records (uniform loop)
-        const int64_t base = meta_base(d, x);
-        const int cnt = n < 255 ? n : 4 * 64;
-        for (int e = 0; e < cnt; e++) {
-            const int code = exc_code(A.k, rb, hdr, e);
-            if (code < 0) break;
-            const int64_t idx = base + e;
-            if ((code & 63) == lane && idx < A.k.exc_cap) {
-                int v[8];
-                exc_load(A.k.exc, idx, v);
-                const int g = code >> 6;
+    const uint16_t sk = (uint16_t)(x ? d.ks >> 16 : d.ks & 0xffffu);
 #pragma unroll
-                for (int c = 0; c < 4; c++)
+    for (int c = 0; c < 4; c++) {
+        uint32_t p[4];
+        rec_pairs(d.ka[x][c], d.kb[x][c], p);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) p[c][i] = g == c ? pair_from_i16(v[2 * i], v[2 * i + 1]) : p[c][i];
+        for (int i = 0; i < 4; i++) p[i] = unbias(p[i]);
+        if (n) {   // rare: exception entries of group c replace records (uniform loop)
+            const int64_t base = meta_base(d, x);
+            const int cnt = n < 255 ? n : 4 * 64;
+            for (int e = 0; e < cnt; e++) {
+                const int code = exc_code(A.k, rb, hdr, e);
+                if (code < 0) break;
+                const int64_t idx = base + e;
+                if ((code >> 6) == c && (code & 63) == lane && idx < A.k.exc_cap) {
+                    int v[8];
+                    exc_load(A.k.exc, idx, v);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) p[i] = pair_from_i16(v[2 * i], v[2 * i + 1]);
+                }
             }
         }
+        if (fast) mul_pairs<4>(p, mk);
+        else dequant_pairs<4>(p, sk, sk);
+        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], as_h8(p[0], p[1], p[2], p[3]), s, 0, 0, 0);
     }
-    if (fast) {
-#pragma unroll
-        for (int c = 0; c < 4; c++) mul_pairs<4>(p[c], mk);
-    } else {
-        const uint16_t sk = (uint16_t)(x ? d.ks >> 16 : d.ks & 0xffffu);
-#pragma unroll
-        for (int c = 0; c < 4; c++) dequant_pairs<4>(p[c], sk, sk);
-    }
-#pragma unroll
-    for (int c = 0; c < 4; c++) kb[c] = as_h8(p[c][0], p[c][1], p[c][2], p[c][3]);
 }
 
-// V of the tile into LDS, dimension-major: vt[d * kVtRow + token / 2] holds
-// (token, token + 1) of dimension d
+// V of the lane's 8 tokens (vector lane % 16): vp[q][i] = fp16 pair of
+// dimensions (8 n + 2 i, 8 n + 2 i + 1) of token q, dequantised.
 __device__ __forceinline__ void tile_v(const AttnArgs& A, const TileRaw& d, int64_t rb0, int lane, bool fast,
-                                       uint32_t mv, uint32_t* vt) {
-    const int j = lane >> 4, xb = (lane >> 3) & 1, u = lane & 7;
-    const int s0 = 16 * j + 2 * u;
-    const uint32_t x0[4] = {d.va0.x, d.va0.y, d.va0.z, d.va0.w}, x1[4] = {d.va1.x, d.va1.y, d.va1.z, d.va1.w};
-    uint32_t pr[4][8];
+                                       const uint32_t mv[8], uint32_t vp[8][4]) {
+    const int n = lane & 15, k8 = lane >> 4, xb = k8 >> 1;
+    const uint32_t aw[8] = {d.va0.x, d.va0.y, d.va0.z, d.va0.w, d.va1.x, d.va1.y, d.va1.z, d.va1.w};
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        rec_pairs_tok(x0[c], d.vb.x >> (8 * c), x1[c], d.vb.y >> (8 * c), pr[c]);
+    for (int q = 0; q < 8; q++) {
+        rec_pairs(aw[q], (q < 4 ? d.vb.x : d.vb.y) >> (8 * (q & 3)), vp[q]);
 #pragma unroll
-        for (int i = 0; i < 8; i++) pr[c][i] = unbias(pr[c][i]);
+        for (int i = 0; i < 4; i++) vp[q][i] = unbias(vp[q][i]);
     }
     const uint64_t h0 = meta_hdr(d, 2), h1 = meta_hdr(d, 3);
-    if ((h0 | h1) & 0xffull) {   // rare: exception entries replace records
-        const uint64_t hdr = xb ? h1 : h0;
-        const int64_t base = xb ? meta_base(d, 3) : meta_base(d, 2);
-        const int n = (int)(hdr & 0xffu);
-        const int cnt = n < 255 ? n : 4 * 64;
-        for (int e = 0; e < cnt; e++) {
-            const int code = exc_code(A.v, rb0 + xb, hdr, e);
-            if (code < 0) break;
-            const int sl = code & 63;
-            const int64_t idx = base + e;
-            if ((sl == s0 || sl == s0 + 1) && idx < A.v.exc_cap) {
-                int v[8];
-                exc_load(A.v.exc, idx, v);
-                const int g = code >> 6, hi = sl - s0;
+    if ((h0 | h1) & 0xffull) {   // rare: exception entries replace records (uniform loops)
+#pragma unroll 1
+        for (int x = 0; x < 2; x++) {
+            const uint64_t hdr = x ? h1 : h0;
+            const int64_t base = x ? meta_base(d, 3) : meta_base(d, 2);
+            const int cnt0 = (int)(hdr & 0xffu);
+            const int cnt = cnt0 < 255 ? cnt0 : 4 * 64;
+            for (int e = 0; e < cnt; e++) {
+                const int code = exc_code(A.v, rb0 + x, hdr, e);
+                if (code < 0) break;
+                const int sl = code & 63, g = code >> 6;
+                const int64_t idx = base + e;
+                // the lane holding (slot sl, group g) of block x, and its token q
+                const bool mine = xb == x && n == 4 * g + (sl >> 4) && (k8 & 1) == ((sl & 15) >> 3);
+                if (mine && idx < A.v.exc_cap) {
+                    int v[8];
+                    exc_load(A.v.exc, idx, v);
+                    const int qq = sl & 7;
 #pragma unroll
-                for (int c = 0; c < 4; c++)
+                    for (int q = 0; q < 8; q++)
 #pragma unroll
-                    for (int i = 0; i < 8; i++) {
-                        h2_t h = __builtin_bit_cast(h2_t, pr[c][i]);
-                        if (g == c) {
-                            if (hi) h[1] = (_Float16)(float)v[i];
-                            else h[0] = (_Float16)(float)v[i];
-                        }
-                        pr[c][i] = __builtin_bit_cast(uint32_t, h);
-                    }
+                        for (int i = 0; i < 4; i++) vp[q][i] = q == qq ? pair_from_i16(v[2 * i], v[2 * i + 1]) : vp[q][i];
+                }
             }
         }
     }
+    const uint32_t sw[4] = {d.vs.x, d.vs.y, d.vs.z, d.vs.w};
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        if (fast) mul_pairs<8>(pr[c], mv);
-        else dequant_pairs<8>(pr[c], (uint16_t)(d.vs & 0xffffu), (uint16_t)(d.vs >> 16));
-#pragma unroll
-        for (int i = 0; i < 8; i++) vt[(8 * (4 * c + j) + i) * kVtRow + 8 * xb + u] = pr[c][i];
+    for (int q = 0; q < 8; q++) {
+        if (fast) {
+            mul_pairs<4>(vp[q], mv[q]);
+        } else {
+            const uint16_t sq = (uint16_t)(sw[q >> 1] >> (16 * (q & 1)));
+            dequant_pairs<4>(vp[q], sq, sq);
+        }
     }
 }
 
@@ -566,29 +566,25 @@ __device__ __forceinline__ void tail_k(const AttnArgs& A, int64_t kvh, int64_t t
     }
 }
 
-__device__ __forceinline__ void tail_v(const AttnArgs& A, int64_t kvh, int64_t t0, int64_t T, int lane, uint32_t* vt) {
-    const int j = lane >> 4, xb = (lane >> 3) & 1, u = lane & 7;
-    const int64_t ta = t0 + 16 * xb + 2 * u;
+__device__ __forceinline__ void tail_v(const AttnArgs& A, int64_t kvh, int64_t t0, int64_t T, int lane,
+                                       uint32_t vp[8][4]) {
+    const int n = lane & 15, k8 = lane >> 4;
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        uint4 w0 = make_uint4(0u, 0u, 0u, 0u), w1 = w0;
-        const int64_t off = 32 * c + 8 * j;
-        if (ta < T) w0 = *reinterpret_cast<const uint4*>(A.tail_v + (kvh * T + ta) * kHd + off);
-        if (ta + 1 < T) w1 = *reinterpret_cast<const uint4*>(A.tail_v + (kvh * T + ta + 1) * kHd + off);
-        const uint32_t x0[4] = {w0.x, w0.y, w0.z, w0.w}, x1[4] = {w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            vt[(8 * (4 * c + j) + 2 * i) * kVtRow + 8 * xb + u] = __builtin_amdgcn_perm(x1[i], x0[i], 0x05040100u);
-            vt[(8 * (4 * c + j) + 2 * i + 1) * kVtRow + 8 * xb + u] = __builtin_amdgcn_perm(x1[i], x0[i], 0x07060302u);
-        }
+    for (int q = 0; q < 8; q++) {
+        const int64_t t = t0 + 8 * k8 + q;
+        uint4 w = make_uint4(0u, 0u, 0u, 0u);
+        if (t < T) w = *reinterpret_cast<const uint4*>(A.tail_v + (kvh * T + t) * kHd + 8 * n);
+        vp[q][0] = w.x; vp[q][1] = w.y; vp[q][2] = w.z; vp[q][3] = w.w;
     }
 }
 
-// Online softmax of one tile's scores, P into LDS, O += P V (V already in LDS).
+// Online softmax of one tile's scores, P through LDS into the A operand,
+// O += P V with the B operands built from the lane's V pairs: MFMA mm takes
+// half mm % 2 of pair mm / 2 of the 8 tokens.
 template <int HPL>
 __device__ __forceinline__ void tile_softmax_pv(int G, const f4_t s[2], const bool valid[2], int lane,
-                                                const uint32_t* vt, uint32_t* pt, float m_run[HPL], float l_run[HPL],
-                                                f4_t o[8]) {
+                                                const uint32_t vp[8][4], uint32_t* pt, float m_run[HPL],
+                                                float l_run[HPL], f4_t o[8]) {
     const float c0 = 1.4426950408889634f / 11.313708498984761f;   // log2(e) / sqrt(128)
     _Float16* ph = reinterpret_cast<_Float16*>(pt);
 #pragma unroll
@@ -609,72 +605,79 @@ __device__ __forceinline__ void tile_softmax_pv(int G, const f4_t s[2], const bo
         ph[row * (2 * kPtRow) + 16 + (lane & 15)] = hv ? (_Float16)p1 : (_Float16)0.f;
     }
     wave_lds_sync();
-    // A = P rows (query heads) x 32 tokens, B = V 32 tokens x 16 dims
+    // A = P rows (query heads) x 32 tokens, B = V 32 tokens x 16 columns
     const uint4 pa = *reinterpret_cast<const uint4*>(pt + (lane & 15) * kPtRow + 4 * (lane >> 4));
     const h8_t pA = __builtin_bit_cast(h8_t, pa);
 #pragma unroll
     for (int mm = 0; mm < 8; mm++) {
-        const uint32_t* vr = vt + (16 * mm + (lane & 15)) * kVtRow + 4 * (lane >> 4);
-        const uint2 lo = *reinterpret_cast<const uint2*>(vr);
-        const uint2 hi = *reinterpret_cast<const uint2*>(vr + 2);
-        o[mm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pA, as_h8(lo.x, lo.y, hi.x, hi.y), o[mm], 0, 0, 0);
+        const uint32_t sel = (mm & 1) ? 0x07060302u : 0x05040100u;
+        const int i = mm >> 1;
+        const h8_t vB = as_h8(__builtin_amdgcn_perm(vp[1][i], vp[0][i], sel), __builtin_amdgcn_perm(vp[3][i], vp[2][i], sel),
+                              __builtin_amdgcn_perm(vp[5][i], vp[4][i], sel), __builtin_amdgcn_perm(vp[7][i], vp[6][i], sel));
+        o[mm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pA, vB, o[mm], 0, 0, 0);
     }
     wave_lds_sync();
 }
 
-// one prefix tile from its registers (rb0: resident block of the tile's first token)
+// Decode of one prefix tile from its registers (rb0: resident block of the
+// tile's first token): the scores s of its two blocks and the V pairs.
 template <int HPL>
-__device__ __forceinline__ void prefix_tile(const AttnArgs& A, const TileRaw& d, int64_t rb0, int64_t t0, int64_t T,
-                                            int lane, const h8_t qa[4], uint32_t* vt, uint32_t* pt,
-                                            float m_run[HPL], float l_run[HPL], f4_t o[8]) {
+__device__ __forceinline__ void prefix_decode(const AttnArgs& A, const TileRaw& d, int64_t rb0, int64_t t0, int64_t T,
+                                              int lane, const h8_t qa[4], f4_t s[2], bool valid[2],
+                                              uint32_t vp[8][4]) {
     // dequant multipliers (s / 2 per token); the packed-multiply path is
     // taken when every scale of the tile allows it (wave-uniform)
-    bool e0, e1, e2;
+    bool e0, e1, ev = true;
     const uint32_t mk0 = half_scales((d.ks & 0xffffu) * 0x10001u, &e0);
     const uint32_t mk1 = half_scales((d.ks >> 16) * 0x10001u, &e1);
-    const uint32_t mv = half_scales(d.vs, &e2);
-    const bool fast = __all(e0 && e1 && e2);
-    f4_t s[2];
-    bool valid[2];
+    const uint32_t sw[4] = {d.vs.x, d.vs.y, d.vs.z, d.vs.w};
+    uint32_t mv[8];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        bool e;
+        const uint32_t hp = half_scales(sw[k], &e);   // (s_2k / 2, s_2k+1 / 2)
+        ev = ev && e;
+        mv[2 * k] = __builtin_amdgcn_perm(hp, hp, 0x01000100u);       // low half twice
+        mv[2 * k + 1] = __builtin_amdgcn_perm(hp, hp, 0x03020302u);   // high half twice
+    }
+    const bool fast = __all(e0 && e1 && ev);
 #pragma unroll
     for (int x = 0; x < 2; x++) {
         s[x] = f4_t{0.f, 0.f, 0.f, 0.f};
         valid[x] = t0 + 16 * x + (lane & 15) < T;
-        if (t0 + 16 * x < T) {   // wave-uniform
-            h8_t kb[4];
-            tile_k(A, d, rb0 + x, x, lane, fast, x ? mk1 : mk0, kb);
-#pragma unroll
-            for (int c = 0; c < 4; c++) s[x] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], kb[c], s[x], 0, 0, 0);
-        }
+        if (t0 + 16 * x < T)   // wave-uniform
+            tile_k(A, d, rb0 + x, x, lane, fast, x ? mk1 : mk0, qa, s[x]);
     }
-    tile_v(A, d, rb0, lane, fast, mv, vt);
-    tile_softmax_pv<HPL>(A.group, s, valid, lane, vt, pt, m_run, l_run, o);
+    tile_v(A, d, rb0, lane, fast, mv, vp);
 }
 
-// The wave's prefix tiles, records loaded one tile ahead (two register sets,
-// no copies).  Tiles are dealt round-robin over all waves of the kv head (wave
-// gw of W takes tiles gw, gw + W, ...): the waves in flight read one
-// contiguous stretch of the prefix at a time instead of W strided ones.
+// The wave's prefix tiles.  One register set: a tile's records are decoded
+// (scores, V pairs) and the set is reloaded with the next tile's records,
+// which are in flight during this tile's softmax and P V (a second set,
+// loading a whole tile ahead, measured no faster).  Tiles are dealt
+// round-robin over all waves of the kv head (wave gw of W takes tiles gw,
+// gw + W, ...): the waves in flight read one contiguous stretch of the
+// prefix at a time instead of W strided ones.
 template <int HPL>
 __device__ __forceinline__ void prefix_tiles(const AttnArgs& A, int64_t kvh, int64_t gw, int64_t W, int64_t T,
-                                             int lane, const h8_t qa[4], uint32_t* vt, uint32_t* pt, float m_run[HPL],
+                                             int lane, const h8_t qa[4], uint32_t* pt, float m_run[HPL],
                                              float l_run[HPL], f4_t o[8]) {
     const int64_t step = W * kTile;
     int64_t ta = gw * kTile;
     if (ta >= T) return;
     const int64_t hb = kvh * A.k.cap_blocks;
-    TileRaw d0, d1;
-    tile_load(A, kvh, ta, T, lane, d0);
+    TileRaw d;
+    tile_load(A, kvh, ta, T, lane, d);
     while (true) {
         const int64_t tb = ta + step;
-        if (tb < T) tile_load(A, kvh, tb, T, lane, d1);
-        prefix_tile<HPL>(A, d0, hb + ta / kRB, ta, T, lane, qa, vt, pt, m_run, l_run, o);
+        f4_t s[2];
+        bool valid[2];
+        uint32_t vp[8][4];
+        prefix_decode<HPL>(A, d, hb + ta / kRB, ta, T, lane, qa, s, valid, vp);
+        if (tb < T) tile_load(A, kvh, tb, T, lane, d);
+        tile_softmax_pv<HPL>(A.group, s, valid, lane, vp, pt, m_run, l_run, o);
         if (tb >= T) break;
-        const int64_t tc = tb + step;
-        if (tc < T) tile_load(A, kvh, tc, T, lane, d0);
-        prefix_tile<HPL>(A, d1, hb + tb / kRB, tb, T, lane, qa, vt, pt, m_run, l_run, o);
-        if (tc >= T) break;
-        ta = tc;
+        ta = tb;
     }
 }
 
@@ -682,7 +685,7 @@ __device__ __forceinline__ void prefix_tiles(const AttnArgs& A, int64_t kvh, int
 // the same round-robin (g = prefix tiles + tail tile), fp16 K / V read directly.
 template <int HPL>
 __device__ __forceinline__ void tail_tiles(const AttnArgs& A, int64_t kvh, int64_t gw, int64_t W, int64_t npt,
-                                           int64_t T, int lane, const h8_t qa[4], uint32_t* vt, uint32_t* pt,
+                                           int64_t T, int lane, const h8_t qa[4], uint32_t* pt,
                                            float m_run[HPL], float l_run[HPL], f4_t o[8]) {
     int64_t g = gw;
     if (g < npt) g += (npt - g + W - 1) / W * W;   // first index of this wave past the prefix
@@ -701,15 +704,16 @@ __device__ __forceinline__ void tail_tiles(const AttnArgs& A, int64_t kvh, int64
                 for (int c = 0; c < 4; c++) s[x] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], kb[c], s[x], 0, 0, 0);
             }
         }
-        tail_v(A, kvh, t0, T, lane, vt);
-        tile_softmax_pv<HPL>(A.group, s, valid, lane, vt, pt, m_run, l_run, o);
+        uint32_t vp[8][4];
+        tail_v(A, kvh, t0, T, lane, vp);
+        tile_softmax_pv<HPL>(A.group, s, valid, lane, vp, pt, m_run, l_run, o);
     }
 }
 
 template <int HPL>
 __global__ __launch_bounds__(kAW * 64) void k_res_attn(AttnArgs A) {
-    __shared__ __align__(16) uint32_t s_vt[kAW][kHd * kVtRow];
     __shared__ __align__(16) uint32_t s_pt[kAW][16 * kPtRow];
+    __shared__ __align__(16) float s_buf[kMergeF];   // the waves' O rows, then the last workgroup's merge
     __shared__ float s_m[kAW][16], s_l[kAW][16];
     __shared__ float s_L[16];
     __shared__ int s_last;
@@ -736,7 +740,6 @@ __global__ __launch_bounds__(kAW * 64) void k_res_attn(AttnArgs A) {
             qa[c] = __builtin_bit_cast(h8_t, w);
         }
     }
-    uint32_t* vt = s_vt[wave];
     uint32_t* pt = s_pt[wave];
     for (int i = lane; i < 16 * kPtRow; i += 64) pt[i] = 0u;
     wave_lds_sync();
@@ -746,44 +749,50 @@ __global__ __launch_bounds__(kAW * 64) void k_res_attn(AttnArgs A) {
     for (int i = 0; i < HPL; i++) { m_run[i] = -INFINITY; l_run[i] = 0.f; }
 #pragma unroll
     for (int mm = 0; mm < 8; mm++) o[mm] = f4_t{0.f, 0.f, 0.f, 0.f};
-    if (A.t_prefix > 0) prefix_tiles<HPL>(A, kvh, gw, W, A.t_prefix, lane, qa, vt, pt, m_run, l_run, o);
-    if (A.t_tail > 0) tail_tiles<HPL>(A, kvh, gw, W, npt, A.t_tail, lane, qa, vt, pt, m_run, l_run, o);
+    if (A.t_prefix > 0) prefix_tiles<HPL>(A, kvh, gw, W, A.t_prefix, lane, qa, pt, m_run, l_run, o);
+    if (A.t_tail > 0) tail_tiles<HPL>(A, kvh, gw, W, npt, A.t_tail, lane, qa, pt, m_run, l_run, o);
 
-    // ---- merge the four waves (LDS), one record per query head
-    __syncthreads();
-    float* wo = reinterpret_cast<float*>(&s_vt[0][0]);   // [wave][16 heads][128]
+    // ---- merge the waves' (m, l, O) in LDS, kMergeH query heads per round;
+    // lane column n of MFMA mm holds dimension 8 n + mm of its rows
+    float lsum[HPL];
 #pragma unroll
-    for (int i = 0; i < HPL; i++) {
-        const int h = (lane >> 4) + 4 * i;
-        const float l = row16_sum(l_run[i]);
-        if (h < G) {
-            if ((lane & 15) == 0) { s_m[wave][h] = m_run[i]; s_l[wave][h] = l; }
-#pragma unroll
-            for (int mm = 0; mm < 8; mm++) wo[(wave * 16 + h) * kHd + 16 * mm + (lane & 15)] = o[mm][i];
-        }
-    }
-    __syncthreads();
+    for (int i = 0; i < HPL; i++) lsum[i] = row16_sum(l_run[i]);
     // Records cross workgroups (and the XCDs' separate L2s): they are written
     // with device-scope stores (written through to the coherent level), which
     // complete before the counter increment, and read back with device-scope
     // loads.  No device-wide fence (an L2 write-back per workgroup) is needed.
     float* rec = A.rec + ((int64_t)kvh * nsp + sp) * G * kRecF;
-    for (int idx = tid; idx < G * kHd; idx += kAW * 64) {
-        const int h = idx / kHd, d = idx % kHd;
-        float M = -INFINITY;
+    for (int hr = 0; hr < G; hr += kMergeH) {
+        __syncthreads();
 #pragma unroll
-        for (int w = 0; w < kAW; w++) M = fmaxf(M, s_m[w][h]);
-        float L = 0.f, Ov = 0.f;
-#pragma unroll
-        for (int w = 0; w < kAW; w++) {
-            const float f = s_m[w][h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s_m[w][h] - M);
-            L += s_l[w][h] * f;
-            Ov += wo[(w * 16 + h) * kHd + d] * f;
+        for (int i = 0; i < HPL; i++) {
+            const int h = (lane >> 4) + 4 * i;
+            if (h < G && h >= hr && h < hr + kMergeH) {
+                if ((lane & 15) == 0) { s_m[wave][h] = m_run[i]; s_l[wave][h] = lsum[i]; }
+                float* dst = s_buf + (wave * kMergeH + h - hr) * kHd + 8 * (lane & 15);
+                *reinterpret_cast<f4_t*>(dst) = f4_t{o[0][i], o[1][i], o[2][i], o[3][i]};
+                *reinterpret_cast<f4_t*>(dst + 4) = f4_t{o[4][i], o[5][i], o[6][i], o[7][i]};
+            }
         }
-        __hip_atomic_store(rec + h * kRecF + 4 + d, Ov, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (d == 0) {
-            __hip_atomic_store(rec + h * kRecF, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(rec + h * kRecF + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        const int nh = G - hr < kMergeH ? G - hr : kMergeH;
+        for (int idx = tid; idx < nh * kHd; idx += kAW * 64) {
+            const int h = hr + idx / kHd, d = idx % kHd;
+            float M = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < kAW; w++) M = fmaxf(M, s_m[w][h]);
+            float L = 0.f, Ov = 0.f;
+#pragma unroll
+            for (int w = 0; w < kAW; w++) {
+                const float f = s_m[w][h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s_m[w][h] - M);
+                L += s_l[w][h] * f;
+                Ov += s_buf[(w * kMergeH + h - hr) * kHd + d] * f;
+            }
+            __hip_atomic_store(rec + h * kRecF + 4 + d, Ov, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (d == 0) {
+                __hip_atomic_store(rec + h * kRecF, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(rec + h * kRecF + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
     }
     __builtin_amdgcn_s_waitcnt(0);   // this thread's record stores have completed
@@ -802,7 +811,7 @@ __global__ __launch_bounds__(kAW * 64) void k_res_attn(AttnArgs A) {
     // end) so that each thread's loads go out as one batch.
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     const float* r0 = A.rec + (int64_t)kvh * nsp * G * kRecF;
-    float* s_cm = reinterpret_cast<float*>(&s_vt[0][0]);
+    float* s_cm = s_buf;
     float* s_cf = s_cm + kMaxRec;
     float* s_cl = s_cf + kMaxRec;
     f4_t* s_part = reinterpret_cast<f4_t*>(s_cl + kMaxRec);
