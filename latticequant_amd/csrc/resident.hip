@@ -504,17 +504,19 @@ __device__ __forceinline__ void tile_k(const AttnArgs& A, const TileRaw& d, int6
     }
 }
 
-// V of the lane's 8 tokens (vector lane % 16): vp[q][i] = fp16 pair of
-// dimensions (8 n + 2 i, 8 n + 2 i + 1) of token q, dequantised.
+// V of the lane's 8 tokens (vector lane % 16), two tokens at a time:
+// vp[k][i] = fp16 pair (dimension 8 n + i of token 2 k, of token 2 k + 1),
+// dequantised -- the operand halves of P V's MFMA i as they are.
 __device__ __forceinline__ void tile_v(const AttnArgs& A, const TileRaw& d, int64_t rb0, int lane, bool fast,
-                                       const uint32_t mv[8], uint32_t vp[8][4]) {
+                                       const uint32_t mv[4], uint32_t vp[4][8]) {
     const int n = lane & 15, k8 = lane >> 4, xb = k8 >> 1;
     const uint32_t aw[8] = {d.va0.x, d.va0.y, d.va0.z, d.va0.w, d.va1.x, d.va1.y, d.va1.z, d.va1.w};
 #pragma unroll
-    for (int q = 0; q < 8; q++) {
-        rec_pairs(aw[q], (q < 4 ? d.vb.x : d.vb.y) >> (8 * (q & 3)), vp[q]);
+    for (int k = 0; k < 4; k++) {
+        const uint32_t bw = k < 2 ? d.vb.x : d.vb.y;
+        rec_pairs_tok(aw[2 * k], bw >> (16 * (k & 1)), aw[2 * k + 1], bw >> (16 * (k & 1) + 8), vp[k]);
 #pragma unroll
-        for (int i = 0; i < 4; i++) vp[q][i] = unbias(vp[q][i]);
+        for (int i = 0; i < 8; i++) vp[k][i] = unbias(vp[k][i]);
     }
     const uint64_t h0 = meta_hdr(d, 2), h1 = meta_hdr(d, 3);
     if ((h0 | h1) & 0xffull) {   // rare: exception entries replace records (uniform loops)
@@ -534,24 +536,25 @@ __device__ __forceinline__ void tile_v(const AttnArgs& A, const TileRaw& d, int6
                 if (mine && idx < A.v.exc_cap) {
                     int v[8];
                     exc_load(A.v.exc, idx, v);
-                    const int qq = sl & 7;
+                    const int q = sl & 7;
 #pragma unroll
-                    for (int q = 0; q < 8; q++)
+                    for (int k = 0; k < 4; k++)
 #pragma unroll
-                        for (int i = 0; i < 4; i++) vp[q][i] = q == qq ? pair_from_i16(v[2 * i], v[2 * i + 1]) : vp[q][i];
+                        for (int i = 0; i < 8; i++) {
+                            h2_t h = __builtin_bit_cast(h2_t, vp[k][i]);
+                            if (q == 2 * k) h[0] = (_Float16)(float)v[i];
+                            if (q == 2 * k + 1) h[1] = (_Float16)(float)v[i];
+                            vp[k][i] = __builtin_bit_cast(uint32_t, h);
+                        }
                 }
             }
         }
     }
-    const uint32_t sw[4] = {d.vs.x, d.vs.y, d.vs.z, d.vs.w};
+    const uint32_t sw[4] = {d.vs.x, d.vs.y, d.vs.z, d.vs.w};   // scales of tokens (2 k, 2 k + 1)
 #pragma unroll
-    for (int q = 0; q < 8; q++) {
-        if (fast) {
-            mul_pairs<4>(vp[q], mv[q]);
-        } else {
-            const uint16_t sq = (uint16_t)(sw[q >> 1] >> (16 * (q & 1)));
-            dequant_pairs<4>(vp[q], sq, sq);
-        }
+    for (int k = 0; k < 4; k++) {
+        if (fast) mul_pairs<8>(vp[k], mv[k]);
+        else dequant_pairs<8>(vp[k], (uint16_t)(sw[k] & 0xffffu), (uint16_t)(sw[k] >> 16));
     }
 }
 
@@ -567,23 +570,29 @@ __device__ __forceinline__ void tail_k(const AttnArgs& A, int64_t kvh, int64_t t
 }
 
 __device__ __forceinline__ void tail_v(const AttnArgs& A, int64_t kvh, int64_t t0, int64_t T, int lane,
-                                       uint32_t vp[8][4]) {
+                                       uint32_t vp[4][8]) {
     const int n = lane & 15, k8 = lane >> 4;
 #pragma unroll
-    for (int q = 0; q < 8; q++) {
-        const int64_t t = t0 + 8 * k8 + q;
-        uint4 w = make_uint4(0u, 0u, 0u, 0u);
-        if (t < T) w = *reinterpret_cast<const uint4*>(A.tail_v + (kvh * T + t) * kHd + 8 * n);
-        vp[q][0] = w.x; vp[q][1] = w.y; vp[q][2] = w.z; vp[q][3] = w.w;
+    for (int k = 0; k < 4; k++) {
+        const int64_t t = t0 + 8 * k8 + 2 * k;
+        uint4 w0 = make_uint4(0u, 0u, 0u, 0u), w1 = w0;
+        if (t < T) w0 = *reinterpret_cast<const uint4*>(A.tail_v + (kvh * T + t) * kHd + 8 * n);
+        if (t + 1 < T) w1 = *reinterpret_cast<const uint4*>(A.tail_v + (kvh * T + t + 1) * kHd + 8 * n);
+        const uint32_t x0[4] = {w0.x, w0.y, w0.z, w0.w}, x1[4] = {w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            vp[k][2 * i] = __builtin_amdgcn_perm(x1[i], x0[i], 0x05040100u);
+            vp[k][2 * i + 1] = __builtin_amdgcn_perm(x1[i], x0[i], 0x07060302u);
+        }
     }
 }
 
 // Online softmax of one tile's scores, P through LDS into the A operand,
-// O += P V with the B operands built from the lane's V pairs: MFMA mm takes
-// half mm % 2 of pair mm / 2 of the 8 tokens.
+// O += P V with the B operand of MFMA mm = the lane's 8 tokens' dimension
+// 8 n + mm, i.e. vp[0..3][mm].
 template <int HPL>
 __device__ __forceinline__ void tile_softmax_pv(int G, const f4_t s[2], const bool valid[2], int lane,
-                                                const uint32_t vp[8][4], uint32_t* pt, float m_run[HPL],
+                                                const uint32_t vp[4][8], uint32_t* pt, float m_run[HPL],
                                                 float l_run[HPL], f4_t o[8]) {
     const float c0 = 1.4426950408889634f / 11.313708498984761f;   // log2(e) / sqrt(128)
     _Float16* ph = reinterpret_cast<_Float16*>(pt);
@@ -609,13 +618,8 @@ __device__ __forceinline__ void tile_softmax_pv(int G, const f4_t s[2], const bo
     const uint4 pa = *reinterpret_cast<const uint4*>(pt + (lane & 15) * kPtRow + 4 * (lane >> 4));
     const h8_t pA = __builtin_bit_cast(h8_t, pa);
 #pragma unroll
-    for (int mm = 0; mm < 8; mm++) {
-        const uint32_t sel = (mm & 1) ? 0x07060302u : 0x05040100u;
-        const int i = mm >> 1;
-        const h8_t vB = as_h8(__builtin_amdgcn_perm(vp[1][i], vp[0][i], sel), __builtin_amdgcn_perm(vp[3][i], vp[2][i], sel),
-                              __builtin_amdgcn_perm(vp[5][i], vp[4][i], sel), __builtin_amdgcn_perm(vp[7][i], vp[6][i], sel));
-        o[mm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pA, vB, o[mm], 0, 0, 0);
-    }
+    for (int mm = 0; mm < 8; mm++)
+        o[mm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pA, as_h8(vp[0][mm], vp[1][mm], vp[2][mm], vp[3][mm]), o[mm], 0, 0, 0);
     wave_lds_sync();
 }
 
@@ -624,21 +628,19 @@ __device__ __forceinline__ void tile_softmax_pv(int G, const f4_t s[2], const bo
 template <int HPL>
 __device__ __forceinline__ void prefix_decode(const AttnArgs& A, const TileRaw& d, int64_t rb0, int64_t t0, int64_t T,
                                               int lane, const h8_t qa[4], f4_t s[2], bool valid[2],
-                                              uint32_t vp[8][4]) {
+                                              uint32_t vp[4][8]) {
     // dequant multipliers (s / 2 per token); the packed-multiply path is
     // taken when every scale of the tile allows it (wave-uniform)
     bool e0, e1, ev = true;
     const uint32_t mk0 = half_scales((d.ks & 0xffffu) * 0x10001u, &e0);
     const uint32_t mk1 = half_scales((d.ks >> 16) * 0x10001u, &e1);
     const uint32_t sw[4] = {d.vs.x, d.vs.y, d.vs.z, d.vs.w};
-    uint32_t mv[8];
+    uint32_t mv[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         bool e;
-        const uint32_t hp = half_scales(sw[k], &e);   // (s_2k / 2, s_2k+1 / 2)
+        mv[k] = half_scales(sw[k], &e);   // (s_2k / 2, s_2k+1 / 2)
         ev = ev && e;
-        mv[2 * k] = __builtin_amdgcn_perm(hp, hp, 0x01000100u);       // low half twice
-        mv[2 * k + 1] = __builtin_amdgcn_perm(hp, hp, 0x03020302u);   // high half twice
     }
     const bool fast = __all(e0 && e1 && ev);
 #pragma unroll
@@ -672,7 +674,7 @@ __device__ __forceinline__ void prefix_tiles(const AttnArgs& A, int64_t kvh, int
         const int64_t tb = ta + step;
         f4_t s[2];
         bool valid[2];
-        uint32_t vp[8][4];
+        uint32_t vp[4][8];
         prefix_decode<HPL>(A, d, hb + ta / kRB, ta, T, lane, qa, s, valid, vp);
         if (tb < T) tile_load(A, kvh, tb, T, lane, d);
         tile_softmax_pv<HPL>(A.group, s, valid, lane, vp, pt, m_run, l_run, o);
@@ -704,7 +706,7 @@ __device__ __forceinline__ void tail_tiles(const AttnArgs& A, int64_t kvh, int64
                 for (int c = 0; c < 4; c++) s[x] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], kb[c], s[x], 0, 0, 0);
             }
         }
-        uint32_t vp[8][4];
+        uint32_t vp[4][8];
         tail_v(A, kvh, t0, T, lane, vp);
         tile_softmax_pv<HPL>(A.group, s, valid, lane, vp, pt, m_run, l_run, o);
     }
