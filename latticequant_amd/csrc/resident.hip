@@ -818,6 +818,27 @@ __global__ __launch_bounds__(kAW * 64) void k_res_attn(AttnArgs A) {
     float* s_cl = s_cf + kMaxRec;
     f4_t* s_part = reinterpret_cast<f4_t*>(s_cl + kMaxRec);
     const int ne = nsp * G;
+    constexpr int kMU = 12;                      // o rows in flight per thread
+    const int ng = G * (kHd / 4);                // float4 groups of the outputs
+    const int tpg = ng >= kAW * 64 ? 1 : kAW * 64 / ng;   // threads per group, each a stride of the splits
+    // When every thread's O rows fit one batch (the usual case), they are
+    // loaded together with the (m, l) words, before any wait: one memory
+    // round trip instead of two.
+    const bool one_batch = ng * tpg <= kAW * 64 && nsp <= kMU * tpg;   // uniform
+    f4_t v0[kMU];
+    {
+        const int it = tid < ng * tpg ? tid : 0;
+        const int gi = it % ng, sub = it / ng;
+        const int h = gi / (kHd / 4), d4 = gi % (kHd / 4);
+        if (one_batch) {
+#pragma unroll
+            for (int k = 0; k < kMU; k++) {
+                const int p = sub + k * tpg;
+                const int pc = p < nsp ? p : nsp - 1;
+                v0[k] = *reinterpret_cast<const f4_t*>(r0 + (int64_t)(pc * G + h) * kRecF + 4 + 4 * d4);
+            }
+        }
+    }
     for (int i = tid; i < ne; i += kAW * 64) {
         const f4_t h4 = *reinterpret_cast<const f4_t*>(r0 + (int64_t)i * kRecF);
         s_cm[i] = h4[0];
@@ -839,27 +860,39 @@ __global__ __launch_bounds__(kAW * 64) void k_res_attn(AttnArgs A) {
         if (lane == 0) s_L[h] = L;
     }
     __syncthreads();
-    constexpr int kMU = 12;                      // o rows in flight per thread
-    const int ng = G * (kHd / 4);                // float4 groups of the outputs
-    const int tpg = ng >= kAW * 64 ? 1 : kAW * 64 / ng;   // threads per group, each a stride of the splits
-    for (int it = tid; it < ng * tpg; it += kAW * 64) {
-        const int gi = it % ng, sub = it / ng;
-        const int h = gi / (kHd / 4), d4 = gi % (kHd / 4);
-        f4_t acc = f4_t{0.f, 0.f, 0.f, 0.f};
-        for (int p0 = sub; p0 < nsp; p0 += kMU * tpg) {
-            f4_t v[kMU];
-            float f[kMU];
+    if (one_batch) {
+        if (tid < ng * tpg) {
+            const int gi = tid % ng, sub = tid / ng;
+            const int h = gi / (kHd / 4);
+            f4_t acc = f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int k = 0; k < kMU; k++) {
-                const int p = p0 + k * tpg;
-                const int pc = p < nsp ? p : nsp - 1;
-                v[k] = *reinterpret_cast<const f4_t*>(r0 + (int64_t)(pc * G + h) * kRecF + 4 + 4 * d4);
-                f[k] = p < nsp ? s_cf[pc * G + h] : 0.f;
+                const int p = sub + k * tpg;
+                const float f = p < nsp ? s_cf[p * G + h] : 0.f;
+                acc += v0[k] * f;
             }
-#pragma unroll
-            for (int k = 0; k < kMU; k++) acc += v[k] * f[k];
+            s_part[tid] = acc;
         }
-        s_part[it] = acc;
+    } else {
+        for (int it = tid; it < ng * tpg; it += kAW * 64) {
+            const int gi = it % ng, sub = it / ng;
+            const int h = gi / (kHd / 4), d4 = gi % (kHd / 4);
+            f4_t acc = f4_t{0.f, 0.f, 0.f, 0.f};
+            for (int p0 = sub; p0 < nsp; p0 += kMU * tpg) {
+                f4_t v[kMU];
+                float f[kMU];
+#pragma unroll
+                for (int k = 0; k < kMU; k++) {
+                    const int p = p0 + k * tpg;
+                    const int pc = p < nsp ? p : nsp - 1;
+                    v[k] = *reinterpret_cast<const f4_t*>(r0 + (int64_t)(pc * G + h) * kRecF + 4 + 4 * d4);
+                    f[k] = p < nsp ? s_cf[pc * G + h] : 0.f;
+                }
+#pragma unroll
+                for (int k = 0; k < kMU; k++) acc += v[k] * f[k];
+            }
+            s_part[it] = acc;
+        }
     }
     __syncthreads();
     for (int gi = tid; gi < ng; gi += kAW * 64) {
