@@ -653,33 +653,39 @@ __device__ __forceinline__ void prefix_decode(const AttnArgs& A, const TileRaw& 
     tile_v(A, d, rb0, lane, fast, mv, vp);
 }
 
-// The wave's prefix tiles.  One register set: a tile's records are decoded
-// (scores, V pairs) and the set is reloaded with the next tile's records,
-// which are in flight during this tile's softmax and P V (a second set,
-// loading a whole tile ahead, measured no faster).  Tiles are dealt
-// round-robin over all waves of the kv head (wave gw of W takes tiles gw,
-// gw + W, ...): the waves in flight read one contiguous stretch of the
-// prefix at a time instead of W strided ones.
+// The wave's prefix tiles.  The workgroup's tiles are the slots j of its
+// round-robin share (wave w of split sp statically owns tiles sp * kAW + w +
+// k * W): each wave starts with slot w, then takes the next free slot from a
+// workgroup counter in LDS, so the waves of a workgroup finish together
+// however their loads are delayed.  One register set: a tile's records are
+// decoded (scores, V pairs) and the set is reloaded with the next tile's
+// records, which are in flight during this tile's softmax and P V (a second
+// set, loading a whole tile ahead, measured no faster).
 template <int HPL>
-__device__ __forceinline__ void prefix_tiles(const AttnArgs& A, int64_t kvh, int64_t gw, int64_t W, int64_t T,
+__device__ __forceinline__ void prefix_tiles(const AttnArgs& A, int64_t kvh, int sp, int wave, int64_t W, int64_t T,
                                              int lane, const h8_t qa[4], uint32_t* pt, float m_run[HPL],
-                                             float l_run[HPL], f4_t o[8]) {
-    const int64_t step = W * kTile;
-    int64_t ta = gw * kTile;
-    if (ta >= T) return;
+                                             float l_run[HPL], f4_t o[8], int* s_next) {
+    const int64_t npt = (T + kTile - 1) / kTile;
+    auto tile_of = [&](int j) -> int64_t { return (int64_t)sp * kAW + (j % kAW) + (int64_t)(j / kAW) * W; };
+    int64_t g = tile_of(wave);
+    if (g >= npt) return;
     const int64_t hb = kvh * A.k.cap_blocks;
     TileRaw d;
-    tile_load(A, kvh, ta, T, lane, d);
+    tile_load(A, kvh, g * kTile, T, lane, d);
     while (true) {
-        const int64_t tb = ta + step;
+        int jn = 0;
+        if (lane == 0) jn = atomicAdd(s_next, 1);
+        jn = __builtin_amdgcn_readfirstlane(jn) + kAW;
+        const int64_t gn = tile_of(jn);
+        const int64_t ta = g * kTile;
         f4_t s[2];
         bool valid[2];
         uint32_t vp[4][8];
         prefix_decode<HPL>(A, d, hb + ta / kRB, ta, T, lane, qa, s, valid, vp);
-        if (tb < T) tile_load(A, kvh, tb, T, lane, d);
+        if (gn < npt) tile_load(A, kvh, gn * kTile, T, lane, d);
         tile_softmax_pv<HPL>(A.group, s, valid, lane, vp, pt, m_run, l_run, o);
-        if (tb >= T) break;
-        ta = tb;
+        if (gn >= npt) break;
+        g = gn;
     }
 }
 
@@ -718,7 +724,7 @@ __global__ __launch_bounds__(kAW * 64) void k_res_attn(AttnArgs A) {
     __shared__ __align__(16) float s_buf[kMergeF];   // the waves' O rows, then the last workgroup's merge
     __shared__ float s_m[kAW][16], s_l[kAW][16];
     __shared__ float s_L[16];
-    __shared__ int s_last;
+    __shared__ int s_last, s_next;
     // the wave index is made wave-uniform explicitly so that all tile control
     // flow stays scalar (no exec-masked paths around in-flight loads)
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -744,14 +750,15 @@ __global__ __launch_bounds__(kAW * 64) void k_res_attn(AttnArgs A) {
     }
     uint32_t* pt = s_pt[wave];
     for (int i = lane; i < 16 * kPtRow; i += 64) pt[i] = 0u;
-    wave_lds_sync();
+    if (tid == 0) s_next = 0;
+    __syncthreads();
     float m_run[HPL], l_run[HPL];
     f4_t o[8];
 #pragma unroll
     for (int i = 0; i < HPL; i++) { m_run[i] = -INFINITY; l_run[i] = 0.f; }
 #pragma unroll
     for (int mm = 0; mm < 8; mm++) o[mm] = f4_t{0.f, 0.f, 0.f, 0.f};
-    if (A.t_prefix > 0) prefix_tiles<HPL>(A, kvh, gw, W, A.t_prefix, lane, qa, pt, m_run, l_run, o);
+    if (A.t_prefix > 0) prefix_tiles<HPL>(A, kvh, sp, wave, W, A.t_prefix, lane, qa, pt, m_run, l_run, o, &s_next);
     if (A.t_tail > 0) tail_tiles<HPL>(A, kvh, gw, W, npt, A.t_tail, lane, qa, pt, m_run, l_run, o);
 
     // ---- merge the waves' (m, l, O) in LDS, kMergeH query heads per round;
