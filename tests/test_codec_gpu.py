@@ -126,3 +126,30 @@ def test_empty_coset_and_zero_head_gpu():
     np.testing.assert_array_equal(enc.scale16.cpu().numpy(), ch.scales)
     _compare_chunk(enc, 0, ch)
     np.testing.assert_array_equal(codec.decode_batch(enc)[0].cpu().numpy(), O.decompress_chunk(ch))
+
+
+@pytest.mark.parametrize("frac1,seed", [(0.02, 21), (0.002, 22)])
+def test_sparse_coset_streams_gpu(frac1, seed):
+    """Lattice-exact input (scale 1): D8 points, plus a small fraction of
+    D8 + 1/2 points, so the coset-1 streams have blocks of a few symbols or
+    none: stream words then span several blocks (bitstream assembly's
+    continuation across short and empty blocks) and the decoder walks long
+    runs of empty bitmap words.  Bit-exact against the oracle."""
+    codec, L = _lq()
+    rng = np.random.default_rng(seed)
+    shape = (1, 8, 1024, 128)
+    y = rng.integers(-3, 4, size=shape[:-1] + (16, 8))
+    y[..., 7] += y.sum(-1) & 1                       # even coordinate sum: D8
+    half = rng.random(shape[:-1] + (16,)) < frac1    # these vectors move to D8 + 1/2
+    x = y.astype(np.float32) + 0.5 * half[..., None]
+    t = torch.from_numpy(x.reshape(shape).astype(np.float16))
+    sc = np.ones(8, np.float32)
+    ch = O.compress_chunk(t.numpy(), 4, scales_f32=sc)
+    enc, _ = codec.encode_batch(t.cuda()[None], 4, scale32=torch.from_numpy(sc))
+    assert int(enc.status.item()) == 0
+    n1 = int(enc.blk_n1.sum().item())
+    assert n1 == int(half.sum())
+    if frac1 < 0.01:
+        assert int((enc.blk_n1 == 0).sum().item()) > 0   # some blocks hold no coset-1 symbol
+    _compare_chunk(enc, 0, ch)
+    np.testing.assert_array_equal(codec.decode_batch(enc)[0].cpu().numpy(), O.decompress_chunk(ch))
