@@ -195,6 +195,9 @@ __global__ void k_scale_fastdiv(const float* __restrict__ scale32, int dtype, in
 
 constexpr int kQThreads = 256;
 constexpr int kQBlocksPerWG = 8;
+// LDS histogram row of one stream: 256 bins indexed by the symbol's low byte,
+// padded so consecutive rows start 8 banks apart
+constexpr int kHRow = 256 + 8;
 constexpr int64_t kMaxBph = 1 << 30;   // vectors per head (2^27 tokens of 128 dims): in-head offsets stay int32
 
 // One workgroup quantizes kQBlocksPerWG consecutive LQ_BLK-vector blocks of one
@@ -209,6 +212,29 @@ constexpr int64_t kMaxBph = 1 << 30;   // vectors per head (2^27 tokens of 128 d
 // symbols, in the window the min fixes).
 // DITHER: the chunk's dither (dither8, seed dseed[chunk]) is added to x / scale
 // before the nearest-point search and taken off again in the dequantised output.
+// Histogram of one staged 16-byte row: int8 symbols of vectors 16g .. 16g + 15
+// of one coset's group g at one coordinate (the sym_pos layout).  Counting
+// from the staged rows rather than per vector puts the lanes of one LDS atomic
+// on 8 coordinates x 8 groups instead of one coordinate, so far fewer lanes
+// meet on one bin (same-address atomics serialise).
+__device__ __forceinline__ void stage_hist(const uint4& w, int row16, int n0, int n1, uint32_t* shist) {
+    const int p = row16 * 16;
+    const int r1 = sym_region(1, n0);
+    const int c = p >= r1;
+    const int q = p - (c ? r1 : 0);
+    const int left = (c ? n1 : n0) - 16 * (q >> 7);   // vectors of this group, >= 1
+    uint32_t* row = shist + (c * 8 + ((q >> 4) & 7)) * kHRow;
+    const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+    if (left >= 16) {
+#pragma unroll
+        for (int k = 0; k < 16; k++) atomicAdd(row + ((d[k >> 2] >> (8 * (k & 3))) & 255u), 1u);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+            if (k < left) atomicAdd(row + ((d[k >> 2] >> (8 * (k & 3))) & 255u), 1u);
+    }
+}
+
 template <typename SymT, bool DITHER>
 __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
     const void* __restrict__ x, int dtype, int64_t n_heads, int64_t bph, int64_t nblk,
@@ -218,7 +244,7 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
     const int64_t* __restrict__ dseed) {
     constexpr bool kWide = sizeof(SymT) == 2;
     constexpr int kSymMin = kWide ? -32768 : -128, kSymMax = kWide ? 32767 : 127;
-    __shared__ uint32_t shist[kWide ? 1 : LQ_STREAMS * 256];
+    __shared__ uint32_t shist[kWide ? 1 : LQ_STREAMS * kHRow];
     __shared__ int smin[LQ_STREAMS], smax[LQ_STREAMS];
     __shared__ __align__(16) SymT stage[kSymStride];
     __shared__ unsigned long long masks[kBlk / 64];
@@ -233,7 +259,7 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
     const int64_t V = n_heads * bph;
 
     if constexpr (!kWide) {
-        for (int i = tid; i < LQ_STREAMS * 256; i += kQThreads) shist[i] = 0;
+        for (int i = tid; i < LQ_STREAMS * kHRow; i += kQThreads) shist[i] = 0;
     }
     if (tid < LQ_STREAMS) { smin[tid] = INT_MAX; smax[tid] = INT_MIN; }
     if (tid == 0) sflag = 0;
@@ -366,12 +392,8 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
                 const int rk = c ? rank1 : rank0;
                 SymT* sp = stage + sym_pos(c, 0, rk, n0);   // column i adds 16 * i
                 if constexpr (!kWide) {
-                    uint32_t* hp = shist + c * 8 * 256 + 128;
 #pragma unroll
-                    for (int i = 0; i < 8; i++) {
-                        sp[16 * i] = (SymT)sy[r][i];
-                        atomicAdd(hp + i * 256 + sy[r][i], 1u);
-                    }
+                    for (int i = 0; i < 8; i++) sp[16 * i] = (SymT)sy[r][i];
                 } else {
 #pragma unroll
                     for (int i = 0; i < 8; i++) {
@@ -394,7 +416,11 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
             const int nbytes = (sym_region(1, n0) + 128 * ((n1 + 15) >> 4)) * (int)sizeof(SymT);
             uint4* dst = reinterpret_cast<uint4*>(sym + gblk * (int64_t)kSymStride);
             const uint4* src = reinterpret_cast<const uint4*>(stage);
-            for (int i = tid; i * 16 < nbytes; i += kQThreads) dst[i] = src[i];
+            for (int i = tid; i * 16 < nbytes; i += kQThreads) {
+                const uint4 w = src[i];
+                dst[i] = w;
+                if constexpr (!kWide) stage_hist(w, i, n0, n1, shist);
+            }
             unsigned long long* cb = reinterpret_cast<unsigned long long*>(coset_bits + gblk * (kBlk / 8));
             if (tid < kBlk / 64) cb[tid] = masks[tid];
             if (tid == 0) blk_n1[gblk] = (uint32_t)n1;
@@ -413,7 +439,7 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
     if constexpr (!kWide) {
         uint32_t* gh = hist + chunk * (LQ_STREAMS * 256);
         for (int i = tid; i < LQ_STREAMS * 256; i += kQThreads) {
-            uint32_t c = shist[i];
+            const uint32_t c = shist[(i >> 8) * kHRow + ((i & 255) ^ 128)];   // bin of symbol (i & 255) - 128
             if (c) atomicAdd(gh + i, c);
         }
     } else {
