@@ -153,3 +153,21 @@ def test_sparse_coset_streams_gpu(frac1, seed):
         assert int((enc.blk_n1 == 0).sum().item()) > 0   # some blocks hold no coset-1 symbol
     _compare_chunk(enc, 0, ch)
     np.testing.assert_array_equal(codec.decode_batch(enc)[0].cpu().numpy(), O.decompress_chunk(ch))
+
+
+def test_fp32_ragged_chunk_vs_oracle_gpu():
+    """fp32 input (IEEE division in the quantizer, no fast path), a vector count
+    that is not a multiple of the 512-vector block, heavy-tailed values: the
+    bitstream is bit-exact and the fp32 read path is q * float(scale16)."""
+    codec, L = _lq()
+    g = torch.Generator().manual_seed(31)
+    x = (torch.randn(1, 2, 4, 77, 128, generator=g) * torch.rand(1, 2, 4, 77, 1, generator=g) * 3).float()
+    x[..., :2] *= 25.0
+    enc, _ = codec.encode_batch(x.cuda(), 4)
+    assert int(enc.status.item()) == 0
+    sc32 = enc.scale32.cpu().numpy()
+    ch = O.compress_chunk(x[0].numpy(), 4, scales_f32=sc32)
+    _compare_chunk(enc, 0, ch)
+    out = codec.decode_batch(enc, out_dtype=torch.float32)
+    np.testing.assert_array_equal(out[0].cpu().numpy(), O.decompress_chunk(ch, out_dtype=np.float32))
+    np.testing.assert_allclose(enc.sigma2.cpu().numpy(), O.head_sigma2(x[0].numpy()), rtol=2e-7)
