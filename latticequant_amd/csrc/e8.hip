@@ -235,7 +235,11 @@ __device__ __forceinline__ void stage_hist(const uint4& w, int row16, int n0, in
     }
 }
 
-template <typename SymT, bool DITHER>
+// k_chunk_quantize (described above).  LEAN: the host guarantees bph >= LQ_BLK
+// (a block spans at most two heads) and no dequantised output; the general
+// paths are compiled out, which frees the scalar registers they held (fewer
+// spills through VGPR lanes in the block loop).
+template <typename SymT, bool DITHER, bool LEAN = false>
 __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
     const void* __restrict__ x, int dtype, int64_t n_heads, int64_t bph, int64_t nblk,
     const float* __restrict__ scale32, const int32_t* __restrict__ fastdiv, SymT* __restrict__ sym,
@@ -283,7 +287,7 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
         const int rblk = (int)(vbase - hblk * bph);
         // with bph >= kBlk a block spans at most two heads: their scale,
         // reciprocal and fast-division flag are read once per block
-        const bool two_heads = bph >= kBlk;
+        const bool two_heads = LEAN || bph >= kBlk;
         const int64_t hq0 = chunk * n_heads + hblk;
         const int64_t hq1 = hblk + 1 < n_heads ? hq0 + 1 : hq0;
         float s0 = 1.f, s1 = 1.f, rs0 = 1.f, rs1 = 1.f;
@@ -348,7 +352,7 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
 #pragma unroll
                     for (int i = 0; i < 8; i++) sy[r][i] = min(max(sy[r][i], kSymMin), kSymMax);
                 }
-                if (deq) {
+                if (!LEAN && deq) {
                     float off = c ? 0.5f : 0.f, y[8];
 #pragma unroll
                     for (int i = 0; i < 8; i++) {
@@ -557,6 +561,10 @@ int lq_chunk_quantize(const void* d_x, int dtype, int64_t n_chunks, int64_t n_he
         hipLaunchKernelGGL((k_chunk_quantize<int8_t, true>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x, dtype,
                            n_heads, bph, nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, d_hist, nullptr,
                            d_status, d_deq, deq_dtype, d_dither_seed);
+    else if (bph >= kBlk && !d_deq)
+        hipLaunchKernelGGL((k_chunk_quantize<int8_t, false, true>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x,
+                           dtype, n_heads, bph, nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, d_hist,
+                           nullptr, d_status, nullptr, deq_dtype, nullptr);
     else
         hipLaunchKernelGGL((k_chunk_quantize<int8_t, false>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x, dtype,
                            n_heads, bph, nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, d_hist, nullptr,
