@@ -18,21 +18,24 @@
 namespace lq {
 
 // LUT entry of one (stream, slot):
-//   [4:0]   31 - k          (shift that leaves the top k buffer bits in place)
-//   [8:5]   k               (renormalisation bits, 0..10)
-//   [18:9]  symbol index    (alphabet value - lo, < 1024)
-//   [31:19] row * L + (x' << k) - L: the next slot before the k new bits are
-//           added, inside an LDS block of up to 8 stream LUTs of L entries in
+//   [5:0]   63 - k: its low 5 bits are 31 - k (the shift that leaves the top
+//           k buffer bits in place) and its 6-bit complement is k itself
+//           (renormalisation bits, 0..10), so one field serves both
+//   [15:6]  symbol index (alphabet value - lo, < 1024)
+//   [17:16] zero
+//   [31:18] row * L + (x' << k) - L: the next slot before the k new bits are
+//           added, inside an LDS block of up to 16 stream LUTs of L entries in
 //           which this stream's LUT is row `row`
 __host__ __device__ inline uint32_t lut_entry(uint32_t sym, uint32_t xp, uint32_t row) {
     uint32_t k = 0;
     while ((xp << k) < (uint32_t)LQ_L) k++;
     const uint32_t next = row * (uint32_t)LQ_L + (xp << k) - (uint32_t)LQ_L;
-    return (31u - k) | (k << 5) | (sym << 9) | (next << 19);
+    return (63u - k) | (sym << 6) | (next << 18);
 }
 
-__device__ __forceinline__ uint32_t lut_sym(uint32_t e) { return (e >> 9) & 1023u; }
-__device__ __forceinline__ uint32_t lut_k(uint32_t e) { return (e >> 5) & 15u; }
+__device__ __forceinline__ uint32_t lut_sym(uint32_t e) { return (e >> 6) & 1023u; }
+__device__ __forceinline__ uint32_t lut_k(uint32_t e) { return ~e & 63u; }
+__device__ __forceinline__ uint32_t lut_next(uint32_t e) { return e >> 18; }
 
 // One lane's decoder of one stream from a checkpoint.
 //
@@ -76,7 +79,7 @@ struct StreamDec {
     __device__ __forceinline__ void step(const uint32_t* lut) {
         const uint32_t bits = (uint32_t)(buf >> 33) >> (e & 31u);
         const uint32_t k = lut_k(e);
-        const uint32_t slot = (e >> 19) + bits;
+        const uint32_t slot = lut_next(e) + bits;
         buf <<= k;
         nbuf -= k;
         e = lut[slot];
@@ -187,7 +190,7 @@ struct PhaseLane {
     // One decode step: stage the current symbol index at stg_j, find its
     // vector, move to the next symbol.  Returns the vector's block position.
     __device__ __forceinline__ int step(uint16_t* stg_j, const char* lutb) {
-        *stg_j = (uint16_t)__builtin_amdgcn_ubfe(e, 9, 10);
+        *stg_j = (uint16_t)lut_sym(e);
         if (wv == 0) {
             wi++;
             wv = wn;
@@ -201,8 +204,8 @@ struct PhaseLane {
         const int vl = (wi << 5) | __builtin_ctz(wv);
         wv &= wv - 1u;
         const uint32_t bits = (uint32_t)(buf >> 33) >> (e & 31u);
-        const uint32_t k = __builtin_amdgcn_ubfe(e, 5, 4);
-        const uint32_t addr = ((e >> 19) + bits) << 2;
+        const uint32_t k = lut_k(e);
+        const uint32_t addr = (lut_next(e) + bits) << 2;
         buf <<= k;
         nbuf -= k;
         e = *reinterpret_cast<const uint32_t*>(lutb + addr);
@@ -235,6 +238,114 @@ struct PhaseLane {
     }
 };
 
+// ---------------------------------------------------------------------------
+// Rank-staged decoding of one (stream, checkpoint block) task per lane, used
+// by the whole-line chunk decoder.  Like PhaseLane, but:
+//   * the ring holds 12 words (three aligned 4-word groups) in a per-wave
+//     column-major layout (word slot s of lane l at rcol[s * 64]), so a
+//     1024-lane workgroup fits its 16 LUTs, rings and staging in LDS;
+//   * the lane does not track vector positions: step j of a phase stages its
+//     symbol index at the caller's slot j, in coset-rank order, and the
+//     caller maps block positions to ranks when it rebuilds vectors;
+//   * phases are always 8 steps: steps past the lane's last symbol decode
+//     garbage from in-bounds LDS and ring words, which the caller never reads.
+// Ring invariant (top-ups of 4 words, at most 3 words moved into pre per
+// phase): a top-up is issued only when the group it lands in is not the one
+// being read (then at most 8 words are unread, so it overwrites no unread
+// word), and every phase starts with at least 3 unread words.
+constexpr int kLineRing = 12;
+
+struct LineLane {
+    const uint32_t* gs;     // the 16-byte aligned group holding the block's first word
+    uint32_t* rcol;         // this lane's ring column (slot stride 64 words)
+    int glim;               // first word (from gs) of the last readable group
+    int ld;                 // next word (from gs) to load into the ring (multiple of 4)
+    int rs;                 // ring slot of the next word to move into pre
+    int ls;                 // ring slot of the next landed group (0, 4 or 8)
+    uint64_t buf;
+    uint32_t nbuf, pre, e;
+    uint4 q;
+    bool inflight;
+
+    __device__ __forceinline__ uint4 group(int i) const {   // i: a multiple of 4
+        return *reinterpret_cast<const uint4*>(gs + (i < glim ? i : glim));
+    }
+    __device__ __forceinline__ void land(int slot, const uint4& g) {   // ring slots slot .. slot + 3
+        uint32_t* p = rcol + slot * 64;
+        p[0] = g.x;
+        p[64] = g.y;
+        p[128] = g.z;
+        p[192] = g.w;
+    }
+
+    // As PhaseLane::init (without the bitmap row).
+    __device__ __forceinline__ void init(const uint32_t* stream_words, uint32_t bit_off, int64_t end_bit, uint32_t state,
+                                         const uint32_t* lut, int row, uint32_t* ring_col) {
+        const uint32_t* sw = stream_words + (bit_off >> 5);
+        const int o = (int)((reinterpret_cast<uintptr_t>(sw) >> 2) & 3u);
+        gs = sw - o;
+        const int wlim = (int)((end_bit >> 5) + 2 - (int64_t)(bit_off >> 5));   // last readable word, from sw
+        glim = (wlim + o) & ~3;
+        rcol = ring_col;
+        const uint4 g0 = group(0), g1 = group(4), g2 = group(8);
+        land(0, g0);
+        land(4, g1);
+        land(8, g2);
+        ld = 12;
+        ls = 0;
+        rs = o + 2;
+        buf = ((uint64_t)__builtin_bitreverse32(rcol[o * 64]) << 32) << (bit_off & 31u);
+        nbuf = 32u - (bit_off & 31u);
+        pre = rcol[(o + 1) * 64];
+        refill();
+        e = lut[row * kL + (int)state - kL];
+        inflight = false;
+    }
+
+    __device__ __forceinline__ void refill() {
+        if (nbuf < 32u) {
+            buf |= (uint64_t)__builtin_bitreverse32(pre) << (32u - nbuf);
+            nbuf += 32u;
+            pre = rcol[rs * 64];
+            rs = rs == kLineRing - 1 ? 0 : rs + 1;
+        }
+    }
+
+    // Phase boundary: land the previous top-up, issue the next one if the
+    // lane still decodes (`more`) and the ring has room for it.
+    __device__ __forceinline__ void boundary(bool more) {
+        if (inflight) {
+            land(ls, q);
+            ls = ls == 8 ? 0 : ls + 4;
+            inflight = false;
+        }
+        if (more && (rs >> 2) != (ls >> 2)) {
+            q = group(ld);
+            ld += 4;
+            inflight = true;
+        }
+    }
+
+    __device__ __forceinline__ void step(uint16_t* stg_j, const char* lutb) {
+        *stg_j = (uint16_t)lut_sym(e);
+        const uint32_t bits = (uint32_t)(buf >> 33) >> (e & 31u);
+        const uint32_t k = lut_k(e);
+        const uint32_t addr = (lut_next(e) + bits) << 2;
+        buf <<= k;
+        nbuf -= k;
+        e = *reinterpret_cast<const uint32_t*>(lutb + addr);
+    }
+
+    // kPhase steps; step j stages at stg[8 j].
+    __device__ __forceinline__ void phase(uint16_t* stg, const char* lutb) {
+#pragma unroll
+        for (int j = 0; j < kPhase; j++) {
+            if (j % 3 == 0) refill();
+            step(stg + 8 * j, lutb);
+        }
+    }
+};
+
 // c7 parity of a staged vector: parity of the seven free coordinates, i.e.
 // of their indices and of the alphabet lows (lpar).
 __device__ __forceinline__ uint32_t staged_parity(const uint4& r, uint32_t lpar) {
@@ -256,6 +367,69 @@ __device__ __forceinline__ uint32_t deq_pair_f16(uint32_t idx2, half2_t lo_off, 
     const half2_t k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
     v = (v - k1024) + lo_off;
     return __builtin_bit_cast(uint32_t, v * sc2);
+}
+
+// Staged vector r (8 symbol indices) dequantised to 8 fp16 values, packed in
+// pairs, given its coset's packed (lo + off) pairs and alphabet-low parity.
+__device__ __forceinline__ uint4 deq_staged_f16(const uint4& r, const half2_t lo2[4], uint32_t lpar, half2_t sc2) {
+    const uint32_t par = staged_parity(r, lpar);
+    const uint32_t w3 = (r.w & 0xffffu) | (((r.w >> 16) * 2u + par) << 16);   // c7 index doubled + parity
+    uint4 o;
+    o.x = deq_pair_f16(r.x, lo2[0], sc2);
+    o.y = deq_pair_f16(r.y, lo2[1], sc2);
+    o.z = deq_pair_f16(r.z, lo2[2], sc2);
+    o.w = deq_pair_f16(w3, lo2[3], sc2);
+    return o;
+}
+
+// Biased symbol fields of the chunk decoder's LUTs.  When every alphabet of a
+// chunk lies in the ranges checked below, the LUT symbol field of coordinate
+// streams 0..6 holds the coordinate value + 512 and that of stream 7 holds
+// floor(c7 / 2) + 256, instead of the alphabet index.  Then a staged vector
+// needs no per-coset constants: the biases are even (the parity of the seven
+// free fields is that of c0..c6), 2 u7 + parity = c7 + 512, and every field
+// u < 1024, so fp16 (1024 + u) - 1536 is the coordinate exactly.
+__device__ __forceinline__ bool chunk_biased(const lq_table* T16) {
+    bool ok = true;
+#pragma unroll
+    for (int st = 0; st < LQ_STREAMS; st++) {
+        const int n = T16[st].n_sym, lo = T16[st].lo;
+        const int lim = (st & 7) < 7 ? 512 : 256;
+        ok = ok && (n == 0 || (lo >= -lim && lo + n - 1 < lim));
+    }
+    return ok;
+}
+
+// A staged vector of biased fields dequantised to 8 fp16 values, packed in
+// pairs: ((1024 + u) - 1536 + off) * scale, exact up to the one rounding of
+// the product (off = 0 or 1/2, |coordinate| <= 512).
+__device__ __forceinline__ uint4 deq_biased_f16(const uint4& r, half2_t off2, half2_t sc2) {
+    const uint32_t px = r.x ^ r.y ^ r.z ^ (r.w & 0xffffu);
+    const uint32_t par = (px ^ (px >> 16)) & 1u;
+    const uint32_t w3 = (r.w & 0xffffu) | (((r.w >> 16) * 2u + par) << 16);
+    const half2_t k1536 = {(_Float16)1536.0f, (_Float16)1536.0f};
+    const uint32_t in[4] = {r.x, r.y, r.z, w3};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        half2_t v = __builtin_bit_cast(half2_t, in[i] | 0x64006400u);
+        v = (v - k1536) + off2;
+        o[i] = __builtin_bit_cast(uint32_t, v * sc2);
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// The lattice point of a staged vector of biased fields, in fp32 (exact).
+__device__ __forceinline__ void lattice_biased_f32(const uint4& r, float off, float y[8]) {
+    const uint32_t px = r.x ^ r.y ^ r.z ^ (r.w & 0xffffu);
+    const int par = (int)((px ^ (px >> 16)) & 1u);
+    const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int j = 0; j < 7; j++) {
+        const int u = (int)((j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu));
+        y[j] = (float)(u - 512) + off;
+    }
+    y[7] = (float)(2 * ((int)(r.w >> 16) - 256) + par) + off;
 }
 
 // Per-workgroup dequantisation constants of one coset of one chunk: the
@@ -290,14 +464,20 @@ struct CosetConsts {
     // The staged vector r (8 symbol indices) dequantised to 8 fp16 values,
     // packed in pairs; needs small.
     __device__ __forceinline__ uint4 deq_f16(const uint4& r, half2_t sc2) const {
-        const uint32_t par = staged_parity(r, lpar);
-        const uint32_t w3 = (r.w & 0xffffu) | (((r.w >> 16) * 2u + par) << 16);   // c7 index doubled + parity
-        uint4 o;
-        o.x = deq_pair_f16(r.x, lo2[0], sc2);
-        o.y = deq_pair_f16(r.y, lo2[1], sc2);
-        o.z = deq_pair_f16(r.z, lo2[2], sc2);
-        o.w = deq_pair_f16(w3, lo2[3], sc2);
-        return o;
+        return deq_staged_f16(r, lo2, lpar, sc2);
+    }
+
+    // The per-coset constants of coset cp, picked per lane from the two cosets' sets.
+    __device__ __forceinline__ void pick(bool cp, const CosetConsts& c0, const CosetConsts& c1) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) lo[j] = cp ? c1.lo[j] : c0.lo[j];
+        lpar = cp ? c1.lpar : c0.lpar;
+        off = cp ? c1.off : c0.off;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            lo2[j] = __builtin_bit_cast(half2_t, cp ? __builtin_bit_cast(uint32_t, c1.lo2[j])
+                                                    : __builtin_bit_cast(uint32_t, c0.lo2[j]));
+        small = cp ? c1.small : c0.small;
     }
 
     // The same values in fp32 (exact products, before any fp16 rounding):

@@ -24,6 +24,19 @@ namespace {
 
 inline int launch_status() { return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_LAUNCH; }
 
+// Compute units of the current device (cached per device; 256 on MI355X).
+inline int64_t device_cus() {
+    static int64_t cache[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cache[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cache[dev] = n;
+    }
+    return cache[dev];
+}
+
 // ---------------------------------------------------------------------------
 // numpy.argsort tie order.  numpy's argsort on x86 AVX512 hosts runs
 // x86-simd-sort: for n <= 256, a bitonic network over 8-lane registers padded
@@ -760,10 +773,14 @@ __global__ void k_chunk_tail(int64_t n_streams, const lq_table* __restrict__ tab
 
 // ------------------------------------------------------------ chunk decode --
 
-// Decoder LUT of every chunk stream (lut_entry format, lq_decode.h); stream
-// st of a chunk sits at row st & 7, so the 8 LUTs of one coset form one LDS
-// block.
-__global__ __launch_bounds__(256) void k_chunk_lut(const lq_table* __restrict__ tables, uint32_t* __restrict__ lut) {
+// Decoder LUT of every chunk stream (lut_entry format, lq_decode.h).
+// mode 0 (decode attention): stream st of a chunk sits at row st & 7 (the 8
+// LUTs of one coset form one LDS block) and the symbol field is the alphabet
+// index.  mode 1 (chunk decoder): row st & 15 (the 16 LUTs of a chunk form
+// one LDS block), and the symbol field is biased (chunk_biased) when the
+// chunk's alphabets allow it.
+__global__ __launch_bounds__(256) void k_chunk_lut(const lq_table* __restrict__ tables, uint32_t* __restrict__ lut,
+                                                   int mode) {
     __shared__ int32_t fr[LQ_MAXSYM];
     __shared__ int32_t cum[LQ_MAXSYM + 1];
     const int64_t sid = blockIdx.x;
@@ -773,91 +790,119 @@ __global__ __launch_bounds__(256) void k_chunk_lut(const lq_table* __restrict__ 
     for (int i = threadIdx.x; i < n; i += 256) fr[i] = (int32_t)enc_f(T->enc[i]);
     __syncthreads();
     exclusive_scan_array(fr, n, cum);
-    const uint32_t row = (uint32_t)(sid & 7);
+    const int st = (int)(sid % LQ_STREAMS);
+    const uint32_t row = (uint32_t)st & (mode ? 15u : 7u);
+    uint32_t bias = 0;
+    if (mode && chunk_biased(tables + (sid - st))) bias = (uint32_t)(T->lo + ((st & 7) < 7 ? 512 : 256));
     for (int slot = threadIdx.x; slot < kL; slot += 256) {
         int lo = 0, hi = n - 1;   // largest s with cum[s] <= slot
         while (lo < hi) {
             int mid = (lo + hi + 1) >> 1;
             if (cum[mid] <= slot) lo = mid; else hi = mid - 1;
         }
-        lut[sid * kL + slot] = lut_entry((uint32_t)lo, (uint32_t)(fr[lo] + slot - cum[lo]), row);
+        lut[sid * kL + slot] = lut_entry((uint32_t)lo + bias, (uint32_t)(fr[lo] + slot - cum[lo]), row);
     }
 }
 
-constexpr int kDecBlocks = 64;   // blocks per decode workgroup (x 8 coordinate streams of one coset)
-constexpr int kStgRow = 72;      // u16 per block of the output staging (8 x 8 + 8 padding: no bank conflicts)
-constexpr int kDecLanes = kDecBlocks * 8;
+// Whole-line chunk decoder.
+//
+// Workgroup: 64 consecutive blocks of one chunk, 16 lanes per block (one
+// wave holds 4 blocks): lane (block b, coset c, coordinate idx) decodes stream
+// c * 8 + idx of block b with LineLane, in phases of 8 steps.  Step j of a
+// phase stages the symbol index of coset-c vector `st + j` of the block at
+// rank slot (st + j) % 16 of the (block, coset) staging, so no lane walks the
+// coset bitmap per symbol.  After each phase the block's 16 lanes flush the
+// output in whole 128-byte lines (8 vectors): a line is flushed once both
+// cosets have staged every vector in it; a flushed vector's rank in its coset
+// is the flushed count plus a popcount of the coset-1 bitmap below it.  Each
+// flush round writes up to 16 consecutive vectors (256 bytes) of a block.
+// A coset runs a phase only if the 8 vectors it stages fit the ring next to
+// its unflushed ones (st - flushed <= 8).  That never blocks for good: the
+// first unflushed line holds at most 8 vectors of each coset, so a coset
+// that has not staged all of them has fewer than 8 unflushed and may run.
+// HEADS_ALIGNED: bph is a multiple of the block size, so a block lies in one
+// head.  DITHER: the chunk's dither (dither8, seed dseed[chunk]) is
+// subtracted from each lattice point before scaling.
+constexpr int kDecBlocks = 64;                  // blocks per decode workgroup
+constexpr int kDecThreads = 16 * kDecBlocks;    // 1024
+constexpr int kDecStage = 16;                   // staged vectors per (block, coset)
+// Staging of (block b, coset c): group b * 2 + c, 16 slots of 8 u16, padded to
+// 68 words so that group bases fall on banks 4 g (mod 64): the 8 groups of a
+// wave write their slots j or j + 8 on disjoint banks.
+constexpr int kDecGroupU16 = 136;
 
-// Stage the 8 coset LUTs of (chunk, coset) and the coset-c membership bits of
-// blocks gbase .. gbase + nb - 1 (tail vectors cleared, one zero word after
-// each row) in LDS.  Cooperative over the workgroup; the caller syncs.
-template <int NB, int LANES>
-__device__ __forceinline__ void stage_coset(const uint32_t* __restrict__ lutg, const uint8_t* __restrict__ coset_bits,
-                                            int64_t chunk, int c, int64_t gbase, int64_t nblk, int64_t V,
-                                            uint32_t* lut, uint32_t (*bm)[kBlk / 32 + 1]) {
+__device__ __forceinline__ int dpp_ror8(int v) {   // lane l <- lane l ^ 8 within each 16-lane row
+    return __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false);
+}
+
+template <int OUT_DT, bool HEADS_ALIGNED, bool DITHER>
+__global__ __launch_bounds__(kDecThreads) void k_chunk_decode(
+        const uint32_t* __restrict__ words, const int64_t* __restrict__ chunk_base, const int64_t* __restrict__ stream_woff,
+        const uint32_t* __restrict__ blk_off, const int64_t* __restrict__ stream_nbits,
+        const uint16_t* __restrict__ blk_state, const uint8_t* __restrict__ coset_bits,
+        const lq_table* __restrict__ tables, const uint16_t* __restrict__ scale16, const uint32_t* __restrict__ lutg,
+        int64_t n_chunks, int64_t n_heads, int64_t bph, int64_t nblk, int64_t gpw, void* __restrict__ out,
+        const int64_t* __restrict__ dseed) {
+    __shared__ uint32_t lut[LQ_STREAMS * kL];                               // 64 KB
+    __shared__ uint32_t ring[kDecThreads / 64][kLineRing][64];              // 48 KB
+    __shared__ __align__(16) uint16_t stg[kDecBlocks * 2 * kDecGroupU16];   // 34 KB
+    __shared__ uint32_t bm1[kDecBlocks][kBlk / 32 + 1];                     // coset-1 bits, one zero word after each row
     const int tid = threadIdx.x;
-    const uint4* src = reinterpret_cast<const uint4*>(lutg + (chunk * LQ_STREAMS + c * 8) * kL);
-    uint4* dst = reinterpret_cast<uint4*>(lut);
-    for (int i = tid; i < 8 * kL / 4; i += LANES) dst[i] = src[i];
-    for (int i = tid; i < NB * (kBlk / 32); i += LANES) {
-        const int b = i / (kBlk / 32), w = i % (kBlk / 32);
-        const int64_t g = gbase + b;
+    const int64_t V = n_heads * bph;
+    const int64_t groups = (nblk + kDecBlocks - 1) / kDecBlocks;   // per chunk
+    const int64_t total = n_chunks * groups;
+    const int64_t first = (int64_t)blockIdx.x * gpw;
+    const int64_t last = first + gpw < total ? first + gpw : total;
+    const int wave = tid >> 6, lane = tid & 63;
+    int64_t lut_chunk = -1;
+    // The workgroup walks groups first .. last - 1 (64 blocks each); its LUTs
+    // are reloaded, between two barriers, only when the chunk changes.  Each
+    // wave stages its own 4 blocks' bitmaps and moves to its next blocks
+    // without waiting for the other waves.
+    for (int64_t gi = first; gi < last; gi++) {
+    const int64_t chunk = gi / groups;
+    const int64_t gbase = (gi % groups) * kDecBlocks;
+    if (chunk != lut_chunk) {
+        __syncthreads();   // every wave is done with the previous chunk's LUTs
+        const uint4* src = reinterpret_cast<const uint4*>(lutg + chunk * LQ_STREAMS * kL);
+        uint4* dst = reinterpret_cast<uint4*>(lut);
+        for (int i = tid; i < LQ_STREAMS * kL / 4; i += kDecThreads) dst[i] = src[i];
+        __syncthreads();
+        lut_chunk = chunk;
+    }
+    __builtin_amdgcn_wave_barrier();
+    for (int i = lane; i < 4 * (kBlk / 32 + 1); i += 64) {
+        const int bl = wave * 4 + i / (kBlk / 32 + 1), w = i % (kBlk / 32 + 1);
+        const int64_t g = gbase + bl;
         uint32_t m = 0;
-        if (g < nblk) {
+        if (w < kBlk / 32 && g < nblk) {
             m = reinterpret_cast<const uint32_t*>(coset_bits + (chunk * nblk + g) * (kBlk / 8))[w];
-            if (!c) m = ~m;
             const int64_t lim = V - g * kBlk - 32 * w;
             m = lim >= 32 ? m : (lim <= 0 ? 0u : m & ((1u << lim) - 1u));
         }
-        bm[b][w] = m;
+        bm1[bl][w] = m;
     }
-    for (int i = tid; i < NB; i += LANES) bm[i][kBlk / 32] = 0u;
-}
-
-// Workgroup: 64 blocks x the 8 streams of one coset of one chunk (512 lanes),
-// decoded by PhaseLane (lq_decode.h).  After each 8-step phase lane idx of a
-// block rebuilds the phase's vector idx (alphabet lo, c7 = 2 floor(c7/2) +
-// parity of c0..c6, coset offset, times the fp16 scale) and writes it as one
-// 16-byte store.  HEADS_ALIGNED: bph is a multiple of the block size, so a
-// block lies in one head.  DITHER: the chunk's dither (dither8, seed
-// dseed[chunk]) is subtracted from each lattice point before scaling.
-template <int OUT_DT, bool HEADS_ALIGNED, bool DITHER>
-__global__ __launch_bounds__(512) void k_chunk_decode(const uint32_t* __restrict__ words, const int64_t* __restrict__ chunk_base,
-                                                      const int64_t* __restrict__ stream_woff, const uint32_t* __restrict__ blk_off,
-                                                      const int64_t* __restrict__ stream_nbits,
-                                                      const uint16_t* __restrict__ blk_state, const uint8_t* __restrict__ coset_bits,
-                                                      const uint32_t* __restrict__ blk_n1, const lq_table* __restrict__ tables,
-                                                      const uint16_t* __restrict__ scale16, const uint32_t* __restrict__ lutg,
-                                                      int64_t n_heads, int64_t bph, int64_t nblk, void* __restrict__ out,
-                                                      const int64_t* __restrict__ dseed) {
-    __shared__ uint32_t lut[8 * kL];
-    __shared__ uint32_t ring[kRing][kDecLanes];
-    __shared__ __align__(16) uint16_t stg[kDecBlocks * kStgRow];
-    __shared__ uint32_t bm[kDecBlocks][kBlk / 32 + 1];
-    const int tid = threadIdx.x;
-    const int64_t V = n_heads * bph;
-    const int64_t groups = (nblk + kDecBlocks - 1) / kDecBlocks;
-    const int64_t chunk = blockIdx.x / (2 * groups);
-    const int64_t rem = blockIdx.x % (2 * groups);
-    const int c = (int)(rem / groups);
-    const int64_t gbase = (rem % groups) * kDecBlocks;
-    const lq_table* T = tables + chunk * LQ_STREAMS + c * 8;
-    if (T[0].n_sym == 0) return;   // the whole coset is empty in this chunk
-    stage_coset<kDecBlocks, kDecLanes>(lutg, coset_bits, chunk, c, gbase, nblk, V, lut, bm);
-    __syncthreads();
-    const int b = tid >> 3, idx = tid & 7;
+    __builtin_amdgcn_wave_barrier();
+    {
+    const int b = tid >> 4, c = (tid >> 3) & 1, idx = tid & 7, l16 = tid & 15;
     const int64_t g = gbase + b;
-    if (g >= nblk) return;   // whole 8-lane groups leave together; no barrier follows
-    const int st = c * 8 + idx;
-    const int64_t sid = chunk * LQ_STREAMS + st;
-    const int64_t task = sid * nblk + g;
+    if (g >= nblk) continue;   // whole blocks (16-lane rows) skip together
     const int64_t vfirst = g * kBlk;                 // first vector of the block, within the chunk
     const int valid = (int)(V - vfirst < kBlk ? V - vfirst : kBlk);
-    const uint32_t n1 = blk_n1[chunk * nblk + g];
-    const int n = c ? (int)n1 : valid - (int)n1;
-    if (n == 0) return;
-    CosetConsts cc;
-    cc.init(T, c);
+    // coset-1 count of the block from its bitmap (equal to blk_n1 for every
+    // chunk the encoder wrote); counting it here ties the loop below to the
+    // bitmap, so it ends even if the metadata disagrees with it
+    int n1 = 0;
+#pragma unroll
+    for (int w = 0; w < kBlk / 32; w++) n1 += __builtin_popcount(bm1[b][w]);
+    const int n = c ? n1 : valid - n1;
+    const lq_table* T = tables + chunk * LQ_STREAMS;
+    const bool biased = chunk_biased(T);
+    CosetConsts cc0, cc1;   // per-coset alphabet lows, for chunks whose fields are not biased
+    if (!biased) {
+        cc0.init(T, 0);
+        cc1.init(T + 8, 1);
+    }
     float sc;
     half2_t sc2;
     auto set_scale = [&](int64_t head) {
@@ -870,42 +915,97 @@ __global__ __launch_bounds__(512) void k_chunk_decode(const uint32_t* __restrict
     set_scale(head0);
     int64_t head_end = (head0 + 1) * bph;            // first chunk vector of the next head
 
-    PhaseLane<kDecLanes> d;
-    const int64_t end_bit = g + 1 < nblk ? (int64_t)blk_off[task + 1] : stream_nbits[sid];
-    d.init(words + chunk_base[chunk] + stream_woff[sid], blk_off[task], end_bit, blk_state[task], lut, idx,
-           &ring[0][tid], bm[b]);
+    const int st_id = c * 8 + idx;
+    const int64_t sid = chunk * LQ_STREAMS + st_id;
+    LineLane d;
+    if (n > 0) {
+        const int64_t task = sid * nblk + g;
+        const int64_t end_bit = g + 1 < nblk ? (int64_t)blk_off[task + 1] : stream_nbits[sid];
+        d.init(words + chunk_base[chunk] + stream_woff[sid], blk_off[task], end_bit, blk_state[task], lut, st_id,
+               &ring[tid >> 6][0][tid & 63]);
+    } else {
+        d.inflight = false;
+    }
     const char* const lutb = reinterpret_cast<const char*>(lut);
     using OutT = typename std::conditional<OUT_DT == LQ_F32, float, uint16_t>::type;
     OutT* const ob = reinterpret_cast<OutT*>(out) + (chunk * V + vfirst) * 8;
-    uint16_t* const my_stg = &stg[b * kStgRow + idx];
     const uint64_t dkey = DITHER ? mix64((uint64_t)dseed[chunk]) : 0u;
+    const uint32_t* const bmr = bm1[b];
+    uint16_t* const my_stg = &stg[(b * 2 + c) * kDecGroupU16 + idx];
+    const int u = (l16 & 3) + 1;     // lines of the flush candidate this lane checks
 
-    for (int s0 = 0; s0 < n; s0 += kPhase) {
-        d.boundary();
-        const int m = n - s0 < kPhase ? n - s0 : kPhase;
-        const int vl = d.phase(m, idx, my_stg, lutb);
-        if (idx < m) {   // lane idx rebuilds the vector of step idx
-            const uint4 r = *reinterpret_cast<const uint4*>(&stg[b * kStgRow + idx * 8]);
-            if (!HEADS_ALIGNED && vfirst + vl >= head_end) {
-                const int64_t head = (vfirst + vl) / bph;
-                head_end = (head + 1) * bph;
-                set_scale(head);
-            }
-            if constexpr (DITHER) {
-                float y[8], dd[8];
-                cc.deq_f32(r, 1.0f, y);   // the lattice point itself (exact)
-                dither8(dkey, vfirst + vl, dd);
+    int st = 0;                      // vectors of my coset staged (symbols of my stream decoded)
+    int fpos = 0, fr0 = 0, fr1 = 0;  // flushed block positions and flushed ranks per coset (block-uniform)
+    while (fpos < valid) {
+        __builtin_amdgcn_wave_barrier();
+        const bool more = st < n;
+        d.boundary(more);
+        if (more && st - (c ? fr1 : fr0) <= kDecStage - 8) {
+            // st % 8 == 0 here, so the phase's slots do not wrap; a last phase
+            // with fewer than 8 symbols stages garbage in slots of ranks >= n,
+            // which hold no unflushed rank (st + 8 - flushed <= 16) and are never read
+            d.phase(my_stg + (st & (kDecStage - 1)) * 8, lutb);
+            st = n - st < kPhase ? n : st + kPhase;
+        }
+        __builtin_amdgcn_wave_barrier();
+        const int st_o = dpp_ror8(st);
+        const int s0 = c ? st_o : st, s1 = c ? st : st_o;
+        // coset-1 bits of positions fpos .. fpos + 31; lanes 0..3 of the block's
+        // row check whether the first 1..4 lines can be flushed (the answers are
+        // monotone, so their count is the number of flushable lines)
+        const int wi = fpos >> 5;
+        const uint32_t W = __builtin_amdgcn_alignbit(bmr[wi + 1], bmr[wi], (uint32_t)(fpos & 31));
+        const int rest = valid - fpos;
+        const int np = rest < 8 * u ? rest : 8 * u;                  // 1 <= np <= 32
+        const int p1 = __builtin_popcount(W << ((32 - np) & 31));   // coset-1 vectors among them
+        const bool ok = 8 * (u - 1) < rest && fr0 + np - p1 <= s0 && fr1 + p1 <= s1;
+        const uint64_t bal = __builtin_amdgcn_ballot_w64(ok);
+        const int nl = __builtin_popcountll((bal >> (tid & 48)) & 0xfull);
+        const int F = 8 * nl < rest ? 8 * nl : rest;   // positions flushed this phase (<= 32)
+        for (int r0 = 0; r0 < F; r0 += 16) {
+            const int q = r0 + l16;
+            if (q < F) {
+                const int p = fpos + q;
+                const bool cp = (W >> q) & 1u;
+                const int n1b = __builtin_popcount(W & ((1u << q) - 1u));
+                const int rank = cp ? fr1 + n1b : fr0 + q - n1b;
+                const uint4 r = *reinterpret_cast<const uint4*>(&stg[(b * 2 + cp) * kDecGroupU16 + (rank & (kDecStage - 1)) * 8]);
+                if (!HEADS_ALIGNED && vfirst + p >= head_end) {
+                    const int64_t head = (vfirst + p) / bph;
+                    head_end = (head + 1) * bph;
+                    set_scale(head);
+                }
+                if (!DITHER && OUT_DT == LQ_F16 && biased) {
+                    const _Float16 o = cp ? (_Float16)0.5f : (_Float16)0.0f;
+                    reinterpret_cast<uint4*>(ob)[p] = deq_biased_f16(r, half2_t{o, o}, sc2);
+                } else {
+                    float y[8];
+                    if (biased) {
+                        lattice_biased_f32(r, cp ? 0.5f : 0.f, y);
+                    } else {
+                        CosetConsts cs;
+                        cs.pick(cp, cc0, cc1);
+                        cs.deq_f32(r, 1.0f, y);   // the lattice point itself (exact)
+                    }
+                    if constexpr (DITHER) {
+                        float dd[8];
+                        dither8(dkey, vfirst + p, dd);
 #pragma unroll
-                for (int j = 0; j < 8; j++) y[j] = (y[j] - dd[j]) * sc;
-                store8(ob, OUT_DT, vl, y);
-            } else if (OUT_DT == LQ_F16 && cc.small) {
-                reinterpret_cast<uint4*>(ob)[vl] = cc.deq_f16(r, sc2);
-            } else {
-                float y[8];
-                cc.deq_f32(r, sc, y);
-                store8(ob, OUT_DT, vl, y);
+                        for (int j = 0; j < 8; j++) y[j] = (y[j] - dd[j]) * sc;
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 8; j++) y[j] *= sc;
+                    }
+                    store8(ob, OUT_DT, p, y);
+                }
             }
         }
+        const int f1 = __builtin_popcount(W) - __builtin_popcount((uint32_t)((uint64_t)W >> F));   // 0 <= F <= 32
+        fr1 += f1;
+        fr0 += F - f1;
+        fpos += F;
+    }
+    }
     }
 }
 
@@ -1126,14 +1226,16 @@ int lq_chunk_decode(const uint32_t* d_words, const int64_t* d_chunk_base, const 
     if (n_chunks <= 0 || n_heads <= 0 || bph <= 0 || out_dtype < 0 || out_dtype > 2) return LQ_ERR_ARG;
     const int64_t V = n_heads * bph;
     const int64_t nblk = (V + kBlk - 1) / kBlk;
-    hipLaunchKernelGGL(k_chunk_lut, dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, d_tables, d_lut_work);
-    const int64_t groups = (nblk + kDecBlocks - 1) / kDecBlocks;
-    const dim3 grid((unsigned)(n_chunks * 2 * groups));
+    hipLaunchKernelGGL(k_chunk_lut, dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, d_tables, d_lut_work, 1);
+    const int64_t groups = n_chunks * ((nblk + kDecBlocks - 1) / kDecBlocks);
+    const int64_t cus = device_cus();
+    const int64_t gpw = (groups + cus - 1) / cus;   // groups per workgroup: one workgroup per CU
+    const dim3 grid((unsigned)((groups + gpw - 1) / gpw));
     const bool aligned = bph % kBlk == 0;
 #define LQ_DECODE(DT, AL, DI)                                                                                     \
-    hipLaunchKernelGGL((k_chunk_decode<DT, AL, DI>), grid, dim3(512), 0, s, d_words, d_chunk_base, d_stream_woff,   \
-                       d_blk_off, d_stream_nbits, d_blk_state, d_coset_bits, d_blk_n1, d_tables, d_scale16, d_lut_work, \
-                       n_heads, bph, nblk, d_out, d_dither_seed)
+    hipLaunchKernelGGL((k_chunk_decode<DT, AL, DI>), grid, dim3(kDecThreads), 0, s, d_words, d_chunk_base, d_stream_woff,   \
+                       d_blk_off, d_stream_nbits, d_blk_state, d_coset_bits, d_tables, d_scale16, d_lut_work,          \
+                       n_chunks, n_heads, bph, nblk, gpw, d_out, d_dither_seed)
 #define LQ_DECODE_DT(DT)                                                                                          \
     do {                                                                                                          \
         if (d_dither_seed) { if (aligned) LQ_DECODE(DT, true, true); else LQ_DECODE(DT, false, true); }           \
@@ -1149,7 +1251,7 @@ int lq_chunk_decode(const uint32_t* d_words, const int64_t* d_chunk_base, const 
 
 int lq_chunk_luts(const lq_table* d_tables, int64_t n_chunks, uint32_t* d_lut, hipStream_t s) {
     if (n_chunks <= 0 || !d_tables || !d_lut) return LQ_ERR_ARG;
-    hipLaunchKernelGGL(k_chunk_lut, dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, d_tables, d_lut);
+    hipLaunchKernelGGL(k_chunk_lut, dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, d_tables, d_lut, 0);
     return launch_status();
 }
 
