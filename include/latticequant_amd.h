@@ -41,6 +41,7 @@ extern "C" {
 #define LQ_ERR_LAUNCH -2
 #define LQ_ERR_ALPHABET -3     /* alphabet > L=1024: the reference never terminates */
 #define LQ_ERR_RANGE -4        /* lattice symbol outside int8 */
+#define LQ_ERR_SCRATCH -5      /* request larger than a static scratch array (allocation-free entry points) */
 
 /* per-chunk status bits written by the device */
 #define LQ_ST_SYM_OVERFLOW 1   /* a lattice symbol did not fit the staging type (int8: use the wide path) */
@@ -392,6 +393,26 @@ int64_t lq_resident_attn_workspace(int64_t n_heads, int group, int64_t t_prefix,
 int lq_resident_attention(const lq_resident *k, const lq_resident *v, int64_t t_prefix, const uint16_t *d_q,
                           int group, const uint16_t *d_tail_k, const uint16_t *d_tail_v, int64_t t_tail,
                           void *d_work, uint16_t *d_out, hipStream_t s);
+
+/* Bytes of the device scratch array behind lq_resident_attention_noalloc. */
+#define LQ_RES_ATTN_SCRATCH_BYTES (4 << 20)
+
+/* lq_resident_attention without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops that
+ * forbid hipMalloc).  No counterpart in the reference.  The counters and split
+ * records live in a file-scope device array of LQ_RES_ATTN_SCRATCH_BYTES per
+ * device, held until the process ends; its address is looked up (and the array
+ * cleared) on the first call on each device, with that device current.  The
+ * array holds completion counters for up to 1024 kv heads at a fixed place
+ * (each completed call leaves them zero) and then the split records: a step
+ * with more kv heads, or whose records exceed the rest of the array, returns
+ * LQ_ERR_SCRATCH without launching.  Nothing is allocated: no hipMalloc or
+ * hipFree.  Calls on one device share the array, so calls that overlap on one
+ * GPU (different streams, or different host threads) race; calls in stream
+ * order do not.  Results equal lq_resident_attention's. */
+int lq_resident_attention_noalloc(const lq_resident *k, const lq_resident *v, int64_t t_prefix, const uint16_t *d_q,
+                                  int group, const uint16_t *d_tail_k, const uint16_t *d_tail_v, int64_t t_tail,
+                                  uint16_t *d_out, hipStream_t s);
 
 #ifdef __cplusplus
 }

@@ -73,6 +73,7 @@ _SIGS = {
     "lq_resident_dequant": ([_P, _I64, _I64, _I64, _I64, _P, _INT, _P], _INT),
     "lq_resident_attn_workspace": ([_I64, _INT, _I64, _I64], _I64),
     "lq_resident_attention": ([_P, _P, _I64, _P, _INT, _P, _P, _I64, _P, _P, _P], _INT),
+    "lq_resident_attention_noalloc": ([_P, _P, _I64, _P, _INT, _P, _P, _I64, _P, _P], _INT),
 }
 
 

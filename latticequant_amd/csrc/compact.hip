@@ -223,6 +223,7 @@ const char* lq_status_string(int code) {
         case LQ_ERR_LAUNCH: return "kernel launch failed";
         case LQ_ERR_ALPHABET: return "rANS alphabet larger than L = 1024";
         case LQ_ERR_RANGE: return "lattice symbol outside int8";
+        case LQ_ERR_SCRATCH: return "request larger than the static scratch array";
         default: return "unknown status";
     }
 }

@@ -34,6 +34,7 @@
 // counter) merges the records and writes the output.
 #include <climits>
 #include <cmath>
+#include <mutex>
 
 #include "lq_device.h"
 
@@ -935,6 +936,51 @@ bool res_ok(const lq_resident* r) {
            r->cap_blocks > 0 && r->exc_cap >= 0;
 }
 
+int attention_launch(const lq_resident* k, const lq_resident* v, int64_t t_prefix, const uint16_t* d_q, int group,
+                     const uint16_t* d_tail_k, const uint16_t* d_tail_v, int64_t t_tail, uint32_t* counters,
+                     float* records, uint16_t* d_out, hipStream_t s);
+
+// Static scratch layout: a fixed region of completion counters for up to
+// kScratchHeads kv heads (so records of one geometry never land on counters
+// another geometry uses), then the split records.
+constexpr int64_t kScratchHeads = 1024;
+constexpr int64_t kScratchCounterBytes = kScratchHeads * kCtrStride * 4;
+
+// Scratch of lq_resident_attention_noalloc: the completion counters and split
+// records of one decode step, one copy per device, held until the process
+// ends.  In host code `scratch` names a host-side stand-in, never the device
+// memory: kernels get the address hipGetSymbolAddress returns for the device.
+static __device__ __align__(256) uint8_t scratch[LQ_RES_ATTN_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices];   // device address of `scratch` per device, null until set up
+
+__global__ void k_zero_u32(uint32_t* p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+// Device address of the current device's scratch array.  On the first call
+// per device: look it up and clear it (a fill kernel on s, stream-ordered
+// before the caller's launch; the counters must start at zero and every
+// completed step leaves them zero).
+int scratch_ptr(void** out, hipStream_t s) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return LQ_ERR_ARG;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return LQ_ERR_LAUNCH;
+        hipLaunchKernelGGL(k_zero_u32, dim3(256), dim3(256), 0, s, static_cast<uint32_t*>(p),
+                           (int64_t)LQ_RES_ATTN_SCRATCH_BYTES / 4);
+        if (hipGetLastError() != hipSuccess) return LQ_ERR_LAUNCH;
+        g_scratch[dev] = p;
+    }
+    *out = g_scratch[dev];
+    return LQ_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -983,7 +1029,40 @@ int64_t lq_resident_attn_workspace(int64_t n_heads, int group, int64_t t_prefix,
 int lq_resident_attention(const lq_resident* k, const lq_resident* v, int64_t t_prefix, const uint16_t* d_q,
                           int group, const uint16_t* d_tail_k, const uint16_t* d_tail_v, int64_t t_tail,
                           void* d_work, uint16_t* d_out, hipStream_t s) {
-    if (!d_q || !d_out || !d_work || group < 1 || group > 16 || t_prefix < 0 || t_tail < 0 ||
+    if (!d_work || !k || k->n_heads <= 0) return LQ_ERR_ARG;
+    uint32_t* counters = static_cast<uint32_t*>(d_work);
+    float* records = reinterpret_cast<float*>(static_cast<char*>(d_work) + k->n_heads * kCtrStride * 4);
+    return attention_launch(k, v, t_prefix, d_q, group, d_tail_k, d_tail_v, t_tail, counters, records, d_out, s);
+}
+
+int lq_resident_attention_noalloc(const lq_resident* k, const lq_resident* v, int64_t t_prefix, const uint16_t* d_q,
+                                  int group, const uint16_t* d_tail_k, const uint16_t* d_tail_v, int64_t t_tail,
+                                  uint16_t* d_out, hipStream_t s) {
+    // size check first, from the host-side geometry alone: an oversize step is
+    // refused before any HIP call
+    if (!k || k->n_heads <= 0) return LQ_ERR_ARG;
+    const int64_t need = lq_resident_attn_workspace(k->n_heads, group, t_prefix, t_tail);
+    if (need < 0) return LQ_ERR_ARG;
+    const int64_t rec_bytes = need - k->n_heads * kCtrStride * 4;
+    if (k->n_heads > kScratchHeads || rec_bytes > (int64_t)LQ_RES_ATTN_SCRATCH_BYTES - kScratchCounterBytes)
+        return LQ_ERR_SCRATCH;
+    void* p = nullptr;
+    const int rc = scratch_ptr(&p, s);
+    if (rc != LQ_OK) return rc;
+    return attention_launch(k, v, t_prefix, d_q, group, d_tail_k, d_tail_v, t_tail, static_cast<uint32_t*>(p),
+                            reinterpret_cast<float*>(static_cast<char*>(p) + kScratchCounterBytes), d_out, s);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Argument checks and launch of k_res_attn with its completion counters (one
+// per kv head, kCtrStride apart, zero on entry and left zero) and split records.
+int attention_launch(const lq_resident* k, const lq_resident* v, int64_t t_prefix, const uint16_t* d_q, int group,
+                     const uint16_t* d_tail_k, const uint16_t* d_tail_v, int64_t t_tail, uint32_t* counters,
+                     float* records, uint16_t* d_out, hipStream_t s) {
+    if (!d_q || !d_out || !counters || !records || group < 1 || group > 16 || t_prefix < 0 || t_tail < 0 ||
         t_prefix + t_tail <= 0 || t_prefix % kRB)
         return LQ_ERR_ARG;
     if (t_tail > 0 && (!d_tail_k || !d_tail_v)) return LQ_ERR_ARG;
@@ -1005,9 +1084,8 @@ int lq_resident_attention(const lq_resident* k, const lq_resident* v, int64_t t_
     A.tail_v = d_tail_v;
     A.group = group;
     A.nsp = (int)n_splits(n_heads, group, t_prefix, t_tail);
-    const int64_t counters = n_heads * kCtrStride * 4;
-    A.counter = static_cast<uint32_t*>(d_work);
-    A.rec = reinterpret_cast<float*>(static_cast<char*>(d_work) + counters);
+    A.counter = counters;
+    A.rec = records;
     A.out = d_out;
     const int64_t grid = n_heads * A.nsp;
     if (grid > INT_MAX || (int64_t)A.nsp * group > kMaxRec) return LQ_ERR_ARG;
@@ -1020,5 +1098,9 @@ int lq_resident_attention(const lq_resident* k, const lq_resident* v, int64_t t_
     }
     return launch_status();
 }
+
+}  // namespace
+
+extern "C" {
 
 }  // extern "C"
