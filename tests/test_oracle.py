@@ -113,6 +113,21 @@ def test_compact_golden():
         np.testing.assert_array_equal(O.unpack_e8(g[f"raw{b}"], b), g[f"unpacked{b}"])
 
 
+def test_check_representable_inrange_fixture():
+    """check_representable (core/compact_storage.py:235-249) on all 6000 replayed
+    inputs per rate equals the reference's inrange{b} mask, rejections
+    included; the replay is confirmed by reproducing the stored in-range points."""
+    from tests.golden.replay import compact_inputs
+    g = np.load(os.path.join(G, "compact.npz"))
+    xs = compact_inputs()
+    for b in (3, 4, 5):
+        q = O.encode_e8(xs[b])
+        ok = O.check_representable(q, b)
+        np.testing.assert_array_equal(q[g[f"inrange{b}"]], g[f"q{b}"])   # replay reproduces the fixture
+        np.testing.assert_array_equal(ok, g[f"inrange{b}"])
+        assert 0 < (~ok).sum() < ok.sum()   # both outcomes occur
+
+
 def test_compact_known_answers_and_rejects():
     # handcrafted points of core/compact_storage.py:398-414, round trip bit-exact
     for b in (3, 4, 5):
