@@ -476,6 +476,64 @@ def to_bytes(enc: EncodedBatch) -> bytes:
     return body + np.uint32(zlib.crc32(body) & 0xFFFFFFFF).tobytes()
 
 
+def _check_wire_geometry(C, nh, bph, shape, arrs):
+    """Field sizes against the batch geometry (the decoder indexes by them)."""
+    S, B = L.LQ_STREAMS, L.LQ_BLK
+    if C < 1 or nh < 1 or bph < 1 or bph > (1 << 30) or len(shape) != 4:
+        raise WireFormatError("bad batch geometry")
+    if shape[0] * shape[1] != nh or shape[2] * shape[3] != 8 * bph:
+        raise WireFormatError("chunk shape does not match n_heads x bph")
+    nb = (nh * bph + B - 1) // B
+    need = {"bits": C, "status": C, "scale32": C * nh, "scale16": C * nh, "chunk_words": C,
+            "stream_nbits": C * S, "stream_state": C * S, "stream_woff": C * S, "table_heads": C * S * 4,
+            "coset_bits": C * nb * B // 8, "blk_n1": C * nb, "words": None, "table_freqs": None,
+            "blk_off": None, "blk_state": None}
+    for name, n in need.items():
+        if name not in arrs:
+            raise WireFormatError(f"missing field {name}")
+        if n is not None and arrs[name].size != n:
+            raise WireFormatError(f"field {name} holds {arrs[name].size} values, the geometry needs {n}")
+    for name, n in (("sigma2", C * nh), ("dither_seed", C)):
+        if name in arrs and arrs[name].size != n:
+            raise WireFormatError(f"field {name} holds {arrs[name].size} values, the geometry needs {n}")
+
+
+def _check_wire_streams(C, nv, nb, present, arrs, off, st):
+    """Cross-checks of every value the chunk decoder uses as an address or a
+    count: the reference word layout of the merged bitstream (present streams
+    in stream order, ceil(n_bits / 32) + 1 words each, the total in
+    chunk_words), block checkpoints (bit offsets from 0, non-decreasing, at
+    most the stream's n_bits; states in [L, 2L)), per-block coset-1 counts equal
+    to the coset bitmap's, and a coset's streams present exactly when it holds
+    vectors."""
+    S, B = L.LQ_STREAMS, L.LQ_BLK
+    nbits = arrs["stream_nbits"].astype(np.int64).reshape(C, S)
+    woff = arrs["stream_woff"].astype(np.int64).reshape(C, S)
+    cw = arrs["chunk_words"].astype(np.int64)
+    if np.any(nbits < 0) or np.any(nbits[~present] != 0) or np.any(nbits >= (1 << 32)):
+        raise WireFormatError("stream bit counts out of range")
+    per = np.where(present, (nbits + 31) // 32 + 1, 0)
+    if not np.array_equal(woff, np.cumsum(per, 1) - per) or not np.array_equal(cw, per.sum(1)):
+        raise WireFormatError("stream word offsets do not follow the merged bitstream layout")
+    o = off.reshape(C, S, nb).astype(np.int64)
+    p = present
+    if np.any(o[p][:, 0] != 0) or np.any(np.diff(o[p], axis=1) < 0) or np.any(o[p] > nbits[p][:, None]):
+        raise WireFormatError("block checkpoint offsets out of order or past the stream end")
+    sv = st.reshape(C, S, nb).astype(np.int64)
+    if np.any(sv[p] < L.LQ_L) or np.any(sv[p] >= 2 * L.LQ_L):
+        raise WireFormatError("block checkpoint states outside [L, 2L)")
+    bits = np.unpackbits(arrs["coset_bits"].reshape(C, nb, B // 8), axis=2, bitorder="little")
+    valid = np.minimum(B, nv - np.arange(nb) * B)
+    bits[:, np.arange(B)[None, :] >= valid[:, None]] = 0
+    n1 = bits.sum(2)
+    if not np.array_equal(n1, arrs["blk_n1"].astype(np.int64).reshape(C, nb)):
+        raise WireFormatError("per-block coset-1 counts disagree with the coset bitmap")
+    tot1 = n1.sum(1)
+    if (np.any(present[:, 8:] != (tot1 > 0)[:, None]) or
+            np.any(present[:, :8] != (nv - tot1 > 0)[:, None])):
+        raise WireFormatError("stream presence disagrees with the coset counts")
+
+
 def from_bytes(buf, device=None) -> EncodedBatch:
     """Restore an EncodedBatch on `device` (default: the current CUDA device).
     Raises WireFormatError on a bad magic, version, checksum or layout."""
@@ -500,6 +558,8 @@ def from_bytes(buf, device=None) -> EncodedBatch:
     pos = 16 + hl
     end = len(mv) - 4
     arrs = {}
+    if not isinstance(header.get("fields"), list):
+        raise WireFormatError("bad header: no field list")
     for name, dts, n in header["fields"]:
         pos += (-pos) % 8
         dt = np.dtype(dts)
@@ -509,11 +569,12 @@ def from_bytes(buf, device=None) -> EncodedBatch:
         arrs[name] = np.frombuffer(mv[pos:pos + nbytes], dt).copy()
         pos += nbytes
     S = L.LQ_STREAMS
+    _check_wire_geometry(C, nh, bph, shape, arrs)
     nv = nh * bph
     nb = (nv + L.LQ_BLK - 1) // L.LQ_BLK
     heads = arrs["table_heads"].reshape(C * S, 4)
     nsym = heads[:, 1].astype(np.int64)
-    if heads.shape[0] != C * S or arrs["table_freqs"].size != int(nsym.sum()) or np.any(nsym > L.LQ_MAXSYM):
+    if arrs["table_freqs"].size != int(nsym.sum()) or np.any(nsym < 0) or np.any(nsym > L.LQ_MAXSYM):
         raise WireFormatError("inconsistent tables")
     # rebuild the device tables: enc[j] = f | cum << 11 | (11 - bitlen(f)) << 21
     tab = np.zeros((C * S, L.TABLE_BYTES // 4), np.uint32)
@@ -541,6 +602,7 @@ def from_bytes(buf, device=None) -> EncodedBatch:
     cw = arrs["chunk_words"].astype(np.int64)
     if arrs["words"].size != int(cw.sum()):
         raise WireFormatError("inconsistent bitstream length")
+    _check_wire_streams(C, nv, nb, present.reshape(C, S), arrs, off, st)
     dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
 
     def T(a, dt):

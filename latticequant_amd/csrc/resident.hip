@@ -928,6 +928,9 @@ int64_t n_splits(int64_t n_heads, int group, int64_t t_prefix, int64_t t_tail) {
     const int64_t most = (tiles + kAW - 1) / kAW;
     if (fill > kMaxRec / group) fill = kMaxRec / group;   // the merge stages nsp * group records
     if (n < fill) n = fill < most ? fill : most;
+    // the merge takes at most kMaxRec records: longer prefixes give each
+    // split's waves more tiles (tiles are dealt dynamically) instead of more splits
+    if (n > kMaxRec / group) n = kMaxRec / group;
     return n > 0 ? n : 1;
 }
 

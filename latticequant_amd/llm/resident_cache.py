@@ -54,6 +54,7 @@ class ResidentKVCache(DynamicCache):
         self.tail_v: List[Optional[torch.Tensor]] = []
         self.chunks: List[list] = []          # per layer: [(EncodedBatch K, EncodedBatch V)]
         self._work = None
+        self._work_heads = 0
 
     # -- storage ----------------------------------------------------------
     def _ensure(self, layer_idx: int):
@@ -128,8 +129,12 @@ class ResidentKVCache(DynamicCache):
             rv = self.res_v[layer_idx] = ResidentKV(B * H, 1024, device=tk.device)
         group = query.shape[1] // H
         n = attn_workspace_size(B * H, group, rk.n_tokens, tk.shape[2])
-        if self._work is None or self._work.numel() < n or self._work.device != tk.device:
+        # the workspace's completion counters sit at [0, 256 * kv heads): a new
+        # head count would put split records where counters were, so re-zero
+        if (self._work is None or self._work.numel() < n or self._work.device != tk.device or
+                self._work_heads != B * H):
             self._work = attn_workspace(B * H, group, rk.n_tokens, tk.shape[2], device=tk.device)
+            self._work_heads = B * H
         out = resident_decode_attention(rk, rv, query.to(torch.float16), tk.to(torch.float16),
                                         tv.to(torch.float16), work=self._work)
         return out.to(query.dtype)
@@ -180,13 +185,22 @@ def resident_attention(module, query, key, value, attention_mask, dropout: float
     """HF attention function "lq_resident": one-token decode steps over a
     ResidentKVCache run lq_resident_attention; everything else (prompts,
     plain tensors) goes to HF's SDPA over the materialised K / V."""
+    from transformers.integrations.sdpa_attention import sdpa_attention_forward
     cache = getattr(key, "_lq_cache", None)
     if cache is None or query.shape[2] != 1:
-        from transformers.integrations.sdpa_attention import sdpa_attention_forward
         return sdpa_attention_forward(module, query, key, value, attention_mask, dropout=dropout, scaling=scaling,
                                       **kwargs)
-    if scaling is not None and abs(scaling - 128 ** -0.5) > 1e-12:
-        raise ValueError("lq_resident attention uses softmax scale 1/sqrt(128)")
+    # The kernel attends to every prefix + tail token with scale 1/sqrt(128).
+    # A decode step that needs anything else -- a mask (HF's SDPA mask builder
+    # returns None for an unpadded causal step, a tensor e.g. for left-padded
+    # batches), a sliding window, logit soft-capping or another scale -- runs
+    # SDPA over the materialised K / V instead, as the reference's cache does.
+    if (attention_mask is not None or kwargs.get("sliding_window") is not None or
+            kwargs.get("softcap") is not None or
+            (scaling is not None and abs(scaling - 128 ** -0.5) > 1e-12)):
+        k, v = cache.materialise(key._lq_layer)
+        return sdpa_attention_forward(module, query, k, v, attention_mask, dropout=dropout, scaling=scaling,
+                                      **kwargs)
     out = cache.attend(key._lq_layer, query)            # (B, Hq, 1, hd)
     return out.transpose(1, 2).contiguous(), None        # HF layout (B, q_len, Hq, hd)
 

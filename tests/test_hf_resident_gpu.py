@@ -77,3 +77,33 @@ def test_hf_decode_over_resident_prefix_gpu(prompt, steps, tail, heads, kv):
     assert flushed % 16 == 0 and n - flushed == a.tail_k[0].shape[2] and a.tail_k[0].shape[2] < tail + 16
     if flushed:
         assert a.compressed_bytes() > 0 and a.resident_bytes() > 0
+
+
+@pytest.mark.gpu
+def test_hf_left_padded_batch_uses_masked_sdpa_gpu(monkeypatch):
+    """Batch 2, row 0 left-padded: decode steps carry an attention mask, so the
+    "lq_resident" attention must run SDPA over the materialised K / V (pad
+    tokens get no weight) and agree with the materialising cache; the
+    unmasked kernel path must not run."""
+    from latticequant_amd.llm.resident_cache import ResidentKVCache
+    model, cfg = _model(heads=4, kv_heads=2)
+    g = torch.Generator().manual_seed(2)
+    ids = torch.randint(0, cfg.vocab_size, (2, 48), generator=g).cuda()
+    mask = torch.ones(2, 48, dtype=torch.long, device="cuda")
+    mask[0, :11] = 0
+    a = ResidentKVCache(bits_per_dim=4, tail_tokens=16)
+    b = _Materialising(bits_per_dim=4, tail_tokens=16).cache
+    calls = []
+    orig = ResidentKVCache.attend
+    monkeypatch.setattr(ResidentKVCache, "attend", lambda self, layer, q: calls.append(layer) or orig(self, layer, q))
+    with torch.no_grad():
+        la = model(ids, attention_mask=mask, past_key_values=a, use_cache=True).logits[:, -1].float()
+        lb = model(ids, attention_mask=mask, past_key_values=b, use_cache=True).logits[:, -1].float()
+        for _ in range(12):
+            nxt = la.argmax(-1, keepdim=True)
+            mask = torch.cat([mask, torch.ones(2, 1, dtype=mask.dtype, device=mask.device)], 1)
+            la = model(nxt, attention_mask=mask, past_key_values=a, use_cache=True).logits[:, -1].float()
+            lb = model(nxt, attention_mask=mask, past_key_values=b, use_cache=True).logits[:, -1].float()
+            assert torch.equal(la, lb)
+    assert calls == []
+    assert a.res_k[0].n_tokens > 0   # the prefix was compressed and is read through materialise()

@@ -120,6 +120,7 @@ def _attn_case(T_chunks, Hkv, group, tail, seed, bits=4, kind="normal"):
     ([512], 4, 1, 1024, 4),        # MHA, long tail (two tail splits)
     ([2048], 4, 7, 64, 5),         # Qwen2.5-7B group 7
     ([96], 1, 16, 3, 6),           # group 16
+    ([8192], 2, 16, 40, 8),        # 32 splits x group 16: the final merge takes its records in several batches
 ])
 def test_resident_attention_vs_oracle_gpu(T_chunks, Hkv, group, tail, seed):
     out, ref = _attn_case(T_chunks, Hkv, group, tail, seed)
@@ -190,5 +191,33 @@ def test_resident_attention_c3_full_size_gpu():
     qf = q.float().view(8, 4, 128)
     s = torch.matmul(qf, K.transpose(1, 2).contiguous()) / 128 ** 0.5
     ref = torch.matmul(torch.softmax(s, -1), V).reshape(32, 128)
+    err = ((out - ref).abs().amax(1) / ref.abs().amax(1)).max().item()
+    assert err <= 1e-3, err
+
+
+def test_resident_attention_long_prefix_split_cap_gpu():
+    """A prefix long enough that the split count is capped at 2048 / group
+    (1 kv head, group 16, 262144 tokens: 128 splits, each wave taking about 8
+    tiles) against float32 attention over the resident prefix's own dequantised
+    values (bit-exact with the oracle at smaller sizes)."""
+    from latticequant_amd import _lib as L
+    from latticequant_amd import codec
+    from latticequant_amd.llm.resident import from_chunk, resident_decode_attention
+    T, G = 262144, 16
+    assert L.lib().lq_resident_attn_workspace(1, G, T, 40) > 0
+    g = torch.Generator(device="cuda").manual_seed(12)
+    k = torch.randn(1, 1, T, 128, generator=g, device="cuda").half()
+    v = torch.randn(1, 1, T, 128, generator=g, device="cuda").half()
+    q = torch.randn(1, G, 1, 128, generator=g, device="cuda").half()
+    tk = torch.randn(1, 1, 40, 128, generator=g, device="cuda").half()
+    tv = torch.randn(1, 1, 40, 128, generator=g, device="cuda").half()
+    ek, _ = codec.encode_batch(k[None], 4)
+    ev, _ = codec.encode_batch(v[None], 4)
+    rk, rv = from_chunk(k, ek), from_chunk(v, ev)
+    out = resident_decode_attention(rk, rv, q, tk, tv).float().view(G, 128)
+    K = torch.cat([rk.dequant().view(T, 128), tk[0, 0]], 0).float()
+    V = torch.cat([rv.dequant().view(T, 128), tv[0, 0]], 0).float()
+    s = torch.matmul(q.float().view(G, 128), K.t().contiguous()) / 128 ** 0.5
+    ref = torch.matmul(torch.softmax(s, -1), V)
     err = ((out - ref).abs().amax(1) / ref.abs().amax(1)).max().item()
     assert err <= 1e-3, err

@@ -14,35 +14,60 @@ from latticequant_amd import codec
 from latticequant_amd import _lib as L
 
 
-def _fake_batch(C=2, nh=2, bph=1024, seed=0):
-    """A structurally valid EncodedBatch on the CPU (random contents)."""
+def _fake_batch(C=2, nh=2, bph=1000, seed=0):
+    """A structurally valid EncodedBatch on the CPU: random tables, bitmap and
+    words, with every cross-field rule of the format kept (the coset-1 counts
+    are the bitmap's, a coset's streams are present exactly when it holds
+    vectors -- chunk 1 has no coset-1 vector --, the word offsets follow the
+    merged layout, checkpoints are non-decreasing from 0 within n_bits).  bph
+    is not a multiple of the block size, so the last block is partial."""
     rng = np.random.default_rng(seed)
-    S, nb = L.LQ_STREAMS, (nh * bph + L.LQ_BLK - 1) // L.LQ_BLK
+    S, B = L.LQ_STREAMS, L.LQ_BLK
+    nv = nh * bph
+    nb = (nv + B - 1) // B
+    bits = (rng.random((C, nb, B)) < 0.5).astype(np.uint8)
+    bits[:, np.arange(B)[None, :] >= np.minimum(B, nv - np.arange(nb) * B)[:, None]] = 0
+    bits[1] = 0
+    coset_bits = np.packbits(bits, axis=2, bitorder="little").reshape(C, -1)
+    n1 = bits.sum(2).astype(np.int32)
+    tot1 = n1.sum(1)
+    present = np.zeros((C, S), bool)
+    present[:, 8:] = (tot1 > 0)[:, None]
+    present[:, :8] = (nv - tot1 > 0)[:, None]
     tab = np.zeros((C * S, L.TABLE_BYTES // 4), np.uint32)
-    for i in range(C * S):
-        if i % 5 == 3:
-            continue                                   # an absent stream
-        n = int(rng.integers(3, 40))
-        # every symbol at least once, the rest at random: sums to L, every f >= 1
-        f = np.bincount(np.concatenate([np.arange(n), rng.integers(0, n, L.LQ_L - n)]), minlength=n)
-        cum = np.cumsum(f) - f
-        bl = np.array([int(v).bit_length() for v in f], np.uint32)
-        tab[i, :4] = np.array([-(n // 2), n, int(rng.integers(1, 999)), 0], np.int32).view(np.uint32)
-        tab[i, 4:4 + n] = f.astype(np.uint32) | (cum.astype(np.uint32) << 11) | ((11 - bl) << 21)
-    cw = rng.integers(10, 50, C)
+    nbits = np.zeros((C, S), np.int64)
+    off = np.zeros((C, S, nb), np.uint32)
+    st = np.full((C, S, nb), L.LQ_L, np.int64)
+    for c in range(C):
+        for k in range(S):
+            if not present[c, k]:
+                continue
+            i = c * S + k
+            n = int(rng.integers(3, 40))
+            # every symbol at least once, the rest at random: sums to L, every f >= 1
+            f = np.bincount(np.concatenate([np.arange(n), rng.integers(0, n, L.LQ_L - n)]), minlength=n)
+            cum = np.cumsum(f) - f
+            bl = np.array([int(v).bit_length() for v in f], np.uint32)
+            tab[i, :4] = np.array([-(n // 2), n, int(rng.integers(1, 999)), 0], np.int32).view(np.uint32)
+            tab[i, 4:4 + n] = f.astype(np.uint32) | (cum.astype(np.uint32) << 11) | ((11 - bl) << 21)
+            nbits[c, k] = int(rng.integers(0, 5000))
+            off[c, k] = np.sort(np.concatenate([[0], rng.integers(0, nbits[c, k] + 1, nb - 1)]))
+            st[c, k] = rng.integers(L.LQ_L, 2 * L.LQ_L, nb)
+    per = np.where(present, (nbits + 31) // 32 + 1, 0)
+    woff = np.cumsum(per, 1) - per
+    cw = per.sum(1)
     words = rng.integers(0, 2 ** 32, int(cw.sum()) + 7, dtype=np.uint64).astype(np.uint32)
     T = lambda a: torch.from_numpy(np.ascontiguousarray(a))
     return codec.EncodedBatch(
-        n_chunks=C, n_heads=nh, bph=bph, shape=(1, nh, bph * 8 // 128, 128), bits=T(np.full(C, 4, np.int32)),
+        n_chunks=C, n_heads=nh, bph=bph, shape=(1, nh, bph * 8 // 64, 64), bits=T(np.full(C, 4, np.int32)),
         scale32=T(rng.random(C * nh).astype(np.float32)), scale16=T(rng.random(C * nh).astype(np.float16)),
         sigma2=T(rng.random(C * nh).astype(np.float32)),
-        coset_bits=T(rng.integers(0, 256, (C, nb * L.LQ_BLK // 8)).astype(np.uint8)),
-        blk_n1=T(rng.integers(0, 513, (C, nb)).astype(np.int32)),
+        coset_bits=T(coset_bits), blk_n1=T(n1),
         tables=T(tab.view(np.uint8).reshape(-1)),
-        blk_off=T(rng.integers(0, 2 ** 31, C * S * nb).astype(np.int32)),
-        blk_state=T(rng.integers(1024, 2048, C * S * nb).astype(np.int16)),
-        stream_nbits=T(rng.integers(0, 10 ** 6, C * S)), stream_state=T(rng.integers(1024, 2048, C * S).astype(np.int32)),
-        stream_woff=T(rng.integers(0, 10 ** 5, C * S)), chunk_words=T(cw.astype(np.int64)),
+        blk_off=T(off.reshape(-1).view(np.int32)),
+        blk_state=T(st.reshape(-1).astype(np.uint16).view(np.int16)),
+        stream_nbits=T(nbits.reshape(-1)), stream_state=T(rng.integers(1024, 2048, C * S).astype(np.int32)),
+        stream_woff=T(woff.reshape(-1)), chunk_words=T(cw.astype(np.int64)),
         chunk_base=T((np.cumsum(cw) - cw + 3).astype(np.int64)), words=T(words.view(np.int32)),
         status=T(np.zeros(C, np.int32)))
 
@@ -94,6 +119,56 @@ def test_wire_rejects_corruption_and_versions_cpu(tmp_path):
     v2[8:12] = np.uint32(99).tobytes()
     with pytest.raises(codec.WireFormatError, match="version"):
         codec.from_bytes(bytes(v2), device="cpu")
+
+
+def _corrupt(field, edit):
+    """A fresh valid batch with one field edited (to_bytes writes a valid CRC)."""
+    e = _fake_batch(seed=3)
+    a = getattr(e, field).clone()
+    edit(a)
+    setattr(e, field, a)
+    return codec.to_bytes(e)
+
+
+def _set(i, v):
+    def f(a):
+        a.view(-1)[i] = v
+    return f
+
+
+@pytest.mark.parametrize("field,edit,match", [
+    ("blk_n1", _set(0, 7), "coset-1 counts"),                            # count not the bitmap's
+    ("coset_bits", lambda a: a.view(-1).__setitem__(5, a.view(-1)[5] ^ 4), "coset-1 counts"),
+    ("stream_woff", _set(3, 1), "layout"),                               # a stream moved
+    ("stream_nbits", _set(2, 10 ** 6), "layout"),                        # longer than its words
+    ("stream_nbits", _set(L.LQ_STREAMS + 9, 64), "bit counts"),          # bits in an absent stream
+    ("blk_off", _set(1, 2 ** 30), "checkpoint offsets"),                 # past the stream end
+    ("blk_off", _set(0, 5), "checkpoint offsets"),                       # the first block not at bit 0
+    ("blk_state", _set(4, 17), "states"),                                # state below L
+    ("scale16", lambda a: None, None),                                   # (unchanged: must load)
+])
+def test_wire_rejects_inconsistent_fields_cpu(field, edit, match):
+    b = _corrupt(field, edit)
+    if match is None:
+        assert codec.from_bytes(b, device="cpu").n_chunks == 2
+        return
+    with pytest.raises(codec.WireFormatError, match=match):
+        codec.from_bytes(b, device="cpu")
+
+
+def test_wire_rejects_bad_sizes_and_shape_cpu():
+    e = _fake_batch(seed=4)
+    e.scale16 = e.scale16[:-1].clone()
+    with pytest.raises(codec.WireFormatError, match="scale16"):
+        codec.from_bytes(codec.to_bytes(e), device="cpu")
+    e = _fake_batch(seed=4)
+    e.shape = (1, 3, 125, 64)
+    with pytest.raises(codec.WireFormatError, match="shape"):
+        codec.from_bytes(codec.to_bytes(e), device="cpu")
+    e = _fake_batch(seed=4)
+    e.blk_n1 = e.blk_n1[:, :-1].clone()
+    with pytest.raises(codec.WireFormatError, match="blk_n1"):
+        codec.from_bytes(codec.to_bytes(e), device="cpu")
 
 
 @pytest.mark.gpu
