@@ -265,8 +265,10 @@ int lq_rans_decode_streams(const int32_t *d_bits, const int32_t *d_bit_off, cons
 /* -------------------------------------------------------- compact form --- */
 
 /* Fixed-rate unpack + dequant, b in {3,4,5}: out = fp16((coord + 0.5*coset) * scale[head_idx]).
+ * d_scales holds n_scales values; a head index outside [0, n_scales) is clamped
+ * (garbage out, no fault, no host check).
  * Replaces _unpack_e8_4bit_kernel (core/triton_dequant.py:45-132). */
-int lq_unpack_compact(const uint8_t *d_packed, int bits, int64_t n, const float *d_scales,
+int lq_unpack_compact(const uint8_t *d_packed, int bits, int64_t n, const float *d_scales, int64_t n_scales,
                       const int32_t *d_head_idx, uint16_t *d_out, hipStream_t s);
 
 /* Fixed-rate pack of in-range E8 points, b in {3,4,5} (core/compact_storage.py:87-154).
@@ -277,11 +279,14 @@ int lq_pack_compact(const float *d_q, int bits, int64_t n, uint8_t *d_packed, in
  * when mask[i] != 0 else copied from fallback[rank_fb(i)]; ranks are computed
  * in-kernel.  head = i / bph.  Replaces _fused_merge_4bit_vec_kernel
  * (llm/fused_triton_merge.py:33-130), with unpack_e8's floor-mod parity.
+ * packed holds n_packed rows, fallback n_fallback; ranks past them (a mask
+ * that selects more rows than the caller holds) are clamped, and a block with
+ * no row at all is written as zeros: garbage out, no fault, no host check.
  * d_work: lq_merge_workspace(total) bytes. */
 int64_t lq_merge_workspace(int64_t total_blocks);
-int lq_fused_merge(const uint8_t *d_packed, int bits, const uint16_t *d_fallback, const uint8_t *d_mask,
-                   const float *d_scales, int64_t total_blocks, int64_t bph, void *d_work, uint16_t *d_out,
-                   hipStream_t s);
+int lq_fused_merge(const uint8_t *d_packed, int64_t n_packed, int bits, const uint16_t *d_fallback,
+                   int64_t n_fallback, const uint8_t *d_mask, const float *d_scales, int64_t total_blocks,
+                   int64_t bph, void *d_work, uint16_t *d_out, hipStream_t s);
 
 /* ----------------------------------------------------------- API helpers -- */
 

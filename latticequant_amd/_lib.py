@@ -54,10 +54,10 @@ _SIGS = {
     "lq_build_tables": ([_P, _P, _P, _I32, _P, _P, _P, _P, _P], _INT),
     "lq_rans_encode_streams": ([_P, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _P], _INT),
     "lq_rans_decode_streams": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _I32, _P, _P], _INT),
-    "lq_unpack_compact": ([_P, _INT, _I64, _P, _P, _P, _P], _INT),
+    "lq_unpack_compact": ([_P, _INT, _I64, _P, _I64, _P, _P, _P], _INT),
     "lq_pack_compact": ([_P, _INT, _I64, _P, _P, _P], _INT),
     "lq_merge_workspace": ([_I64], _I64),
-    "lq_fused_merge": ([_P, _INT, _P, _P, _P, _I64, _I64, _P, _P, _P], _INT),
+    "lq_fused_merge": ([_P, _I64, _INT, _P, _I64, _P, _P, _I64, _I64, _P, _P, _P], _INT),
     "lq_e8_validate": ([_P, _I64, ctypes.c_float, _INT, _P, _P], _INT),
     "lq_unpack_e8": ([_P, _INT, _I64, _P, _P], _INT),
     "lq_symbol_index": ([_P, _I64, _P, _I32, _INT, _P, _P], _INT),
@@ -155,6 +155,13 @@ def stream_ptr(device=None) -> int:
 
 def ptr(t) -> int | None:
     return None if t is None else t.data_ptr()
+
+
+def debug_checks() -> bool:
+    """LQ_DEBUG_CHECKS=1: wrappers also validate device-side index ranges on
+    the host (each such check syncs with the device); by default they rely on
+    the kernels' own clamping."""
+    return os.environ.get("LQ_DEBUG_CHECKS", "") not in ("", "0")
 
 
 def check(rc: int, what: str):

@@ -387,6 +387,114 @@ def chunk_streams_host(enc: EncodedBatch, c: int):
     return res
 
 
+class PendingEncode:
+    """Host-side completion of a batch that encode_batch_deferred wrote
+    without any host sync.  A non-blocking copy of the chunks' status flags
+    and word counts to pinned host memory is queued behind the encode, with an
+    event.  result() (idempotent; waits for the event if needed) returns the
+    final batch: the same batch with its bitstream arena trimmed to the exact
+    size (a device copy; the bound-sized arena is released), or -- if a chunk's
+    lattice symbols overflowed int8 -- the batch re-encoded on the int16 path
+    from the kept input and the same scales.  Where encode_batch would raise
+    AlphabetError, result() raises it, and again on every later call.
+    ready() says, without blocking, whether result() can run without waiting."""
+
+    # batches of at most this many vectors are not tracked: no copy or event is
+    # queued per batch (those cost more than a small batch's encode on the
+    # host); they are settled together by settle_many, or one by one on access
+    TRACK_MIN_VECTORS = 1 << 16
+
+    def __init__(self, enc: "EncodedBatch", x: torch.Tensor, bits, dither_seed):
+        C = enc.n_chunks
+        self._enc, self._x, self._bits, self._seed = enc, x, bits, dither_seed
+        self._done = None
+        self._error = None
+        self._host = self._event = None
+        self.tracked = C * enc.n_vectors > self.TRACK_MIN_VECTORS
+        if self.tracked:
+            self._host = torch.empty(2 * C, dtype=torch.int64, pin_memory=True)
+            self._host.copy_(self._meta(), non_blocking=True)
+            self._event = torch.cuda.Event()
+            self._event.record(torch.cuda.current_stream(x.device))
+
+    def _meta(self) -> torch.Tensor:
+        return torch.cat([self._enc.status.to(torch.int64), self._enc.chunk_words])
+
+    def ready(self) -> bool:
+        """Settled, or tracked and its read-back has arrived (non-blocking)."""
+        if self._done is not None or self._error is not None:
+            return True
+        return self.tracked and self._event.query()
+
+    def result(self) -> "EncodedBatch":
+        if self._done is not None:
+            return self._done
+        if self._error is not None:
+            raise self._error
+        try:
+            return self._settle()
+        except AlphabetError as e:   # kept: every later access raises it again
+            self._error = e
+            self._enc = self._x = None
+            raise
+
+    def _settle(self, host=None) -> "EncodedBatch":
+        if host is None:
+            if self.tracked:
+                self._event.synchronize()
+                host = self._host
+            else:
+                host = self._meta().cpu()
+        enc = self._enc
+        C = enc.n_chunks
+        st = 0
+        for v in host[:C].tolist():
+            st |= int(v)
+        if st & L.LQ_ST_SYM_OVERFLOW:
+            done, _ = encode_batch(self._x, self._bits, scale32=enc.scale32, exact_size=True, wide=True,
+                                   dither_seed=self._seed)
+        else:
+            if st & L.LQ_ST_ALPHABET:
+                raise AlphabetError("a stream's alphabet exceeds L = 1024 symbols (the reference's table "
+                                    "normalisation never terminates there); use more bits or smaller chunks")
+            n = int(host[C:].sum())
+            enc.words = enc.words[:n + 2].clone()   # decoder read-ahead slack
+            done = enc
+        self._done = done
+        self._enc = self._x = None
+        return done
+
+
+def settle_many(pends) -> None:
+    """Settle pending batches with one device-to-host copy for all of them
+    (their metadata concatenated on the device).  Batches whose alphabet check
+    fails keep their AlphabetError for their next result()."""
+    todo = [p for p in pends if p._done is None and p._error is None]
+    if not todo:
+        return
+    host = torch.cat([p._meta() for p in todo]).cpu()
+    o = 0
+    for p in todo:
+        n = 2 * p._enc.n_chunks
+        try:
+            p._done = p._settle(host[o:o + n])
+            p._enc = p._x = None
+        except AlphabetError as e:
+            p._error = e
+            p._enc = p._x = None
+        o += n
+
+
+def encode_batch_deferred(x: torch.Tensor, bits, deq_out: bool = False, dither_seed=None):
+    """encode_batch with no host sync (int8 staging, bound-sized arena):
+    returns (enc, deq, PendingEncode).  enc may be used for device work in
+    stream order right away unless a chunk overflowed int8; the pending
+    handle's result() is the batch to keep (see PendingEncode)."""
+    x = _check_input(x)
+    enc, deq = encode_batch(x, bits, deq_out=deq_out, exact_size=False, wide=False, dither_seed=dither_seed)
+    return enc, deq, PendingEncode(enc, x, bits, dither_seed)
+
+
 # ------------------------------------------------------------ wire format --
 #
 # A self-describing, versioned byte form of an EncodedBatch for offload and

@@ -37,12 +37,14 @@ def unpack_e8_dequant(packed: torch.Tensor, scales: torch.Tensor, head_indices: 
     hi = head_indices.to(device=dev, dtype=torch.int32).contiguous()
     if hi.numel() != n:
         raise ValueError("head_indices must hold one index per vector")
-    if n:
+    if sc.numel() == 0:
+        raise ValueError("scales is empty")
+    if n and L.debug_checks():   # a host sync; the kernel clamps out-of-range indices otherwise
         lo_i, hi_i = (int(v) for v in torch.aminmax(hi))
         if lo_i < 0 or hi_i >= sc.numel():
             raise ValueError(f"head_indices must lie in [0, {sc.numel()}), got [{lo_i}, {hi_i}]")
     out = torch.empty(n, 8, dtype=torch.float16, device=dev)
     with torch.cuda.device(dev):
-        L.check(L.lib().lq_unpack_compact(p.data_ptr(), bits_per_dim, n, sc.data_ptr(), hi.data_ptr(), out.data_ptr(),
-                                          L.stream_ptr(dev)), "lq_unpack_compact")
+        L.check(L.lib().lq_unpack_compact(p.data_ptr(), bits_per_dim, n, sc.data_ptr(), sc.numel(), hi.data_ptr(),
+                                          out.data_ptr(), L.stream_ptr(dev)), "lq_unpack_compact")
     return out

@@ -39,7 +39,7 @@ __device__ __forceinline__ void unpack_word(uint64_t w, int bits, float q[8]) {
 }
 
 __global__ void k_unpack(const uint8_t* __restrict__ packed, int bits, int64_t n, const float* __restrict__ scales,
-                         const int32_t* __restrict__ head_idx, uint16_t* __restrict__ out) {
+                         int64_t n_scales, const int32_t* __restrict__ head_idx, uint16_t* __restrict__ out) {
     int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (v >= n) return;
     uint64_t w;
@@ -51,7 +51,9 @@ __global__ void k_unpack(const uint8_t* __restrict__ packed, int bits, int64_t n
     }
     float q[8], y[8];
     unpack_word(w, bits, q);
-    float s = scales[head_idx[v]];
+    // an index outside [0, n_scales) is clamped: garbage out, never a fault
+    const int64_t h = head_idx[v];
+    float s = scales[h < 0 ? 0 : (h >= n_scales ? n_scales - 1 : h)];
 #pragma unroll
     for (int i = 0; i < 8; i++) y[i] = q[i] * s;
     store8(out, LQ_F16, v, y);
@@ -134,6 +136,7 @@ __global__ void k_merge_scan(int64_t n_tiles, int64_t* __restrict__ tile_cnt) { 
 __global__ __launch_bounds__(256) void k_merge(const uint8_t* __restrict__ packed, int bits,
                                                const uint16_t* __restrict__ fallback, const uint8_t* __restrict__ mask,
                                                const float* __restrict__ scales, int64_t total, int64_t bph,
+                                               int64_t n_packed, int64_t n_fallback,
                                                const int64_t* __restrict__ tile_off, uint16_t* __restrict__ out) {
     __shared__ int wcnt[kTile / 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -153,7 +156,10 @@ __global__ __launch_bounds__(256) void k_merge(const uint8_t* __restrict__ packe
         int before = 0;
         for (int k = 0; k < r * 4 + wave; k++) before += wcnt[k];
         int64_t rr = tile_off[blockIdx.x] + before + __popcll(bal & ((1ull << lane) - 1ull));
-        if (m[r]) {
+        // ranks past the rows the caller holds (a mask that selects more rows
+        // than packed / fallback have) are clamped: garbage out, never a fault
+        if (m[r] && n_packed > 0) {
+            rr = rr < n_packed ? rr : n_packed - 1;
             uint64_t w = bits == 4 ? (uint64_t)__builtin_bswap32(reinterpret_cast<const uint32_t*>(packed)[rr])
                                    : load_be(packed + rr * bits, bits);
             float q[8], y[8];
@@ -162,9 +168,12 @@ __global__ __launch_bounds__(256) void k_merge(const uint8_t* __restrict__ packe
 #pragma unroll
             for (int i = 0; i < 8; i++) y[i] = q[i] * s;
             store8(out, LQ_F16, b, y);
-        } else {
+        } else if (!m[r] && n_fallback > 0) {
             int64_t fr = b - rr;
+            fr = fr < n_fallback ? fr : n_fallback - 1;
             reinterpret_cast<uint4*>(out)[b] = reinterpret_cast<const uint4*>(fallback)[fr];
+        } else {
+            reinterpret_cast<uint4*>(out)[b] = make_uint4(0u, 0u, 0u, 0u);
         }
     }
 }
@@ -173,12 +182,12 @@ __global__ __launch_bounds__(256) void k_merge(const uint8_t* __restrict__ packe
 
 extern "C" {
 
-int lq_unpack_compact(const uint8_t* d_packed, int bits, int64_t n, const float* d_scales, const int32_t* d_head_idx,
-                      uint16_t* d_out, hipStream_t s) {
-    if (bits < 3 || bits > 5 || n < 0) return LQ_ERR_ARG;
+int lq_unpack_compact(const uint8_t* d_packed, int bits, int64_t n, const float* d_scales, int64_t n_scales,
+                      const int32_t* d_head_idx, uint16_t* d_out, hipStream_t s) {
+    if (bits < 3 || bits > 5 || n < 0 || n_scales <= 0) return LQ_ERR_ARG;
     if (n == 0) return LQ_OK;
     hipLaunchKernelGGL(k_unpack, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, d_packed, bits, n, d_scales,
-                       d_head_idx, d_out);
+                       n_scales, d_head_idx, d_out);
     return launch_status();
 }
 
@@ -194,17 +203,17 @@ int64_t lq_merge_workspace(int64_t total_blocks) {
     return ((total_blocks + kTile - 1) / kTile + 1) * 8;
 }
 
-int lq_fused_merge(const uint8_t* d_packed, int bits, const uint16_t* d_fallback, const uint8_t* d_mask,
-                   const float* d_scales, int64_t total_blocks, int64_t bph, void* d_work, uint16_t* d_out,
-                   hipStream_t s) {
-    if (bits < 3 || bits > 5 || total_blocks < 0 || bph <= 0) return LQ_ERR_ARG;
+int lq_fused_merge(const uint8_t* d_packed, int64_t n_packed, int bits, const uint16_t* d_fallback, int64_t n_fallback,
+                   const uint8_t* d_mask, const float* d_scales, int64_t total_blocks, int64_t bph, void* d_work,
+                   uint16_t* d_out, hipStream_t s) {
+    if (bits < 3 || bits > 5 || total_blocks < 0 || bph <= 0 || n_packed < 0 || n_fallback < 0) return LQ_ERR_ARG;
     if (total_blocks == 0) return LQ_OK;
     const int64_t tiles = (total_blocks + kTile - 1) / kTile;
     int64_t* off = reinterpret_cast<int64_t*>(d_work);
     hipLaunchKernelGGL(k_merge_count, dim3((unsigned)tiles), dim3(256), 0, s, d_mask, total_blocks, off);
     hipLaunchKernelGGL(k_merge_scan, dim3(1), dim3(256), 0, s, tiles, off);
     hipLaunchKernelGGL(k_merge, dim3((unsigned)tiles), dim3(256), 0, s, d_packed, bits, d_fallback, d_mask, d_scales,
-                       total_blocks, bph, off, d_out);
+                       total_blocks, bph, n_packed, n_fallback, off, d_out);
     return launch_status();
 }
 

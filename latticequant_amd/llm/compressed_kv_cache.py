@@ -77,10 +77,12 @@ class OptimizedChunk:
     The reference's host-side fields are properties materialised on first use."""
 
     def __init__(self, enc: Optional[codec.EncodedBatch], index: int, scales: torch.Tensor, orig_shape, n_vectors: int,
-                 n_heads: int, blocks_per_head: int, bits_per_dim: float, orig_dtype: torch.dtype):
+                 n_heads: int, blocks_per_head: int, bits_per_dim: float, orig_dtype: torch.dtype,
+                 pending: Optional[codec.PendingEncode] = None):
         self._enc = enc
         self._index = index
-        self._one = enc.select(index) if enc is not None else None
+        self._pending = pending
+        self._one_raw = enc.select(index) if enc is not None else None
         self.scales = scales
         self.orig_shape = tuple(orig_shape)
         self.n_vectors = n_vectors
@@ -89,6 +91,18 @@ class OptimizedChunk:
         self.bits_per_dim = bits_per_dim
         self.orig_dtype = orig_dtype
         self._host = None
+
+    @property
+    def _one(self) -> Optional[codec.EncodedBatch]:
+        """The chunk's one-chunk batch; a batch written without host syncs is
+        settled first (its exact-size arena, or its int16 re-encode)."""
+        if self._pending is not None:
+            enc = self._pending.result()
+            self._enc = enc
+            self._one_raw = enc.select(self._index)
+            self._host = None
+            self._pending = None
+        return self._one_raw
 
     @property
     def encoded(self) -> Optional[codec.EncodedBatch]:
@@ -280,6 +294,7 @@ class CompressedKVCache(DynamicCache):
         self._resident_v: List[Optional[_Resident]] = []
         self.total_vectors = 0
         self._model_dtype = None
+        self._pending: list = []   # (PendingEncode, chunks) written without host syncs, not yet settled
 
     # -- compression ----------------------------------------------------
     def _compress_many(self, tensors: List[torch.Tensor], bits=None):
@@ -294,20 +309,47 @@ class CompressedKVCache(DynamicCache):
         n_heads = batch * heads
         bph = seq * (hd // 8)
         n_vectors = n_heads * bph
+        pend = None
         if self.eval_only_no_entropy:
             _, scale16, deq = codec.quantize_batch(x, bits)
             enc = None
         else:
-            enc, deq = codec.encode_batch(x, bits, deq_out=True, exact_size=True)
+            # no host sync here: the chunks' status and exact sizes are settled
+            # later (_settle_ready at the next update, or on first access)
+            enc, deq, pend = codec.encode_batch_deferred(x, bits, deq_out=True)
             scale16 = enc.scale16
         out = []
         per = scale16.view(len(tensors), -1)
+        chunks = []
         for i, t in enumerate(tensors):
             b = bits if isinstance(bits, int) else bits[i]
-            ch = OptimizedChunk(enc, i, per[i], t.shape, n_vectors, n_heads, bph, b, t.dtype)
+            ch = OptimizedChunk(enc, i, per[i], t.shape, n_vectors, n_heads, bph, b, t.dtype, pending=pend)
             self.total_vectors += n_vectors
+            chunks.append(ch)
             out.append((ch, deq[i]))
+        if pend is not None:
+            self._pending.append((pend, chunks))
         return out
+
+    def _settle_ready(self):
+        """Settle the batches whose status read-back has arrived (non-blocking),
+        and, once 256 small (untracked) batches are pending, all of those with
+        one copy: their chunks move to the exact-size arena (or the int16
+        re-encode)."""
+        small = [p for p, _ in self._pending if not p.tracked]
+        if len(small) >= 256:
+            codec.settle_many(small)
+        keep = []
+        for pend, chunks in self._pending:
+            if pend.ready():
+                try:
+                    for ch in chunks:
+                        ch._one   # rebinds the chunk to the settled batch
+                except codec.AlphabetError:
+                    pass          # the chunks raise it when they are read
+            else:
+                keep.append((pend, chunks))
+        self._pending = keep
 
     def _compress_tensor(self, tensor: torch.Tensor) -> Tuple[Any, torch.Tensor]:
         """(chunk, decompressed) or ('uncompressible', tensor).  llm/compressed_kv_cache.py:176-287"""
@@ -341,6 +383,7 @@ class CompressedKVCache(DynamicCache):
         device = key_states.device
         if self._model_dtype is None:
             self._model_dtype = key_states.dtype
+        self._settle_ready()
         bk, bv = self._layer_bits(layer_idx)
         if key_states.shape == value_states.shape:
             (comp_k, k_new), (comp_v, v_new) = self._compress_many([key_states, value_states],

@@ -39,19 +39,22 @@ def fused_decompress_chunk(chunk: CompressedChunk) -> torch.Tensor:
     n_repr = int(packed.shape[0])
     if packed.dim() != 2 or (n_repr and packed.shape[1] != bits):
         raise ValueError(f"packed must be (n_repr, {bits}) uint8")
-    # the kernel indexes packed / fallback by mask ranks: their row counts must match the mask
-    n_set = int(mask.sum().item())
-    if n_set != n_repr or total - n_set != fallback.shape[0]:
-        raise ValueError(f"mask selects {n_set} packed / {total - n_set} fallback blocks, chunk holds "
-                         f"{n_repr} / {fallback.shape[0]}")
+    # the kernel indexes packed / fallback by mask ranks and clamps ranks past
+    # their row counts; LQ_DEBUG_CHECKS=1 also checks the counts on the host (a sync)
+    if L.debug_checks():
+        n_set = int(mask.sum().item())
+        if n_set != n_repr or total - n_set != fallback.shape[0]:
+            raise ValueError(f"mask selects {n_set} packed / {total - n_set} fallback blocks, chunk holds "
+                             f"{n_repr} / {fallback.shape[0]}")
     sc = chunk.scales.to(device=dev, dtype=torch.float32).contiguous()
     if sc.numel() < batch * heads:
         raise ValueError("one scale per head required")
     out = torch.empty(total * 8, dtype=torch.float16, device=dev)
     work = torch.empty(max(int(L.lib().lq_merge_workspace(total)), 8), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
-        L.check(L.lib().lq_fused_merge(packed.data_ptr(), bits, fallback.data_ptr(), mask.data_ptr(), sc.data_ptr(),
-                                       total, bph, work.data_ptr(), out.data_ptr(), L.stream_ptr(dev)),
+        L.check(L.lib().lq_fused_merge(packed.data_ptr(), n_repr, bits, fallback.data_ptr(), int(fallback.shape[0]),
+                                       mask.data_ptr(), sc.data_ptr(), total, bph, work.data_ptr(), out.data_ptr(),
+                                       L.stream_ptr(dev)),
                 "lq_fused_merge")
     return out.reshape(batch, heads, seq, hd)
 

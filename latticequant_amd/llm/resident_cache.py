@@ -52,7 +52,7 @@ class ResidentKVCache(DynamicCache):
         self.res_v: List[Optional[ResidentKV]] = []
         self.tail_k: List[Optional[torch.Tensor]] = []
         self.tail_v: List[Optional[torch.Tensor]] = []
-        self.chunks: List[list] = []          # per layer: [(EncodedBatch K, EncodedBatch V)]
+        self.chunks: List[list] = []          # per layer: [(_AtRest K, _AtRest V)] rANS chunks at rest
         self._work = None
         self._work_heads = 0
 
@@ -70,7 +70,8 @@ class ResidentKVCache(DynamicCache):
         tk, tv = self.tail_k[layer_idx], self.tail_v[layer_idx]
         B, H, _, hd = tk.shape
         xk, xv = tk[:, :, :n].contiguous(), tv[:, :, :n].contiguous()
-        enc, _ = codec.encode_batch(torch.stack([xk, xv]), self.bits)
+        # no host sync: the at-rest chunks are settled on first access
+        enc, _, pend = codec.encode_batch_deferred(torch.stack([xk, xv]), self.bits)
         ek, ev = enc.select(0), enc.select(1)
         for i, (res, x, e) in enumerate(((self.res_k, xk, ek), (self.res_v, xv, ev))):
             r = res[layer_idx]
@@ -80,7 +81,7 @@ class ResidentKVCache(DynamicCache):
             elif r.n_tokens + n > r.cap_blocks * RB:
                 r.reserve(max(2 * r.cap_blocks * RB, r.n_tokens + n))
             r.append(x, e.scale32, e.scale16)
-        self.chunks[layer_idx].append((ek, ev))
+        self.chunks[layer_idx].append((_AtRest(pend, 0), _AtRest(pend, 1)))
         self.tail_k[layer_idx] = tk[:, :, n:].contiguous()
         self.tail_v[layer_idx] = tv[:, :, n:].contiguous()
 
@@ -163,7 +164,7 @@ class ResidentKVCache(DynamicCache):
     def compressed_bytes(self) -> int:
         """Bytes of the at-rest chunks as the reference counts them
         (bitstream + coset bits + fp16 scales, llm/compressed_kv_cache.py:113-119)."""
-        return sum(int(e.reference_bytes().sum()) for ch in self.chunks for pair in ch for e in pair)
+        return sum(int(e.batch.reference_bytes().sum()) for ch in self.chunks for pair in ch for e in pair)
 
     def resident_bytes(self) -> int:
         """Bytes of the resident decode form (records, meta, scales, exceptions)."""
@@ -171,6 +172,17 @@ class ResidentKVCache(DynamicCache):
 
     def tail_bytes(self) -> int:
         return sum(t.numel() * t.element_size() for t in self.tail_k + self.tail_v if t is not None)
+
+
+class _AtRest:
+    """One K or V half of a flushed chunk pair, settled on first access."""
+
+    def __init__(self, pend, index: int):
+        self._pend, self._index = pend, index
+
+    @property
+    def batch(self):
+        return self._pend.result().select(self._index)
 
 
 def attn_workspace_size(n_heads: int, group: int, t_prefix: int, t_tail: int) -> int:

@@ -144,7 +144,7 @@ def test_validate_and_representable_gpu():
             cs.pack_e8(torch.tensor([bad]).cuda(), 4)
 
 
-def test_triton_unpack_4bit_gpu():
+def test_triton_unpack_4bit_gpu(monkeypatch):
     from latticequant_amd.core import triton_dequant as td
     rng = np.random.default_rng(3)
     n, H = 50000, 8
@@ -157,6 +157,7 @@ def test_triton_unpack_4bit_gpu():
     out = td.triton_unpack_e8_4bit(torch.from_numpy(packed).cuda(), torch.from_numpy(scales).cuda(),
                                    torch.from_numpy(head).cuda())
     np.testing.assert_array_equal(out.cpu().numpy(), O.dequant_compact(packed, 4, scales, head))
+    monkeypatch.setenv("LQ_DEBUG_CHECKS", "1")   # the host-side range check (a sync) is opt-in
     with pytest.raises(ValueError):
         td.triton_unpack_e8_4bit(torch.from_numpy(packed).cuda(), torch.from_numpy(scales).cuda(),
                                  torch.from_numpy(head + H).cuda())
@@ -314,3 +315,33 @@ def test_fixed_rate_merge_gpu():
         np.testing.assert_array_equal(fused, want)
         np.testing.assert_array_equal(ch.repr_mask.cpu().numpy(), O.check_representable(qo, b))
         assert 0 < int(ch.repr_mask.sum()) < ch.n_vectors
+
+
+def test_compact_index_clamping_gpu(monkeypatch):
+    """No host sync by default: out-of-range head indices and masks that select
+    more rows than packed / fallback hold are clamped in the kernels (garbage,
+    never a fault); LQ_DEBUG_CHECKS=1 restores the host-side ValueErrors."""
+    from latticequant_amd.core import triton_dequant as td
+    from latticequant_amd.llm.compressed_kv_cache import compress_fixed_rate
+    from latticequant_amd.llm.fused_triton_merge import fused_decompress_chunk
+    gen = torch.Generator().manual_seed(23)
+    packed = torch.randint(0, 256, (64, 4), generator=gen, dtype=torch.uint8).cuda()
+    sc = torch.rand(3, generator=gen).cuda()
+    hi = torch.zeros(64, dtype=torch.int32)
+    hi[:5] = torch.tensor([0, 1, 2, 7, -3], dtype=torch.int32)
+    out = td.triton_unpack_e8_4bit(packed, sc, hi.cuda())
+    assert torch.equal(out, td.triton_unpack_e8_4bit(packed, sc, hi.clamp(0, 2).cuda()))
+    t = torch.randn(1, 2, 64, 128, generator=gen)
+    t[..., :3] *= 12.0
+    ch = compress_fixed_rate(t.half().cuda(), bits_per_dim=4, storage_bits=4)
+    good = fused_decompress_chunk(ch)
+    n_pk = int(ch.packed.shape[0])
+    assert 1 < n_pk < ch.n_vectors
+    ch.packed = ch.packed[:n_pk // 2].clone()          # the mask now selects rows past the end
+    bad = fused_decompress_chunk(ch)
+    assert bad.shape == good.shape
+    monkeypatch.setenv("LQ_DEBUG_CHECKS", "1")
+    with pytest.raises(ValueError, match="head_indices"):
+        td.triton_unpack_e8_4bit(packed, sc, hi.cuda())
+    with pytest.raises(ValueError, match="mask selects"):
+        fused_decompress_chunk(ch)

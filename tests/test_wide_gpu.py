@@ -107,8 +107,10 @@ def test_int8_overflow_flag_without_auto_gpu():
 
 def test_variable_rate_cache_heavy_tailed_gpu():
     """Layer-wise rates on heavy-tailed K: each chunk equals the oracle's at its
-    rate (wide path where needed), or the update raises where the alphabet
-    exceeds L (the reference never terminates there)."""
+    rate (wide path where needed), or -- where the alphabet exceeds L (the
+    reference never terminates there) -- the chunk raises AlphabetError when
+    it is settled (update() writes without host syncs; the first read of the
+    chunk settles it), and keeps raising on later reads."""
     from latticequant_amd import codec
     from latticequant_amd.allocation.eval_alloc import VariableRateKVCache, cyclic_schedule
     sched = cyclic_schedule(3, seed=0)   # 3, 4, 5 bits
@@ -122,7 +124,10 @@ def test_variable_rate_cache_heavy_tailed_gpu():
         kk = torch.from_numpy(k).cuda()
         try:
             cache.update(kk, torch.from_numpy(v).cuda(), layer)
+            cache._comp_keys[layer].chunks[-1].encoded
         except codec.AlphabetError:
+            with pytest.raises(codec.AlphabetError):
+                cache._comp_keys[layer].chunks[-1].encoded
             s2 = O.head_sigma2(k.astype(np.float32))
             s32, _ = O.cache_scales(s2, b)
             assert max(oracle_alphabets(k, b, s32)) > O.L - 8   # device sigma^2 may differ in the last bit
