@@ -277,3 +277,27 @@ def test_rht_golden():
 def test_golden_meta():
     m = json.load(open(os.path.join(G, "meta.json")))
     assert m["cpu_capability"] and m["numpy"]
+
+
+def test_as_written_tier_matches_oracle():
+    """oracle/aswritten.py (the reference's CPU structure: torch ops + per-symbol
+    Python loops, timed as bench.py's "as written" cpu_baseline tier) writes the
+    oracle's streams and decodes to the oracle's values."""
+    import torch
+    from oracle import aswritten as A
+    rng = np.random.default_rng(31)
+    t = rng.standard_normal((1, 2, 64, 128)).astype(np.float16)
+    t[..., :3] *= 10
+    for bits in (3, 4, 5):
+        ch = O.compress_chunk(t, bits)
+        streams, s16, cos = A.compress(torch.from_numpy(t), bits, scales_f32=ch.scales_f32)
+        assert len(streams) == len(ch.streams)
+        for (c, i, words, state, nb, lo, freqs, n), s in zip(streams, ch.streams):
+            assert (c, i, n, state, nb, lo) == (s.coset, s.idx, s.n_symbols, s.state, s.n_bits, s.table.alphabet[0])
+            np.testing.assert_array_equal(words, s.words)
+            np.testing.assert_array_equal(freqs, s.table.freqs)
+        np.testing.assert_array_equal(s16.numpy(), ch.scales)
+        np.testing.assert_array_equal(A.decompress(streams, cos, s16, t.shape), O.decompress_chunk(ch))
+    # without injected scales the torch sigma^2 path gives the oracle's fp16 scales
+    _, s16, _ = A.compress(torch.from_numpy(t), 4)
+    np.testing.assert_array_equal(s16.numpy(), O.compress_chunk(t, 4).scales)
