@@ -1,22 +1,34 @@
 """Benchmark of the E8 + rANS compressed-KV hot path on one MI355X.
 
-Workload ("C2"): a Llama-3.1-8B-shaped KV cache,
-32 layers x {K, V} x [batch 1, 8 kv heads, 8192 tokens, head_dim 128] fp16,
-N(0, 1) with 4 fixed outlier channels per head scaled x10, 4 bits/dim, one
-chunk (one _compress_tensor call, per-chunk tables) per layer and K/V.
+Headline workload ("C2"): a Llama-3.1-8B-shaped KV
+cache, 32 layers x {K, V} x [batch 1, 8 kv heads, 8192 tokens, head_dim 128]
+fp16, N(0, 1) with 4 fixed outlier channels per head scaled x10, 4 bits/dim,
+one chunk (one _compress_tensor call, per-chunk tables) per layer and K/V.
+Inputs come from torch's CPU generator (seed 1000*layer + kv), their SHA-256
+is in the line, and they are resident in HBM before timing starts.
 
 One step = write (compress all 64 chunks: scales, E8, tables, rANS encode,
 bitstream assembly) + read (decode + dequantise all 64 chunks back to fp16).
-Inputs are resident in HBM before timing starts.
 
 value = algorithmic bytes / time with B = 4*D + 2*C (write reads 2D fp16
 bytes and writes C; read reads C and writes 2D), D = fp16 elements,
 C = stored compressed bytes (bitstream + coset bits + scales + tables +
 checkpoints).
 
+Also on the line, each with its own roofline fraction: C3 (the 32k-context
+decode step), C1 (fixed-rate round trip), C4 (28-layer 3/4/5-bit schedule,
+heavy-tailed K) and C5 (batch-8 x 131072-token rotated + dithered cache,
+sustained write and read); and cpu_baseline with three CPU tiers (oracle on one
+core, oracle on every affinity core, the reference's as-written structure on a
+slice), the core count, torch's threads and the CPU model.
+
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+                    [--skip c1,c3,c4,c5] [--c5-layers N]
+    python bench.py --only c1|c3|c4|c5      one leg alone (the profiling entry points)
+    python bench.py --e2e                   model decode tok/s through the HF cache interface
 """
 import argparse
+import hashlib
 import json
 import os
 import sys
@@ -34,33 +46,391 @@ HBM_PEAK_GBS = 8000.0
 LAYERS, HEADS, TOKENS, HD, BITS = 32, 8, 8192, 128, 4
 
 
+def _sha(t: torch.Tensor) -> str:
+    """SHA-256 of a CPU tensor's bytes."""
+    return hashlib.sha256(memoryview(t.contiguous().numpy()).cast("B")).hexdigest()
+
+
 def make_kv(device):
-    """64 chunks (layer-major, K then V), seed 1000*layer + kv, 4 outlier channels x10 per head."""
+    """C2 input: 64 chunks (layer-major, K then V), each N(0,1) from torch's CPU
+    generator seeded 1000*layer + kv, 4 outlier channels per head
+    (randperm(128)[:4] of a second CPU generator with the same seed, one draw
+    per head) scaled x10, rounded to fp16, moved to `device`.
+    Returns (x, SHA-256 over the fp16 bytes of the 64 chunks in order)."""
     x = torch.empty(LAYERS * 2, 1, HEADS, TOKENS, HD, dtype=torch.float16, device=device)
+    h = hashlib.sha256()
     for layer in range(LAYERS):
         for kv in range(2):
-            g = torch.Generator(device=device).manual_seed(1000 * layer + kv)
-            t = torch.randn(HEADS, TOKENS, HD, generator=g, device=device, dtype=torch.float32)
+            t = torch.randn(HEADS, TOKENS, HD, generator=torch.Generator().manual_seed(1000 * layer + kv))
             gc = torch.Generator().manual_seed(1000 * layer + kv)
-            for h in range(HEADS):
-                ch = torch.randperm(HD, generator=gc)[:4].to(device)
-                t[h][:, ch] *= 10.0
-            x[2 * layer + kv, 0] = t.to(torch.float16)
-    return x
+            for hd_ in range(HEADS):
+                ch = torch.randperm(HD, generator=gc)[:4]
+                t[hd_][:, ch] *= 10.0
+            t16 = t.to(torch.float16)
+            h.update(memoryview(t16.numpy()).cast("B"))
+            x[2 * layer + kv, 0] = t16.to(device)
+    return x, h.hexdigest()
 
 
-def cpu_baseline(x_host_chunks, bits, scale_rows):
-    """The CPU oracle (C restatement, single thread) on a bounded sample of chunks."""
+def cpu_info():
+    """Cores this process may use, torch's intra-op threads and the CPU model."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"affinity_cores": len(os.sched_getaffinity(0)), "torch_threads": torch.get_num_threads(),
+            "cpu_model": model}
+
+
+def _port_chunk(args):
+    """One C2 chunk through the oracle (compress + decompress) in a worker
+    process; returns its algorithmic bytes 4 D + 2 C."""
+    t, sc, bits = args
     from oracle import oracle as O
+    ch = O.compress_chunk(t, bits, scales_f32=sc)
+    O.decompress_chunk(ch)
+    return 4 * t.size + 2 * ch.compressed_bytes
+
+
+def _port_ready(_):
+    from oracle import oracle as O
+    O.lib()
+    return os.getpid()
+
+
+def cpu_baseline(x_chunks, bits, scale_rows, gpu_words, gpu_out):
+    """CPU baselines of C2 on the GPU box's host, bounded samples, byte formula
+    B = 4 D + 2 C as on the GPU:
+      port        the C/numpy oracle, one thread, on len(x_chunks) chunks, each
+                  checked bit for bit against the GPU's stream words and decoded
+                  output of the same chunk;
+      port_cores  the same oracle in one worker process per affinity core (one
+                  chunk each; processes, since the numpy parts hold the GIL);
+      as_written  the reference's CPU structure (oracle/aswritten.py: torch-CPU
+                  E8 on all torch threads, per-symbol Python rANS loops on one)
+                  on 1/64 of one chunk (128 of its 8192 tokens), extrapolated
+                  linearly to the full cache.
+    Returns (tiers, indices of the bit-exact chunks)."""
+    import multiprocessing as mp
+    from concurrent.futures import ProcessPoolExecutor
+    from oracle import aswritten as A
+    from oracle import oracle as O
+    info = cpu_info()
+    tiers = {}
     t0 = time.perf_counter()
-    nbytes = 0
-    for t, sc in zip(x_host_chunks, scale_rows):
+    nbytes, exact = 0, []
+    for i, (t, sc) in enumerate(zip(x_chunks, scale_rows)):
         ch = O.compress_chunk(t, bits, scales_f32=sc)
-        O.decompress_chunk(ch)
-        d = t.size
-        nbytes += 4 * d + 2 * ch.compressed_bytes
+        dec = O.decompress_chunk(ch)
+        nbytes += 4 * t.size + 2 * ch.compressed_bytes
+        if np.array_equal(gpu_words[i], ch.bitstream) and np.array_equal(gpu_out[i], dec):
+            exact.append(i)
     dt = time.perf_counter() - t0
-    return nbytes / dt / 1e9, dt
+    tiers["port"] = {"value": round(nbytes / dt / 1e9, 5), "unit": "GB/s", "cores": 1, "kind": "port",
+                     "wall_s": round(dt, 2),
+                     "sample": f"{len(x_chunks)} of the 64 C2 chunks ([1,8,8192,128] fp16 each): compress + "
+                               f"decompress with the single-threaded C/numpy oracle"}
+    nc = max(1, info["affinity_cores"])
+    jobs = [(x_chunks[i % len(x_chunks)], scale_rows[i % len(x_chunks)], bits) for i in range(nc)]
+    with ProcessPoolExecutor(max_workers=nc, mp_context=mp.get_context("spawn")) as ex:
+        list(ex.map(_port_ready, range(nc)))          # workers started and the oracle loaded, untimed
+        t0 = time.perf_counter()
+        nb = sum(ex.map(_port_chunk, jobs))
+        dt = time.perf_counter() - t0
+    tiers["port_cores"] = {"value": round(nb / dt / 1e9, 5), "unit": "GB/s", "cores": nc, "kind": "port",
+                           "wall_s": round(dt, 2),
+                           "sample": f"{nc} C2 chunks, one per worker process on {nc} affinity cores"}
+    t = x_chunks[0][:, :, :TOKENS // 64]
+    t0 = time.perf_counter()
+    streams, s16, cos = A.compress(torch.from_numpy(t), bits, scales_f32=scale_rows[0])
+    A.decompress(streams, cos, s16, t.shape)
+    dt = time.perf_counter() - t0
+    csz = sum(len(st[2]) for st in streams) * 4 + (len(cos) + 7) // 8 + 2 * HEADS
+    b_slice = 4 * t.size + 2 * csz
+    tiers["as_written"] = {"value": round(b_slice / dt / 1e9, 7), "unit": "GB/s",
+                           "cores": info["torch_threads"], "kind": "port", "wall_s": round(dt, 2),
+                           "extrapolated_full_cache_s": round(dt * 64 * 64, 0),
+                           "sample": "1/64 of one C2 chunk ([1,8,128,128] fp16): torch-CPU E8 on "
+                                     f"{info['torch_threads']} threads, per-symbol Python rANS table / encode / "
+                                     "decode on one, as the reference structures them; the full cache time is "
+                                     "that slice x 64 x 64 (extrapolated)"}
+    return tiers, exact, info
+
+
+def timed_median(fn, n, flush=None):
+    """Median event time (us) of fn over n runs on the current stream.  Before
+    each run: the flush fill (evicts L2 and MALL) when given, then a queued GPU
+    spin, so the start event is reached after the host has submitted fn."""
+    ts = []
+    for i in range(n):
+        if flush is not None:
+            flush.fill_(i & 0xff)
+        gpu_busy()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1e3)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def _roof(nbytes, us, what):
+    ach = nbytes / (us * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(ach / HBM_PEAK_GBS, 4), "bytes": int(nbytes), "us": round(us, 2), "what": what}
+
+
+def bench_c1(dev, iters=20):
+    """C1: K [1,8,2048,128] = randn(fp32, CPU
+    generator seed 0).half(), 4 bits/dim, no entropy coding: quantize ->
+    fixed-rate compact form (4-byte words of the in-range vectors, fp16
+    fallback for the rest, 1-bit mask, per-head scales) -> fused merge back to
+    fp16.  B = 4 D + 2 P, P = 4 V_in + 16 V_oor + ceil(V/8) + 2 H.
+
+    Timed: the round trip through the API (compress_fixed_rate: quantize,
+    representability, compaction by boolean index -- 3 host syncs, as the
+    reference's tensor-indexing structure has -- then fused_decompress_chunk),
+    and the merge kernel alone (the reference's own throughput method,
+    core/triton_dequant.py:238-286), each with a 512 MiB flush before every run
+    and warm (the 12 MB working set then sits in the 256 MB MALL)."""
+    from latticequant_amd import codec
+    from latticequant_amd.llm.compressed_kv_cache import compress_fixed_rate
+    from latticequant_amd.llm.fused_triton_merge import fused_decompress_chunk
+    from oracle import oracle as O
+    k = torch.randn(1, 8, 2048, 128, generator=torch.Generator().manual_seed(0)).half()
+    sha = _sha(k)
+    kd = k.to(dev)
+    ch = compress_fixed_rate(kd, 4)
+    out = fused_decompress_chunk(ch)
+    # parity: lattice points (at the fp32 scales the device quantized with), mask,
+    # packed words and merged fp16 (at the stored fp16 scales) against the oracle
+    s32 = codec.quantize_points(kd, 4)[1].cpu().numpy()
+    qo = O.quantize_heads(k.float().numpy(), s32)
+    mask = O.check_representable(qo, 4)
+    sw = ch.scales.cpu().numpy()
+    want = (qo.reshape(8, -1, 8) * sw[:, None, None]).astype(np.float32).astype(np.float16).reshape(k.shape)
+    exact = bool(np.array_equal(ch.repr_mask.cpu().numpy(), mask)
+                 and np.array_equal(ch.packed.cpu().numpy(), O.pack_e8(qo[mask], 4))
+                 and np.array_equal(out.cpu().numpy(), want))
+    D = k.numel()
+    V = D // 8
+    v_in = int(mask.sum())
+    P = 4 * v_in + 16 * (V - v_in) + (V + 7) // 8 + 2 * 8
+    B = 4 * D + 2 * P
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    rt = lambda: fused_decompress_chunk(compress_fixed_rate(kd, 4))
+    mg = lambda: fused_decompress_chunk(ch)
+    us_rt_f, us_rt_w = timed_median(rt, iters, flush), timed_median(rt, iters)
+    us_mg_f, us_mg_w = timed_median(mg, iters, flush), timed_median(mg, iters)
+    del flush
+    return {"workload": "C1: K [1,8,2048,128] fp16 (randn seed 0, CPU), 4 b/d, compact 4-byte form + fp16 "
+                        "fallback, no entropy coding", "input_sha256": sha, "bit_exact": exact,
+            "in_range_frac": round(v_in / V, 4), "P_bytes": P, "B_bytes": B,
+            "round_trip_flushed": _roof(B, us_rt_f, "compress_fixed_rate + fused_decompress_chunk, 512 MiB flush "
+                                                   "before each run; includes the API's 3 host syncs"),
+            "round_trip_warm": _roof(B, us_rt_w, "same, warm (MALL-resident working set)"),
+            "merge_flushed": _roof(P + 2 * D, us_mg_f, "lq_fused_merge alone (reads P, writes 2 D), flushed"),
+            "merge_warm": _roof(P + 2 * D, us_mg_w, "lq_fused_merge alone, warm (MALL-resident)")}
+
+
+def _student_t(shape, g):
+    """Student-t with nu = 3 from one CPU generator: z / sqrt(chi2_3 / 3),
+    chi2_3 the sum of three squared standard normals."""
+    z = torch.randn(shape, generator=g)
+    c = torch.randn((3,) + tuple(shape), generator=g).square_().sum(0)
+    return z / (c / 3.0).sqrt()
+
+
+def make_c4():
+    """C4 input, 28 layers of [1,4,16384,128] on the
+    CPU: K Student-t(3) (generator seed 1000*layer) with 8 outlier channels per
+    head (randperm(128)[:8] from the same generator, after the values) x20; V
+    N(0,1) (seed 1000*layer + 1); fp16.  Bits per layer from
+    allocation.eval_alloc.cyclic_schedule(28, seed=0): [3,4,5][l % 3].
+    Returns (K list, V list, schedule, SHA-256 over K0 V0 K1 V1 ...)."""
+    from latticequant_amd.allocation.eval_alloc import cyclic_schedule
+    T = 16384
+    sched = cyclic_schedule(28, seed=0)
+    ks, vs = [], []
+    h = hashlib.sha256()
+    for layer in range(28):
+        g = torch.Generator().manual_seed(1000 * layer)
+        k = _student_t((4, T, HD), g)
+        for hh in range(4):
+            k[hh][:, torch.randperm(HD, generator=g)[:8]] *= 20.0
+        v = torch.randn(4, T, HD, generator=torch.Generator().manual_seed(1000 * layer + 1))
+        k16, v16 = k.half()[None], v.half()[None]
+        h.update(memoryview(k16.numpy()).cast("B"))
+        h.update(memoryview(v16.numpy()).cast("B"))
+        ks.append(k16)
+        vs.append(v16)
+    return ks, vs, sched, h.hexdigest()
+
+
+def bench_c4(dev, steps=5):
+    """C4: the 28-layer Qwen2.5-7B-shaped cache at its 3/4/5-bit schedule, one
+    chunk per (layer, K/V), per-chunk tables.  K chunks whose coding needs a
+    stream alphabet above L = 1024 symbols (the reference's table normalisation
+    never terminates there; the library raises AlphabetError) are found by an
+    untimed pass through encode_batch's checked path and left out of the timed
+    cache; the rest are grouped by rate (K on the int16 staging path, V on
+    int8).  One step = encode every group + decode every group.
+    B = 4 D + 2 C over the coded chunks."""
+    from latticequant_amd import codec
+    from oracle import oracle as O
+    ks_h, vs_h, sched, sha = make_c4()
+    ks = [k.to(dev) for k in ks_h]
+    vs = [v.to(dev) for v in vs_h]
+    codable, refused = [], []
+    for l, k in enumerate(ks):
+        try:
+            codec.encode_batch(k[None], sched[l]["K"])
+            codable.append(l)
+        except codec.AlphabetError:
+            refused.append(l)
+    groups = []   # (x stacked (C,1,4,T,128), bits, wide)
+    for r in (3, 4, 5):
+        kl = [l for l in codable if sched[l]["K"] == r]
+        vl = [l for l in range(28) if sched[l]["V"] == r]
+        if kl:
+            groups.append((torch.stack([ks[l] for l in kl]), r, True, [("K", l) for l in kl]))
+        groups.append((torch.stack([vs[l] for l in vl]), r, False, [("V", l) for l in vl]))
+    del ks, vs
+    outs = [torch.empty_like(g[0]) for g in groups]
+    arenas = [torch.empty(codec.words_bound(g[0].shape[0], g[0][0].numel() // 8), dtype=torch.int32, device=dev)
+              for g in groups]
+    encs = [None] * len(groups)
+
+    def step():
+        for i, (x, r, wide, _) in enumerate(groups):
+            encs[i], _ = codec.encode_batch(x, r, exact_size=False, words_out=arenas[i], wide=wide)
+        for i in range(len(groups)):
+            codec.decode_batch(encs[i], out=outs[i])
+
+    step()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True); e1 = torch.cuda.Event(enable_timing=True)
+    gpu_busy()
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    st = int(np.bitwise_or.reduce(torch.cat([e.status for e in encs]).cpu().numpy()))
+    D = sum(g[0].numel() for g in groups)
+    Cb = sum(int(e.reference_bytes().sum() + e.side_bytes().sum()) for e in encs)
+    B = 4 * D + 2 * Cb
+    # parity: the first V chunk at 3 bits against the oracle's bitstream and decode;
+    # every coded K chunk decodes to its lattice points times the fp16 scale (lossless)
+    gi = next(i for i, g in enumerate(groups) if not g[2])
+    e = encs[gi]
+    x0 = groups[gi][0][0].cpu().numpy()
+    ch = O.compress_chunk(x0, groups[gi][1], scales_f32=e.scale32.view(-1, 4)[0].cpu().numpy())
+    nw = int(e.chunk_words[0])
+    exact = bool(np.array_equal(e.words[:nw].cpu().numpy().view(np.uint32), ch.bitstream)
+                 and np.array_equal(outs[gi][0].cpu().numpy(), O.decompress_chunk(ch)))
+    lossless = True
+    for i, (x, r, wide, names) in enumerate(groups):
+        if not wide:
+            continue
+        for c in range(x.shape[0]):
+            q, _, _ = codec.quantize_points(x[c], r, scale32=encs[i].scale32.view(-1, 4)[c])
+            want = (q.view(4, -1, 8) * encs[i].scale16.view(-1, 4)[c].float().view(4, 1, 1)).view(x[c].shape).half()
+            lossless &= bool(torch.equal(outs[i][c], want))
+    return {"workload": "C4: 28 layers x K,V x [1,4,16384,128] fp16, K Student-t(3) + 8 outlier channels x20, "
+                        "V N(0,1), bits [3,4,5][l % 3], per-chunk tables",
+            "input_sha256": sha, "chunks_coded": sum(g[0].shape[0] for g in groups), "chunks_total": 56,
+            "k_layers_refused_alphabet_over_1024": refused, "status_flags": st,
+            "bit_exact_v_chunk": exact, "k_chunks_lossless": lossless,
+            "step_us": round(us, 1), "D": D, "compressed_bytes": Cb,
+            "effective_bits_per_dim": round(8 * Cb / D, 4),
+            "roofline": _roof(B, us, "encode + decode of every coded chunk, B = 4 D + 2 C over them")}
+
+
+def bench_c5(dev, layers):
+    """C5: batch 8 x 131072 tokens of the
+    Llama-3.1-8B shape, `layers` layers x K,V, one [8,8,131072,128] fp16 chunk
+    per (layer, K/V), all resident in HBM; per-vector HeadRHT (seed
+    layer*10000 + head*10 + kv) and subtractive dither, 4 bits/dim.  Inputs:
+    torch.randn(fp32, device generator seeded 1000*layer + kv).half() (the CPU
+    generator would take minutes at 137 GB), hashed on the host chunk by
+    chunk.  Sustained write: encode_rotated of every chunk back to back
+    (exact-size arenas: one size read-back per chunk); sustained read:
+    decode_rotated of every chunk into two alternating fp16 buffers.  Bytes
+    2 D + C per direction."""
+    from concurrent.futures import ThreadPoolExecutor
+    from latticequant_amd.llm import rotated as R
+    shape = (1, 8, 8, 131072, HD)
+    free, _ = torch.cuda.mem_get_info(dev)
+    per_layer = 2 * (2 << 30) * 1.4     # two 2 GiB inputs + their chunks, blocks and staging
+    fit = int((free - (24 << 30)) // per_layer)
+    if fit < layers:
+        print(f"[bench] C5: {free / 2**30:.0f} GiB free holds {fit} layers, not {layers}", file=sys.stderr, flush=True)
+        layers = max(1, fit)
+    n = 2 * layers
+    xs, names = [], []
+    shas = [None] * n
+    pool = ThreadPoolExecutor(max_workers=max(1, min(8, len(os.sched_getaffinity(0)))))
+    futs = []
+    for layer in range(layers):
+        for kv in range(2):
+            g = torch.Generator(device=dev).manual_seed(1000 * layer + kv)
+            x = torch.randn(shape, generator=g, device=dev, dtype=torch.float32).half()
+            xs.append(x)
+            names.append((layer, kv))
+            if len(futs) >= 8:
+                futs.pop(0).result()
+            futs.append(pool.submit(lambda i, h: shas.__setitem__(i, _sha(h)), len(xs) - 1, x.cpu()))
+    for f in futs:
+        f.result()
+    pool.shutdown()
+    sha = hashlib.sha256("".join(shas).encode()).hexdigest()
+    outs = [torch.empty(shape, dtype=torch.float16, device=dev) for _ in range(2)]
+    enc0, _ = R.encode_rotated(xs[0], BITS, [0], [0], exact_size=True, wide=False)   # warm-up
+    R.decode_rotated(enc0, out=outs[0])
+    del enc0
+    torch.cuda.synchronize()
+    encs = [None] * n
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    gpu_busy()
+    e[0].record()
+    for i, x in enumerate(xs):
+        encs[i], _ = R.encode_rotated(x, BITS, [names[i][0]], [names[i][1]], exact_size=True, wide=False)
+    e[1].record()
+    for i in range(n):
+        R.decode_rotated(encs[i], out=outs[i & 1])
+    e[2].record()
+    torch.cuda.synchronize()
+    w_us, r_us = e[0].elapsed_time(e[1]) * 1e3, e[1].elapsed_time(e[2]) * 1e3
+    st = int(np.bitwise_or.reduce(torch.cat([en.status for en in encs]).cpu().numpy()))
+    D = sum(x.numel() for x in xs)
+    Cb = sum(int(en.reference_bytes().sum() + en.side_bytes().sum()) for en in encs)
+    # size-independent check on the last chunk: subtractive-dither error per head
+    # = G(E8) a^2 (uniform on the scaled Voronoi cell), mean ~ 0
+    y = outs[(n - 1) & 1]
+    err = y.float() - xs[-1].float()
+    sc = encs[-1].scale16.float().view(8, 8)
+    mse = (err * err).mean(dim=(3, 4))[0] / (sc * sc)
+    props = {"mse_over_G_scale2_min": round(float((mse / R.G_E8).min()), 4),
+             "mse_over_G_scale2_max": round(float((mse / R.G_E8).max()), 4),
+             "mean_err": float(err.mean())}
+    del err, y
+    return {"workload": f"C5: {layers} layers x K,V x [8,8,131072,128] fp16 resident ({D * 2 / 1e9:.1f} GB), "
+                        "HeadRHT + subtractive dither, 4 b/d, one chunk per (layer, K/V)",
+            "layers": layers, "chunks": n, "input_sha256_of_chunk_sha256s": sha, "status_flags": st,
+            "D": D, "compressed_bytes": Cb, "effective_bits_per_dim": round(8 * Cb / D, 4),
+            "dither_error_check": props,
+            "write": _roof(2 * D + Cb, w_us, "encode_rotated of every chunk back to back, B = 2 D + C"),
+            "read": _roof(2 * D + Cb, r_us, "decode_rotated of every chunk back to back, B = C + 2 D")}
 
 
 def bench_decode_step(dev, iters=30, prefix=32768, tail=128):
@@ -79,12 +449,16 @@ def bench_decode_step(dev, iters=30, prefix=32768, tail=128):
     from latticequant_amd import codec
     from latticequant_amd.llm.decode_attention import attn_workspace as rans_workspace, decode_attention
     from latticequant_amd.llm.resident import attn_workspace, from_chunk, resident_decode_attention
-    g = torch.Generator(device=dev).manual_seed(3)
-    k = torch.randn(1, 1, HEADS, prefix, HD, generator=g, device=dev).to(torch.float16)
-    v = torch.randn(1, 1, HEADS, prefix, HD, generator=g, device=dev).to(torch.float16)
-    q = torch.randn(1, 32, 1, HD, generator=g, device=dev).to(torch.float16)
-    tk = torch.randn(1, HEADS, tail, HD, generator=g, device=dev).to(torch.float16)
-    tv = torch.randn(1, HEADS, tail, HD, generator=g, device=dev).to(torch.float16)
+    g = torch.Generator().manual_seed(3)
+    k = torch.randn(1, 1, HEADS, prefix, HD, generator=g).half()
+    v = torch.randn(1, 1, HEADS, prefix, HD, generator=g).half()
+    q = torch.randn(1, 32, 1, HD, generator=g).half()
+    tk = torch.randn(1, HEADS, tail, HD, generator=g).half()
+    tv = torch.randn(1, HEADS, tail, HD, generator=g).half()
+    sha = hashlib.sha256()
+    for t in (k, v, q, tk, tv):
+        sha.update(memoryview(t.numpy()).cast("B"))
+    k, v, q, tk, tv = (t.to(dev) for t in (k, v, q, tk, tv))
     ek, _ = codec.encode_batch(k, BITS)
     ev, _ = codec.encode_batch(v, BITS)
     rk, rv = from_chunk(k[0], ek), from_chunk(v[0], ev)
@@ -93,21 +467,7 @@ def bench_decode_step(dev, iters=30, prefix=32768, tail=128):
     rwork = rans_workspace(ek, 4)
     out2 = decode_attention(ek, ev, q, tk, tv, work=rwork)
     flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
-
-    def timed(fn, n):
-        ts = []
-        for i in range(n):
-            flush.fill_(i & 0xff)
-            gpu_busy()
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            e0.record()
-            fn()
-            e1.record()
-            torch.cuda.synchronize()
-            ts.append(e0.elapsed_time(e1) * 1e3)
-        ts.sort()
-        return ts[len(ts) // 2]
+    timed = lambda fn, n: timed_median(fn, n, flush)
 
     us = timed(lambda: resident_decode_attention(rk, rv, q, tk, tv, work=work, out=out), iters)
     us_rans = timed(lambda: decode_attention(ek, ev, q, tk, tv, work=rwork, out=out2), max(5, iters // 3))
@@ -122,6 +482,7 @@ def bench_decode_step(dev, iters=30, prefix=32768, tail=128):
             "decode_step_resident_GBps": round(rbytes / (us * 1e-6) / 1e9, 1),
             "decode_tokens_per_s_32_layers": round(1e6 / (32 * us), 2),
             "decode_step_rans_direct_us": round(us_rans, 2),
+            "input_sha256": sha.hexdigest(),
             "decode_step_workload": f"C3: q [1,32,1,128], prefix K,V [1,8,{prefix},128] E8+rANS {BITS} b/d "
                                     f"(attention reads its resident b=5 form), tail [1,8,{tail},128] fp16, "
                                     f"L2/MALL flushed before each step"}
@@ -304,8 +665,12 @@ def main():
                     help="streams the chunk groups of a step are dealt to (measured: one 64-chunk group on one "
                          "stream is fastest; concurrent groups do not overlap usefully)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-chunks", type=int, default=8)
-    ap.add_argument("--no-decode-step", action="store_true", help="skip the C3 decode-step measurement")
+    ap.add_argument("--cpu-chunks", type=int, default=6,
+                    help="C2 chunks the single-thread oracle codes (each also checked bit for bit)")
+    ap.add_argument("--skip", default="", help="comma list of legs to leave out of the default run: c1,c3,c4,c5")
+    ap.add_argument("--only", choices=["c1", "c3", "c4", "c5"],
+                    help="run one leg alone and print its JSON (the profiling entry points)")
+    ap.add_argument("--c5-layers", type=int, default=32, help="layers of the C5 cache (x K,V chunks of 2 GiB)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run one 1 GiB device copy (the HBM-counter calibration kernel under rocprofv3 --pmc)")
     ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "OUT_JSON"),
@@ -322,28 +687,39 @@ def main():
     if args.summarize_trace:
         summarize_trace(args.summarize_trace)
         return
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for {args.gpus}); "
+              "the per-chunk work is independent and would shard by layer / K-V with no communication.",
+              file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    from latticequant_amd import _lib as L
+    L.lib()
     if args.e2e:
-        dev = torch.device("cuda", 0)
-        torch.cuda.set_device(dev)
         r = e2e_decode_throughput(dev)
         print(json.dumps({"metric": "decode tok/s (1 GPU, batch 1, 64 decode tokens after the prefill)",
                           "unit": "tok/s", "higher_is_better": True, "n_gpus": 1, "data": "synthetic",
                           "dtype": "fp16", "config": {"model": "Llama-3.1-8B architecture, random weights",
                                                      "bits_per_dim": BITS}, "results": r}))
         return
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for {args.gpus}); "
-              "the per-chunk work is independent and would shard by layer / K-V with no communication.",
-              file=sys.stderr)
-        sys.exit(2)
+    legs = {"c1": lambda: bench_c1(dev), "c3": lambda: bench_decode_step(dev), "c4": lambda: bench_c4(dev),
+            "c5": lambda: bench_c5(dev, args.c5_layers)}
+    if args.only:
+        res = legs[args.only]()
+        if args.copy_calib:
+            copy_calibration(dev)
+        print(json.dumps(res))
+        return
+    skip = {v.strip() for v in args.skip.split(",") if v.strip()}
 
     from latticequant_amd import codec
-    from latticequant_amd import _lib as L
 
-    dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
-    L.lib()
-    x = make_kv(dev)
+    def progress(msg):
+        print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+    progress("C2 inputs (CPU generator)")
+    x, x_sha = make_kv(dev)
     C = x.shape[0]
     G = args.group
     groups = [(i, min(i + G, C)) for i in range(0, C, G)]
@@ -377,6 +753,7 @@ def main():
         for st in streams:
             cur.wait_stream(st)
 
+    progress("C2 timed steps")
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -406,43 +783,46 @@ def main():
     B = 4 * D + 2 * Cb
     value = B / (ms_per_step * 1e-3) / 1e9
 
-    # correctness spot check: decoded chunk 0 equals fp16(q * scale16) from the oracle
-    from oracle import oracle as O
-    xs = [x[i, 0].cpu().numpy()[None] for i in range(max(1, args.cpu_chunks))]
-    scs = [encs[i // G].scale32.view(-1, HEADS)[i % G].cpu().numpy() for i in range(len(xs))]
-    ch0 = O.compress_chunk(xs[0], BITS, scales_f32=scs[0])
-    base = int(encs[0].chunk_base[0]); nw = int(encs[0].chunk_words[0])
-    bit_exact = bool(np.array_equal(encs[0].words[base:base + nw].cpu().numpy().view(np.uint32), ch0.bitstream)
-                     and np.array_equal(out[0].cpu().numpy(), O.decompress_chunk(ch0)))
+    # the chunks the CPU baseline codes, with the GPU's words and decoded output
+    # of the same chunks for the bit-exact check
+    ncpu = max(1, args.cpu_chunks)
+    xs = [x[i, 0].cpu().numpy()[None] for i in range(ncpu)]
+    scs = [encs[i // G].scale32.view(-1, HEADS)[i % G].cpu().numpy() for i in range(ncpu)]
+    gw, go = [], []
+    for i in range(ncpu):
+        e = encs[i // G]
+        base = int(e.chunk_base[i % G]); nw = int(e.chunk_words[i % G])
+        gw.append(e.words[base:base + nw].cpu().numpy().view(np.uint32))
+        go.append(out[i].cpu().numpy())
 
     # rooflines of the two largest kernels, each timed per launch with events on
     # its own stream: k_chunk_quantize (write) and k_chunk_decode (read, with
     # its k_chunk_lut table build); the longer one is the headline roofline
     # (measured on single launches over all 64 chunks, outside the step)
-    rgroups = [(0, C)]
-    renc = [codec.encode_batch(x, BITS, exact_size=False, wide=False)[0]]
+    progress("C2 per-kernel rooflines")
+    renc = codec.encode_batch(x, BITS, exact_size=False, wide=False)[0]
     rluts = torch.empty(C * L.LQ_STREAMS * L.LQ_L, dtype=torch.int32, device=dev)
-    dec_ms, q_ms = [], []
-    for gi, (a, b) in enumerate(rgroups):
+    dec_ms = []
+    for _ in range(3):
         s0 = torch.cuda.Event(enable_timing=True); s1 = torch.cuda.Event(enable_timing=True)
         gpu_busy()
-        s0.record(); codec.decode_batch(renc[gi], out=out[a:b], lut_work=rluts); s1.record()
+        s0.record(); codec.decode_batch(renc, out=out, lut_work=rluts); s1.record()
         torch.cuda.synchronize()
         dec_ms.append(s0.elapsed_time(s1))
-        q_ms.append(time_quantize(x[a:b], renc[gi]))
+    q_ms = time_quantize(x, renc)
     # algorithmic bytes: decode reads the stored chunk and writes 16 B of fp16 per
     # vector; the quantizer reads 16 B of fp16 and writes 8 B of int8 symbols and
     # one coset bit per vector
-    dec_bytes = float(np.mean([2 * (b - a) * V * 8 + int(renc[gi].reference_bytes().sum() + renc[gi].side_bytes().sum())
-                               for gi, (a, b) in enumerate(rgroups)]))
-    q_bytes = float(np.mean([(b - a) * V * (16 + 8) + (b - a) * V // 8 for a, b in rgroups]))
+    dec_bytes = 2 * C * V * 8 + int(renc.reference_bytes().sum() + renc.side_bytes().sum())
+    q_bytes = C * V * (16 + 8) + C * V // 8
     traffic = load_traffic()
     kern = {
         "k_chunk_decode": {"ms": float(np.mean(dec_ms)), "bytes": dec_bytes,
                            "desc": f"k_chunk_decode (+k_chunk_lut), {C}-chunk launch, algorithmic bytes = stored chunk + 16 B fp16 out per vector"},
-        "k_chunk_quantize": {"ms": float(np.mean(q_ms)), "bytes": q_bytes,
+        "k_chunk_quantize": {"ms": q_ms, "bytes": q_bytes,
                              "desc": f"k_chunk_quantize, {C}-chunk launch, algorithmic bytes = 16 B fp16 in + 8 B int8 symbols + 1 coset bit per vector"},
     }
+    del renc, rluts
     roof = {}
     for name, k in kern.items():
         ach = k["bytes"] / (k["ms"] * 1e-3) / 1e9
@@ -452,18 +832,42 @@ def main():
                       "kernel": k["desc"], "avg_launch_us": round(k["ms"] * 1e3, 1),
                       "algorithmic_bytes": int(k["bytes"])}
     dominant = max(kern, key=lambda n: kern[n]["ms"])
-
-    step = {} if args.no_decode_step else bench_decode_step(dev)
     if args.copy_calib:
         copy_calibration(dev)
 
-    cpu = None
-    if not args.no_cpu_baseline:
-        v, dt = cpu_baseline(xs, BITS, scs)
-        cpu = {"value": round(v, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": f"{len(xs)} of 64 chunks ([1,8,8192,128] fp16 each), compress + decompress with the "
-                         f"single-threaded C/numpy oracle, {dt:.1f} s"}
+    extra = {}
+    if "c3" not in skip:
+        progress("C3 decode step")
+        extra["c3"] = bench_decode_step(dev)
+    del encs, arenas, luts
+    if "c1" not in skip:
+        progress("C1 round trip")
+        extra["c1"] = bench_c1(dev)
+    if "c4" not in skip:
+        progress("C4 28-layer schedule")
+        extra["c4"] = bench_c4(dev)
+    if "c5" not in skip:
+        del x, out
+        torch.cuda.empty_cache()
+        progress(f"C5 {args.c5_layers} layers")
+        extra["c5"] = bench_c5(dev, args.c5_layers)
+        torch.cuda.empty_cache()
 
+    cpu, exact_idx, info = None, [], cpu_info()
+    if not args.no_cpu_baseline:
+        progress("CPU baselines")
+        tiers, exact_idx, info = cpu_baseline(xs, BITS, scs, gw, go)
+        cpu = dict(tiers["port"])
+        cpu.update({"cpu_model": info["cpu_model"], "affinity_cores": info["affinity_cores"],
+                    "torch_threads": info["torch_threads"], "tiers": tiers})
+    else:
+        from oracle import oracle as O
+        for i in range(ncpu):
+            ch = O.compress_chunk(xs[i], BITS, scales_f32=scs[i])
+            if np.array_equal(gw[i], ch.bitstream) and np.array_equal(go[i], O.decompress_chunk(ch)):
+                exact_idx.append(i)
+
+    c3 = extra.get("c3") or {}
     res = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
@@ -471,18 +875,21 @@ def main():
         "config": {"workload": "C2: Llama-3.1-8B KV cache write+read, 32 layers x K,V x [1,8,8192,128] fp16, "
                                "N(0,1) + 4 outlier channels x10 per head, 4 bits/dim, one chunk per layer/K-V",
                    "chunks": C, "group": G, "streams": NS, "bits_per_dim": BITS},
+        "input_sha256": x_sha,
         "write_ms": round(t_write_ms, 4), "read_ms": round(t_read_ms, 4),
         "write_GBps": round((2 * D + Cb) / (t_write_ms * 1e-3) / 1e9, 2),
         "read_GBps": round((2 * D + Cb) / (t_read_ms * 1e-3) / 1e9, 2),
         "compressed_bytes": Cb, "reference_accounting_bytes": ref_bytes, "side_info_bytes": side_bytes,
         "effective_bits_per_dim": round(8 * Cb / D, 4),
         "reference_bits_per_dim": round(8 * ref_bytes / D, 4),
-        "status_flags": int(np.bitwise_or.reduce(status)), "bit_exact_chunk0": bit_exact,
+        "status_flags": int(np.bitwise_or.reduce(status)),
+        "bit_exact_chunks": f"{len(exact_idx)}/{ncpu}", "bit_exact": len(exact_idx) == ncpu,
         "roofline": roof[dominant],
         "roofline_other": {n: r for n, r in roof.items() if n != dominant},
         "cpu_baseline": cpu,
-        "decode_step_us": step.get("decode_step_us"),
-        "decode_step": step or None,
+        "decode_step_us": c3.get("decode_step_us"),
+        "decode_step": c3 or None,
+        "c1": extra.get("c1"), "c4": extra.get("c4"), "c5": extra.get("c5"),
         "wall_s": round(wall, 3),
     }
     print(json.dumps(res))
