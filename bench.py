@@ -611,9 +611,17 @@ def copy_calibration(dev, nbytes=1 << 30):
     torch.cuda.synchronize()
 
 
+def _kernel_base(name: str) -> str:
+    """Kernel name without return type, namespace, template arguments or parameters."""
+    n = name.replace("(anonymous namespace)::", "")
+    if n.startswith("void "):
+        n = n[5:]
+    return n.split("(")[0].split("<")[0].strip()
+
+
 def summarize_pmc(fetch_csv, write_csv, out_path, calib_bytes=1 << 30):
     """Turn two rocprofv3 --pmc counter_collection.csv files (FETCH_SIZE, then
-    WRITE_SIZE, KiB per dispatch) of a `bench.py --copy-calib` run into HBM
+    WRITE_SIZE, KiB per dispatch) of a run that ends with --copy-calib into HBM
     bytes per launch: each counter is scaled by what it reads for the 1 GiB
     copy (the largest __amd_rocclr_copyBuffer dispatch).  Per kernel the
     dispatches with the largest grid (the full-batch launches) are averaged."""
@@ -624,14 +632,16 @@ def summarize_pmc(fetch_csv, write_csv, out_path, calib_bytes=1 << 30):
         df = df[df["Counter_Name"] == ctr]
         cp = df[df["Kernel_Name"].str.contains("copyBuffer")]
         factors[ctr] = float(cp["Counter_Value"].max()) * 1024.0 / calib_bytes
-        for name in ("k_chunk_quantize", "k_chunk_decode"):
-            d = df[df["Kernel_Name"].str.contains(name)]
-            if len(d) == 0:
+        df = df.assign(base=df["Kernel_Name"].map(_kernel_base))
+        for name, d in df.groupby("base"):
+            if not name.startswith("k_"):
                 continue
             d = d[d["Grid_Size"] == d["Grid_Size"].max()]
             vals.setdefault(name, {})[ctr] = float(d["Counter_Value"].mean()) * 1024.0
+            vals[name]["grid"] = int(d["Grid_Size"].max())
+            vals[name]["dispatches"] = int(len(d))
     res = {"bytes_per_launch": {n: round(v["FETCH_SIZE"] / factors["FETCH_SIZE"] + v["WRITE_SIZE"] / factors["WRITE_SIZE"])
-                                for n, v in vals.items() if len(v) == 2},
+                                for n, v in vals.items() if "FETCH_SIZE" in v and "WRITE_SIZE" in v},
            "raw_bytes": vals, "copy_factor": factors, "calib_bytes": calib_bytes}
     with open(out_path, "w") as f:
         json.dump(res, f, indent=1)
