@@ -89,6 +89,18 @@ int lq_head_scales(const void *d_x, int dtype, int64_t n_chunks, int64_t n_heads
                    const int32_t *d_chunk_bits, double *d_work, float *d_sigma2, float *d_scale32,
                    uint16_t *d_scale16, int32_t *d_fastdiv, hipStream_t s);
 
+/* Rotated rows (the long-context path): as lq_head_scales on w = RHT(x), the
+ * randomized Hadamard transform of each head_dim row (forward: FWHT(x * s) /
+ * sqrt(head_dim) in fp32, sign row s = d_signs[head], head = chunk * n_heads + h,
+ * d_signs (n_chunks * n_heads, head_dim) fp32 +-1), computed in registers:
+ * no rotated copy is written.  head_dim a power of two in [8, 128], bph a
+ * multiple of head_dim / 8.  d_fastdiv receives 0 (rotated values are fp32).
+ * Replaces core/pipeline.py:100-108 (RHT.forward) + llm/perplexity_eval.py:35-61
+ * (HeadRHT) feeding llm/compressed_kv_cache.py:188-196. */
+int lq_head_scales_rht(const void *d_x, int dtype, int64_t n_chunks, int64_t n_heads, int64_t bph, int head_dim,
+                       const float *d_signs, const int32_t *d_chunk_bits, double *d_work, float *d_sigma2,
+                       float *d_scale32, uint16_t *d_scale16, int32_t *d_fastdiv, hipStream_t s);
+
 /* Fast-division flags for caller-supplied fp32 scales (exhaustive check of all
  * 2048 fp16 significands per head).  Same d_fastdiv layout as above. */
 int lq_scale_fastdiv(const float *d_scale32, int64_t n_heads_total, int dtype, int32_t *d_fastdiv,
@@ -112,6 +124,16 @@ int lq_chunk_quantize(const void *d_x, int dtype, int64_t n_chunks, int64_t n_he
                       const float *d_scale32, const int32_t *d_fastdiv, int8_t *d_sym,
                       uint8_t *d_coset_bits, uint32_t *d_blk_n1, uint32_t *d_hist, int32_t *d_status,
                       void *d_deq, int deq_dtype, const int64_t *d_dither_seed, hipStream_t s);
+
+/* Rotated rows: lq_chunk_quantize of w = RHT(x) (as lq_head_scales_rht), the
+ * rotation in registers, IEEE division by scale32, optional dither; no
+ * dequantised output.  Same outputs and layouts as lq_chunk_quantize on a
+ * materialised fp32 rotation.  Replaces core/pipeline.py:100-108 +
+ * llm/perplexity_eval.py:35-61 feeding llm/compressed_kv_cache.py:199-231,270. */
+int lq_chunk_quantize_rht(const void *d_x, int dtype, int64_t n_chunks, int64_t n_heads, int64_t bph, int head_dim,
+                          const float *d_signs, const float *d_scale32, int8_t *d_sym, uint8_t *d_coset_bits,
+                          uint32_t *d_blk_n1, uint32_t *d_hist, int32_t *d_status, const int64_t *d_dither_seed,
+                          hipStream_t s);
 
 /* Wide path (alphabets up to L = 1024 symbols, e.g. heavy-tailed K at low
  * rates): as lq_chunk_quantize with int16 symbols (n_chunks * nblk *
@@ -192,6 +214,17 @@ int lq_chunk_decode(const uint32_t *d_words, const int64_t *d_chunk_base, const 
                     const uint32_t *d_blk_n1, const lq_table *d_tables, const uint16_t *d_scale16,
                     int64_t n_chunks, int64_t n_heads, int64_t bph, uint32_t *d_lut_work, void *d_out,
                     int out_dtype, const int64_t *d_dither_seed, hipStream_t s);
+
+/* lq_chunk_decode of chunks written by lq_chunk_quantize_rht: each row's
+ * fp32 dequantised values ((q - d) * scale16) are rotated back (FWHT / sqrt(head_dim),
+ * then * s, d_signs as for lq_chunk_quantize_rht) before the out_dtype store;
+ * head_dim a power of two in [8, 128].  Replaces llm/compressed_kv_cache.py:289-332
+ * followed by core/pipeline.py:110-118 (RHT.inverse). */
+int lq_chunk_decode_rht(const uint32_t *d_words, const int64_t *d_chunk_base, const int64_t *d_stream_woff,
+                        const uint32_t *d_blk_off, const int64_t *d_stream_nbits, const uint16_t *d_blk_state,
+                        const uint8_t *d_coset_bits, const lq_table *d_tables, const uint16_t *d_scale16,
+                        int64_t n_chunks, int64_t n_heads, int64_t bph, int head_dim, const float *d_signs,
+                        uint32_t *d_lut_work, void *d_out, int out_dtype, const int64_t *d_dither_seed, hipStream_t s);
 
 /* Decoder LUTs of every stream of a chunk batch (n_chunks * 16 * 1024 uint32:
  * per slot: 31 - k | k << 5 | symbol index << 9 | (row * 1024 + (x' << k) - 1024) << 19,

@@ -68,6 +68,9 @@ _SIGS = {
     "lq_attn_workspace": ([_I64, _I64, _I64, _INT], _I64),
     "lq_decode_attention": ([_P, _P, _P, _INT, _P, _P, _I64, _P, _P, _P], _INT),
     "lq_rht": ([_P, _INT, _I64, _INT, _P, _I64, _INT, _INT, _P, _INT, _P], _INT),
+    "lq_head_scales_rht": ([_P, _INT, _I64, _I64, _I64, _INT, _P, _P, _P, _P, _P, _P, _P, _P], _INT),
+    "lq_chunk_quantize_rht": ([_P, _INT, _I64, _I64, _I64, _INT, _P, _P, _P, _P, _P, _P, _P, _P, _P], _INT),
+    "lq_chunk_decode_rht": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _INT, _P, _P, _P, _INT, _P, _P], _INT),
     "lq_resident_workspace": ([_I64, _I64], _I64),
     "lq_resident_quantize": ([_P, _INT, _I64, _I64, _P, _P, _P, _I64, _I64, _P, _P], _INT),
     "lq_resident_dequant": ([_P, _I64, _I64, _I64, _I64, _P, _INT, _P], _INT),

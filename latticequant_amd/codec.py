@@ -128,10 +128,11 @@ def _bits_tensor(bits, C, dev):
     return b.to(dev)
 
 
-def _head_scales(x: torch.Tensor, bits, scale32: Optional[torch.Tensor]):
+def _head_scales(x: torch.Tensor, bits, scale32: Optional[torch.Tensor], rht_signs: Optional[torch.Tensor] = None):
     """Per-head scales of a (C, B, H, T, hd) batch: from sigma^2 on the device
     (llm/compressed_kv_cache.py:188-196) or the caller's fp32 scales, plus the
-    fast-division flags of the quantizer."""
+    fast-division flags of the quantizer.  rht_signs: sigma^2 of the rows
+    rotated in the kernel (the flags are then 0: rotated values are fp32)."""
     lib = L.lib()
     C, B, H, T, hd = x.shape
     dev = x.device
@@ -146,15 +147,44 @@ def _head_scales(x: torch.Tensor, bits, scale32: Optional[torch.Tensor]):
         sigma2 = _empty(C * nh, torch.float32, dev)
         scale32 = _empty(C * nh, torch.float32, dev)
         scale16 = _empty(C * nh, torch.float16, dev)
-        L.check(lib.lq_head_scales(x.data_ptr(), dt, C, nh, bph, bits_t.data_ptr(), work.data_ptr(), sigma2.data_ptr(),
-                                   scale32.data_ptr(), scale16.data_ptr(), fastdiv.data_ptr(), s), "lq_head_scales")
+        if rht_signs is not None:
+            L.check(lib.lq_head_scales_rht(x.data_ptr(), dt, C, nh, bph, hd, rht_signs.data_ptr(), bits_t.data_ptr(),
+                                           work.data_ptr(), sigma2.data_ptr(), scale32.data_ptr(), scale16.data_ptr(),
+                                           fastdiv.data_ptr(), s), "lq_head_scales_rht")
+        else:
+            L.check(lib.lq_head_scales(x.data_ptr(), dt, C, nh, bph, bits_t.data_ptr(), work.data_ptr(),
+                                       sigma2.data_ptr(), scale32.data_ptr(), scale16.data_ptr(), fastdiv.data_ptr(), s),
+                    "lq_head_scales")
     else:
         scale32 = scale32.to(device=dev, dtype=torch.float32).contiguous().view(-1)
         if scale32.numel() != C * nh:
             raise ValueError("scale32 must hold one scale per head of every chunk")
         scale16 = scale32.to(torch.float16)
-        L.check(lib.lq_scale_fastdiv(scale32.data_ptr(), C * nh, dt, fastdiv.data_ptr(), s), "lq_scale_fastdiv")
+        fd_dt = L.LQ_F32 if rht_signs is not None else dt
+        L.check(lib.lq_scale_fastdiv(scale32.data_ptr(), C * nh, fd_dt, fastdiv.data_ptr(), s), "lq_scale_fastdiv")
     return bits_t, scale32, scale16, sigma2, fastdiv
+
+
+def _check_signs(signs: torch.Tensor, rows: int, hd: int, dev) -> torch.Tensor:
+    """RHT sign rows as the kernels read them: (rows, hd) fp32 on the device."""
+    if hd < 8 or hd > 512 or hd & (hd - 1):
+        raise ValueError(f"the rotation needs a power-of-two head_dim in [8, 512], got {hd}")
+    sg = signs.to(device=dev, dtype=torch.float32).contiguous()
+    if sg.numel() != rows * hd:
+        raise ValueError(f"rht_signs must hold {rows} rows of {hd} signs")
+    return sg.view(rows, hd)
+
+
+def rotate_rows(x: torch.Tensor, signs: torch.Tensor, inverse: bool, out_dtype=torch.float32) -> torch.Tensor:
+    """RHT of every hd-row of a (C, B, H, T, hd) batch, row (c*B + b)*H + h of
+    `signs` for head (c, b, h) (lq_rht; fp32 arithmetic)."""
+    lib = L.lib()
+    C, B, H, T, hd = x.shape
+    out = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    L.check(lib.lq_rht(x.data_ptr(), L.dtype_code(x.dtype), x.numel() // hd, hd, signs.data_ptr(), T,
+                       signs.shape[0], 1 if inverse else 0, out.data_ptr(), L.dtype_code(out_dtype),
+                       L.stream_ptr(x.device)), "lq_rht")
+    return out
 
 
 def _check_input(x: torch.Tensor) -> torch.Tensor:
@@ -222,7 +252,7 @@ class AlphabetError(ValueError):
 
 def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, deq_out: bool = False,
                  exact_size: bool = True, words_out: Optional[torch.Tensor] = None, wide="auto",
-                 dither_seed=None):
+                 dither_seed=None, rht_signs: Optional[torch.Tensor] = None):
     """Compress a batch of chunks.
 
     x: (C, B, H, T, hd) fp16 / bf16 / fp32 CUDA tensor, hd % 8 == 0.
@@ -240,17 +270,28 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
     back (wide="auto" or True with exact_size) and is otherwise left in enc.status.
     dither_seed: int or (C,) ints: subtractive dither per chunk (the rotated
       path; the seeds are kept in enc.extra and decode_batch removes the dither).
+    rht_signs: (C*B*H, hd) fp32 sign rows: the chunks are coded as their
+      forward rotations w = RHT(x) (row of head h: sign row h), computed inside
+      the scale and quantize kernels (hd a power of two <= 128); with deq_out,
+      wide=True or an int8 overflow the rotation is materialised instead, with
+      the same result.  deq is then the dequantised w.
     Returns (EncodedBatch, deq or None)."""
     lib = L.lib()
     x = _check_input(x)
     C, B, H, T, hd = x.shape
+    if rht_signs is not None:
+        rht_signs = _check_signs(rht_signs, C * B * H, hd, x.device)
+        fused = not deq_out and wide is not True and hd <= 128
+        if not fused:
+            w = rotate_rows(x, rht_signs, inverse=False)
+            return encode_batch(w, bits, scale32, deq_out, exact_size, words_out, wide, dither_seed)
     dev = x.device
     nh, bph = B * H, T * hd // 8
     V = nh * bph
     nblk = (V + L.LQ_BLK - 1) // L.LQ_BLK
     dt = L.dtype_code(x.dtype)
     s = L.stream_ptr(dev)
-    bits_t, scale32, scale16, sigma2, fastdiv = _head_scales(x, bits, scale32)
+    bits_t, scale32, scale16, sigma2, fastdiv = _head_scales(x, bits, scale32, rht_signs)
     coset_bits = _zeros(C * nblk * L.LQ_BLK // 8, torch.uint8, dev)
     blk_n1 = _empty(C * nblk, torch.int32, dev)
     status = _zeros(C, torch.int32, dev)
@@ -266,10 +307,19 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
     if not use_wide:
         sym = _empty(C * nblk * L.LQ_SYM_STRIDE, torch.int8, dev)
         hist = _zeros(C * L.LQ_STREAMS * 256, torch.int32, dev)
-        L.check(lib.lq_chunk_quantize(x.data_ptr(), dt, C, nh, bph, scale32.data_ptr(), fastdiv.data_ptr(),
-                                      sym.data_ptr(), coset_bits.data_ptr(), blk_n1.data_ptr(), hist.data_ptr(),
-                                      status.data_ptr(), L.ptr(deq), dt, L.ptr(dseed), s), "lq_chunk_quantize")
+        if rht_signs is not None:
+            L.check(lib.lq_chunk_quantize_rht(x.data_ptr(), dt, C, nh, bph, hd, rht_signs.data_ptr(),
+                                              scale32.data_ptr(), sym.data_ptr(), coset_bits.data_ptr(),
+                                              blk_n1.data_ptr(), hist.data_ptr(), status.data_ptr(), L.ptr(dseed), s),
+                    "lq_chunk_quantize_rht")
+        else:
+            L.check(lib.lq_chunk_quantize(x.data_ptr(), dt, C, nh, bph, scale32.data_ptr(), fastdiv.data_ptr(),
+                                          sym.data_ptr(), coset_bits.data_ptr(), blk_n1.data_ptr(), hist.data_ptr(),
+                                          status.data_ptr(), L.ptr(deq), dt, L.ptr(dseed), s), "lq_chunk_quantize")
         if wide == "auto" and _status_or(status) & L.LQ_ST_SYM_OVERFLOW:
+            if rht_signs is not None:   # the int16 path reads the materialised rotation
+                w = rotate_rows(x, rht_signs, inverse=False)
+                return encode_batch(w, bits, scale32, deq_out, exact_size, words_out, wide, dither_seed)
             use_wide = True
             status.zero_()
         else:
@@ -331,10 +381,12 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
 
 
 def decode_batch(enc: EncodedBatch, out_dtype: torch.dtype = torch.float16, out: Optional[torch.Tensor] = None,
-                 lut_work: Optional[torch.Tensor] = None) -> torch.Tensor:
+                 lut_work: Optional[torch.Tensor] = None, rht_signs: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Decompress every chunk of the batch: (C, B, H, T, hd) in out_dtype,
     fp16(q * float(scale16[head])) as _decompress_chunk computes it
-    (llm/compressed_kv_cache.py:289-332)."""
+    (llm/compressed_kv_cache.py:289-332).  rht_signs (C*B*H, hd): the rows are
+    rotated back (inverse RHT of the fp32 dequantised rows, then out_dtype)
+    inside the decoder for hd <= 128, else by a separate pass."""
     lib = L.lib()
     dev = enc.words.device
     C = enc.n_chunks
@@ -342,6 +394,20 @@ def decode_batch(enc: EncodedBatch, out_dtype: torch.dtype = torch.float16, out:
         out = torch.empty((C,) + tuple(enc.shape), dtype=out_dtype, device=dev)
     if lut_work is None:
         lut_work = _empty(C * L.LQ_STREAMS * L.LQ_L, torch.int32, dev)
+    if rht_signs is not None:
+        hd = enc.shape[-1]
+        rht_signs = _check_signs(rht_signs, C * enc.n_heads, hd, dev)
+        if hd > 128:
+            w = decode_batch(enc, out_dtype=torch.float32, lut_work=lut_work)
+            out.copy_(rotate_rows(w, rht_signs, inverse=True, out_dtype=out.dtype))
+            return out
+        L.check(lib.lq_chunk_decode_rht(enc.words.data_ptr(), enc.chunk_base.data_ptr(), enc.stream_woff.data_ptr(),
+                                        enc.blk_off.data_ptr(), enc.stream_nbits.data_ptr(), enc.blk_state.data_ptr(),
+                                        enc.coset_bits.data_ptr(), enc.tables.data_ptr(), enc.scale16.data_ptr(), C,
+                                        enc.n_heads, enc.bph, hd, rht_signs.data_ptr(), lut_work.data_ptr(),
+                                        out.data_ptr(), L.dtype_code(out.dtype),
+                                        L.ptr(enc.extra.get("dither_seed")), L.stream_ptr(dev)), "lq_chunk_decode_rht")
+        return out
     L.check(lib.lq_chunk_decode(enc.words.data_ptr(), enc.chunk_base.data_ptr(), enc.stream_woff.data_ptr(),
                                 enc.blk_off.data_ptr(), enc.stream_nbits.data_ptr(), enc.blk_state.data_ptr(),
                                 enc.coset_bits.data_ptr(),

@@ -127,17 +127,12 @@ __global__ void k_unpack_bits(const uint8_t* __restrict__ packed, int64_t n, uin
     out[i] = (uint8_t)((packed[i >> 3] >> (i & 7)) & 1u);
 }
 
-// Randomized Hadamard transform of d-dim rows (core/pipeline.py:49-118,
-// llm/perplexity_eval.py:35-61): forward w = FWHT(x * s) / sqrt(d), inverse
-// v = FWHT(w) / sqrt(d) * s, in fp32.  Each butterfly stage h = 1, 2, .., d/2
-// replaces (a, b) = (y[i], y[i + h]) by (a + b, a - b) exactly as the
-// reference loop does, so the fp32 result is the reference's bit for bit.
-// d/8 lanes per row, 8 consecutive elements per lane: stages h < 8 run in
-// registers, h >= 8 across lanes (partner lane ^ h/8).
-// Row r uses sign row (r / rows_per_sign) % n_sign.
+// Randomized Hadamard transform of d-dim rows (rht_lanes: core/pipeline.py:49-118,
+// llm/perplexity_eval.py:35-61), d/8 lanes per row, 8 consecutive elements per
+// lane.  Row r uses sign row (r / rows_per_sign) % n_sign.
 template <int IN_DT, int OUT_DT>
 __global__ __launch_bounds__(256) void k_rht(const void* __restrict__ x, int64_t n_rows, int d, const float* __restrict__ signs,
-                                             int64_t rows_per_sign, int n_sign, float inv_norm_div, int inverse,
+                                             int64_t rows_per_sign, int n_sign, float div, int inverse,
                                              void* __restrict__ out) {
     const int lpr = d >> 3;   // lanes per row (1..64, power of two)
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -148,37 +143,9 @@ __global__ __launch_bounds__(256) void k_rht(const void* __restrict__ x, int64_t
     const int64_t v = rr * lpr + part;   // 8-element vector index
     float y[8], s[8];
     load8(x, IN_DT, v, y);
-    const float* sg = signs + ((rr / rows_per_sign) % n_sign) * (int64_t)d + 8 * part;
-#pragma unroll
-    for (int i = 0; i < 8; i++) s[i] = sg[i];
-    if (!inverse) {
-#pragma unroll
-        for (int i = 0; i < 8; i++) y[i] = y[i] * s[i];
-    }
-#pragma unroll
-    for (int h = 1; h < 8; h <<= 1) {
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            if (i & h) continue;
-            const float a = y[i], b = y[i + h];
-            y[i] = a + b;
-            y[i + h] = a - b;
-        }
-    }
+    load_signs8(signs + ((rr / rows_per_sign) % n_sign) * (int64_t)d + 8 * part, s);
     // lanes of one row are consecutive and lpr divides 64, so rows never straddle a wave
-    for (int hl = 1; hl < lpr; hl <<= 1) {
-        const bool upper = (part & hl) != 0;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float o = __shfl_xor(y[i], hl, 64);
-            y[i] = upper ? o - y[i] : y[i] + o;   // lower keeps a + b, upper gets a - b
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        y[i] = y[i] / inv_norm_div;
-        if (inverse) y[i] = y[i] * s[i];
-    }
+    rht_lanes(y, s, part, lpr, div, inverse != 0);
     if (live) store8(out, OUT_DT, v, y);
 }
 

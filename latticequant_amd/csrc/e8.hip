@@ -82,12 +82,17 @@ __global__ void k_quantize_heads(const void* __restrict__ x, int dtype, int64_t 
 
 // ---------------------------------------------------------- head scales --
 
-// Partial sums of x^2 per head in double: grid (heads, parts).
+// Partial sums of x^2 per head in double: grid (heads, parts).  ROT: of the
+// forward-rotated rows w = RHT(x) instead (sign row = the head, lpr lanes per
+// row; the parts split on row boundaries), summed exactly like an fp32 input
+// holding w, so the scales equal those of the materialised rotation.
+template <bool ROT>
 __global__ void k_head_sumsq(const void* __restrict__ x, int dtype, int64_t vec_per_head, int parts,
-                             double* __restrict__ work) {
+                             double* __restrict__ work, const float* __restrict__ signs, int lpr, float rdiv) {
     int64_t h = blockIdx.x;
     int p = blockIdx.y;
     int64_t per = (vec_per_head + parts - 1) / parts;
+    if (ROT) per = (per + lpr - 1) / lpr * lpr;
     int64_t v0 = (int64_t)p * per, v1 = v0 + per < vec_per_head ? v0 + per : vec_per_head;
     // Per vector: the 8 squares (exact in fp32 for fp16 / bf16 inputs) summed
     // in fp32 by a chain of FMAs, then accumulated in fp64; four independent
@@ -101,7 +106,20 @@ __global__ void k_head_sumsq(const void* __restrict__ x, int dtype, int64_t vec_
         for (int i = 1; i < 8; i++) a = __builtin_fmaf(xv[i], xv[i], a);
         return (double)a;
     };
-    if (dtype == LQ_F32) {   // fp32 squares are not exact: keep every product in fp64
+    if (ROT) {
+        // rows are whole within [v0, v1) and lpr divides the block size, so the
+        // lanes of a row enter and leave the loop together
+        const int part = (int)(threadIdx.x % lpr);
+        float sg[8];
+        load_signs8(signs + h * (8 * (int64_t)lpr) + 8 * part, sg);
+        for (; v < v1; v += bd) {
+            float xv[8];
+            load8(x, dtype, h * vec_per_head + v, xv);
+            rht_lanes(xv, sg, part, lpr, rdiv, false);
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc4[0] += (double)xv[i] * (double)xv[i];
+        }
+    } else if (dtype == LQ_F32) {   // fp32 squares are not exact: keep every product in fp64
         for (; v < v1; v += bd) {
             float xv[8];
             load8(x, dtype, h * vec_per_head + v, xv);
@@ -238,14 +256,17 @@ __device__ __forceinline__ void stage_hist(const uint4& w, int row16, int n0, in
 // k_chunk_quantize (described above).  LEAN: the host guarantees bph >= LQ_BLK
 // (a block spans at most two heads) and no dequantised output; the general
 // paths are compiled out, which frees the scalar registers they held (fewer
-// spills through VGPR lanes in the block loop).
-template <typename SymT, bool DITHER, bool LEAN = false>
+// spills through VGPR lanes in the block loop).  ROT: the input rows are first
+// rotated in registers (rht_lanes, sign row = the head, lpr lanes per row),
+// exactly the fp32 values a materialised forward rotation holds; no
+// dequantised output.
+template <typename SymT, bool DITHER, bool LEAN = false, bool ROT = false>
 __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
     const void* __restrict__ x, int dtype, int64_t n_heads, int64_t bph, int64_t nblk,
     const float* __restrict__ scale32, const int32_t* __restrict__ fastdiv, SymT* __restrict__ sym,
     uint8_t* __restrict__ coset_bits, uint32_t* __restrict__ blk_n1, uint32_t* __restrict__ hist,
     int32_t* __restrict__ minmax, int32_t* __restrict__ status, void* __restrict__ deq, int deq_dtype,
-    const int64_t* __restrict__ dseed) {
+    const int64_t* __restrict__ dseed, const float* __restrict__ signs, int lpr, float rdiv) {
     constexpr bool kWide = sizeof(SymT) == 2;
     constexpr int kSymMin = kWide ? -32768 : -128, kSymMax = kWide ? 32767 : 127;
     __shared__ uint32_t shist[kWide ? 1 : LQ_STREAMS * kHRow];
@@ -295,7 +316,7 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
         if (two_heads) {
             s0 = scale32[hq0]; s1 = scale32[hq1];
             rs0 = 1.0f / s0; rs1 = 1.0f / s1;
-            f0 = fastdiv[hq0] != 0; f1 = fastdiv[hq1] != 0;
+            f0 = !ROT && fastdiv[hq0] != 0; f1 = !ROT && fastdiv[hq1] != 0;   // rotated values are fp32
         }
         int32_t sy[2][8];
         int cs[2];
@@ -309,21 +330,33 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
                 const int64_t v = vbase + vl;
                 float s, rs;
                 bool fast;
+                int64_t hq;
                 if (two_heads) {
                     const bool nxt = rblk + vl >= (int)bph;
                     s = nxt ? s1 : s0;
                     rs = nxt ? rs1 : rs0;
                     fast = nxt ? f1 : f0;
+                    hq = nxt ? hq1 : hq0;
                 } else {
                     int rr = rblk + vl;
                     int64_t h = hq0;
                     while (rr >= (int)bph) { rr -= (int)bph; h++; }
                     s = scale32[h];
                     rs = 1.0f / s;
-                    fast = fastdiv[h] != 0;
+                    fast = !ROT && fastdiv[h] != 0;
+                    hq = h;
                 }
                 float xv[8], t[8], ic[8], dd[8];
                 load8(x, dtype, chunk * V + v, xv);
+                if constexpr (ROT) {
+                    // rows start at multiples of lpr vectors and blocks at
+                    // multiples of 512, so the lane's place in its row is tid % lpr;
+                    // valid is a multiple of lpr, so whole rows are live together
+                    float sg[8];
+                    const int part = tid & (lpr - 1);
+                    load_signs8(signs + hq * (8 * (int64_t)lpr) + 8 * part, sg);
+                    rht_lanes(xv, sg, part, lpr, rdiv, false);
+                }
                 if (fast) {
 #pragma unroll
                     for (int i = 0; i < 8; i++) t[i] = div_scaled(xv[i], s, rs, true);
@@ -352,7 +385,7 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
 #pragma unroll
                     for (int i = 0; i < 8; i++) sy[r][i] = min(max(sy[r][i], kSymMin), kSymMax);
                 }
-                if (!LEAN && deq) {
+                if (!LEAN && !ROT && deq) {
                     float off = c ? 0.5f : 0.f, y[8];
 #pragma unroll
                     for (int i = 0; i < 8; i++) {
@@ -528,9 +561,29 @@ int lq_head_scales(const void* d_x, int dtype, int64_t n_chunks, int64_t n_heads
     const int64_t H = n_chunks * n_heads;
     int64_t want = (4096 + H - 1) / H, cap = bph / 512 > 1 ? bph / 512 : 1;
     const int parts = (int)(want < cap ? want : cap);
-    hipLaunchKernelGGL(k_head_sumsq, dim3((unsigned)H, parts), dim3(256), 0, s, d_x, dtype, bph, parts, d_work);
+    hipLaunchKernelGGL(k_head_sumsq<false>, dim3((unsigned)H, parts), dim3(256), 0, s, d_x, dtype, bph, parts, d_work,
+                       nullptr, 1, 1.0f);
     hipLaunchKernelGGL(k_head_finalize, dim3((unsigned)H), dim3(256), 0, s, d_work, parts, bph * 8, n_heads,
                        d_chunk_bits, dtype, d_sigma2, d_scale32, d_scale16, d_fastdiv);
+    return launch_status();
+}
+
+// Rotated rows (head_dim a power of two in [8, 128], bph a multiple of
+// head_dim / 8): the scales of w = RHT(x) without materialising w; the
+// fast-division flags are 0 (w is fp32).
+int lq_head_scales_rht(const void* d_x, int dtype, int64_t n_chunks, int64_t n_heads, int64_t bph, int head_dim,
+                       const float* d_signs, const int32_t* d_chunk_bits, double* d_work, float* d_sigma2,
+                       float* d_scale32, uint16_t* d_scale16, int32_t* d_fastdiv, hipStream_t s) {
+    if (n_chunks <= 0 || n_heads <= 0 || bph <= 0 || dtype < 0 || dtype > 2 || !d_signs) return LQ_ERR_ARG;
+    if (head_dim < 8 || head_dim > 128 || (head_dim & (head_dim - 1)) || bph % (head_dim / 8)) return LQ_ERR_ARG;
+    const int64_t H = n_chunks * n_heads;
+    int64_t want = (4096 + H - 1) / H, cap = bph / 512 > 1 ? bph / 512 : 1;
+    const int parts = (int)(want < cap ? want : cap);
+    const float div = (float)sqrt((double)head_dim);
+    hipLaunchKernelGGL(k_head_sumsq<true>, dim3((unsigned)H, parts), dim3(256), 0, s, d_x, dtype, bph, parts, d_work,
+                       d_signs, head_dim / 8, div);
+    hipLaunchKernelGGL(k_head_finalize, dim3((unsigned)H), dim3(256), 0, s, d_work, parts, bph * 8, n_heads,
+                       d_chunk_bits, (int)LQ_F32, d_sigma2, d_scale32, d_scale16, d_fastdiv);
     return launch_status();
 }
 
@@ -560,15 +613,41 @@ int lq_chunk_quantize(const void* d_x, int dtype, int64_t n_chunks, int64_t n_he
     if (d_dither_seed)
         hipLaunchKernelGGL((k_chunk_quantize<int8_t, true>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x, dtype,
                            n_heads, bph, nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, d_hist, nullptr,
-                           d_status, d_deq, deq_dtype, d_dither_seed);
+                           d_status, d_deq, deq_dtype, d_dither_seed, nullptr, 1, 1.0f);
     else if (bph >= kBlk && !d_deq)
         hipLaunchKernelGGL((k_chunk_quantize<int8_t, false, true>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x,
                            dtype, n_heads, bph, nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, d_hist,
-                           nullptr, d_status, nullptr, deq_dtype, nullptr);
+                           nullptr, d_status, nullptr, deq_dtype, nullptr, nullptr, 1, 1.0f);
     else
         hipLaunchKernelGGL((k_chunk_quantize<int8_t, false>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x, dtype,
                            n_heads, bph, nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, d_hist, nullptr,
-                           d_status, d_deq, deq_dtype, nullptr);
+                           d_status, d_deq, deq_dtype, nullptr, nullptr, 1, 1.0f);
+    return launch_status();
+}
+
+// Rotated rows: as lq_chunk_quantize on w = RHT(x) (sign row = the head,
+// head_dim a power of two in [8, 128], bph a multiple of head_dim / 8), with
+// IEEE division by the scale and no dequantised output.
+int lq_chunk_quantize_rht(const void* d_x, int dtype, int64_t n_chunks, int64_t n_heads, int64_t bph, int head_dim,
+                          const float* d_signs, const float* d_scale32, int8_t* d_sym, uint8_t* d_coset_bits,
+                          uint32_t* d_blk_n1, uint32_t* d_hist, int32_t* d_status, const int64_t* d_dither_seed,
+                          hipStream_t s) {
+    if (n_chunks <= 0 || n_heads <= 0 || bph <= 0 || bph > kMaxBph || dtype < 0 || dtype > 2 || !d_signs)
+        return LQ_ERR_ARG;
+    if (head_dim < 8 || head_dim > 128 || (head_dim & (head_dim - 1)) || bph % (head_dim / 8)) return LQ_ERR_ARG;
+    const int64_t V = n_heads * bph;
+    const int64_t nblk = (V + kBlk - 1) / kBlk;
+    const int64_t wg = n_chunks * ((nblk + kQBlocksPerWG - 1) / kQBlocksPerWG);
+    const float div = (float)sqrt((double)head_dim);
+    const int lpr = head_dim / 8;
+    if (d_dither_seed)
+        hipLaunchKernelGGL((k_chunk_quantize<int8_t, true, false, true>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x,
+                           dtype, n_heads, bph, nblk, d_scale32, nullptr, d_sym, d_coset_bits, d_blk_n1, d_hist, nullptr,
+                           d_status, nullptr, (int)LQ_F32, d_dither_seed, d_signs, lpr, div);
+    else
+        hipLaunchKernelGGL((k_chunk_quantize<int8_t, false, false, true>), dim3((unsigned)wg), dim3(kQThreads), 0, s,
+                           d_x, dtype, n_heads, bph, nblk, d_scale32, nullptr, d_sym, d_coset_bits, d_blk_n1, d_hist,
+                           nullptr, d_status, nullptr, (int)LQ_F32, nullptr, d_signs, lpr, div);
     return launch_status();
 }
 
@@ -584,11 +663,11 @@ int lq_chunk_quantize_wide(const void* d_x, int dtype, int64_t n_chunks, int64_t
     if (d_dither_seed)
         hipLaunchKernelGGL((k_chunk_quantize<int16_t, true>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x, dtype,
                            n_heads, bph, nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, nullptr, d_minmax,
-                           d_status, d_deq, deq_dtype, d_dither_seed);
+                           d_status, d_deq, deq_dtype, d_dither_seed, nullptr, 1, 1.0f);
     else
         hipLaunchKernelGGL((k_chunk_quantize<int16_t, false>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x, dtype,
                            n_heads, bph, nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, nullptr, d_minmax,
-                           d_status, d_deq, deq_dtype, nullptr);
+                           d_status, d_deq, deq_dtype, nullptr, nullptr, 1, 1.0f);
     return launch_status();
 }
 

@@ -174,6 +174,61 @@ __device__ __forceinline__ float div_scaled(float x, float s, float r, bool fast
     return x / s;
 }
 
+// ----------------------------------------------------------------- RHT ---
+//
+// Randomized Hadamard transform of d-dim rows (core/pipeline.py:49-118,
+// llm/perplexity_eval.py:35-61): forward w = FWHT(x * s) / sqrt(d), inverse
+// v = FWHT(w) / sqrt(d) * s, in fp32.  Each butterfly stage h = 1, 2, .., d/2
+// replaces (a, b) = (y[i], y[i + h]) by (a + b, a - b) as the reference loop
+// does, so the fp32 result is the reference's bit for bit.  A row lies in
+// lpr = d / 8 consecutive lanes (lpr divides 64), 8 consecutive elements per
+// lane: stages h < 8 run in registers, h >= 8 across lanes (partner lane ^ h/8).
+// Every lane of a row must execute this together.  div = f32(sqrt(d)).
+// One butterfly stage across lanes: partner lane ^ hl (stage h = 8 hl).
+__device__ __forceinline__ void fwht_cross(float y[8], int part, int hl) {
+    const bool upper = (part & hl) != 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float o = __shfl_xor(y[i], hl, 64);
+        y[i] = upper ? o - y[i] : y[i] + o;   // lower keeps a + b, upper gets a - b
+    }
+}
+
+// Butterfly stages h = 1 .. 4 nl of rows spread over nl lanes: h < 8 in
+// registers, then across lanes.
+__device__ __forceinline__ void fwht_stages(float y[8], int part, int nl) {
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            if (i & h) continue;
+            const float a = y[i], b = y[i + h];
+            y[i] = a + b;
+            y[i + h] = a - b;
+        }
+    }
+    for (int hl = 1; hl < nl; hl <<= 1) fwht_cross(y, part, hl);
+}
+
+__device__ __forceinline__ void rht_lanes(float y[8], const float s[8], int part, int lpr, float div, bool inverse) {
+    if (!inverse) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) y[i] = y[i] * s[i];
+    }
+    fwht_stages(y, part, lpr);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        y[i] = y[i] / div;
+        if (inverse) y[i] = y[i] * s[i];
+    }
+}
+
+__device__ __forceinline__ void load_signs8(const float* p, float s[8]) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+    s[0] = a.x; s[1] = a.y; s[2] = a.z; s[3] = a.w;
+    s[4] = b.x; s[5] = b.y; s[6] = b.z; s[7] = b.w;
+}
+
 // -------------------------------------------------------------- dither ---
 //
 // Subtractive dither of the rotated path (build-defined: the reference has no

@@ -835,14 +835,14 @@ __device__ __forceinline__ int dpp_ror8(int v) {   // lane l <- lane l ^ 8 withi
     return __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false);
 }
 
-template <int OUT_DT, bool HEADS_ALIGNED, bool DITHER>
+template <int OUT_DT, bool HEADS_ALIGNED, bool DITHER, bool ROT = false>
 __global__ __launch_bounds__(kDecThreads) void k_chunk_decode(
         const uint32_t* __restrict__ words, const int64_t* __restrict__ chunk_base, const int64_t* __restrict__ stream_woff,
         const uint32_t* __restrict__ blk_off, const int64_t* __restrict__ stream_nbits,
         const uint16_t* __restrict__ blk_state, const uint8_t* __restrict__ coset_bits,
         const lq_table* __restrict__ tables, const uint16_t* __restrict__ scale16, const uint32_t* __restrict__ lutg,
         int64_t n_chunks, int64_t n_heads, int64_t bph, int64_t nblk, int64_t gpw, void* __restrict__ out,
-        const int64_t* __restrict__ dseed) {
+        const int64_t* __restrict__ dseed, const float* __restrict__ signs, int lpr, float rdiv) {
     __shared__ uint32_t lut[LQ_STREAMS * kL];                               // 64 KB
     __shared__ uint32_t ring[kDecThreads / 64][kLineRing][64];              // 48 KB
     __shared__ __align__(16) uint16_t stg[kDecBlocks * 2 * kDecGroupU16];   // 34 KB
@@ -905,11 +905,13 @@ __global__ __launch_bounds__(kDecThreads) void k_chunk_decode(
     }
     float sc;
     half2_t sc2;
+    const float* sgp = nullptr;   // ROT: the head's sign row
     auto set_scale = [&](int64_t head) {
         const uint16_t s16 = scale16[chunk * n_heads + head];
         sc = h2f(s16);
         const _Float16 sh = __builtin_bit_cast(_Float16, s16);
         sc2 = half2_t{sh, sh};
+        if (ROT) sgp = signs + (chunk * n_heads + head) * (8 * (int64_t)lpr);
     };
     const int64_t head0 = vfirst / bph;
     set_scale(head0);
@@ -934,6 +936,7 @@ __global__ __launch_bounds__(kDecThreads) void k_chunk_decode(
     uint16_t* const my_stg = &stg[(b * 2 + c) * kDecGroupU16 + idx];
     const int u = (l16 & 3) + 1;     // lines of the flush candidate this lane checks
 
+    float pend[ROT ? 8 : 1];         // ROT: butterfly stages of a deferred first half-row (lanes 0..7)
     int st = 0;                      // vectors of my coset staged (symbols of my stream decoded)
     int fpos = 0, fr0 = 0, fr1 = 0;  // flushed block positions and flushed ranks per coset (block-uniform)
     while (fpos < valid) {
@@ -962,41 +965,101 @@ __global__ __launch_bounds__(kDecThreads) void k_chunk_decode(
         const uint64_t bal = __builtin_amdgcn_ballot_w64(ok);
         const int nl = __builtin_popcountll((bal >> (tid & 48)) & 0xfull);
         const int F = 8 * nl < rest ? 8 * nl : rest;   // positions flushed this phase (<= 32)
-        for (int r0 = 0; r0 < F; r0 += 16) {
-            const int q = r0 + l16;
-            if (q < F) {
-                const int p = fpos + q;
-                const bool cp = (W >> q) & 1u;
-                const int n1b = __builtin_popcount(W & ((1u << q) - 1u));
-                const int rank = cp ? fr1 + n1b : fr0 + q - n1b;
-                const uint4 r = *reinterpret_cast<const uint4*>(&stg[(b * 2 + cp) * kDecGroupU16 + (rank & (kDecStage - 1)) * 8]);
-                if (!HEADS_ALIGNED && vfirst + p >= head_end) {
-                    const int64_t head = (vfirst + p) / bph;
-                    head_end = (head + 1) * bph;
-                    set_scale(head);
-                }
-                if (!DITHER && OUT_DT == LQ_F16 && biased) {
-                    const _Float16 o = cp ? (_Float16)0.5f : (_Float16)0.0f;
-                    reinterpret_cast<uint4*>(ob)[p] = deq_biased_f16(r, half2_t{o, o}, sc2);
+        // fp32 output row of position p (fpos <= p < fpos + F): the lattice
+        // point from its staged symbols, dither removed, times the head's scale
+        auto lattice_y = [&](int p, float y[8]) {
+            const int q = p - fpos;
+            const bool cp = (W >> q) & 1u;
+            const int n1b = __builtin_popcount(W & ((1u << q) - 1u));
+            const int rank = cp ? fr1 + n1b : fr0 + q - n1b;
+            const uint4 r = *reinterpret_cast<const uint4*>(&stg[(b * 2 + cp) * kDecGroupU16 + (rank & (kDecStage - 1)) * 8]);
+            if (!HEADS_ALIGNED && vfirst + p >= head_end) {
+                const int64_t head = (vfirst + p) / bph;
+                head_end = (head + 1) * bph;
+                set_scale(head);
+            }
+            if (biased) {
+                lattice_biased_f32(r, cp ? 0.5f : 0.f, y);
+            } else {
+                CosetConsts cs;
+                cs.pick(cp, cc0, cc1);
+                cs.deq_f32(r, 1.0f, y);   // the lattice point itself (exact)
+            }
+            if constexpr (DITHER) {
+                float dd[8];
+                dither8(dkey, vfirst + p, dd);
+#pragma unroll
+                for (int j = 0; j < 8; j++) y[j] = (y[j] - dd[j]) * sc;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; j++) y[j] *= sc;
+            }
+        };
+        if constexpr (ROT) {
+            // Lane l16 stores the positions p == l16 (mod 16) of the flush, so a
+            // 16-vector row's first half always sits in lanes 0..7 and its second
+            // half in lanes 8..15.  Rows of lpr <= 8 vectors lie inside one line
+            // and are rotated back whole.  When a 16-vector row's first line
+            // flushes before its second, that half's butterfly stages (h <= 32)
+            // wait in registers (pend) and its store is deferred; when the second
+            // line comes both halves take the last stage (h = 64) together: the
+            // operations and their order are those of the whole-row transform.
+            for (int base = fpos & ~15; F > 0 && base < fpos + F; base += 16) {
+                const int p = base + l16;
+                const bool mine = p >= fpos && p < fpos + F;
+                float y[8];
+                if (mine) lattice_y(p, y);
+                float sg[8];
+                load_signs8(sgp + 8 * (l16 & (lpr - 1)), sg);
+                if (lpr < 16) {
+                    if (mine) {
+                        rht_lanes(y, sg, l16 & (lpr - 1), lpr, rdiv, true);
+                        store8(ob, OUT_DT, p, y);
+                    }
                 } else {
-                    float y[8];
-                    if (biased) {
-                        lattice_biased_f32(r, cp ? 0.5f : 0.f, y);
-                    } else {
-                        CosetConsts cs;
-                        cs.pick(cp, cc0, cc1);
-                        cs.deq_f32(r, 1.0f, y);   // the lattice point itself (exact)
-                    }
-                    if constexpr (DITHER) {
-                        float dd[8];
-                        dither8(dkey, vfirst + p, dd);
+                    const bool fh = base >= fpos && base + 8 <= fpos + F;   // the row's first line flushes now
+                    const bool sh = base + 16 <= fpos + F;                   // its second line flushes now
+                    if (mine) fwht_stages(y, l16 & 7, 8);
+                    if (!sh) {
+                        if (fh && mine) {
 #pragma unroll
-                        for (int j = 0; j < 8; j++) y[j] = (y[j] - dd[j]) * sc;
+                            for (int j = 0; j < 8; j++) pend[j] = y[j];
+                        }
                     } else {
+                        if (!fh && l16 < 8) {
 #pragma unroll
-                        for (int j = 0; j < 8; j++) y[j] *= sc;
+                            for (int j = 0; j < 8; j++) y[j] = pend[j];
+                        }
+                        fwht_cross(y, l16, 8);
+#pragma unroll
+                        for (int j = 0; j < 8; j++) y[j] = (y[j] / rdiv) * sg[j];
+                        store8(ob, OUT_DT, base + l16, y);
                     }
-                    store8(ob, OUT_DT, p, y);
+                }
+            }
+        } else {
+            for (int r0 = 0; r0 < F; r0 += 16) {
+                const int q = r0 + l16;
+                if (q < F) {
+                    const int p = fpos + q;
+                    if (!DITHER && OUT_DT == LQ_F16 && biased) {
+                        const bool cp = (W >> q) & 1u;
+                        const int n1b = __builtin_popcount(W & ((1u << q) - 1u));
+                        const int rank = cp ? fr1 + n1b : fr0 + q - n1b;
+                        const uint4 r = *reinterpret_cast<const uint4*>(
+                            &stg[(b * 2 + cp) * kDecGroupU16 + (rank & (kDecStage - 1)) * 8]);
+                        if (!HEADS_ALIGNED && vfirst + p >= head_end) {
+                            const int64_t head = (vfirst + p) / bph;
+                            head_end = (head + 1) * bph;
+                            set_scale(head);
+                        }
+                        const _Float16 o = cp ? (_Float16)0.5f : (_Float16)0.0f;
+                        reinterpret_cast<uint4*>(ob)[p] = deq_biased_f16(r, half2_t{o, o}, sc2);
+                    } else {
+                        float y[8];
+                        lattice_y(p, y);
+                        store8(ob, OUT_DT, p, y);
+                    }
                 }
             }
         }
@@ -1218,11 +1281,12 @@ int lq_chunk_pack(int64_t n_chunks, int64_t n_vectors, const lq_table* d_tables,
     return launch_status();
 }
 
-int lq_chunk_decode(const uint32_t* d_words, const int64_t* d_chunk_base, const int64_t* d_stream_woff,
-                    const uint32_t* d_blk_off, const int64_t* d_stream_nbits, const uint16_t* d_blk_state,
-                    const uint8_t* d_coset_bits, const uint32_t* d_blk_n1, const lq_table* d_tables,
-                    const uint16_t* d_scale16, int64_t n_chunks, int64_t n_heads, int64_t bph, uint32_t* d_lut_work,
-                    void* d_out, int out_dtype, const int64_t* d_dither_seed, hipStream_t s) {
+static int chunk_decode_launch(const uint32_t* d_words, const int64_t* d_chunk_base, const int64_t* d_stream_woff,
+                               const uint32_t* d_blk_off, const int64_t* d_stream_nbits, const uint16_t* d_blk_state,
+                               const uint8_t* d_coset_bits, const lq_table* d_tables, const uint16_t* d_scale16,
+                               int64_t n_chunks, int64_t n_heads, int64_t bph, uint32_t* d_lut_work, void* d_out,
+                               int out_dtype, const int64_t* d_dither_seed, int head_dim, const float* d_signs,
+                               hipStream_t s) {
     if (n_chunks <= 0 || n_heads <= 0 || bph <= 0 || out_dtype < 0 || out_dtype > 2) return LQ_ERR_ARG;
     const int64_t V = n_heads * bph;
     const int64_t nblk = (V + kBlk - 1) / kBlk;
@@ -1232,21 +1296,52 @@ int lq_chunk_decode(const uint32_t* d_words, const int64_t* d_chunk_base, const 
     const int64_t gpw = (groups + cus - 1) / cus;   // groups per workgroup: one workgroup per CU
     const dim3 grid((unsigned)((groups + gpw - 1) / gpw));
     const bool aligned = bph % kBlk == 0;
-#define LQ_DECODE(DT, AL, DI)                                                                                     \
-    hipLaunchKernelGGL((k_chunk_decode<DT, AL, DI>), grid, dim3(kDecThreads), 0, s, d_words, d_chunk_base, d_stream_woff,   \
-                       d_blk_off, d_stream_nbits, d_blk_state, d_coset_bits, d_tables, d_scale16, d_lut_work,          \
-                       n_chunks, n_heads, bph, nblk, gpw, d_out, d_dither_seed)
-#define LQ_DECODE_DT(DT)                                                                                          \
+    const int lpr = d_signs ? head_dim / 8 : 1;
+    const float div = d_signs ? (float)sqrt((double)head_dim) : 1.0f;
+#define LQ_DECODE(DT, AL, DI, RO)                                                                                 \
+    hipLaunchKernelGGL((k_chunk_decode<DT, AL, DI, RO>), grid, dim3(kDecThreads), 0, s, d_words, d_chunk_base,          \
+                       d_stream_woff, d_blk_off, d_stream_nbits, d_blk_state, d_coset_bits, d_tables, d_scale16,       \
+                       d_lut_work, n_chunks, n_heads, bph, nblk, gpw, d_out, d_dither_seed, d_signs, lpr, div)
+#define LQ_DECODE_DT(DT, RO)                                                                                      \
     do {                                                                                                          \
-        if (d_dither_seed) { if (aligned) LQ_DECODE(DT, true, true); else LQ_DECODE(DT, false, true); }           \
-        else { if (aligned) LQ_DECODE(DT, true, false); else LQ_DECODE(DT, false, false); }                       \
+        if (d_dither_seed) { if (aligned) LQ_DECODE(DT, true, true, RO); else LQ_DECODE(DT, false, true, RO); }   \
+        else { if (aligned) LQ_DECODE(DT, true, false, RO); else LQ_DECODE(DT, false, false, RO); }               \
     } while (0)
-    if (out_dtype == LQ_F16) LQ_DECODE_DT(LQ_F16);
-    else if (out_dtype == LQ_BF16) LQ_DECODE_DT(LQ_BF16);
-    else LQ_DECODE_DT(LQ_F32);
+    if (d_signs) {
+        if (out_dtype == LQ_F16) LQ_DECODE_DT(LQ_F16, true);
+        else if (out_dtype == LQ_BF16) LQ_DECODE_DT(LQ_BF16, true);
+        else LQ_DECODE_DT(LQ_F32, true);
+    } else {
+        if (out_dtype == LQ_F16) LQ_DECODE_DT(LQ_F16, false);
+        else if (out_dtype == LQ_BF16) LQ_DECODE_DT(LQ_BF16, false);
+        else LQ_DECODE_DT(LQ_F32, false);
+    }
 #undef LQ_DECODE_DT
 #undef LQ_DECODE
     return launch_status();
+}
+
+int lq_chunk_decode(const uint32_t* d_words, const int64_t* d_chunk_base, const int64_t* d_stream_woff,
+                    const uint32_t* d_blk_off, const int64_t* d_stream_nbits, const uint16_t* d_blk_state,
+                    const uint8_t* d_coset_bits, const uint32_t* d_blk_n1, const lq_table* d_tables,
+                    const uint16_t* d_scale16, int64_t n_chunks, int64_t n_heads, int64_t bph, uint32_t* d_lut_work,
+                    void* d_out, int out_dtype, const int64_t* d_dither_seed, hipStream_t s) {
+    (void)d_blk_n1;   // the decoder counts each block's coset-1 vectors from the bitmap
+    return chunk_decode_launch(d_words, d_chunk_base, d_stream_woff, d_blk_off, d_stream_nbits, d_blk_state,
+                               d_coset_bits, d_tables, d_scale16, n_chunks, n_heads, bph, d_lut_work, d_out, out_dtype,
+                               d_dither_seed, 0, nullptr, s);
+}
+
+int lq_chunk_decode_rht(const uint32_t* d_words, const int64_t* d_chunk_base, const int64_t* d_stream_woff,
+                        const uint32_t* d_blk_off, const int64_t* d_stream_nbits, const uint16_t* d_blk_state,
+                        const uint8_t* d_coset_bits, const lq_table* d_tables, const uint16_t* d_scale16,
+                        int64_t n_chunks, int64_t n_heads, int64_t bph, int head_dim, const float* d_signs,
+                        uint32_t* d_lut_work, void* d_out, int out_dtype, const int64_t* d_dither_seed, hipStream_t s) {
+    if (!d_signs || head_dim < 8 || head_dim > 128 || (head_dim & (head_dim - 1)) || bph <= 0 || bph % (head_dim / 8))
+        return LQ_ERR_ARG;
+    return chunk_decode_launch(d_words, d_chunk_base, d_stream_woff, d_blk_off, d_stream_nbits, d_blk_state,
+                               d_coset_bits, d_tables, d_scale16, n_chunks, n_heads, bph, d_lut_work, d_out, out_dtype,
+                               d_dither_seed, head_dim, d_signs, s);
 }
 
 int lq_chunk_luts(const lq_table* d_tables, int64_t n_chunks, uint32_t* d_lut, hipStream_t s) {

@@ -15,9 +15,12 @@ a times the E8 Voronoi cell and independent of x (per-dimension MSE
 G(E8) a^2, G(E8) = 0.0716821).  Chunk seeds default to the HeadRHT-style
 layer*10000 + kv*10 + 7.
 
-Everything runs in the library's kernels: lq_rht (rotation), lq_head_scales,
-lq_chunk_quantize with the dither, tables, encode, pack, and lq_chunk_decode
-with the dither removed.
+Everything runs in the library's kernels: lq_head_scales_rht and
+lq_chunk_quantize_rht rotate each row in registers (no rotated copy in
+memory) before the scale sums and the nearest-point search, then tables,
+encode, pack; lq_chunk_decode_rht removes the dither and rotates each row back
+before its fp16 store.  The rotation's fp32 arithmetic is the one lq_rht
+applies to a materialised copy, so the streams are the same either way.
 """
 from __future__ import annotations
 
@@ -53,6 +56,23 @@ def chunk_signs(shape, layers: Sequence[int], kvs: Sequence[int]) -> torch.Tenso
     return torch.stack(rows)
 
 
+_DEV_SIGNS = {}
+
+
+def _device_signs(shape, layers, kvs, device) -> torch.Tensor:
+    """chunk_signs on the device, kept per (geometry, layers, K/V, device): the
+    sustained write / read loops then issue no host-to-device copy per call."""
+    C, B, H, _, hd = shape
+    key = (C, B, H, hd, tuple(layers), tuple(kvs), str(device))
+    t = _DEV_SIGNS.get(key)
+    if t is None:
+        if len(_DEV_SIGNS) >= 256:
+            _DEV_SIGNS.clear()
+        t = chunk_signs(shape, layers, kvs).to(device)
+        _DEV_SIGNS[key] = t
+    return t
+
+
 def default_dither_seed(layer: int, kv: int) -> int:
     return layer * 10000 + kv * 10 + 7
 
@@ -68,17 +88,17 @@ def _lists(C, layers, kvs):
 def encode_rotated(x: torch.Tensor, bits, layers, kvs, dither_seeds: Optional[Sequence[int]] = None,
                    deq_out: bool = False, **kw) -> Tuple[codec.EncodedBatch, Optional[torch.Tensor]]:
     """Rotate, dither and compress a (C, B, H, T, hd) batch (chunk c belongs to
-    layer layers[c], K (0) or V (1) kvs[c]).  Returns (EncodedBatch, deq or
-    None), deq being the reconstruction in x's dtype (what a cache would hand
-    to attention)."""
+    layer layers[c], K (0) or V (1) kvs[c]).  The rotation runs inside the
+    scale and quantize kernels (no rotated copy in memory) unless deq_out asks
+    for the reconstruction.  Returns (EncodedBatch, deq or None), deq being the
+    reconstruction in x's dtype (what a cache would hand to attention)."""
     if x.dim() != 5:
         raise ValueError("x must be (C, B, H, T, hd)")
     C, B, H, T, hd = x.shape
     layers, kvs = _lists(C, layers, kvs)
     seeds = list(dither_seeds) if dither_seeds is not None else [default_dither_seed(l, k) for l, k in zip(layers, kvs)]
-    signs = chunk_signs(x.shape, layers, kvs)
-    w = _rht(x, signs, inverse=False, rows_per_sign=T, out_dtype=torch.float32)
-    enc, deq = codec.encode_batch(w, bits, deq_out=deq_out, dither_seed=seeds, **kw)
+    signs = _device_signs(x.shape, layers, kvs, x.device)
+    enc, deq = codec.encode_batch(x, bits, deq_out=deq_out, dither_seed=seeds, rht_signs=signs, **kw)
     enc.extra["rht"] = (layers, kvs)
     if deq is not None:
         deq = _rht(deq, signs, inverse=True, rows_per_sign=T, out_dtype=x.dtype)
@@ -87,14 +107,11 @@ def encode_rotated(x: torch.Tensor, bits, layers, kvs, dither_seeds: Optional[Se
 
 def decode_rotated(enc: codec.EncodedBatch, out_dtype: torch.dtype = torch.float16,
                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Decode a batch written by encode_rotated: (C, B, H, T, hd) in out_dtype."""
+    """Decode a batch written by encode_rotated: (C, B, H, T, hd) in out_dtype
+    (out's dtype when out is given); the inverse rotation runs inside the
+    decoder."""
     layers, kvs = enc.extra["rht"]
     C = enc.n_chunks
     B, H, T, hd = enc.shape
-    w = codec.decode_batch(enc, out_dtype=torch.float32)
-    signs = chunk_signs((C, B, H, T, hd), layers, kvs)
-    res = _rht(w, signs, inverse=True, rows_per_sign=T, out_dtype=out_dtype)
-    if out is not None:
-        out.copy_(res)
-        return out
-    return res
+    signs = _device_signs((C, B, H, T, hd), layers, kvs, enc.words.device)
+    return codec.decode_batch(enc, out_dtype=out.dtype if out is not None else out_dtype, out=out, rht_signs=signs)
