@@ -127,6 +127,65 @@ __device__ int64_t block_sum(int64_t v) {
     return s;
 }
 
+// Block-wide maximum of v (blockDim.x multiple of 64, <= 1024).
+__device__ int64_t block_max(int64_t v) {
+    __shared__ int64_t part[16];
+    for (int o = 32; o > 0; o >>= 1) {
+        const int64_t u = __shfl_xor(v, o, 64);
+        v = u > v ? u : v;
+    }
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+    __syncthreads();
+    int64_t m = part[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); w++) m = part[w] > m ? part[w] : m;
+    return m;
+}
+
+// Bitonic sort of c[0 .. N) ascending (N a power of two, c padded with
+// UINT64_MAX past the live entries).
+__device__ void bitonic_sort_u64(uint64_t* c, int N) {
+    for (int k = 2; k <= N; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int t = threadIdx.x; t < N / 2; t += blockDim.x) {
+                const int i = 2 * t - (t & (j - 1));   // low index of the pair: bit j clear
+                const int l = i + j;
+                const bool up = (i & k) == 0;
+                const uint64_t x = c[i], y = c[l];
+                if ((x > y) == up) { c[i] = y; c[l] = x; }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// adjust_pass for alphabets above 256 symbols: the stable (key, index) order
+// (the order the tie flag stands for) from one bitonic sort of composite keys
+// instead of per-entry rank counts.  At most one tie group straddles the cut
+// at sorted position rem: the one holding positions rem - 1 and rem.
+__device__ void adjust_pass_sorted(int n, int32_t* freqs, int diff, int full, int rem, const int64_t* kk, int16_t* a,
+                                   int8_t* inset, uint64_t* sk, int* st) {
+    int N = 512;
+    while (N < n) N <<= 1;
+    for (int i = threadIdx.x; i < N; i += blockDim.x)   // kk in [-(2^32 - 1), 0]: biased key in 33 bits
+        sk[i] = i < n ? (((uint64_t)(kk[i] + (int64_t)4294967296LL)) << 11) | (uint64_t)i : ~0ull;
+    __syncthreads();
+    bitonic_sort_u64(sk, N);
+    for (int p = threadIdx.x; p < n; p += blockDim.x) {
+        const int i = (int)(sk[p] & 2047u);
+        a[p] = (int16_t)i;
+        inset[i] = p < rem ? 1 : 0;
+    }
+    __syncthreads();
+    int matters = 0;
+    if (rem > 0 && rem < n && (sk[rem - 1] >> 11) == (sk[rem] >> 11)) {   // uniform
+        const uint64_t kstar = sk[rem] >> 11;
+        for (int p = threadIdx.x; p < n; p += blockDim.x)
+            if ((sk[p] >> 11) == kstar && (diff > 0 || freqs[a[p]] - full > 1)) matters = 1;
+    }
+    if (block_sum(matters) != 0 && threadIdx.x == 0) *st |= LQ_ST_TIE_UNPINNED;
+}
+
 // One pass of the build_rans_table adjustment loop (core/gpu_ans.py:73-84)
 // with m = |diff|: j = 0 .. m-1 visits order[j % n], i.e. every entry
 // `full` = m / n times plus the first rem = m % n entries of the argsort order
@@ -135,11 +194,21 @@ __device__ int64_t block_sum(int64_t v) {
 // straddling position rem, and only if a different subset of that group would
 // change a frequency; the numpy network runs only then.
 __device__ void adjust_pass(const int64_t* counts, int n, int32_t* freqs, int diff, int64_t* k, int16_t* a,
-                            int64_t* kk, int8_t* inset, int* st) {
+                            int64_t* kk, int8_t* inset, int* st, uint64_t* sk) {
     const int m = diff > 0 ? diff : -diff;
     const int full = m / n, rem = m % n;
     for (int i = threadIdx.x; i < n; i += blockDim.x) kk[i] = diff > 0 ? -counts[i] : -(int64_t)freqs[i];
     __syncthreads();
+    if (n > 256 && sk) {
+        adjust_pass_sorted(n, freqs, diff, full, rem, kk, a, inset, sk, st);
+        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            const int v = full + (inset[i] == 1 ? 1 : 0);
+            const int f = freqs[i];
+            freqs[i] = diff > 0 ? f + v : (f - v > 1 ? f - v : 1);
+        }
+        __syncthreads();
+        return;
+    }
     int matters = 0;
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
         const int64_t ki = kk[i];
@@ -177,9 +246,13 @@ __device__ void adjust_pass(const int64_t* counts, int n, int32_t* freqs, int di
 // excess is below n (only the max(., 1) bumps exceed L), so a pass whose
 // excess covers all G entries with f > 1 decrements exactly those, whatever
 // the order; such passes are counted in closed form and only the last,
-// partial pass (excess < G) goes through adjust_pass.
+// partial pass (excess < G) goes through adjust_pass.  The number t of full
+// passes is the least t with G_t = 0 or C(t + 1) > excess, where
+// G_t = #{f_i - t > 1} and C(t) = G_0 + .. + G_(t-1) = sum_i min(t, f_i - 1)
+// is nondecreasing: a binary search over t in [0, max f - 1], not one pass
+// per t (a single dominant symbol makes t as large as the excess).
 __device__ void normalise(const int64_t* counts, int n, int32_t* freqs, int64_t* k, int16_t* a, int64_t* kk,
-                          int8_t* inset, int* st) {
+                          int8_t* inset, int* st, uint64_t* sk = nullptr) {
     int64_t tl = 0;
     for (int i = threadIdx.x; i < n; i += blockDim.x) tl += counts[i];
     const int64_t total = block_sum(tl);
@@ -196,20 +269,30 @@ __device__ void normalise(const int64_t* counts, int n, int32_t* freqs, int64_t*
     }
     const int diff = (int)(kL - block_sum(fl));
     if (diff > 0) {
-        adjust_pass(counts, n, freqs, diff, k, a, kk, inset, st);
+        adjust_pass(counts, n, freqs, diff, k, a, kk, inset, st, sk);
     } else if (diff < 0) {
-        int excess = -diff, t = 0;
-        for (;;) {
-            int64_t g = 0;
-            for (int i = threadIdx.x; i < n; i += blockDim.x) g += freqs[i] - t > 1;
-            const int G = (int)block_sum(g);
-            if (G == 0 || excess < G) break;
-            excess -= G;
-            t++;
+        const int excess0 = -diff;
+        int64_t fm = 0;
+        for (int i = threadIdx.x; i < n; i += blockDim.x) fm = freqs[i] > fm ? freqs[i] : fm;
+        const int fmax = (int)block_max(fm);
+        auto C = [&](int tt) {   // passes 0 .. tt-1 decrement sum_i min(tt, f_i - 1) entries in total
+            int64_t c = 0;
+            for (int i = threadIdx.x; i < n; i += blockDim.x) {
+                const int r = freqs[i] - 1;
+                c += r < tt ? r : tt;
+            }
+            return block_sum(c);
+        };
+        int lo = 0, hi = fmax - 1 > 0 ? fmax - 1 : 0;   // t = fmax - 1 has G_t = 0
+        while (lo < hi) {   // least t in [0, hi) with C(t + 1) > excess, else hi
+            const int mid = (lo + hi) >> 1;
+            if (C(mid + 1) > excess0) hi = mid; else lo = mid + 1;
         }
+        const int t = lo;
+        const int excess = (int)(excess0 - C(t));
         for (int i = threadIdx.x; i < n; i += blockDim.x) freqs[i] = freqs[i] - t > 1 ? freqs[i] - t : 1;
         __syncthreads();
-        if (excess > 0) adjust_pass(counts, n, freqs, -excess, k, a, kk, inset, st);
+        if (excess > 0) adjust_pass(counts, n, freqs, -excess, k, a, kk, inset, st, sk);
     }
 }
 
@@ -310,7 +393,8 @@ __global__ __launch_bounds__(256) void k_chunk_tables(const uint32_t* __restrict
     // n <= 1028; the network holds 256 keys (larger alphabets take the rank path)
     __shared__ int64_t kk[LQ_MAXSYM];
     __shared__ int8_t inset[LQ_MAXSYM];
-    normalise(counts, n, freqs, keys, perm, kk, inset, &s_st);
+    __shared__ uint64_t sk[WIDE ? 2048 : 1];   // wide alphabets: composite sort keys
+    normalise(counts, n, freqs, keys, perm, kk, inset, &s_st, WIDE ? sk : nullptr);
     __shared__ int32_t cum[LQ_MAXSYM + 1];
     exclusive_scan_array(freqs, n, cum);
     for (int i = tid; i < n; i += 256) T->enc[i] = enc_pack((uint32_t)freqs[i], (uint32_t)cum[i]);
@@ -442,16 +526,22 @@ __device__ __forceinline__ void for_each_rev(const SymT* p, int n, F&& f) {
 }
 
 struct EncWork {  // offsets into the encode workspace
-    int64_t bits, scratch, total;
+    int64_t bits, scratch, tiles, total;
 };
+
+// Streams longer than kScanTile blocks are scanned in tiles (k_scan_tiles /
+// k_scan_top / k_scan_apply); shorter ones by one workgroup each (k_chunk_scan).
+constexpr int kScanTile = 4096;
 
 __host__ __device__ inline EncWork enc_layout(int64_t n_chunks, int64_t n_vectors) {
     int64_t nblk = (n_vectors + kBlk - 1) / kBlk;
     int64_t tasks = n_chunks * LQ_STREAMS * nblk;
+    int64_t n_tiles = nblk > kScanTile ? n_chunks * LQ_STREAMS * ((nblk + kScanTile - 1) / kScanTile) : 0;
     EncWork w;
     w.bits = 0;
     w.scratch = ((tasks * 4 + 255) / 256) * 256;
-    w.total = w.scratch + tasks * (int64_t)kCapW * 4;
+    w.tiles = w.scratch + tasks * (int64_t)kCapW * 4;
+    w.total = w.tiles + n_tiles * 8;
     return w;
 }
 
@@ -614,6 +704,86 @@ __global__ __launch_bounds__(256) void k_chunk_scan(const uint32_t* __restrict__
         bool present = tables[sid].n_sym > 0;
         stream_nbits[sid] = present ? (int64_t)part[255] : 0;
         stream_state[sid] = present ? (int32_t)blk_state[sid * nblk] : 0;
+    }
+}
+
+// Tiled scan of long streams.  Tile t of stream sid covers blocks
+// t * kScanTile .. + kScanTile - 1; thread i of its workgroup owns the 16
+// consecutive blocks from t * kScanTile + 16 i.
+__device__ __forceinline__ uint64_t block_exclusive_scan256(uint64_t v, uint64_t* part, uint64_t* total) {
+    const int tid = threadIdx.x;
+    part[tid] = v;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {   // inclusive Hillis-Steele scan
+        const uint64_t u = tid >= off ? part[tid - off] : 0;
+        __syncthreads();
+        part[tid] += u;
+        __syncthreads();
+    }
+    *total = part[255];
+    return tid ? part[tid - 1] : 0;
+}
+
+__global__ __launch_bounds__(256) void k_scan_tiles(const uint32_t* __restrict__ blk_bits, int64_t nblk, int64_t tiles,
+                                                    uint64_t* __restrict__ tile_sum) {
+    __shared__ uint64_t part[256];
+    const int64_t sid = blockIdx.x / tiles, t = blockIdx.x % tiles;
+    const uint32_t* bb = blk_bits + sid * nblk;
+    const int64_t b0 = t * kScanTile + 16 * (int64_t)threadIdx.x;
+    uint64_t s = 0;
+#pragma unroll
+    for (int k = 0; k < 16; k++)
+        if (b0 + k < nblk) s += bb[b0 + k];
+    uint64_t tot;
+    block_exclusive_scan256(s, part, &tot);
+    if (threadIdx.x == 0) tile_sum[sid * tiles + t] = tot;
+}
+
+// per stream: exclusive prefix of its tile sums (in place), n_bits, final state
+__global__ __launch_bounds__(256) void k_scan_top(uint64_t* __restrict__ tile_sum, int64_t tiles,
+                                                  const uint16_t* __restrict__ blk_state, int64_t nblk,
+                                                  const lq_table* __restrict__ tables, int64_t* __restrict__ stream_nbits,
+                                                  int32_t* __restrict__ stream_state) {
+    __shared__ uint64_t part[256];
+    const int64_t sid = blockIdx.x;
+    uint64_t* ts = tile_sum + sid * tiles;
+    uint64_t carry = 0;
+    for (int64_t t0 = 0; t0 < tiles; t0 += 256) {   // uniform trip count
+        const int64_t t = t0 + threadIdx.x;
+        const uint64_t v = t < tiles ? ts[t] : 0;
+        uint64_t tot;
+        const uint64_t ex = block_exclusive_scan256(v, part, &tot);
+        if (t < tiles) ts[t] = carry + ex;
+        carry += tot;
+        __syncthreads();   // part is reused by the next round
+    }
+    if (threadIdx.x == 0) {
+        const bool present = tables[sid].n_sym > 0;
+        stream_nbits[sid] = present ? (int64_t)carry : 0;
+        stream_state[sid] = present ? (int32_t)blk_state[sid * nblk] : 0;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_scan_apply(const uint32_t* __restrict__ blk_bits, int64_t nblk, int64_t tiles,
+                                                    const uint64_t* __restrict__ tile_off, uint32_t* __restrict__ blk_off) {
+    __shared__ uint64_t part[256];
+    const int64_t sid = blockIdx.x / tiles, t = blockIdx.x % tiles;
+    const uint32_t* bb = blk_bits + sid * nblk;
+    uint32_t* bo = blk_off + sid * nblk;
+    const int64_t b0 = t * kScanTile + 16 * (int64_t)threadIdx.x;
+    uint32_t v[16];
+    uint64_t s = 0;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        v[k] = b0 + k < nblk ? bb[b0 + k] : 0u;
+        s += v[k];
+    }
+    uint64_t tot;
+    uint64_t run = tile_off[sid * tiles + t] + block_exclusive_scan256(s, part, &tot);
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        if (b0 + k < nblk) bo[b0 + k] = (uint32_t)run;
+        run += v[k];
     }
 }
 
@@ -1217,8 +1387,18 @@ int encode_launch(const SymT* d_sym, const uint32_t* d_blk_n1, int64_t n_chunks,
     const int64_t groups = (nblk + kEncBlocks - 1) / kEncBlocks;
     hipLaunchKernelGGL((k_chunk_encode<SymT>), dim3((unsigned)groups, (unsigned)n_chunks), dim3(256), 0, s, d_sym,
                        d_blk_n1, nblk, n_vectors, d_tables, bits, scratch, d_blk_state);
-    hipLaunchKernelGGL(k_chunk_scan, dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, bits, d_blk_state, d_tables,
-                       nblk, d_blk_off, d_stream_nbits, d_stream_state);
+    if (nblk > kScanTile) {
+        const int64_t tiles = (nblk + kScanTile - 1) / kScanTile;
+        uint64_t* tsum = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(d_work) + w.tiles);
+        const dim3 tg((unsigned)(tiles * n_chunks * LQ_STREAMS));   // (stream, tile) = divmod(block, tiles)
+        hipLaunchKernelGGL(k_scan_tiles, tg, dim3(256), 0, s, bits, nblk, tiles, tsum);
+        hipLaunchKernelGGL(k_scan_top, dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, tsum, tiles, d_blk_state,
+                           nblk, d_tables, d_stream_nbits, d_stream_state);
+        hipLaunchKernelGGL(k_scan_apply, tg, dim3(256), 0, s, bits, nblk, tiles, tsum, d_blk_off);
+    } else {
+        hipLaunchKernelGGL(k_chunk_scan, dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, bits, d_blk_state,
+                           d_tables, nblk, d_blk_off, d_stream_nbits, d_stream_state);
+    }
     hipLaunchKernelGGL(k_chunk_offsets, dim3((unsigned)((n_chunks + 63) / 64)), dim3(64), 0, s, d_stream_nbits, d_tables,
                        n_chunks, d_stream_woff, d_chunk_words);
     return launch_status();

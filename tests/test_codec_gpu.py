@@ -171,3 +171,21 @@ def test_fp32_ragged_chunk_vs_oracle_gpu():
     out = codec.decode_batch(enc, out_dtype=torch.float32)
     np.testing.assert_array_equal(out[0].cpu().numpy(), O.decompress_chunk(ch, out_dtype=np.float32))
     np.testing.assert_allclose(enc.sigma2.cpu().numpy(), O.head_sigma2(x[0].numpy()), rtol=2e-7)
+
+
+def test_long_stream_tiled_scan_vs_oracle_gpu():
+    """A chunk with more than 4096 blocks per stream (2 x 73728 tokens x 128:
+    4608 blocks, one full 4096-block scan tile and a partial one): the
+    block offsets come from the tiled scan; bitstream, offsets and decode are
+    bit-exact against the oracle."""
+    codec, L = _lq()
+    x = torch.randn(1, 1, 2, 73728, 128, generator=torch.Generator().manual_seed(73)).half()
+    enc, _ = codec.encode_batch(x.cuda(), 4)
+    assert enc.nblk > 4096 and int(enc.status.item()) == 0
+    ch = O.compress_chunk(x[0].numpy(), 4, scales_f32=enc.scale32.cpu().numpy())
+    _compare_chunk(enc, 0, ch)
+    # per stream the block offsets rise by each block's bit count and end at n_bits
+    off = enc.blk_off.view(16, -1).cpu().numpy().astype(np.int64)
+    nb = enc.stream_nbits.cpu().numpy()
+    assert (np.diff(off, axis=1) >= 0).all() and (off[:, 0] == 0).all() and (off[:, -1] <= nb).all()
+    np.testing.assert_array_equal(codec.decode_batch(enc)[0].cpu().numpy(), O.decompress_chunk(ch))
