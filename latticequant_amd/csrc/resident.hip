@@ -473,7 +473,8 @@ __device__ __forceinline__ int exc_code(const lq_resident& r, int64_t rb, uint64
 // Scores of block x: s += q . k over the four record groups, each group's K
 // operand decoded (and, rarely, patched with exception entries) just before
 // its MFMA, so that only one group's pairs are live at a time.
-__device__ __forceinline__ void tile_k(const AttnArgs& A, const TileRaw& d, int64_t rb, int x, int lane, bool fast,
+template <bool FAST>
+__device__ __forceinline__ void tile_k(const AttnArgs& A, const TileRaw& d, int64_t rb, int x, int lane,
                                        uint32_t mk, const h8_t qa[4], f4_t& s) {
     const uint64_t hdr = meta_hdr(d, x);
     const int n = (int)(hdr & 0xffu);
@@ -499,7 +500,7 @@ __device__ __forceinline__ void tile_k(const AttnArgs& A, const TileRaw& d, int6
                 }
             }
         }
-        if (fast) mul_pairs<4>(p, mk);
+        if (FAST) mul_pairs<4>(p, mk);
         else dequant_pairs<4>(p, sk, sk);
         s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], as_h8(p[0], p[1], p[2], p[3]), s, 0, 0, 0);
     }
@@ -508,7 +509,8 @@ __device__ __forceinline__ void tile_k(const AttnArgs& A, const TileRaw& d, int6
 // V of the lane's 8 tokens (vector lane % 16), two tokens at a time:
 // vp[k][i] = fp16 pair (dimension 8 n + i of token 2 k, of token 2 k + 1),
 // dequantised -- the operand halves of P V's MFMA i as they are.
-__device__ __forceinline__ void tile_v(const AttnArgs& A, const TileRaw& d, int64_t rb0, int lane, bool fast,
+template <bool FAST>
+__device__ __forceinline__ void tile_v(const AttnArgs& A, const TileRaw& d, int64_t rb0, int lane,
                                        const uint32_t mv[4], uint32_t vp[4][8]) {
     const int n = lane & 15, k8 = lane >> 4, xb = k8 >> 1;
     const uint32_t aw[8] = {d.va0.x, d.va0.y, d.va0.z, d.va0.w, d.va1.x, d.va1.y, d.va1.z, d.va1.w};
@@ -554,7 +556,7 @@ __device__ __forceinline__ void tile_v(const AttnArgs& A, const TileRaw& d, int6
     const uint32_t sw[4] = {d.vs.x, d.vs.y, d.vs.z, d.vs.w};   // scales of tokens (2 k, 2 k + 1)
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        if (fast) mul_pairs<8>(vp[k], mv[k]);
+        if (FAST) mul_pairs<8>(vp[k], mv[k]);
         else dequant_pairs<8>(vp[k], (uint16_t)(sw[k] & 0xffffu), (uint16_t)(sw[k] >> 16));
     }
 }
@@ -644,14 +646,57 @@ __device__ __forceinline__ void prefix_decode(const AttnArgs& A, const TileRaw& 
         ev = ev && e;
     }
     const bool fast = __all(e0 && e1 && ev);
+    // one wave-uniform branch per tile: the usual all-normal-scales path carries
+    // none of the small-scale path's work
+    if (fast) {
 #pragma unroll
-    for (int x = 0; x < 2; x++) {
-        s[x] = f4_t{0.f, 0.f, 0.f, 0.f};
-        valid[x] = t0 + 16 * x + (lane & 15) < T;
-        if (t0 + 16 * x < T)   // wave-uniform
-            tile_k(A, d, rb0 + x, x, lane, fast, x ? mk1 : mk0, qa, s[x]);
+        for (int x = 0; x < 2; x++) {
+            s[x] = f4_t{0.f, 0.f, 0.f, 0.f};
+            valid[x] = t0 + 16 * x + (lane & 15) < T;
+            if (t0 + 16 * x < T)   // wave-uniform
+                tile_k<true>(A, d, rb0 + x, x, lane, x ? mk1 : mk0, qa, s[x]);
+        }
+        tile_v<true>(A, d, rb0, lane, mv, vp);
+    } else {
+#pragma unroll
+        for (int x = 0; x < 2; x++) {
+            s[x] = f4_t{0.f, 0.f, 0.f, 0.f};
+            valid[x] = t0 + 16 * x + (lane & 15) < T;
+            if (t0 + 16 * x < T)
+                tile_k<false>(A, d, rb0 + x, x, lane, x ? mk1 : mk0, qa, s[x]);
+        }
+        tile_v<false>(A, d, rb0, lane, mv, vp);
     }
-    tile_v(A, d, rb0, lane, fast, mv, vp);
+}
+
+// The tail tiles this wave owns: tail tile tt goes to the kv head's wave
+// (tt * W) / ntt, so the tiles spread over all splits instead of piling onto
+// the first waves.  Each is taken before the wave's prefix tiles (their loads
+// overlap the first prefix tile's), its K and V loads issued together.
+template <int HPL>
+__device__ __forceinline__ void tail_owned(const AttnArgs& A, int64_t kvh, int64_t gw, int64_t W, int64_t T, int lane,
+                                           const h8_t qa[4], uint32_t* pt, float m_run[HPL], float l_run[HPL],
+                                           f4_t o[8]) {
+    const int64_t ntt = (T + kTile - 1) / kTile;
+    const int64_t t_begin = (gw * ntt + W - 1) / W, t_end = ((gw + 1) * ntt + W - 1) / W;
+    for (int64_t tt = t_begin; tt < t_end; tt++) {
+        const int64_t t0 = tt * kTile;
+        h8_t kb[2][4];
+        uint32_t vp[4][8];
+#pragma unroll
+        for (int x = 0; x < 2; x++) tail_k(A, kvh, t0 + 16 * x, T, lane, kb[x]);
+        tail_v(A, kvh, t0, T, lane, vp);
+        f4_t s[2];
+        bool valid[2];
+#pragma unroll
+        for (int x = 0; x < 2; x++) {
+            s[x] = f4_t{0.f, 0.f, 0.f, 0.f};
+            valid[x] = t0 + 16 * x + (lane & 15) < T;
+#pragma unroll
+            for (int c = 0; c < 4; c++) s[x] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], kb[x][c], s[x], 0, 0, 0);
+        }
+        tile_softmax_pv<HPL>(A.group, s, valid, lane, vp, pt, m_run, l_run, o);
+    }
 }
 
 // The wave's prefix tiles.  The workgroup's tiles are the slots j of its
@@ -667,12 +712,17 @@ __device__ __forceinline__ void prefix_tiles(const AttnArgs& A, int64_t kvh, int
                                              int lane, const h8_t qa[4], uint32_t* pt, float m_run[HPL],
                                              float l_run[HPL], f4_t o[8], int* s_next) {
     const int64_t npt = (T + kTile - 1) / kTile;
+    const int64_t gw = (int64_t)sp * kAW + wave;
     auto tile_of = [&](int j) -> int64_t { return (int64_t)sp * kAW + (j % kAW) + (int64_t)(j / kAW) * W; };
     int64_t g = tile_of(wave);
-    if (g >= npt) return;
+    if (g >= npt) {
+        if (A.t_tail > 0) tail_owned<HPL>(A, kvh, gw, W, A.t_tail, lane, qa, pt, m_run, l_run, o);
+        return;
+    }
     const int64_t hb = kvh * A.k.cap_blocks;
     TileRaw d;
     tile_load(A, kvh, g * kTile, T, lane, d);
+    if (A.t_tail > 0) tail_owned<HPL>(A, kvh, gw, W, A.t_tail, lane, qa, pt, m_run, l_run, o);
     while (true) {
         int jn = 0;
         if (lane == 0) jn = atomicAdd(s_next, 1);
@@ -687,35 +737,6 @@ __device__ __forceinline__ void prefix_tiles(const AttnArgs& A, int64_t kvh, int
         tile_softmax_pv<HPL>(A.group, s, valid, lane, vp, pt, m_run, l_run, o);
         if (gn >= npt) break;
         g = gn;
-    }
-}
-
-// The tail tiles of this wave: tile indices continue after the prefix's in
-// the same round-robin (g = prefix tiles + tail tile), fp16 K / V read directly.
-template <int HPL>
-__device__ __forceinline__ void tail_tiles(const AttnArgs& A, int64_t kvh, int64_t gw, int64_t W, int64_t npt,
-                                           int64_t T, int lane, const h8_t qa[4], uint32_t* pt,
-                                           float m_run[HPL], float l_run[HPL], f4_t o[8]) {
-    int64_t g = gw;
-    if (g < npt) g += (npt - g + W - 1) / W * W;   // first index of this wave past the prefix
-    for (; (g - npt) * kTile < T; g += W) {
-        const int64_t t0 = (g - npt) * kTile;
-        f4_t s[2];
-        bool valid[2];
-#pragma unroll
-        for (int x = 0; x < 2; x++) {
-            s[x] = f4_t{0.f, 0.f, 0.f, 0.f};
-            valid[x] = t0 + 16 * x + (lane & 15) < T;
-            if (t0 + 16 * x < T) {
-                h8_t kb[4];
-                tail_k(A, kvh, t0 + 16 * x, T, lane, kb);
-#pragma unroll
-                for (int c = 0; c < 4; c++) s[x] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], kb[c], s[x], 0, 0, 0);
-            }
-        }
-        uint32_t vp[4][8];
-        tail_v(A, kvh, t0, T, lane, vp);
-        tile_softmax_pv<HPL>(A.group, s, valid, lane, vp, pt, m_run, l_run, o);
     }
 }
 
@@ -736,7 +757,6 @@ __global__ __launch_bounds__(kAW * 64) void k_res_attn(AttnArgs A) {
     const int64_t kvh = (int64_t)blockIdx.x / nsp;
     const int sp = (int)((int64_t)blockIdx.x % nsp);
     const int64_t gw = (int64_t)sp * kAW + wave, W = (int64_t)nsp * kAW;
-    const int64_t npt = (A.t_prefix + kTile - 1) / kTile;
 
     // Q fragments: row m of the A operand is query head 4 (m % 4) + m / 4
     h8_t qa[4];
@@ -760,7 +780,7 @@ __global__ __launch_bounds__(kAW * 64) void k_res_attn(AttnArgs A) {
 #pragma unroll
     for (int mm = 0; mm < 8; mm++) o[mm] = f4_t{0.f, 0.f, 0.f, 0.f};
     if (A.t_prefix > 0) prefix_tiles<HPL>(A, kvh, sp, wave, W, A.t_prefix, lane, qa, pt, m_run, l_run, o, &s_next);
-    if (A.t_tail > 0) tail_tiles<HPL>(A, kvh, gw, W, npt, A.t_tail, lane, qa, pt, m_run, l_run, o);
+    else tail_owned<HPL>(A, kvh, gw, W, A.t_tail, lane, qa, pt, m_run, l_run, o);
 
     // ---- merge the waves' (m, l, O) in LDS, kMergeH query heads per round;
     // lane column n of MFMA mm holds dimension 8 n + mm of its rows
