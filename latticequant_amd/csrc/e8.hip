@@ -18,7 +18,7 @@ __global__ void k_e8_encode(const float* __restrict__ x, int64_t n, int mode, fl
     if (mode == 1) {
         d8_round(xv, r);
     } else {
-        int cos = e8_nearest(xv, r);
+        int cos = e8_nearest_fast(xv, r);
         float off = cos ? 0.5f : 0.f;
 #pragma unroll
         for (int i = 0; i < 8; i++) r[i] = r[i] + off;
@@ -74,7 +74,7 @@ __global__ void k_quantize_heads(const void* __restrict__ x, int dtype, int64_t 
     load8(x, dtype, v, xv);
 #pragma unroll
     for (int i = 0; i < 8; i++) t[i] = div_scaled(xv[i], s, rs, fast);
-    const float off = e8_nearest(t, ic) ? 0.5f : 0.f;
+    const float off = e8_nearest_fast(t, ic) ? 0.5f : 0.f;
 #pragma unroll
     for (int i = 0; i < 8; i++) ic[i] = ic[i] + off;
     store8(q, LQ_F32, v, ic);
@@ -261,7 +261,7 @@ __device__ __forceinline__ void stage_hist(const uint4& w, int row16, int n0, in
 // exactly the fp32 values a materialised forward rotation holds; no
 // dequantised output.
 template <typename SymT, bool DITHER, bool LEAN = false, bool ROT = false>
-__global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
+__global__ __launch_bounds__(kQThreads, LEAN ? 7 : 1) void k_chunk_quantize(
     const void* __restrict__ x, int dtype, int64_t n_heads, int64_t bph, int64_t nblk,
     const float* __restrict__ scale32, const int32_t* __restrict__ fastdiv, SymT* __restrict__ sym,
     uint8_t* __restrict__ coset_bits, uint32_t* __restrict__ blk_n1, uint32_t* __restrict__ hist,
@@ -369,7 +369,23 @@ __global__ __launch_bounds__(kQThreads) void k_chunk_quantize(
 #pragma unroll
                     for (int i = 0; i < 8; i++) t[i] = t[i] + dd[i];
                 }
-                int c = e8_nearest(t, ic);
+                int c;
+                if constexpr (ROT) {   // the rotation is cross-lane: keep t for the rare exact path
+                    c = e8_nearest_fast(t, ic);
+                } else {               // the rare exact path recomputes t from x
+                    c = e8_nearest_fast(t, ic, [&](float tt[8]) {
+                        float xx[8];
+                        load8(x, dtype, chunk * V + v, xx);
+#pragma unroll
+                        for (int i = 0; i < 8; i++) tt[i] = div_scaled(xx[i], s, rs, fast);
+                        if constexpr (DITHER) {
+                            float d2[8];
+                            dither8(mix64((uint64_t)dseed[chunk]), v, d2);
+#pragma unroll
+                            for (int i = 0; i < 8; i++) tt[i] = tt[i] + d2[i];
+                        }
+                    });
+                }
                 cs[r] = c;
                 int32_t lo = INT_MAX, hi = INT_MIN;
 #pragma unroll

@@ -31,7 +31,7 @@ __device__ __forceinline__ int sym_pos(int c, int i, int r, int n0) {
 }
 
 // torch.arange(8, dtype=f32) * 1e-7  ==  RN32(i * f32(1e-7))   (core/e8_quantizer.py:42-44)
-__device__ __forceinline__ float tiebreak(int i) {
+__host__ __device__ __forceinline__ float tiebreak(int i) {
     constexpr float tb[8] = {0.0f,           0x1.ad7f2ap-24f, 0x1.ad7f2ap-23f, 0x1.421f60p-22f,
                              0x1.ad7f2ap-22f, 0x1.0c6f7ap-21f, 0x1.421f60p-21f, 0x1.77cf44p-21f};
     return tb[i];
@@ -96,7 +96,7 @@ __device__ __forceinline__ uint16_t f2dtype(float f, int dtype) { return dtype =
 // Nearest D8 point (core/e8_quantizer.py:20-58): round half-even, and when the
 // coordinate sum is odd move the coordinate with the smallest
 // RN(RN(1 - 2|r|) + tiebreak_i) (first index on ties) one step away from x.
-__device__ __forceinline__ void d8_round(const float x[8], float r[8]) {
+__host__ __device__ __forceinline__ void d8_round(const float x[8], float r[8]) {
     float res[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) r[i] = rintf(x[i]);
@@ -141,7 +141,7 @@ __device__ __forceinline__ void d8_round(const float x[8], float r[8]) {
 // coordinates of the chosen coset representative (c1 itself, or c2 - 1/2) and
 // the coset bit; the squared distances are summed left to right like torch's
 // CPU sum over an 8-wide row.
-__device__ __forceinline__ int e8_nearest(const float x[8], float ic[8]) {
+__host__ __device__ __forceinline__ int e8_nearest(const float x[8], float ic[8]) {
     float r1[8], r2[8], y[8];
     d8_round(x, r1);
 #pragma unroll
@@ -160,6 +160,125 @@ __device__ __forceinline__ int e8_nearest(const float x[8], float ic[8]) {
 #pragma unroll
     for (int i = 0; i < 8; i++) ic[i] = use1 ? r1[i] : r2[i];
     return use1 ? 0 : 1;
+}
+
+// The same nearest E8 point as e8_nearest, with less arithmetic on the common
+// path.  Both D8 roundings are taken as in d8_round, but their flips are not
+// applied until the coset is known (one flip instead of two).  The coset
+// choice d1 <= d2 is first decided from an estimate of d1 - d2 with a proven
+// error bound; only when the estimate lies within that bound of zero are the
+// two distances summed in the reference's order from the same halves.
+//
+// With e1 = x - r1 and e2 = y - r2 (y = RN(x - 1/2); both differences exact),
+//   d1 = sum e1^2 + odd1 (1 - 2 |e1_j|),  d2 = sum e2^2 + odd2 (1 - 2 |e2_k|)
+// (j, k the flipped coordinates).  |e2_i| = 1/2 - |e1_i| + s_i with |s_i| <= U,
+// U the ulp of max(1, max |x_i|) (the rounding of y), so
+// e1_i^2 - e2_i^2 = |e1_i| - 1/4 + O(1.01 U), and with f_i = RN(1 - 2 |e1_i|)
+// (the flip costs d8_half computes anyway)
+//   d1 - d2 ~ est = 2 - (sum f_i) / 2 + odd1 f1_j - odd2 f2_k.
+// The error of est against the exact d1 - d2 (the s_i, the rounding of the
+// reference's differences x - c, of the f_i and of the fp32 evaluation, <= 1.9e-6)
+// plus the reference's own rounding of its sums (<= 9 * 2^-24 relative on
+// d <= 4) stays below 1e-5 + 32 U; beyond that margin the sign of est is the
+// sign of the reference's fp32 d1 - d2.  max |x_i| >= 2^21 (or inf / NaN
+// through est) takes the exact path.
+struct D8Half {
+    float r[8], e[8];
+    bool sel[8];   // first-index argmin of RN(RN(1 - 2|e_i|) + tiebreak_i)
+    float es;      // e at that index
+    float fsum;    // sum of RN(1 - 2|e_i|) (left to right), when asked for
+    bool odd;      // the fp32 coordinate sum is odd
+};
+
+template <bool FSUM>
+__host__ __device__ __forceinline__ void d8_half(const float x[8], D8Half& h) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        h.r[i] = rintf(x[i]);
+        h.e[i] = x[i] - h.r[i];
+    }
+    float s = h.r[0];
+#pragma unroll
+    for (int i = 1; i < 8; i++) s += h.r[i];
+    h.odd = fabsf(s) < 16777216.0f && (((int32_t)s) & 1);
+    float best = 0.f, es = h.e[0], fs = 0.f;
+    bool upd[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float fc = __builtin_fmaf(-2.0f, fabsf(h.e[i]), 1.0f);
+        if (FSUM) fs = i == 0 ? fc : fs + fc;
+        const float adj = i == 0 ? fc : fc + tiebreak(i);
+        upd[i] = i == 0 || adj < best;
+        best = upd[i] ? adj : best;
+        es = upd[i] ? h.e[i] : es;
+    }
+    bool later = false;
+#pragma unroll
+    for (int i = 7; i >= 0; i--) {
+        h.sel[i] = upd[i] && !later;
+        later = later || upd[i];
+    }
+    h.es = es;
+    h.fsum = fs;
+}
+
+// Reference-order coset choice (core/e8_quantizer.py:79-83) given the halves.
+__host__ __device__ __forceinline__ bool e8_choose_exact(const float x[8], const D8Half& a, const D8Half& b,
+                                                         float fa, float fb) {
+    float d1 = 0.f, d2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float c1 = a.r[i] + (a.sel[i] ? fa : 0.f);
+        const float c2 = (b.r[i] + (b.sel[i] ? fb : 0.f)) + 0.5f;
+        const float u = x[i] - c1, v = x[i] - c2;
+        const float u2 = u * u, v2 = v * v;
+        d1 = (i == 0) ? u2 : d1 + u2;
+        d2 = (i == 0) ? v2 : d2 + v2;
+    }
+    return d1 <= d2;
+}
+
+// reload(float x[8]) writes x again for the rare exact path, so that x need
+// not stay live through the common path.
+template <typename Reload>
+__host__ __device__ __forceinline__ int e8_nearest_fast(const float x[8], float ic[8], Reload&& reload) {
+    D8Half a, b;
+    d8_half<true>(x, a);
+    float y[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) y[i] = x[i] - 0.5f;
+    d8_half<false>(y, b);
+    float est = __builtin_fmaf(a.fsum, -0.5f, 2.0f);
+    if (a.odd) est += __builtin_fmaf(-2.0f, fabsf(a.es), 1.0f);
+    if (b.odd) est -= __builtin_fmaf(-2.0f, fabsf(b.es), 1.0f);
+    float t = fmaxf(fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))),
+                    fmaxf(fmaxf(fabsf(x[4]), fabsf(x[5])), fmaxf(fabsf(x[6]), fabsf(x[7]))));
+    t = fmaxf(t, 1.0f);
+    const float p2 = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, t) & 0x7f800000u);   // 2^floor(log2 t)
+    const float margin = __builtin_fmaf(32.0f * 0x1p-23f, p2, 1e-5f);   // 1e-5 + 32 ulp(t)
+    // each half's flip as a float step (0 when its sum is even)
+    const float fa = a.odd ? (a.es < 0.f ? -1.f : 1.f) : 0.f;
+    const float fb = b.odd ? (b.es < 0.f ? -1.f : 1.f) : 0.f;
+    bool use1 = est < 0.f;
+    if (!(t < 2097152.0f) || !(fabsf(est) > margin)) {
+        float xr[8];
+        reload(xr);
+        use1 = e8_choose_exact(xr, a, b, fa, fb);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float ca = a.r[i] + (a.sel[i] ? fa : 0.f);
+        const float cb = b.r[i] + (b.sel[i] ? fb : 0.f);
+        ic[i] = use1 ? ca : cb;
+    }
+    return use1 ? 0 : 1;
+}
+
+__host__ __device__ __forceinline__ int e8_nearest_fast(const float x[8], float ic[8]) {
+    return e8_nearest_fast(x, ic, [&](float xr[8]) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) xr[i] = x[i];
+    });
 }
 
 // x / s rounded to nearest.  The three-op form (q0 = x*r, e = fma(-q0, s, x),

@@ -167,7 +167,7 @@ __device__ __forceinline__ int res_point(const void* x, int dtype, int64_t T, in
     load8(x, dtype, (hh * T + t) * (kHd / 8) + g, xv);
 #pragma unroll
     for (int i = 0; i < 8; i++) tv[i] = xv[i] / s;
-    return e8_nearest(tv, ic);
+    return e8_nearest_fast(tv, ic);
 }
 
 // grid (t_tokens / 16, n_heads), 256 threads: wave = group, lane = slot
