@@ -82,6 +82,31 @@ __global__ void k_quantize_heads(const void* __restrict__ x, int dtype, int64_t 
 
 // ---------------------------------------------------------- head scales --
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+// Sum of the 8 squares of one fp16 / bf16 vector in fp32 (each square is exact
+// in fp32): v_dot2 on fp16 pairs, an FMA chain for bf16.
+__device__ __forceinline__ float sq_vec16(const u32x4 w, bool f16) {
+    const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+    float a = 0.f;
+    if (f16) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const half2_t h = __builtin_bit_cast(half2_t, d[i]);
+            a = __builtin_amdgcn_fdot2(h, h, a, false);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float lo = __uint_as_float(d[i] << 16), hi = __uint_as_float(d[i] & 0xffff0000u);
+            a = __builtin_fmaf(lo, lo, a);
+            a = __builtin_fmaf(hi, hi, a);
+        }
+    }
+    return a;
+}
+
 // Partial sums of x^2 per head in double: grid (heads, parts).  ROT: of the
 // forward-rotated rows w = RHT(x) instead (sign row = the head, lpr lanes per
 // row; the parts split on row boundaries), summed exactly like an fp32 input
@@ -95,17 +120,10 @@ __global__ void k_head_sumsq(const void* __restrict__ x, int dtype, int64_t vec_
     if (ROT) per = (per + lpr - 1) / lpr * lpr;
     int64_t v0 = (int64_t)p * per, v1 = v0 + per < vec_per_head ? v0 + per : vec_per_head;
     // Per vector: the 8 squares (exact in fp32 for fp16 / bf16 inputs) summed
-    // in fp32 by a chain of FMAs, then accumulated in fp64; four independent
-    // loads in flight per thread per step, four accumulators.
+    // in fp32, then accumulated in fp64 (four accumulators).
     double acc4[4] = {0.0, 0.0, 0.0, 0.0};
     const int64_t bd = blockDim.x;
     int64_t v = v0 + threadIdx.x;
-    auto sq8 = [](const float xv[8]) {
-        float a = xv[0] * xv[0];
-#pragma unroll
-        for (int i = 1; i < 8; i++) a = __builtin_fmaf(xv[i], xv[i], a);
-        return (double)a;
-    };
     if (ROT) {
         // rows are whole within [v0, v1) and lpr divides the block size, so the
         // lanes of a row enter and leave the loop together
@@ -127,18 +145,19 @@ __global__ void k_head_sumsq(const void* __restrict__ x, int dtype, int64_t vec_
             for (int i = 0; i < 8; i++) acc4[0] += (double)xv[i] * (double)xv[i];
         }
     } else {
-        for (; v + 3 * bd < v1; v += 4 * bd) {
-            float xv[4][8];
+        // eight streaming (nontemporal) 16-byte loads in flight per thread:
+        // the input is read once here and once by the quantizer, too far
+        // apart for the caches to keep it
+        const bool f16 = dtype == LQ_F16;
+        const u32x4* src = reinterpret_cast<const u32x4*>(x) + h * vec_per_head;
+        for (; v + 7 * bd < v1; v += 8 * bd) {
+            u32x4 w[8];
 #pragma unroll
-            for (int u = 0; u < 4; u++) load8(x, dtype, h * vec_per_head + v + u * bd, xv[u]);
+            for (int u = 0; u < 8; u++) w[u] = __builtin_nontemporal_load(src + v + u * bd);
 #pragma unroll
-            for (int u = 0; u < 4; u++) acc4[u] += sq8(xv[u]);
+            for (int u = 0; u < 8; u++) acc4[u & 3] += (double)sq_vec16(w[u], f16);
         }
-        for (; v < v1; v += bd) {
-            float xv[8];
-            load8(x, dtype, h * vec_per_head + v, xv);
-            acc4[0] += sq8(xv);
-        }
+        for (; v < v1; v += bd) acc4[0] += (double)sq_vec16(__builtin_nontemporal_load(src + v), f16);
     }
     const double acc = (acc4[0] + acc4[1]) + (acc4[2] + acc4[3]);
     __shared__ double red[256];
