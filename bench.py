@@ -162,14 +162,34 @@ def cpu_baseline(x_chunks, bits, scale_rows, gpu_words, gpu_out):
     return tiers, exact, info
 
 
+class CacheFlush:
+    """Evicts L2 and MALL before a timed run by reading (summing) a 512 MiB
+    buffer: the caches then hold clean lines of unrelated data, the state a
+    step meets after other kernels have streamed their inputs.  With
+    write=True it writes the buffer instead, which also leaves MALL full of
+    dirty lines that the timed kernel must write back as it reads (kept as a
+    second, pessimistic measurement)."""
+
+    def __init__(self, dev, write=False, nbytes=512 << 20):
+        self.write = write
+        self.buf = torch.ones(nbytes // 4, dtype=torch.float32, device=dev)
+        self.acc = torch.zeros((), dtype=torch.float32, device=dev)
+
+    def __call__(self, i):
+        if self.write:
+            self.buf.fill_(float(i & 0xff))
+        else:
+            torch.sum(self.buf, dim=0, out=self.acc)
+
+
 def timed_median(fn, n, flush=None):
     """Median event time (us) of fn over n runs on the current stream.  Before
-    each run: the flush fill (evicts L2 and MALL) when given, then a queued GPU
-    spin, so the start event is reached after the host has submitted fn."""
+    each run: the cache flush (CacheFlush) when given, then a queued GPU spin,
+    so the start event is reached after the host has submitted fn."""
     ts = []
     for i in range(n):
         if flush is not None:
-            flush.fill_(i & 0xff)
+            flush(i)
         gpu_busy()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
@@ -195,12 +215,13 @@ def bench_c1(dev, iters=20):
     fallback for the rest, 1-bit mask, per-head scales) -> fused merge back to
     fp16.  B = 4 D + 2 P, P = 4 V_in + 16 V_oor + ceil(V/8) + 2 H.
 
-    Timed: the round trip through the API (compress_fixed_rate: quantize,
-    representability, compaction by boolean index -- 3 host syncs, as the
-    reference's tensor-indexing structure has -- then fused_decompress_chunk),
-    and the merge kernel alone (the reference's own throughput method,
-    core/triton_dequant.py:238-286), each with a 512 MiB flush before every run
-    and warm (the 12 MB working set then sits in the 256 MB MALL)."""
+    Timed: the device round trip (per-head scales, codec.compact_encode: one
+    quantize + compaction pass, codec.compact_merge: no host sync); the round
+    trip through the API (compress_fixed_rate, whose one host sync reads the
+    row counts that size the chunk's tensors, then fused_decompress_chunk); and
+    the merge kernel alone (the reference's own throughput method,
+    core/triton_dequant.py:238-286); each after a 512 MiB cache flush and warm
+    (the 12 MB working set then sits in the 256 MB MALL)."""
     from latticequant_amd import codec
     from latticequant_amd.llm.compressed_kv_cache import compress_fixed_rate
     from latticequant_amd.llm.fused_triton_merge import fused_decompress_chunk
@@ -225,18 +246,30 @@ def bench_c1(dev, iters=20):
     v_in = int(mask.sum())
     P = 4 * v_in + 16 * (V - v_in) + (V + 7) // 8 + 2 * 8
     B = 4 * D + 2 * P
-    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    # the device round trip gives the same mask, packed words and output
+    cb = codec.compact_encode(kd, 4)
+    dout = codec.compact_merge(cb)
+    n_in = int(cb.totals[0])
+    exact = exact and bool(np.array_equal(cb.mask.cpu().numpy().astype(bool), mask)
+                           and np.array_equal(cb.packed[:n_in].cpu().numpy(), O.pack_e8(qo[mask], 4))
+                           and np.array_equal(dout.cpu().numpy(), want))
+    flush = CacheFlush(dev)
+    dv = lambda: codec.compact_merge(codec.compact_encode(kd, 4), out=dout)
     rt = lambda: fused_decompress_chunk(compress_fixed_rate(kd, 4))
     mg = lambda: fused_decompress_chunk(ch)
+    us_dv_f, us_dv_w = timed_median(dv, iters, flush), timed_median(dv, iters)
     us_rt_f, us_rt_w = timed_median(rt, iters, flush), timed_median(rt, iters)
     us_mg_f, us_mg_w = timed_median(mg, iters, flush), timed_median(mg, iters)
     del flush
     return {"workload": "C1: K [1,8,2048,128] fp16 (randn seed 0, CPU), 4 b/d, compact 4-byte form + fp16 "
                         "fallback, no entropy coding", "input_sha256": sha, "bit_exact": exact,
             "in_range_frac": round(v_in / V, 4), "P_bytes": P, "B_bytes": B,
-            "round_trip_flushed": _roof(B, us_rt_f, "compress_fixed_rate + fused_decompress_chunk, 512 MiB flush "
-                                                   "before each run; includes the API's 3 host syncs"),
-            "round_trip_warm": _roof(B, us_rt_w, "same, warm (MALL-resident working set)"),
+            "round_trip_flushed": _roof(B, us_dv_f, "head scales + compact_encode (quantize, pack, compact in one "
+                                                   "pass) + compact_merge, no host sync; 512 MiB flush before each run"),
+            "round_trip_warm": _roof(B, us_dv_w, "same, warm (MALL-resident working set)"),
+            "api_round_trip_flushed": _roof(B, us_rt_f, "compress_fixed_rate + fused_decompress_chunk (one host "
+                                                       "sync for the row counts), flushed"),
+            "api_round_trip_warm": _roof(B, us_rt_w, "same, warm"),
             "merge_flushed": _roof(P + 2 * D, us_mg_f, "lq_fused_merge alone (reads P, writes 2 D), flushed"),
             "merge_warm": _roof(P + 2 * D, us_mg_w, "lq_fused_merge alone, warm (MALL-resident)")}
 
@@ -441,8 +474,9 @@ def bench_decode_step(dev, iters=30, prefix=32768, tail=128):
     The prefix is compressed by the chunk codec (its rANS chunks are the at-rest
     form) and held resident as the same lattice points in the fixed-width form
     lq_resident_attention reads (b = 5 code words + exceptions).  Per iteration a
-    512 MiB write evicts everything from L2 / MALL first and a queued GPU spin
-    keeps host submission out of the events, so the step reads from HBM.
+    512 MiB read evicts everything from L2 / MALL first (CacheFlush) and a
+    queued GPU spin keeps host submission out of the events, so the step reads
+    from HBM; also reported: after a 512 MiB write (dirty MALL lines) and warm.
     Also reported: the same step decoding the rANS chunks directly
     (lq_decode_attention).  Returns dict with the median step times and the
     roofline figures (algorithmic bytes C_K + C_V + tail + q + out)."""
@@ -466,10 +500,13 @@ def bench_decode_step(dev, iters=30, prefix=32768, tail=128):
     out = resident_decode_attention(rk, rv, q, tk, tv, work=work)
     rwork = rans_workspace(ek, 4)
     out2 = decode_attention(ek, ev, q, tk, tv, work=rwork)
-    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    flush = CacheFlush(dev)
     timed = lambda fn, n: timed_median(fn, n, flush)
 
-    us = timed(lambda: resident_decode_attention(rk, rv, q, tk, tv, work=work, out=out), iters)
+    step = lambda: resident_decode_attention(rk, rv, q, tk, tv, work=work, out=out)
+    us = timed(step, iters)
+    us_dirty = timed_median(step, iters, CacheFlush(dev, write=True))
+    us_warm = timed_median(step, iters)
     us_rans = timed(lambda: decode_attention(ek, ev, q, tk, tv, work=rwork, out=out2), max(5, iters // 3))
     cb = int(ek.reference_bytes().sum() + ek.side_bytes().sum() + ev.reference_bytes().sum() + ev.side_bytes().sum())
     small = tk.numel() * 2 + tv.numel() * 2 + q.numel() * 2 + out.numel() * 2
@@ -482,6 +519,8 @@ def bench_decode_step(dev, iters=30, prefix=32768, tail=128):
             "decode_step_resident_GBps": round(rbytes / (us * 1e-6) / 1e9, 1),
             "decode_tokens_per_s_32_layers": round(1e6 / (32 * us), 2),
             "decode_step_rans_direct_us": round(us_rans, 2),
+            "decode_step_us_write_flush": round(us_dirty, 2),
+            "decode_step_us_warm": round(us_warm, 2),
             "input_sha256": sha.hexdigest(),
             "decode_step_workload": f"C3: q [1,32,1,128], prefix K,V [1,8,{prefix},128] E8+rANS {BITS} b/d "
                                     f"(attention reads its resident b=5 form), tail [1,8,{tail},128] fp16, "

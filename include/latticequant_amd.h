@@ -310,7 +310,8 @@ int lq_pack_compact(const float *d_q, int bits, int64_t n, uint8_t *d_packed, in
 
 /* Single-pass repr/fallback merge: block i is decoded from packed[rank_repr(i)]
  * when mask[i] != 0 else copied from fallback[rank_fb(i)]; ranks are computed
- * in-kernel.  head = i / bph.  Replaces _fused_merge_4bit_vec_kernel
+ * in-kernel (wave ballots within 1024-block tiles, a chained look-back across
+ * them; the workspace is cleared by the call).  head = i / bph.  Replaces _fused_merge_4bit_vec_kernel
  * (llm/fused_triton_merge.py:33-130), with unpack_e8's floor-mod parity.
  * packed holds n_packed rows, fallback n_fallback; ranks past them (a mask
  * that selects more rows than the caller holds) are clamped, and a block with
@@ -320,6 +321,32 @@ int64_t lq_merge_workspace(int64_t total_blocks);
 int lq_fused_merge(const uint8_t *d_packed, int64_t n_packed, int bits, const uint16_t *d_fallback,
                    int64_t n_fallback, const uint8_t *d_mask, const float *d_scales, int64_t total_blocks,
                    int64_t bph, void *d_work, uint16_t *d_out, hipStream_t s);
+
+/* Fixed-rate compression of a (n_heads, bph) batch in one pass: x / scale32[head]
+ * (three-op division where d_fastdiv says so, as lq_chunk_quantize) -> nearest
+ * E8 point; a point in range at `bits` goes to d_packed (b bytes, the
+ * pack_e8 layout) at its rank among the in-range points, any other to
+ * d_fallback as fp16(q * float(scale16[head])) at its rank among the rest;
+ * d_mask gets 1 / 0 per vector, d_repr_heads (nullable) the head of each
+ * packed point in packed order, d_tile_off the number of in-range points
+ * before each 1024-vector tile (what lq_compact_merge takes) and d_totals
+ * (n_packed, n_fallback).  d_packed / d_fallback hold room for every vector
+ * (n * b and n * 16 bytes); only the first d_totals rows are written.  No host
+ * sync.  A look-back wait that does not end sets the error word after d_work's
+ * tile words (4 bytes at offset (tiles + 1) * 8).  d_work: lq_compact_encode_workspace(n) bytes (cleared by the call).
+ * Replaces core/compact_storage.py:338-357 (quantize_and_pack) with the fp16
+ * fallback of the fixed-rate cache (llm/fused_triton_merge.py chunk fields). */
+int64_t lq_compact_encode_workspace(int64_t n);
+int lq_compact_encode(const void *d_x, int dtype, int64_t n_heads, int64_t bph, const float *d_scale32,
+                      const int32_t *d_fastdiv, const uint16_t *d_scale16, int bits, uint8_t *d_mask,
+                      uint8_t *d_packed, uint16_t *d_fallback, int32_t *d_repr_heads, int64_t *d_tile_off,
+                      int64_t *d_totals, void *d_work, hipStream_t s);
+
+/* lq_fused_merge with the tile offsets lq_compact_encode wrote (no count or
+ * scan pass).  Replaces llm/fused_triton_merge.py:33-172 as lq_fused_merge. */
+int lq_compact_merge(const uint8_t *d_packed, int64_t n_packed, int bits, const uint16_t *d_fallback,
+                     int64_t n_fallback, const uint8_t *d_mask, const float *d_scales, int64_t total_blocks,
+                     int64_t bph, const int64_t *d_tile_off, uint16_t *d_out, hipStream_t s);
 
 /* ----------------------------------------------------------- API helpers -- */
 

@@ -237,6 +237,72 @@ def quantize_points(t: torch.Tensor, bits, scale32: Optional[torch.Tensor] = Non
     return q, scale32, scale16
 
 
+@dataclass
+class CompactBatch:
+    """Device output of compact_encode: the fixed-rate form of one tensor with
+    buffers sized for every vector (packed / fallback rows beyond the totals
+    are unused) and the counts still on the device."""
+    mask: torch.Tensor         # (V,) uint8, 1 = packed
+    packed: torch.Tensor       # (V, bits) uint8; rows < totals[0] hold the packed points
+    fallback: torch.Tensor     # (V, 8) fp16; rows < totals[1] hold the out-of-range vectors
+    repr_heads: torch.Tensor   # (V,) int32; rows < totals[0]: head of each packed point
+    tile_off: torch.Tensor     # (tiles,) int64: packed points before each 1024-vector tile
+    totals: torch.Tensor       # (2,) int64: (n_packed, n_fallback)
+    scale32: torch.Tensor      # (n_heads,) fp32 quantization scales
+    scale16: torch.Tensor      # (n_heads,) fp16 stored scales
+    shape: tuple
+    bph: int
+    bits: int
+
+
+def compact_encode(t: torch.Tensor, bits: int, storage_bits: Optional[int] = None,
+                   scale32: Optional[torch.Tensor] = None) -> CompactBatch:
+    """Fixed-rate compression of one (B, H, T, hd) tensor without a host sync:
+    scales at `bits` (or the caller's scale32), lattice points packed at
+    `storage_bits` (default `bits`) where they fit, fp16 fallback elsewhere,
+    compacted in one pass (lq_compact_encode)."""
+    lib = L.lib()
+    sb = storage_bits or bits
+    if sb not in (3, 4, 5):
+        raise ValueError("storage bits must be 3, 4 or 5")
+    x = _check_input(t[None])
+    _, B, H, T, hd = x.shape
+    nh, bph = B * H, T * hd // 8
+    V = nh * bph
+    dev = x.device
+    _, scale32, scale16, _, fastdiv = _head_scales(x, bits, scale32)
+    tiles = (V + 1023) // 1024
+    mask = _empty(V, torch.uint8, dev)
+    packed = _empty(V * sb, torch.uint8, dev).view(V, sb)
+    fallback = _empty(V * 8, torch.float16, dev).view(V, 8)
+    heads = _empty(V, torch.int32, dev)
+    tile_off = _empty(tiles, torch.int64, dev)
+    totals = _empty(2, torch.int64, dev)
+    work = _empty(lib.lq_compact_encode_workspace(V), torch.uint8, dev)
+    L.check(lib.lq_compact_encode(x.data_ptr(), L.dtype_code(x.dtype), nh, bph, scale32.data_ptr(), fastdiv.data_ptr(),
+                                  scale16.data_ptr(), sb, mask.data_ptr(), packed.data_ptr(), fallback.data_ptr(),
+                                  heads.data_ptr(), tile_off.data_ptr(), totals.data_ptr(), work.data_ptr(),
+                                  L.stream_ptr(dev)), "lq_compact_encode")
+    return CompactBatch(mask=mask, packed=packed, fallback=fallback, repr_heads=heads, tile_off=tile_off,
+                        totals=totals, scale32=scale32, scale16=scale16, shape=(B, H, T, hd), bph=bph, bits=sb)
+
+
+def compact_merge(cb: CompactBatch, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """fp16 (B, H, T, hd) from a CompactBatch (lq_compact_merge: packed points
+    dequantised with float(scale16), fallback rows copied), no host sync."""
+    lib = L.lib()
+    B, H, T, hd = cb.shape
+    V = cb.mask.numel()
+    dev = cb.mask.device
+    if out is None:
+        out = torch.empty(B, H, T, hd, dtype=torch.float16, device=dev)
+    sc = cb.scale16.float()
+    L.check(lib.lq_compact_merge(cb.packed.data_ptr(), V, cb.bits, cb.fallback.data_ptr(), V, cb.mask.data_ptr(),
+                                 sc.data_ptr(), V, cb.bph, cb.tile_off.data_ptr(), out.data_ptr(), L.stream_ptr(dev)),
+            "lq_compact_merge")
+    return out
+
+
 def _status_or(status: torch.Tensor) -> int:
     """OR of the per-chunk LQ_ST_* bits (one device-to-host copy)."""
     st = 0

@@ -97,65 +97,117 @@ __global__ void k_pack(const float* __restrict__ q, int bits, int64_t n, uint8_t
 
 // ------------------------------------------------------------- merge ----
 constexpr int kTile = 1024;
+constexpr int kTileThreads = 1024;   // one vector per thread
+constexpr int kTileRounds = kTile / kTileThreads;
 
-__global__ void k_merge_count(const uint8_t* __restrict__ mask, int64_t total, int64_t* __restrict__ tile_cnt) {
-    __shared__ int part[4];
-    const int64_t t0 = (int64_t)blockIdx.x * kTile;
-    int c = 0;
-    for (int i = threadIdx.x; i < kTile; i += 256) {
-        int64_t b = t0 + i;
-        c += (b < total && mask[b]) ? 1 : 0;
-    }
-    for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = c;
-    __syncthreads();
-    if (threadIdx.x == 0) tile_cnt[blockIdx.x] = part[0] + part[1] + part[2] + part[3];
+// ------------------------------------------------ chained tile prefix --
+//
+// Decoupled look-back over kTile-vector tiles in start order: a workgroup
+// takes a ticket (its tile), publishes the tile's count, then adds the counts
+// of the tiles before it (64 at a time) until it meets one whose inclusive
+// prefix is known.
+// Tickets are taken in the order workgroups start, so every tile waited on is
+// running or done and none of them waits on a later tile: the chain drains.
+// status[] and the ticket counter must be zero before the launch (k_zero64);
+// a wait that exceeds kSpinLimit polls sets *err instead of hanging.
+constexpr uint64_t kStAgg = 1ull << 62, kStIncl = 2ull << 62, kStVal = (1ull << 62) - 1ull;
+constexpr uint32_t kSpinLimit = 1u << 22;
+
+__device__ __forceinline__ void st_status(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__global__ void k_merge_scan(int64_t n_tiles, int64_t* __restrict__ tile_cnt) {   // in place, exclusive
-    __shared__ int64_t part[256];
-    const int tid = threadIdx.x;
-    const int64_t per = (n_tiles + 255) / 256;
-    const int64_t a = tid * per, b = a + per < n_tiles ? a + per : n_tiles;
-    int64_t s = 0;
-    for (int64_t i = a; i < b; i++) s += tile_cnt[i];
-    part[tid] = s;
-    __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {
-        int64_t v = tid >= off ? part[tid - off] : 0;
-        __syncthreads();
-        part[tid] += v;
-        __syncthreads();
+// Wave 0 (all 64 lanes) only: exclusive prefix of tile t's count.  The lanes
+// read the 64 status words before the current window end at once; the window
+// is summed up to the nearest tile whose inclusive prefix is known, and moved
+// back by 64 tiles when it holds only aggregates.
+__device__ int64_t tile_lookback(uint64_t* status, int64_t t, int64_t count, int32_t* err) {
+    const int lane = threadIdx.x & 63;
+    if (t == 0) {
+        if (lane == 0) st_status(status, kStIncl | (uint64_t)count);
+        return 0;
     }
-    int64_t run = tid ? part[tid - 1] : 0;
-    for (int64_t i = a; i < b; i++) { int64_t c = tile_cnt[i]; tile_cnt[i] = run; run += c; }
+    if (lane == 0) st_status(status + t, kStAgg | (uint64_t)count);
+    int64_t excl = 0, end = t;   // window: tiles end - 64 .. end - 1, lane j reads end - 1 - j
+    uint32_t spins = 0;
+    while (end > 0) {
+        const int64_t j = end - 1 - lane;
+        const uint64_t st = j >= 0 ? __hip_atomic_load(status + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : kStIncl;
+        const uint64_t incl = __ballot((st >> 62) == 2);
+        const int first = incl ? __builtin_ctzll(incl) : 64;   // nearest inclusive prefix in the window
+        const uint64_t notready = __ballot((st >> 62) == 0) & (first < 64 ? (2ull << first) - 1ull : ~0ull);
+        if (notready) {   // a tile before the nearest inclusive one has not published yet
+            if (++spins > kSpinLimit) {
+                if (lane == 0) atomicOr(err, 1);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            continue;
+        }
+        int64_t v = lane <= first && j >= 0 ? (int64_t)(st & kStVal) : 0;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+        excl += v;
+        if (first < 64) break;
+        end -= 64;
+    }
+    if (lane == 0) st_status(status + t, kStIncl | (uint64_t)(excl + count));
+    return excl;
+}
+
+__global__ void k_zero64(uint64_t* __restrict__ p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0ull;
 }
 
 // One tile of kTile blocks per workgroup; ranks from the tile offset plus
 // wave ballots, then either unpack the packed word or copy the fp16 fallback.
-__global__ __launch_bounds__(256) void k_merge(const uint8_t* __restrict__ packed, int bits,
+// LB: the tile offsets come from the chained look-back (tile = ticket order)
+// instead of tile_off (tile = workgroup index).
+template <bool LB>
+__global__ __launch_bounds__(kTileThreads) void k_merge(const uint8_t* __restrict__ packed, int bits,
                                                const uint16_t* __restrict__ fallback, const uint8_t* __restrict__ mask,
                                                const float* __restrict__ scales, int64_t total, int64_t bph,
                                                int64_t n_packed, int64_t n_fallback,
-                                               const int64_t* __restrict__ tile_off, uint16_t* __restrict__ out) {
+                                               const int64_t* __restrict__ tile_off, uint16_t* __restrict__ out,
+                                               uint64_t* __restrict__ status, uint32_t* __restrict__ ticket,
+                                               int32_t* __restrict__ err) {
     __shared__ int wcnt[kTile / 64];
+    __shared__ int s_t;
+    __shared__ int64_t s_off;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t t0 = (int64_t)blockIdx.x * kTile;
-    int m[4];
-    for (int r = 0; r < 4; r++) {
-        int64_t b = t0 + r * 256 + tid;
+    int64_t tile = blockIdx.x;
+    if constexpr (LB) {
+        if (tid == 0) s_t = (int)atomicAdd(ticket, 1u);
+        __syncthreads();
+        tile = s_t;
+    }
+    const int64_t t0 = tile * kTile;
+    int m[kTileRounds];
+    for (int r = 0; r < kTileRounds; r++) {
+        int64_t b = t0 + r * kTileThreads + tid;
         m[r] = (b < total && mask[b]) ? 1 : 0;
         unsigned long long bal = __ballot(m[r]);
-        if (lane == 0) wcnt[r * 4 + wave] = __popcll(bal);
+        if (lane == 0) wcnt[r * (kTileThreads / 64) + wave] = __popcll(bal);
     }
     __syncthreads();
-    for (int r = 0; r < 4; r++) {
-        int64_t b = t0 + r * 256 + tid;
+    if constexpr (LB) {
+        if (wave == 0) {
+            int cnt = 0;
+            for (int k = 0; k < kTile / 64; k++) cnt += wcnt[k];
+            const int64_t off = tile_lookback(status, tile, cnt, err);
+            if (lane == 0) s_off = off;
+        }
+        __syncthreads();
+    }
+    const int64_t toff = LB ? s_off : tile_off[tile];
+    for (int r = 0; r < kTileRounds; r++) {
+        int64_t b = t0 + r * kTileThreads + tid;
         unsigned long long bal = __ballot(m[r]);
         if (b >= total) continue;
         int before = 0;
-        for (int k = 0; k < r * 4 + wave; k++) before += wcnt[k];
-        int64_t rr = tile_off[blockIdx.x] + before + __popcll(bal & ((1ull << lane) - 1ull));
+        for (int k = 0; k < r * (kTileThreads / 64) + wave; k++) before += wcnt[k];
+        int64_t rr = toff + before + __popcll(bal & ((1ull << lane) - 1ull));
         // ranks past the rows the caller holds (a mask that selects more rows
         // than packed / fallback have) are clamped: garbage out, never a fault
         if (m[r] && n_packed > 0) {
@@ -174,6 +226,109 @@ __global__ __launch_bounds__(256) void k_merge(const uint8_t* __restrict__ packe
             reinterpret_cast<uint4*>(out)[b] = reinterpret_cast<const uint4*>(fallback)[fr];
         } else {
             reinterpret_cast<uint4*>(out)[b] = make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+}
+
+
+// Fixed-rate compression of a (n_heads, bph) batch of vectors in one pass
+// (llm/compressed_kv_cache.py compress path of core/compact_storage.py:338-357
+// plus the fp16 fallback of the fixed-rate cache): x / scale32[head] -> nearest
+// E8 point; in range at `bits` -> its packed word at its rank among the
+// in-range vectors, else q * float(scale16[head]) in fp16 at its rank among
+// the others; the mask byte; the head of each packed point (optional); tile
+// offsets for the merge; the two totals.
+__global__ __launch_bounds__(kTileThreads) void k_compact_encode(
+        const void* __restrict__ x, int dtype, int64_t n, int64_t bph, const float* __restrict__ scale32,
+        const int32_t* __restrict__ fastdiv, const uint16_t* __restrict__ scale16, int bits,
+        uint8_t* __restrict__ mask, uint8_t* __restrict__ packed, uint16_t* __restrict__ fallback,
+        int32_t* __restrict__ repr_heads, int64_t* __restrict__ tile_off, int64_t* __restrict__ totals,
+        uint64_t* __restrict__ status,
+        uint32_t* __restrict__ ticket, int32_t* __restrict__ err) {
+    __shared__ int s_t, s_wcnt[kTile / 64];
+    __shared__ int64_t s_excl;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) s_t = (int)atomicAdd(ticket, 1u);
+    __syncthreads();
+    const int64_t t = s_t;
+    const int64_t ntiles = (n + kTile - 1) / kTile;
+    const int R = 1 << (bits - 1);
+    uint64_t word[kTileRounds];
+    float y[kTileRounds][8];
+    int m[kTileRounds];
+#pragma unroll
+    for (int r = 0; r < kTileRounds; r++) {
+        const int64_t v = t * kTile + r * kTileThreads + tid;
+        m[r] = 0;
+        word[r] = 0;
+        if (v < n) {
+            const int64_t h = v / bph;
+            const float s = scale32[h];
+            const bool fast = fastdiv[h] != 0;
+            const float rs = 1.0f / s;
+            float xv[8], tq[8], ic[8];
+            load8(x, dtype, v, xv);
+#pragma unroll
+            for (int i = 0; i < 8; i++) tq[i] = div_scaled(xv[i], s, rs, fast);
+            const int c = e8_nearest_fast(tq, ic, [&](float tt[8]) {
+                float xx[8];
+                load8(x, dtype, v, xx);
+#pragma unroll
+                for (int i = 0; i < 8; i++) tt[i] = div_scaled(xx[i], s, rs, fast);
+            });
+            bool in = true;
+            uint64_t w = (uint64_t)c;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int ci = (int)ic[i];
+                in = in && ci >= -R && ci <= R - 1;
+                const uint64_t u = (uint64_t)(uint32_t)(ci + R) & ((1ull << bits) - 1ull);
+                w = i < 7 ? (w << bits) | u : (w << (bits - 1)) | (u >> 1);
+            }
+            m[r] = in ? 1 : 0;
+            word[r] = w;
+            const float sf = h2f(scale16[h]), off = c ? 0.5f : 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) y[r][i] = (ic[i] + off) * sf;
+        }
+        const unsigned long long bal = __ballot(m[r]);
+        if (lane == 0) s_wcnt[r * (kTileThreads / 64) + wave] = __popcll(bal);
+    }
+    __syncthreads();
+    if (wave == 0) {
+        int cnt = 0;
+        for (int k = 0; k < kTile / 64; k++) cnt += s_wcnt[k];
+        const int64_t excl = tile_lookback(status, t, cnt, err);
+        if (lane == 0) {
+            s_excl = excl;
+            tile_off[t] = excl;
+            if (t == ntiles - 1) {
+                totals[0] = excl + cnt;
+                totals[1] = n - (excl + cnt);
+            }
+        }
+    }
+    __syncthreads();
+    const int64_t excl = s_excl;
+#pragma unroll
+    for (int r = 0; r < kTileRounds; r++) {
+        const int64_t v = t * kTile + r * kTileThreads + tid;
+        const unsigned long long bal = __ballot(m[r]);
+        if (v >= n) continue;
+        int before = 0;
+        for (int k = 0; k < r * (kTileThreads / 64) + wave; k++) before += s_wcnt[k];
+        const int64_t rr = excl + before + __popcll(bal & ((1ull << lane) - 1ull));
+        mask[v] = (uint8_t)m[r];
+        if (m[r]) {
+            if (repr_heads) repr_heads[rr] = (int32_t)(v / bph);
+            if (bits == 4) {
+                reinterpret_cast<uint32_t*>(packed)[rr] = __builtin_bswap32((uint32_t)word[r]);
+            } else {
+                uint64_t w = word[r];
+                for (int b = bits - 1; b >= 0; b--) { packed[rr * bits + b] = (uint8_t)(w & 0xff); w >>= 8; }
+            }
+        } else {
+            store8(fallback, LQ_F16, v - rr, y[r]);
         }
     }
 }
@@ -200,7 +355,7 @@ int lq_pack_compact(const float* d_q, int bits, int64_t n, uint8_t* d_packed, in
 
 int64_t lq_merge_workspace(int64_t total_blocks) {
     if (total_blocks < 0) return -1;
-    return ((total_blocks + kTile - 1) / kTile + 1) * 8;
+    return ((total_blocks + kTile - 1) / kTile + 2) * 8;   // tile status words, ticket counter, error flag
 }
 
 int lq_fused_merge(const uint8_t* d_packed, int64_t n_packed, int bits, const uint16_t* d_fallback, int64_t n_fallback,
@@ -209,11 +364,49 @@ int lq_fused_merge(const uint8_t* d_packed, int64_t n_packed, int bits, const ui
     if (bits < 3 || bits > 5 || total_blocks < 0 || bph <= 0 || n_packed < 0 || n_fallback < 0) return LQ_ERR_ARG;
     if (total_blocks == 0) return LQ_OK;
     const int64_t tiles = (total_blocks + kTile - 1) / kTile;
-    int64_t* off = reinterpret_cast<int64_t*>(d_work);
-    hipLaunchKernelGGL(k_merge_count, dim3((unsigned)tiles), dim3(256), 0, s, d_mask, total_blocks, off);
-    hipLaunchKernelGGL(k_merge_scan, dim3(1), dim3(256), 0, s, tiles, off);
-    hipLaunchKernelGGL(k_merge, dim3((unsigned)tiles), dim3(256), 0, s, d_packed, bits, d_fallback, d_mask, d_scales,
-                       total_blocks, bph, n_packed, n_fallback, off, d_out);
+    uint64_t* status = reinterpret_cast<uint64_t*>(d_work);
+    uint32_t* ticket = reinterpret_cast<uint32_t*>(status + tiles);
+    int32_t* err = reinterpret_cast<int32_t*>(status + tiles + 1);
+    hipLaunchKernelGGL(k_zero64, dim3((unsigned)((tiles + 2 + 255) / 256)), dim3(256), 0, s, status, tiles + 2);
+    hipLaunchKernelGGL(k_merge<true>, dim3((unsigned)tiles), dim3(kTileThreads), 0, s, d_packed, bits, d_fallback, d_mask,
+                       d_scales, total_blocks, bph, n_packed, n_fallback, nullptr, d_out, status, ticket, err);
+    return launch_status();
+}
+
+int64_t lq_compact_encode_workspace(int64_t n) {
+    if (n < 0) return -1;
+    return ((n + kTile - 1) / kTile + 2) * 8;   // tile status words, then the ticket counter and error flag
+}
+
+int lq_compact_encode(const void* d_x, int dtype, int64_t n_heads, int64_t bph, const float* d_scale32,
+                      const int32_t* d_fastdiv, const uint16_t* d_scale16, int bits, uint8_t* d_mask,
+                      uint8_t* d_packed, uint16_t* d_fallback, int32_t* d_repr_heads, int64_t* d_tile_off,
+                      int64_t* d_totals, void* d_work, hipStream_t s) {
+    if (bits < 3 || bits > 5 || n_heads <= 0 || bph <= 0 || dtype < 0 || dtype > 2) return LQ_ERR_ARG;
+    if (!d_x || !d_scale32 || !d_fastdiv || !d_scale16 || !d_mask || !d_packed || !d_fallback || !d_tile_off ||
+        !d_totals || !d_work)
+        return LQ_ERR_ARG;
+    const int64_t n = n_heads * bph;
+    const int64_t tiles = (n + kTile - 1) / kTile;
+    uint64_t* status = reinterpret_cast<uint64_t*>(d_work);
+    uint32_t* ticket = reinterpret_cast<uint32_t*>(status + tiles);
+    int32_t* err = reinterpret_cast<int32_t*>(status + tiles + 1);
+    hipLaunchKernelGGL(k_zero64, dim3((unsigned)((tiles + 2 + 255) / 256)), dim3(256), 0, s, status, tiles + 2);
+    hipLaunchKernelGGL(k_compact_encode, dim3((unsigned)tiles), dim3(kTileThreads), 0, s, d_x, dtype, n, bph, d_scale32,
+                       d_fastdiv, d_scale16, bits, d_mask, d_packed, d_fallback, d_repr_heads, d_tile_off, d_totals,
+                       status, ticket, err);
+    return launch_status();
+}
+
+int lq_compact_merge(const uint8_t* d_packed, int64_t n_packed, int bits, const uint16_t* d_fallback,
+                     int64_t n_fallback, const uint8_t* d_mask, const float* d_scales, int64_t total_blocks,
+                     int64_t bph, const int64_t* d_tile_off, uint16_t* d_out, hipStream_t s) {
+    if (bits < 3 || bits > 5 || total_blocks < 0 || bph <= 0 || n_packed < 0 || n_fallback < 0 || !d_tile_off)
+        return LQ_ERR_ARG;
+    if (total_blocks == 0) return LQ_OK;
+    const int64_t tiles = (total_blocks + kTile - 1) / kTile;
+    hipLaunchKernelGGL(k_merge<false>, dim3((unsigned)tiles), dim3(kTileThreads), 0, s, d_packed, bits, d_fallback, d_mask,
+                       d_scales, total_blocks, bph, n_packed, n_fallback, d_tile_off, d_out, nullptr, nullptr, nullptr);
     return launch_status();
 }
 

@@ -389,8 +389,8 @@ __global__ __launch_bounds__(kQThreads, LEAN ? 7 : 1) void k_chunk_quantize(
                     for (int i = 0; i < 8; i++) t[i] = t[i] + dd[i];
                 }
                 int c;
-                if constexpr (ROT) {   // the rotation is cross-lane: keep t for the rare exact path
-                    c = e8_nearest_fast(t, ic);
+                if constexpr (ROT) {   // the rotation is cross-lane, so t cannot be recomputed in a
+                    c = e8_nearest(t, ic);   // divergent branch; keeping it live costs this variant a wave
                 } else {               // the rare exact path recomputes t from x
                     c = e8_nearest_fast(t, ic, [&](float tt[8]) {
                         float xx[8];

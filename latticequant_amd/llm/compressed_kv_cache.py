@@ -524,20 +524,17 @@ def compress_fixed_rate(tensor: torch.Tensor, bits_per_dim: int = 4, storage_bit
     """Quantize like _compress_tensor (scales at `bits_per_dim`) and store the
     lattice points in the fixed-rate layout at `storage_bits` (default: the
     same), out-of-range vectors as fp16 fallback.  Scales are the fp16-stored
-    ones widened to fp32, so merge output equals _decompress_chunk's."""
-    from ..core import compact_storage as cs
-    sb = storage_bits or bits_per_dim
+    ones widened to fp32, so merge output equals _decompress_chunk's.  One
+    compaction pass on the device (codec.compact_encode); the only host sync
+    reads the two row counts that size the chunk's tensors."""
     B, H, T, hd = tensor.shape
     if hd % 8:
         raise ValueError("head_dim must be a multiple of 8")
     x = (tensor.cuda() if not tensor.is_cuda else tensor).contiguous()
+    cb = codec.compact_encode(x, bits_per_dim, storage_bits, scale32)
+    n_repr, n_oor = (int(v) for v in cb.totals.tolist())
     nh, bph = B * H, T * hd // 8
-    q, s32, s16 = codec.quantize_points(x, bits_per_dim, scale32)
-    mask = cs.check_representable(q, sb)
-    sc = s16.float()
-    head = torch.arange(nh * bph, device=x.device, dtype=torch.int64) // bph
-    packed = cs.pack_e8(q[mask], sb) if bool(mask.any()) else torch.zeros(0, sb, dtype=torch.uint8, device=x.device)
-    fb = (q[~mask] * sc[head[~mask]][:, None]).to(torch.float16)
-    return CompressedChunk(repr_mask=mask, packed=packed, fallback=fb, scales=sc, repr_head_ids=head[mask].to(torch.int32),
+    return CompressedChunk(repr_mask=cb.mask.bool(), packed=cb.packed[:n_repr], fallback=cb.fallback[:n_oor],
+                           scales=cb.scale16.float(), repr_head_ids=cb.repr_heads[:n_repr],
                            orig_shape=(B, H, T, hd), n_vectors=nh * bph, n_heads=nh, blocks_per_head=bph,
-                           bits_per_dim=sb, orig_dtype=torch.float16)
+                           bits_per_dim=cb.bits, orig_dtype=torch.float16)

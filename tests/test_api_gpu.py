@@ -345,3 +345,37 @@ def test_compact_index_clamping_gpu(monkeypatch):
         td.triton_unpack_e8_4bit(packed, sc, hi.cuda())
     with pytest.raises(ValueError, match="mask selects"):
         fused_decompress_chunk(ch)
+
+
+@pytest.mark.parametrize("bits,storage", [(4, 4), (4, 3), (4, 5), (3, 3)])
+def test_compact_encode_merge_device_gpu(bits, storage):
+    """Sync-free fixed-rate round trip (codec.compact_encode -> compact_merge)
+    over 73 tiles of 1024 vectors (the last one partial): packed words, mask,
+    fp16 fallback rows, head ids, tile offsets and totals against the oracle
+    (quantize_heads / check_representable / pack_e8 at the device's scales),
+    and the merged output equal to q * float(scale16)."""
+    from latticequant_amd import codec
+    gen = torch.Generator().manual_seed(40 + 3 * bits + storage)
+    t = torch.randn(1, 3, 24870, 8, generator=gen)          # 74610 vectors: 72 full tiles + a partial one
+    t[..., :2] *= 9.0
+    t = t.half()
+    cb = codec.compact_encode(t.cuda(), bits, storage)
+    n_repr, n_oor = (int(v) for v in cb.totals.tolist())
+    V = t.numel() // 8
+    s32 = cb.scale32.cpu().numpy()
+    qo = O.quantize_heads(t.float().numpy(), s32)
+    m = O.check_representable(qo, storage)
+    assert n_repr == int(m.sum()) and n_oor == V - n_repr and 0 < n_repr < V
+    np.testing.assert_array_equal(cb.mask.cpu().numpy().astype(bool), m)
+    np.testing.assert_array_equal(cb.packed[:n_repr].cpu().numpy(), O.pack_e8(qo[m], storage))
+    bph = V // 3
+    heads = np.arange(V) // bph
+    np.testing.assert_array_equal(cb.repr_heads[:n_repr].cpu().numpy(), heads[m])
+    s16 = cb.scale16.float().cpu().numpy()
+    full = (qo * s16[heads][:, None]).astype(np.float32).astype(np.float16)
+    np.testing.assert_array_equal(cb.fallback[:n_oor].cpu().numpy(), full[~m])
+    tiles = (V + 1023) // 1024
+    want_off = np.concatenate([[0], np.cumsum(m.reshape(-1)[:tiles * 1024 - 1024].reshape(tiles - 1, 1024).sum(1))])
+    np.testing.assert_array_equal(cb.tile_off.cpu().numpy(), want_off)
+    out = codec.compact_merge(cb)
+    np.testing.assert_array_equal(out.cpu().numpy().reshape(-1, 8), full)
