@@ -44,6 +44,27 @@ inline int64_t device_cus() {
 // Executed here stage by stage in LDS, one comparator per thread.
 // ---------------------------------------------------------------------------
 
+// The table code runs on a cooperative group: a whole workgroup (one stream
+// per workgroup), or one wave (one stream per wave, wave-synchronous: no
+// workgroup barrier).  G::tid / G::size / G::sync are the group's lane, size
+// and LDS barrier.
+struct BlockGroup {
+    static __device__ __forceinline__ int tid() { return (int)threadIdx.x; }
+    static __device__ __forceinline__ int size() { return (int)blockDim.x; }
+    static __device__ __forceinline__ void sync() { __syncthreads(); }
+    static constexpr bool kWave = false;
+};
+struct WaveGroup {
+    static __device__ __forceinline__ int tid() { return (int)(threadIdx.x & 63); }
+    static __device__ __forceinline__ int size() { return 64; }
+    static __device__ __forceinline__ void sync() {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    static constexpr bool kWave = true;
+};
+
 __device__ __forceinline__ void cmpx(int64_t* k, int16_t* a, int p, int q) {
     int64_t kp = k[p], kq = k[q];
     if (kp > kq) {
@@ -61,100 +82,108 @@ __device__ __forceinline__ int pair_lane(int m, int p) {
     }
 }
 
+template <typename G>
 __device__ void reg_stage(int64_t* k, int16_t* a, int nv, int m) {
-    for (int t = threadIdx.x; t < nv * 4; t += blockDim.x) {
+    for (int t = G::tid(); t < nv * 4; t += G::size()) {
         int reg = t >> 2, i = pair_lane(m, t & 3);
         cmpx(k, a, reg * 8 + i, reg * 8 + (i ^ m));
     }
-    __syncthreads();
+    G::sync();
 }
 
 // keys k[0..n) (int64), pad = value larger than every key; result in a[0..n).
+template <typename G>
 __device__ void net_argsort(int64_t* k, int16_t* a, int n) {
     int nv = 1;
     while (nv * 8 < n) nv *= 2;
-    for (int i = threadIdx.x; i < nv * 8; i += blockDim.x) {
+    for (int i = G::tid(); i < nv * 8; i += G::size()) {
         if (i >= n) k[i] = INT64_MAX;
         a[i] = (int16_t)(i < n ? i : -1);
     }
-    __syncthreads();
+    G::sync();
     const int s8[6] = {1, 3, 1, 7, 2, 1};
-    for (int st = 0; st < 6; st++) reg_stage(k, a, nv, s8[st]);
+    for (int st = 0; st < 6; st++) reg_stage<G>(k, a, nv, s8[st]);
     for (int per = 2; per <= nv; per *= 2) {
-        for (int t = threadIdx.x; t < nv * 4; t += blockDim.x) {   // mirror compare across registers
+        for (int t = G::tid(); t < nv * 4; t += G::size()) {   // mirror compare across registers
             int grp = t / (per * 4), rem = t % (per * 4);
             int i = rem / 8, l = rem % 8, off = grp * per;
             cmpx(k, a, 8 * (off + i) + l, 8 * (off + per - 1 - i) + 7 - l);
         }
-        __syncthreads();
+        G::sync();
         for (int num = per / 2; num >= 2; num /= 2) {               // register half cleaners
-            for (int t = threadIdx.x; t < nv * 4; t += blockDim.x) {
+            for (int t = G::tid(); t < nv * 4; t += G::size()) {
                 int grp = t / (per * 4), rem = t % (per * 4);
                 int l = rem % 8, q = rem / 8;
                 int jj = q / (num / 2), i = q % (num / 2);
                 int r1 = grp * per + jj * num + i;
                 cmpx(k, a, 8 * r1 + l, 8 * (r1 + num / 2) + l);
             }
-            __syncthreads();
+            G::sync();
         }
-        reg_stage(k, a, nv, 4);
-        reg_stage(k, a, nv, 2);
-        reg_stage(k, a, nv, 1);
+        reg_stage<G>(k, a, nv, 4);
+        reg_stage<G>(k, a, nv, 2);
+        reg_stage<G>(k, a, nv, 1);
     }
 }
 
 // Stable order (key, index) for n > 256, where numpy runs a SIMD quicksort
 // whose tie order is not restated; the caller flags ties at a cut.
+template <typename G>
 __device__ void rank_argsort(const int64_t* k, int16_t* a, int n) {
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    for (int i = G::tid(); i < n; i += G::size()) {
         int64_t ki = k[i];
         int r = 0;
         for (int j = 0; j < n; j++) r += (k[j] < ki) || (k[j] == ki && j < i);
         a[r] = (int16_t)i;
     }
-    __syncthreads();
+    G::sync();
 }
 
-// Block-wide sum of v (blockDim.x multiple of 64, <= 1024).
+// Block-wide sum of v (G::size() multiple of 64, <= 1024).
+template <typename G>
 __device__ int64_t block_sum(int64_t v) {
-    __shared__ int64_t part[16];
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
-    __syncthreads();
+    if constexpr (G::kWave) return v;
+    __shared__ int64_t part[16];
+    G::sync();
+    if ((G::tid() & 63) == 0) part[G::tid() >> 6] = v;
+    G::sync();
     int64_t s = 0;
-    for (int w = 0; w < (int)(blockDim.x >> 6); w++) s += part[w];
+    for (int w = 0; w < (int)(G::size() >> 6); w++) s += part[w];
     return s;
 }
 
-// Block-wide maximum of v (blockDim.x multiple of 64, <= 1024).
+// Block-wide maximum of v (G::size() multiple of 64, <= 1024).
+template <typename G>
 __device__ int64_t block_max(int64_t v) {
-    __shared__ int64_t part[16];
     for (int o = 32; o > 0; o >>= 1) {
         const int64_t u = __shfl_xor(v, o, 64);
         v = u > v ? u : v;
     }
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
-    __syncthreads();
+    if constexpr (G::kWave) return v;
+    __shared__ int64_t part[16];
+    G::sync();
+    if ((G::tid() & 63) == 0) part[G::tid() >> 6] = v;
+    G::sync();
     int64_t m = part[0];
-    for (int w = 1; w < (int)(blockDim.x >> 6); w++) m = part[w] > m ? part[w] : m;
+    for (int w = 1; w < (int)(G::size() >> 6); w++) m = part[w] > m ? part[w] : m;
     return m;
 }
 
 // Bitonic sort of c[0 .. N) ascending (N a power of two, c padded with
 // UINT64_MAX past the live entries).
+template <typename G>
 __device__ void bitonic_sort_u64(uint64_t* c, int N) {
     for (int k = 2; k <= N; k <<= 1) {
         for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int t = threadIdx.x; t < N / 2; t += blockDim.x) {
+            for (int t = G::tid(); t < N / 2; t += G::size()) {
                 const int i = 2 * t - (t & (j - 1));   // low index of the pair: bit j clear
                 const int l = i + j;
                 const bool up = (i & k) == 0;
                 const uint64_t x = c[i], y = c[l];
                 if ((x > y) == up) { c[i] = y; c[l] = x; }
             }
-            __syncthreads();
+            G::sync();
         }
     }
 }
@@ -163,27 +192,28 @@ __device__ void bitonic_sort_u64(uint64_t* c, int N) {
 // (the order the tie flag stands for) from one bitonic sort of composite keys
 // instead of per-entry rank counts.  At most one tie group straddles the cut
 // at sorted position rem: the one holding positions rem - 1 and rem.
+template <typename G>
 __device__ void adjust_pass_sorted(int n, int32_t* freqs, int diff, int full, int rem, const int64_t* kk, int16_t* a,
                                    int8_t* inset, uint64_t* sk, int* st) {
     int N = 512;
     while (N < n) N <<= 1;
-    for (int i = threadIdx.x; i < N; i += blockDim.x)   // kk in [-(2^32 - 1), 0]: biased key in 33 bits
+    for (int i = G::tid(); i < N; i += G::size())   // kk in [-(2^32 - 1), 0]: biased key in 33 bits
         sk[i] = i < n ? (((uint64_t)(kk[i] + (int64_t)4294967296LL)) << 11) | (uint64_t)i : ~0ull;
-    __syncthreads();
-    bitonic_sort_u64(sk, N);
-    for (int p = threadIdx.x; p < n; p += blockDim.x) {
+    G::sync();
+    bitonic_sort_u64<G>(sk, N);
+    for (int p = G::tid(); p < n; p += G::size()) {
         const int i = (int)(sk[p] & 2047u);
         a[p] = (int16_t)i;
         inset[i] = p < rem ? 1 : 0;
     }
-    __syncthreads();
+    G::sync();
     int matters = 0;
     if (rem > 0 && rem < n && (sk[rem - 1] >> 11) == (sk[rem] >> 11)) {   // uniform
         const uint64_t kstar = sk[rem] >> 11;
-        for (int p = threadIdx.x; p < n; p += blockDim.x)
+        for (int p = G::tid(); p < n; p += G::size())
             if ((sk[p] >> 11) == kstar && (diff > 0 || freqs[a[p]] - full > 1)) matters = 1;
     }
-    if (block_sum(matters) != 0 && threadIdx.x == 0) *st |= LQ_ST_TIE_UNPINNED;
+    if (block_sum<G>(matters) != 0 && G::tid() == 0) *st |= LQ_ST_TIE_UNPINNED;
 }
 
 // One pass of the build_rans_table adjustment loop (core/gpu_ans.py:73-84)
@@ -193,24 +223,25 @@ __device__ void adjust_pass_sorted(int n, int32_t* freqs, int diff, int full, in
 // max(f - visits, 1).  The argsort tie order only matters for the tie group
 // straddling position rem, and only if a different subset of that group would
 // change a frequency; the numpy network runs only then.
+template <typename G>
 __device__ void adjust_pass(const int64_t* counts, int n, int32_t* freqs, int diff, int64_t* k, int16_t* a,
                             int64_t* kk, int8_t* inset, int* st, uint64_t* sk) {
     const int m = diff > 0 ? diff : -diff;
     const int full = m / n, rem = m % n;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) kk[i] = diff > 0 ? -counts[i] : -(int64_t)freqs[i];
-    __syncthreads();
+    for (int i = G::tid(); i < n; i += G::size()) kk[i] = diff > 0 ? -counts[i] : -(int64_t)freqs[i];
+    G::sync();
     if (n > 256 && sk) {
-        adjust_pass_sorted(n, freqs, diff, full, rem, kk, a, inset, sk, st);
-        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        adjust_pass_sorted<G>(n, freqs, diff, full, rem, kk, a, inset, sk, st);
+        for (int i = G::tid(); i < n; i += G::size()) {
             const int v = full + (inset[i] == 1 ? 1 : 0);
             const int f = freqs[i];
             freqs[i] = diff > 0 ? f + v : (f - v > 1 ? f - v : 1);
         }
-        __syncthreads();
+        G::sync();
         return;
     }
     int matters = 0;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    for (int i = G::tid(); i < n; i += G::size()) {
         const int64_t ki = kk[i];
         int lt = 0, eq = 0;
         for (int j = 0; j < n; j++) { lt += kk[j] < ki; eq += kk[j] == ki; }
@@ -218,24 +249,24 @@ __device__ void adjust_pass(const int64_t* counts, int n, int32_t* freqs, int di
         inset[i] = in;
         if (in == 2 && (diff > 0 || freqs[i] - full > 1)) matters = 1;
     }
-    if (block_sum(matters) != 0) {
-        for (int i = threadIdx.x; i < n; i += blockDim.x) k[i] = kk[i];
-        __syncthreads();
+    if (block_sum<G>(matters) != 0) {
+        for (int i = G::tid(); i < n; i += G::size()) k[i] = kk[i];
+        G::sync();
         if (n <= 256) {
-            net_argsort(k, a, n);
+            net_argsort<G>(k, a, n);
         } else {   // numpy's quicksort tie order is not restated for n > 256
-            rank_argsort(kk, a, n);
-            if (threadIdx.x == 0) *st |= LQ_ST_TIE_UNPINNED;
+            rank_argsort<G>(kk, a, n);
+            if (G::tid() == 0) *st |= LQ_ST_TIE_UNPINNED;
         }
-        for (int p = threadIdx.x; p < n; p += blockDim.x) inset[a[p]] = p < rem ? 1 : 0;
-        __syncthreads();
+        for (int p = G::tid(); p < n; p += G::size()) inset[a[p]] = p < rem ? 1 : 0;
+        G::sync();
     }
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    for (int i = G::tid(); i < n; i += G::size()) {
         const int v = full + (inset[i] == 1 ? 1 : 0);
         const int f = freqs[i];
         freqs[i] = diff > 0 ? f + v : (f - v > 1 ? f - v : 1);
     }
-    __syncthreads();
+    G::sync();
 }
 
 // build_rans_table normalisation (core/gpu_ans.py:62-86) on LDS arrays:
@@ -251,13 +282,14 @@ __device__ void adjust_pass(const int64_t* counts, int n, int32_t* freqs, int di
 // G_t = #{f_i - t > 1} and C(t) = G_0 + .. + G_(t-1) = sum_i min(t, f_i - 1)
 // is nondecreasing: a binary search over t in [0, max f - 1], not one pass
 // per t (a single dominant symbol makes t as large as the excess).
+template <typename G>
 __device__ void normalise(const int64_t* counts, int n, int32_t* freqs, int64_t* k, int16_t* a, int64_t* kk,
                           int8_t* inset, int* st, uint64_t* sk = nullptr) {
     int64_t tl = 0;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) tl += counts[i];
-    const int64_t total = block_sum(tl);
+    for (int i = G::tid(); i < n; i += G::size()) tl += counts[i];
+    const int64_t total = block_sum<G>(tl);
     int64_t fl = 0;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    for (int i = G::tid(); i < n; i += G::size()) {
         int32_t f = 1;
         if (total != 0) {
             double q = (double)counts[i] / (double)total * (double)kL;   // (counts / total * L)
@@ -267,21 +299,21 @@ __device__ void normalise(const int64_t* counts, int n, int32_t* freqs, int64_t*
         freqs[i] = f;
         fl += f;
     }
-    const int diff = (int)(kL - block_sum(fl));
+    const int diff = (int)(kL - block_sum<G>(fl));
     if (diff > 0) {
-        adjust_pass(counts, n, freqs, diff, k, a, kk, inset, st, sk);
+        adjust_pass<G>(counts, n, freqs, diff, k, a, kk, inset, st, sk);
     } else if (diff < 0) {
         const int excess0 = -diff;
         int64_t fm = 0;
-        for (int i = threadIdx.x; i < n; i += blockDim.x) fm = freqs[i] > fm ? freqs[i] : fm;
-        const int fmax = (int)block_max(fm);
+        for (int i = G::tid(); i < n; i += G::size()) fm = freqs[i] > fm ? freqs[i] : fm;
+        const int fmax = (int)block_max<G>(fm);
         auto C = [&](int tt) {   // passes 0 .. tt-1 decrement sum_i min(tt, f_i - 1) entries in total
             int64_t c = 0;
-            for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            for (int i = G::tid(); i < n; i += G::size()) {
                 const int r = freqs[i] - 1;
                 c += r < tt ? r : tt;
             }
-            return block_sum(c);
+            return block_sum<G>(c);
         };
         int lo = 0, hi = fmax - 1 > 0 ? fmax - 1 : 0;   // t = fmax - 1 has G_t = 0
         while (lo < hi) {   // least t in [0, hi) with C(t + 1) > excess, else hi
@@ -290,44 +322,60 @@ __device__ void normalise(const int64_t* counts, int n, int32_t* freqs, int64_t*
         }
         const int t = lo;
         const int excess = (int)(excess0 - C(t));
-        for (int i = threadIdx.x; i < n; i += blockDim.x) freqs[i] = freqs[i] - t > 1 ? freqs[i] - t : 1;
-        __syncthreads();
-        if (excess > 0) adjust_pass(counts, n, freqs, -excess, k, a, kk, inset, st, sk);
+        for (int i = G::tid(); i < n; i += G::size()) freqs[i] = freqs[i] - t > 1 ? freqs[i] - t : 1;
+        G::sync();
+        if (excess > 0) adjust_pass<G>(counts, n, freqs, -excess, k, a, kk, inset, st, sk);
     }
 }
 
-// Inclusive scan of v over the block (blockDim.x <= 1024, multiple of 64).
+// Inclusive scan of v over the block (G::size() <= 1024, multiple of 64).
+template <typename G>
 __device__ int block_incl_scan(int v) {
-    __shared__ int wsum[16];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = G::tid() & 63, w = G::tid() >> 6;
     for (int o = 1; o < 64; o <<= 1) {
         int t = __shfl_up(v, o, 64);
         if (lane >= o) v += t;
     }
-    __syncthreads();
+    if constexpr (G::kWave) return v;
+    __shared__ int wsum[16];
+    G::sync();
     if (lane == 63) wsum[w] = v;
-    __syncthreads();
+    G::sync();
     for (int i = 0; i < w; i++) v += wsum[i];
     return v;
 }
 
 // out[i] = in[0] + .. + in[i-1] for i <= n (block-cooperative, any n).
+template <typename G>
 __device__ void exclusive_scan_array(const int32_t* in, int n, int32_t* out) {
+    if constexpr (G::kWave) {   // the carry stays in registers (uniform over the wave)
+        int carry = 0;
+        for (int b = 0; b < n; b += 64) {
+            const int i = b + G::tid();
+            const int v = i < n ? in[i] : 0;
+            const int incl = block_incl_scan<G>(v);
+            if (i < n) out[i] = carry + incl - v;
+            carry += __shfl(incl, 63, 64);
+        }
+        if (G::tid() == 0) out[n] = carry;
+        G::sync();
+        return;
+    }
     __shared__ int carry;
-    if (threadIdx.x == 0) carry = 0;
-    __syncthreads();
-    for (int b = 0; b < n; b += blockDim.x) {
-        int i = b + threadIdx.x;
+    if (G::tid() == 0) carry = 0;
+    G::sync();
+    for (int b = 0; b < n; b += G::size()) {
+        int i = b + G::tid();
         int v = i < n ? in[i] : 0;
-        int incl = block_incl_scan(v);
+        int incl = block_incl_scan<G>(v);
         int c = carry;
         if (i < n) out[i] = c + incl - v;
-        __syncthreads();
-        if (threadIdx.x == blockDim.x - 1) carry = c + incl;
-        __syncthreads();
+        G::sync();
+        if (G::tid() == G::size() - 1) carry = c + incl;
+        G::sync();
     }
-    if (threadIdx.x == 0) out[n] = carry;
-    __syncthreads();
+    if (G::tid() == 0) out[n] = carry;
+    G::sync();
 }
 
 // ------------------------------------------------------------ chunk tables --
@@ -394,9 +442,9 @@ __global__ __launch_bounds__(256) void k_chunk_tables(const uint32_t* __restrict
     __shared__ int64_t kk[LQ_MAXSYM];
     __shared__ int8_t inset[LQ_MAXSYM];
     __shared__ uint64_t sk[WIDE ? 2048 : 1];   // wide alphabets: composite sort keys
-    normalise(counts, n, freqs, keys, perm, kk, inset, &s_st, WIDE ? sk : nullptr);
+    normalise<BlockGroup>(counts, n, freqs, keys, perm, kk, inset, &s_st, WIDE ? sk : nullptr);
     __shared__ int32_t cum[LQ_MAXSYM + 1];
-    exclusive_scan_array(freqs, n, cum);
+    exclusive_scan_array<BlockGroup>(freqs, n, cum);
     for (int i = tid; i < n; i += 256) T->enc[i] = enc_pack((uint32_t)freqs[i], (uint32_t)cum[i]);
     if (tid == 0) {
         T->lo = lo;
@@ -404,6 +452,72 @@ __global__ __launch_bounds__(256) void k_chunk_tables(const uint32_t* __restrict
         T->n_symbols = (int32_t)s_tot;
         T->status = s_st;
         if (s_st) atomicOr(status + sid / LQ_STREAMS, s_st);
+    }
+}
+
+// int8 path: one wave per stream, kTabWaves streams per workgroup; the
+// stream's table built wave-synchronously (WaveGroup) in its own LDS arrays,
+// with the same normalisation and tie order as k_chunk_tables<false>.
+constexpr int kTabWaves = 4;
+constexpr int kCap8 = 264;   // range(min - 2, max + 2) of int8 values: at most 260 symbols
+
+__global__ __launch_bounds__(64 * kTabWaves) void k_chunk_tables_wave(const uint32_t* __restrict__ hist,
+                                                                      int64_t n_streams, lq_table* __restrict__ tables,
+                                                                      int32_t* __restrict__ status) {
+    __shared__ int64_t counts[kTabWaves][kCap8];
+    __shared__ int32_t freqs[kTabWaves][kCap8];
+    __shared__ int64_t keys[kTabWaves][256];
+    __shared__ int16_t perm[kTabWaves][kCap8];
+    __shared__ int64_t kk[kTabWaves][kCap8];
+    __shared__ int8_t inset[kTabWaves][kCap8];
+    __shared__ int32_t cum[kTabWaves][kCap8 + 1];
+    __shared__ int s_st[kTabWaves];
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = (int)(threadIdx.x & 63);
+    const int64_t sid = (int64_t)blockIdx.x * kTabWaves + w;
+    if (sid >= n_streams) return;   // wave-uniform; no workgroup barrier below
+    lq_table* T = tables + sid;
+    const uint32_t* hs = hist + sid * 256;
+    uint32_t hv[4];
+    int mn = 256, mx = -1;
+    uint32_t tl = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int b = lane + 64 * j;
+        hv[j] = hs[b];
+        if (hv[j]) {
+            mn = b < mn ? b : mn;
+            mx = b > mx ? b : mx;
+            tl += hv[j];
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const int a = __shfl_xor(mn, o, 64), c = __shfl_xor(mx, o, 64);
+        mn = a < mn ? a : mn;
+        mx = c > mx ? c : mx;
+        tl += __shfl_xor(tl, o, 64);
+    }
+    if (mx < 0) {   // absent stream (empty coset)
+        if (lane == 0) { T->lo = 0; T->n_sym = 0; T->n_symbols = 0; T->status = 0; }
+        return;
+    }
+    const int lo = mn - 128 - 2, n = mx - mn + 5;
+    for (int i = lane; i < n; i += 64) {
+        const int b = lo + i + 128;
+        counts[w][i] = (b >= 0 && b < 256) ? (int64_t)hs[b] : 0;
+    }
+    if (lane == 0) s_st[w] = 0;
+    WaveGroup::sync();
+    normalise<WaveGroup>(counts[w], n, freqs[w], keys[w], perm[w], kk[w], inset[w], &s_st[w]);
+    exclusive_scan_array<WaveGroup>(freqs[w], n, cum[w]);
+    for (int i = lane; i < n; i += 64) T->enc[i] = enc_pack((uint32_t)freqs[w][i], (uint32_t)cum[w][i]);
+    if (lane == 0) {
+        const int st = s_st[w];
+        T->lo = lo;
+        T->n_sym = n;
+        T->n_symbols = (int32_t)tl;
+        T->status = st;
+        if (st) atomicOr(status + sid / LQ_STREAMS, st);
     }
 }
 
@@ -432,30 +546,31 @@ __device__ __forceinline__ Col<SymT> column(const SymT* sym, const uint32_t* blk
     return col;
 }
 
-// Encoder table entry: f | nb << 11 | base << 15 with nb = 11 - bitlen(f) and
-// base = L + cum - f, so a step is  k = nb - 1 + (x >= f << nb);  x = (x >> k) + base.
+// Encoder table entry: thr | (nb - 1) << 16 | base << 20 with nb = 11 - bitlen(f),
+// thr = f << nb (in [L, 2L): the renormalisation threshold) and
+// base = L + cum - f, so a step is  k = nb - 1 + (x >= thr);  x = (x >> k) + base.
+// thr fills the low half-word on its own, so the comparison reads it in place.
 __device__ __forceinline__ uint32_t encx_of(uint32_t e) {
     uint32_t f = enc_f(e), c = enc_c(e), nb = enc_nb(e);
-    return f | (nb << 11) | (((uint32_t)kL + c - f) << 15);
+    return (f << nb) | ((nb - 1u) << 16) | (((uint32_t)kL + c - f) << 20);
 }
 __device__ __forceinline__ uint32_t encx_step(uint32_t x, uint32_t e, uint32_t* k_out) {
-    uint32_t f = e & 0x7ffu, nb = (e >> 11) & 0xfu, base = e >> 15;
-    uint32_t k = nb - 1u + (x >= (f << nb) ? 1u : 0u);
+    const uint32_t k = ((e >> 16) & 0xfu) + (x >= (e & 0xffffu) ? 1u : 0u);
     *k_out = k;
-    return (x >> k) + base;
+    return (x >> k) + (e >> 20);
 }
 
 // Interval step: every state in [lo, hi] encodes the symbol; the image is
 // exact when the interval lies on one side of the renormalisation threshold,
 // otherwise the whole image range of the symbol.
 __device__ __forceinline__ void hull_step(uint32_t& lo, uint32_t& hi, uint32_t e) {
-    uint32_t f = e & 0x7ffu, nb = (e >> 11) & 0xfu, base = e >> 15;
-    uint32_t thr = f << nb;
+    const uint32_t thr = e & 0xffffu, nbm1 = (e >> 16) & 0xfu, base = e >> 20;
     if (hi < thr || lo >= thr) {
-        uint32_t k = nb - 1u + (lo >= thr ? 1u : 0u);
+        uint32_t k = nbm1 + (lo >= thr ? 1u : 0u);
         lo = (lo >> k) + base;
         hi = (hi >> k) + base;
     } else {
+        const uint32_t f = thr >> (nbm1 + 1u);
         lo = f + base;
         hi = 2u * f - 1u + base;
     }
@@ -530,7 +645,8 @@ struct EncWork {  // offsets into the encode workspace
 };
 
 // Streams longer than kScanTile blocks are scanned in tiles (k_scan_tiles /
-// k_scan_top / k_scan_apply); shorter ones by one workgroup each (k_chunk_scan).
+// k_scan_top / k_scan_apply, then k_chunk_offsets); shorter ones by one
+// workgroup per chunk (k_chunk_scan_offsets).
 constexpr int kScanTile = 4096;
 
 __host__ __device__ inline EncWork enc_layout(int64_t n_chunks, int64_t n_vectors) {
@@ -585,7 +701,7 @@ __global__ __launch_bounds__(256) void k_chunk_encode(const SymT* __restrict__ s
 
     // ---- state entering block g (encode order runs from the stream end down)
     uint32_t x = kL;
-    int window = 24;
+    int window = 16;   // symbols after the block; the interval collapses within 16 on typical tables
     for (;;) {
         // top of the window: `window` symbols after block g, or the stream end
         int64_t h = g + 1;
@@ -674,36 +790,64 @@ __global__ __launch_bounds__(256) void k_chunk_encode(const SymT* __restrict__ s
     blk_state[task] = (uint16_t)x;
 }
 
-// per (chunk, stream): exclusive prefix of block bit counts, n_bits, final state
-__global__ __launch_bounds__(256) void k_chunk_scan(const uint32_t* __restrict__ blk_bits, const uint16_t* __restrict__ blk_state,
-                                                    const lq_table* __restrict__ tables, int64_t nblk,
-                                                    uint32_t* __restrict__ blk_off, int64_t* __restrict__ stream_nbits,
-                                                    int32_t* __restrict__ stream_state) {
-    __shared__ uint64_t part[256];
-    const int64_t sid = blockIdx.x;
-    const int tid = threadIdx.x;
-    const int64_t per = (nblk + 255) / 256;
-    const int64_t b0 = tid * per, b1 = b0 + per < nblk ? b0 + per : nblk;
+// Short streams (nblk <= kScanTile), one workgroup per chunk, wave w = stream
+// w: exclusive prefix of the block bit counts (64 blocks per round, a wave
+// scan plus the running carry), n_bits and final state; then the chunk's word
+// offsets (n_words + 1 words per present stream) and total.  Replaces
+// k_chunk_scan + k_chunk_offsets for such batches.
+constexpr int kScanRounds = 16;   // rounds of 64 blocks whose loads are in flight together
+
+__global__ __launch_bounds__(1024) void k_chunk_scan_offsets(const uint32_t* __restrict__ blk_bits,
+                                                             const uint16_t* __restrict__ blk_state,
+                                                             const lq_table* __restrict__ tables, int64_t nblk,
+                                                             uint32_t* __restrict__ blk_off,
+                                                             int64_t* __restrict__ stream_nbits,
+                                                             int32_t* __restrict__ stream_state,
+                                                             int64_t* __restrict__ stream_woff,
+                                                             int64_t* __restrict__ chunk_words) {
+    __shared__ int64_t s_nbits[LQ_STREAMS];
+    __shared__ int s_present[LQ_STREAMS];
+    const int64_t c = blockIdx.x;
+    const int lane = threadIdx.x & 63, st = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t sid = c * LQ_STREAMS + st;
     const uint32_t* bb = blk_bits + sid * nblk;
-    uint64_t s = 0;
-    for (int64_t b = b0; b < b1; b++) s += bb[b];
-    part[tid] = s;
-    __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {   // inclusive Hillis-Steele scan
-        uint64_t v = tid >= off ? part[tid - off] : 0;
-        __syncthreads();
-        part[tid] += v;
-        __syncthreads();
+    uint32_t* bo = blk_off + sid * nblk;
+    uint64_t carry = 0;
+    for (int64_t r0 = 0; r0 < nblk; r0 += 64 * kScanRounds) {
+        uint32_t v[kScanRounds];
+#pragma unroll
+        for (int k = 0; k < kScanRounds; k++) {
+            const int64_t b = r0 + 64 * k + lane;
+            v[k] = b < nblk ? bb[b] : 0u;
+        }
+#pragma unroll
+        for (int k = 0; k < kScanRounds; k++) {
+            uint32_t x = v[k];   // inclusive wave scan (counts < 2^13, sums < 2^19)
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t y = __shfl_up(x, o, 64);
+                x += lane >= o ? y : 0u;
+            }
+            const int64_t b = r0 + 64 * k + lane;
+            if (b < nblk) bo[b] = (uint32_t)(carry + x - v[k]);
+            carry += (uint32_t)__shfl(x, 63, 64);
+        }
     }
-    uint64_t run = tid ? part[tid - 1] : 0;
-    for (int64_t b = b0; b < b1; b++) {
-        blk_off[sid * nblk + b] = (uint32_t)run;
-        run += bb[b];
-    }
-    if (tid == 255) {
-        bool present = tables[sid].n_sym > 0;
-        stream_nbits[sid] = present ? (int64_t)part[255] : 0;
+    if (lane == 0) {
+        const bool present = tables[sid].n_sym > 0;
+        s_present[st] = present ? 1 : 0;
+        s_nbits[st] = present ? (int64_t)carry : 0;
+        stream_nbits[sid] = present ? (int64_t)carry : 0;
         stream_state[sid] = present ? (int32_t)blk_state[sid * nblk] : 0;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int64_t w = 0;
+        for (int k = 0; k < LQ_STREAMS; k++) {
+            stream_woff[c * LQ_STREAMS + k] = w;
+            if (s_present[k]) w += (s_nbits[k] + 31) / 32 + 1;
+        }
+        chunk_words[c] = w;
     }
 }
 
@@ -959,7 +1103,7 @@ __global__ __launch_bounds__(256) void k_chunk_lut(const lq_table* __restrict__ 
     if (n == 0) return;
     for (int i = threadIdx.x; i < n; i += 256) fr[i] = (int32_t)enc_f(T->enc[i]);
     __syncthreads();
-    exclusive_scan_array(fr, n, cum);
+    exclusive_scan_array<BlockGroup>(fr, n, cum);
     const int st = (int)(sid % LQ_STREAMS);
     const uint32_t row = (uint32_t)st & (mode ? 15u : 7u);
     uint32_t bias = 0;
@@ -1265,9 +1409,9 @@ __global__ __launch_bounds__(256) void k_build_tables(const int64_t* __restrict_
     __syncthreads();
     __shared__ int64_t kk[kL];
     __shared__ int8_t inset[kL];
-    normalise(cnt, n, fr, keys, perm, kk, inset, &s_st);
+    normalise<BlockGroup>(cnt, n, fr, keys, perm, kk, inset, &s_st);
     __shared__ int32_t cum[kL + 1];
-    exclusive_scan_array(fr, n, cum);
+    exclusive_scan_array<BlockGroup>(fr, n, cum);
     for (int i = threadIdx.x; i < n; i += 256) freqs_out[o + i] = fr[i];
     for (int i = threadIdx.x; i <= n; i += 256) cum_out[o + t + i] = cum[i];
     for (int slot = threadIdx.x; slot < kL; slot += 256) {   // largest s with cum[s] <= slot
@@ -1395,12 +1539,13 @@ int encode_launch(const SymT* d_sym, const uint32_t* d_blk_n1, int64_t n_chunks,
         hipLaunchKernelGGL(k_scan_top, dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, tsum, tiles, d_blk_state,
                            nblk, d_tables, d_stream_nbits, d_stream_state);
         hipLaunchKernelGGL(k_scan_apply, tg, dim3(256), 0, s, bits, nblk, tiles, tsum, d_blk_off);
+        hipLaunchKernelGGL(k_chunk_offsets, dim3((unsigned)((n_chunks + 63) / 64)), dim3(64), 0, s, d_stream_nbits,
+                           d_tables, n_chunks, d_stream_woff, d_chunk_words);
     } else {
-        hipLaunchKernelGGL(k_chunk_scan, dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, bits, d_blk_state,
-                           d_tables, nblk, d_blk_off, d_stream_nbits, d_stream_state);
+        hipLaunchKernelGGL(k_chunk_scan_offsets, dim3((unsigned)n_chunks), dim3(64 * LQ_STREAMS), 0, s, bits,
+                           d_blk_state, d_tables, nblk, d_blk_off, d_stream_nbits, d_stream_state, d_stream_woff,
+                           d_chunk_words);
     }
-    hipLaunchKernelGGL(k_chunk_offsets, dim3((unsigned)((n_chunks + 63) / 64)), dim3(64), 0, s, d_stream_nbits, d_tables,
-                       n_chunks, d_stream_woff, d_chunk_words);
     return launch_status();
 }
 
@@ -1410,8 +1555,9 @@ extern "C" {
 
 int lq_chunk_tables(const uint32_t* d_hist, int64_t n_chunks, lq_table* d_tables, int32_t* d_status, hipStream_t s) {
     if (n_chunks <= 0) return LQ_ERR_ARG;
-    hipLaunchKernelGGL((k_chunk_tables<false>), dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, d_hist, nullptr,
-                       d_tables, d_status);
+    const int64_t ns = n_chunks * LQ_STREAMS;
+    hipLaunchKernelGGL(k_chunk_tables_wave, dim3((unsigned)((ns + kTabWaves - 1) / kTabWaves)), dim3(64 * kTabWaves), 0,
+                       s, d_hist, ns, d_tables, d_status);
     return launch_status();
 }
 
