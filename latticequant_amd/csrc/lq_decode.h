@@ -18,9 +18,9 @@
 namespace lq {
 
 // LUT entry of one (stream, slot):
-//   [5:0]   63 - k: its low 5 bits are 31 - k (the shift that leaves the top
-//           k buffer bits in place) and its 6-bit complement is k itself
-//           (renormalisation bits, 0..10), so one field serves both
+//   [3:0]   k, the renormalisation bits of the step (0..10)
+//   [5:4]   zero, so that a 6-bit shift count or a 5-bit field width read
+//           from the entry is k itself
 //   [15:6]  symbol index (alphabet value - lo, < 1024)
 //   [17:16] zero
 //   [31:18] row * L + (x' << k) - L: the next slot before the k new bits are
@@ -30,59 +30,43 @@ __host__ __device__ inline uint32_t lut_entry(uint32_t sym, uint32_t xp, uint32_
     uint32_t k = 0;
     while ((xp << k) < (uint32_t)LQ_L) k++;
     const uint32_t next = row * (uint32_t)LQ_L + (xp << k) - (uint32_t)LQ_L;
-    return (63u - k) | (sym << 6) | (next << 18);
+    return k | (sym << 6) | (next << 18);
 }
 
 __device__ __forceinline__ uint32_t lut_sym(uint32_t e) { return (e >> 6) & 1023u; }
-__device__ __forceinline__ uint32_t lut_k(uint32_t e) { return ~e & 63u; }
 __device__ __forceinline__ uint32_t lut_next(uint32_t e) { return e >> 18; }
 
-// One lane's decoder of one stream from a checkpoint.
-//
-// buf holds the next unread stream bits, most significant first (words are
-// bit-reversed on the way in), nbuf of them valid; pre is the next word.
-// Loads never go past word (p >> 5) + 2 of the stream, p the first unread
-// bit, so a stream needs two readable words after its n_words + 1.
-struct StreamDec {
-    const uint32_t* wp;   // next word to fetch into pre
+// A lane's bit buffer: the next unread stream bits, most significant first
+// (words are bit-reversed on the way in), then a single 1 bit (the sentinel),
+// then zeros.  The sentinel stands in for a count of valid bits: fewer than
+// 32 bits are valid exactly when the low word is zero, and push() finds the
+// free space below the valid bits from its position.
+struct BitBuf {
     uint64_t buf;
-    uint32_t nbuf, pre, e;
 
-    // Start at stream bit `bit_off` with state `state` (in [L, 2L)); `lut` is
-    // the LDS LUT block, `row` this stream's row in it.
-    __device__ __forceinline__ void init(const uint32_t* stream_words, uint32_t bit_off, uint32_t state,
-                                         const uint32_t* lut, int row) {
-        const uint32_t* w = stream_words + (bit_off >> 5);
-        buf = ((uint64_t)__builtin_bitreverse32(w[0]) << 32) << (bit_off & 31u);
-        nbuf = 32u - (bit_off & 31u);
-        pre = w[1];
-        wp = w + 2;
-        refill();
-        e = lut[row * kL + (int)state - kL];
+    // Start at bit `off` (0..31) of word w: 32 - off valid bits.
+    __device__ __forceinline__ void init(uint32_t w, uint32_t off) {
+        buf = (((uint64_t)__builtin_bitreverse32(w) << 32) | 0x80000000u) << (off & 31u);
     }
-
-    // Make at least 32 bits available (three steps' worth).
-    __device__ __forceinline__ void refill() {
-        if (nbuf < 32u) {
-            buf |= (uint64_t)__builtin_bitreverse32(pre) << (32u - nbuf);
-            nbuf += 32u;
-            pre = *wp++;
-        }
+    __device__ __forceinline__ bool low() const { return (uint32_t)buf == 0u; }
+    // Append the 32 bits of word w below the valid ones; needs low().
+    __device__ __forceinline__ void push(uint32_t w) {
+        const uint32_t hi = (uint32_t)(buf >> 32);
+        const uint32_t t = (uint32_t)__builtin_ctz(hi);   // sentinel bit of hi (hi != 0 when low())
+        const uint64_t y = (((uint64_t)__builtin_bitreverse32(w) << 32) | 0x80000000u) >> (31u - t);
+        // high word: (hi & (hi - 1)) | y_hi, i.e. the old sentinel cleared
+        // (bitop3 truth table 0xEA: (S0 & S1) | S2)
+        const uint32_t nhi = __builtin_amdgcn_bitop3_b32(hi, hi - 1u, (uint32_t)(y >> 32), 0xEA);
+        buf = ((uint64_t)nhi << 32) | (uint32_t)y;
     }
-
-    // Symbol index of the current symbol.
-    __device__ __forceinline__ uint32_t sym() const { return lut_sym(e); }
-
-    // Move to the next symbol: take the current symbol's k renormalisation
-    // bits and look up the next slot.  Needs nbuf >= k (refill() every three
-    // steps guarantees it).
-    __device__ __forceinline__ void step(const uint32_t* lut) {
-        const uint32_t bits = (uint32_t)(buf >> 33) >> (e & 31u);
-        const uint32_t k = lut_k(e);
-        const uint32_t slot = lut_next(e) + bits;
-        buf <<= k;
-        nbuf -= k;
-        e = lut[slot];
+    // Take the k bits of LUT entry e (at least k bits valid): their value,
+    // first bit most significant.  They are the bits that a 64-bit shift by
+    // k moves out of the high word (k = 0 moves none), so the value is one
+    // shift of the high word, zero-extended, read directly by the entry.
+    __device__ __forceinline__ uint32_t take(uint32_t e) {
+        const uint32_t bits = (uint32_t)(((uint64_t)(uint32_t)(buf >> 32) << (e & 63u)) >> 32);
+        buf <<= (e & 63u);
+        return bits;
     }
 };
 
@@ -114,8 +98,8 @@ struct PhaseLane {
     uint32_t* rcol;         // this lane's ring column
     int glim;               // first word (group index * 4, from gs) of the last readable group
     int ld, rd;             // next word (from gs) to load into the ring / to move into pre
-    uint64_t buf;
-    uint32_t nbuf, pre, e;
+    BitBuf bb;
+    uint32_t pre, e;
     uint4 q;
     bool inflight;
     const uint32_t* bmr;    // the block's coset bitmap row (kBlk / 32 + 1 words, last one zero)
@@ -150,8 +134,7 @@ struct PhaseLane {
         land(8, g2);
         ld = 12;
         rd = o + 2;
-        buf = ((uint64_t)__builtin_bitreverse32(rcol[o * LANES]) << 32) << (bit_off & 31u);
-        nbuf = 32u - (bit_off & 31u);
+        bb.init(rcol[o * LANES], bit_off);
         pre = rcol[(o + 1) * LANES];
         refill();
         e = lut[row * kL + (int)state - kL];
@@ -163,9 +146,8 @@ struct PhaseLane {
     }
 
     __device__ __forceinline__ void refill() {
-        if (nbuf < 32u) {
-            buf |= (uint64_t)__builtin_bitreverse32(pre) << (32u - nbuf);
-            nbuf += 32u;
+        if (bb.low()) {
+            bb.push(pre);
             pre = rcol[(rd & (kRing - 1)) * LANES];
             rd++;
         }
@@ -203,11 +185,7 @@ struct PhaseLane {
         }
         const int vl = (wi << 5) | __builtin_ctz(wv);
         wv &= wv - 1u;
-        const uint32_t bits = (uint32_t)(buf >> 33) >> (e & 31u);
-        const uint32_t k = lut_k(e);
-        const uint32_t addr = (lut_next(e) + bits) << 2;
-        buf <<= k;
-        nbuf -= k;
+        const uint32_t addr = (lut_next(e) + bb.take(e)) << 2;
         e = *reinterpret_cast<const uint32_t*>(lutb + addr);
         return vl;
     }
@@ -255,23 +233,25 @@ struct PhaseLane {
 // word), and every phase starts with at least 3 unread words.
 constexpr int kLineRing = 12;
 
+// A 32-bit LDS word pointer: arithmetic and compares on it stay 32-bit.
+typedef __attribute__((address_space(3))) uint32_t lds_u32;
+
 struct LineLane {
     const uint32_t* gs;     // the 16-byte aligned group holding the block's first word
-    uint32_t* rcol;         // this lane's ring column (slot stride 64 words)
+    lds_u32* rcol;          // this lane's ring column (slot stride 64 words)
     int glim;               // first word (from gs) of the last readable group
     int ld;                 // next word (from gs) to load into the ring (multiple of 4)
-    int rs;                 // ring slot of the next word to move into pre
-    int ls;                 // ring slot of the next landed group (0, 4 or 8)
-    uint64_t buf;
-    uint32_t nbuf, pre, e;
+    const lds_u32* rq;      // ring word to move into pre next
+    lds_u32* lp;            // first ring word of the group the next top-up lands in
+    BitBuf bb;
+    uint32_t pre, e;
     uint4 q;
     bool inflight;
 
     __device__ __forceinline__ uint4 group(int i) const {   // i: a multiple of 4
         return *reinterpret_cast<const uint4*>(gs + (i < glim ? i : glim));
     }
-    __device__ __forceinline__ void land(int slot, const uint4& g) {   // ring slots slot .. slot + 3
-        uint32_t* p = rcol + slot * 64;
+    __device__ __forceinline__ static void land(lds_u32* p, const uint4& g) {   // the 4 ring slots from p
         p[0] = g.x;
         p[64] = g.y;
         p[128] = g.z;
@@ -286,16 +266,15 @@ struct LineLane {
         gs = sw - o;
         const int wlim = (int)((end_bit >> 5) + 2 - (int64_t)(bit_off >> 5));   // last readable word, from sw
         glim = (wlim + o) & ~3;
-        rcol = ring_col;
+        rcol = (lds_u32*)ring_col;
         const uint4 g0 = group(0), g1 = group(4), g2 = group(8);
-        land(0, g0);
-        land(4, g1);
-        land(8, g2);
+        land(rcol, g0);
+        land(rcol + 4 * 64, g1);
+        land(rcol + 8 * 64, g2);
         ld = 12;
-        ls = 0;
-        rs = o + 2;
-        buf = ((uint64_t)__builtin_bitreverse32(rcol[o * 64]) << 32) << (bit_off & 31u);
-        nbuf = 32u - (bit_off & 31u);
+        lp = rcol;
+        rq = rcol + (o + 2) * 64;
+        bb.init(rcol[o * 64], bit_off);
         pre = rcol[(o + 1) * 64];
         refill();
         e = lut[row * kL + (int)state - kL];
@@ -303,11 +282,10 @@ struct LineLane {
     }
 
     __device__ __forceinline__ void refill() {
-        if (nbuf < 32u) {
-            buf |= (uint64_t)__builtin_bitreverse32(pre) << (32u - nbuf);
-            nbuf += 32u;
-            pre = rcol[rs * 64];
-            rs = rs == kLineRing - 1 ? 0 : rs + 1;
+        if (bb.low()) {
+            bb.push(pre);
+            pre = *rq;
+            rq = rq == rcol + (kLineRing - 1) * 64 ? rcol : rq + 64;
         }
     }
 
@@ -315,11 +293,13 @@ struct LineLane {
     // lane still decodes (`more`) and the ring has room for it.
     __device__ __forceinline__ void boundary(bool more) {
         if (inflight) {
-            land(ls, q);
-            ls = ls == 8 ? 0 : ls + 4;
+            land(lp, q);
+            lp = lp == rcol + 8 * 64 ? rcol : lp + 4 * 64;
             inflight = false;
         }
-        if (more && (rs >> 2) != (ls >> 2)) {
+        // rq lies in the landing group iff it is 0 .. 1023 bytes past lp
+        const uint32_t qoff = (uint32_t)(uintptr_t)rq - (uint32_t)(uintptr_t)lp;
+        if (more && qoff >= 4u * 64u * 4u) {
             q = group(ld);
             ld += 4;
             inflight = true;
@@ -328,11 +308,7 @@ struct LineLane {
 
     __device__ __forceinline__ void step(uint16_t* stg_j, const char* lutb) {
         *stg_j = (uint16_t)lut_sym(e);
-        const uint32_t bits = (uint32_t)(buf >> 33) >> (e & 31u);
-        const uint32_t k = lut_k(e);
-        const uint32_t addr = (lut_next(e) + bits) << 2;
-        buf <<= k;
-        nbuf -= k;
+        const uint32_t addr = (lut_next(e) + bb.take(e)) << 2;
         e = *reinterpret_cast<const uint32_t*>(lutb + addr);
     }
 
