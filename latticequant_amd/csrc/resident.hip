@@ -12,12 +12,14 @@
 // group * 64 + slot, so one group of a block is 64 records in a row.
 //
 // Decoding a record to fp16 is bit arithmetic: a 5-bit field u placed at bit
-// 1 of a half whose high bits are 0x64 gives the fp16 number 1024 + 2u + coset
-// (the coset bit sits at bit 0), so one AND-OR turns two fields into a packed
-// pair; subtracting 1056 leaves 2c exactly (c the lattice coordinate), and a
-// packed multiply by s / 2 gives fp16(c * s), the value _decompress_chunk
-// writes for the token's fp16 scale s.  The MFMA operands are therefore the
-// fp16 K / V the reference's attention reads.
+// 1 of a half whose high bits are 0x60 gives the fp16 number 512 + u +
+// coset / 2 (the coset bit sits at bit 0; the spacing of fp16 numbers in
+// [512, 1024) is 1/2), so one AND-OR turns two fields into a packed pair;
+// subtracting 528 leaves c exactly (c the lattice coordinate, a multiple of
+// 1/2), and a packed multiply by the token's fp16 scale s rounds the exact
+// product once: fp16(c * s), the value _decompress_chunk writes, for every
+// fp16 s (subnormal products included).  The MFMA operands are therefore
+// the fp16 K / V the reference's attention reads.
 //
 // lq_resident_attention: per (kv head, split) one workgroup of eight waves; a
 // wave takes 32-token tiles:
@@ -50,7 +52,7 @@ typedef float f4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kHd = 128;
 constexpr int kRB = 16;                       // tokens per resident block
-constexpr uint32_t kPairBias = 0x64206420u;   // fp16 pair (1056, 1056)
+constexpr uint32_t kPairBias = 0x60206020u;   // fp16 pair (528, 528)
 constexpr uint32_t kFieldMask = 0x003E003Eu;  // bits 1..5 of both halves
 constexpr uint32_t kLsbMask = 0x08420842u;    // low bits of u0..u5 in the a word
 
@@ -59,9 +61,9 @@ __device__ __forceinline__ uint32_t unbias(uint32_t v) {
     return __builtin_bit_cast(uint32_t, r);
 }
 
-// One record -> four fp16 pairs 1056 + 2c of coordinates (0,1) (2,3) (4,5) (6,7).
+// One record -> four fp16 pairs 528 + c of coordinates (0,1) (2,3) (4,5) (6,7).
 __device__ __forceinline__ void rec_pairs(uint32_t a, uint32_t b, uint32_t p[4]) {
-    const uint32_t kc = 0x64006400u | ((a & 1u) * 0x00010001u);
+    const uint32_t kc = 0x60006000u | ((a & 1u) * 0x00010001u);
     p[0] = (a & kFieldMask) | kc;
     p[1] = ((a >> 5) & kFieldMask) | kc;
     p[2] = ((a >> 10) & kFieldMask) | kc;
@@ -72,11 +74,11 @@ __device__ __forceinline__ void rec_pairs(uint32_t a, uint32_t b, uint32_t p[4])
 }
 
 // Records of tokens t and t+1 (same vector) -> eight fp16 pairs
-// (coordinate i of t, coordinate i of t+1), values 1056 + 2c.
+// (coordinate i of t, coordinate i of t+1), values 528 + c.
 __device__ __forceinline__ void rec_pairs_tok(uint32_t a0, uint32_t b0, uint32_t a1, uint32_t b1, uint32_t p[8]) {
     const uint32_t lo = __builtin_amdgcn_perm(a1, a0, 0x05040100u);   // a0[15:0] | a1[15:0] << 16
     const uint32_t hi = __builtin_amdgcn_perm(a1, a0, 0x07060302u);   // a0[31:16] | a1[31:16] << 16
-    const uint32_t kc = 0x64006400u | (lo & 0x00010001u);             // coset of t at bit 0, of t+1 at bit 16
+    const uint32_t kc = 0x60006000u | (lo & 0x00010001u);             // coset of t at bit 0, of t+1 at bit 16
     p[0] = (lo & kFieldMask) | kc;
     p[2] = ((lo >> 5) & kFieldMask) | kc;
     p[4] = ((lo >> 10) & kFieldMask) | kc;
@@ -91,42 +93,14 @@ __device__ __forceinline__ void rec_pairs_tok(uint32_t a0, uint32_t b0, uint32_t
     p[7] = kc | (((h0 << 1) | q0) << 1) | (((h1 << 1) | q1) << 17);
 }
 
-// int16 lattice values 2c -> fp16 pair
+// int16 lattice values 2c -> fp16 pair of the coordinates c (exact)
 __device__ __forceinline__ uint32_t pair_from_i16(int a, int b) {
-    const h2_t r = {(_Float16)(float)a, (_Float16)(float)b};
+    const h2_t r = {(_Float16)((float)a * 0.5f), (_Float16)((float)b * 0.5f)};
     return __builtin_bit_cast(uint32_t, r);
 }
 
-// fp16 pairs of exact lattice values 2c -> the pairs fp16(c * s) with s the
-// fp16 scale of the low / high element, rounded once as _decompress_chunk
-// rounds (llm/compressed_kv_cache.py:330).  c * s is exact in fp32, so one
-// packed fp16 multiply by s / 2 rounds it the same way whenever s / 2 is a
-// normal fp16 number (s >= 2^-13); smaller scales take the fp32 route.
-template <int N>
-__device__ __forceinline__ void dequant_pairs(uint32_t p[N], uint16_t s_lo, uint16_t s_hi) {
-    const float flo = h2f(s_lo), fhi = h2f(s_hi);
-    if (fminf(flo, fhi) >= 0x1p-13f) {
-        const h2_t m = {(_Float16)(0.5f * flo), (_Float16)(0.5f * fhi)};
-#pragma unroll
-        for (int i = 0; i < N; i++) p[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, p[i]) * m);
-    } else {
-#pragma unroll
-        for (int i = 0; i < N; i++) {
-            const h2_t h = __builtin_bit_cast(h2_t, p[i]);
-            const h2_t r = {(_Float16)(((float)h[0] * 0.5f) * flo), (_Float16)(((float)h[1] * 0.5f) * fhi)};
-            p[i] = __builtin_bit_cast(uint32_t, r);
-        }
-    }
-}
-
-// The pair (s_lo / 2, s_hi / 2) for dequant_pairs' fast path and whether it
-// applies (both scales >= 2^-13, so that the halves are exact).
-__device__ __forceinline__ uint32_t half_scales(uint32_t s_pair, bool* exact) {
-    const h2_t sp = __builtin_bit_cast(h2_t, s_pair);
-    *exact = (float)sp[0] >= 0x1p-13f && (float)sp[1] >= 0x1p-13f;
-    const h2_t half = {(_Float16)0.5f, (_Float16)0.5f};
-    return __builtin_bit_cast(uint32_t, sp * half);
-}
+// fp16 pairs of coordinates c times the packed fp16 scales m = (s_lo, s_hi):
+// fp16(c * s), one rounding of the exact product
 template <int N>
 __device__ __forceinline__ void mul_pairs(uint32_t p[N], uint32_t m) {
 #pragma unroll
@@ -321,8 +295,8 @@ __global__ __launch_bounds__(256) void k_res_dequant(lq_resident r, int64_t h0, 
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const h2_t h = __builtin_bit_cast(h2_t, p[i]);
-            v2[2 * i] = (int)(float)h[0] - 1056;
-            v2[2 * i + 1] = (int)(float)h[1] - 1056;
+            v2[2 * i] = (int)((float)h[0] * 2.0f) - 1056;   // 2 (528 + c) - 1056 = 2 c
+            v2[2 * i + 1] = (int)((float)h[1] * 2.0f) - 1056;
         }
     }
     const float s = h2f(r.scale[(h0 + hh) * r.cap_blocks * kRB + (blk0 + bb) * kRB + (slot & 15)]);
@@ -473,12 +447,11 @@ __device__ __forceinline__ int exc_code(const lq_resident& r, int64_t rb, uint64
 // Scores of block x: s += q . k over the four record groups, each group's K
 // operand decoded (and, rarely, patched with exception entries) just before
 // its MFMA, so that only one group's pairs are live at a time.
-template <bool FAST>
 __device__ __forceinline__ void tile_k(const AttnArgs& A, const TileRaw& d, int64_t rb, int x, int lane,
-                                       uint32_t mk, const h8_t qa[4], f4_t& s) {
+                                       const h8_t qa[4], f4_t& s) {
     const uint64_t hdr = meta_hdr(d, x);
     const int n = (int)(hdr & 0xffu);
-    const uint16_t sk = (uint16_t)(x ? d.ks >> 16 : d.ks & 0xffffu);
+    const uint32_t mk = (x ? d.ks >> 16 : d.ks & 0xffffu) * 0x00010001u;   // (s, s) of the lane's token
 #pragma unroll
     for (int c = 0; c < 4; c++) {
         uint32_t p[4];
@@ -500,8 +473,7 @@ __device__ __forceinline__ void tile_k(const AttnArgs& A, const TileRaw& d, int6
                 }
             }
         }
-        if (FAST) mul_pairs<4>(p, mk);
-        else dequant_pairs<4>(p, sk, sk);
+        mul_pairs<4>(p, mk);
         s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], as_h8(p[0], p[1], p[2], p[3]), s, 0, 0, 0);
     }
 }
@@ -509,9 +481,8 @@ __device__ __forceinline__ void tile_k(const AttnArgs& A, const TileRaw& d, int6
 // V of the lane's 8 tokens (vector lane % 16), two tokens at a time:
 // vp[k][i] = fp16 pair (dimension 8 n + i of token 2 k, of token 2 k + 1),
 // dequantised -- the operand halves of P V's MFMA i as they are.
-template <bool FAST>
 __device__ __forceinline__ void tile_v(const AttnArgs& A, const TileRaw& d, int64_t rb0, int lane,
-                                       const uint32_t mv[4], uint32_t vp[4][8]) {
+                                       uint32_t vp[4][8]) {
     const int n = lane & 15, k8 = lane >> 4, xb = k8 >> 1;
     const uint32_t aw[8] = {d.va0.x, d.va0.y, d.va0.z, d.va0.w, d.va1.x, d.va1.y, d.va1.z, d.va1.w};
 #pragma unroll
@@ -545,8 +516,8 @@ __device__ __forceinline__ void tile_v(const AttnArgs& A, const TileRaw& d, int6
 #pragma unroll
                         for (int i = 0; i < 8; i++) {
                             h2_t h = __builtin_bit_cast(h2_t, vp[k][i]);
-                            if (q == 2 * k) h[0] = (_Float16)(float)v[i];
-                            if (q == 2 * k + 1) h[1] = (_Float16)(float)v[i];
+                            if (q == 2 * k) h[0] = (_Float16)((float)v[i] * 0.5f);
+                            if (q == 2 * k + 1) h[1] = (_Float16)((float)v[i] * 0.5f);
                             vp[k][i] = __builtin_bit_cast(uint32_t, h);
                         }
                 }
@@ -555,10 +526,7 @@ __device__ __forceinline__ void tile_v(const AttnArgs& A, const TileRaw& d, int6
     }
     const uint32_t sw[4] = {d.vs.x, d.vs.y, d.vs.z, d.vs.w};   // scales of tokens (2 k, 2 k + 1)
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        if (FAST) mul_pairs<8>(vp[k], mv[k]);
-        else dequant_pairs<8>(vp[k], (uint16_t)(sw[k] & 0xffffu), (uint16_t)(sw[k] >> 16));
-    }
+    for (int k = 0; k < 4; k++) mul_pairs<8>(vp[k], sw[k]);
 }
 
 // ---- tail tiles (fp16 K / V, t_tail tokens, no prefetch)
@@ -628,45 +596,17 @@ __device__ __forceinline__ void tile_softmax_pv(int G, const f4_t s[2], const bo
 
 // Decode of one prefix tile from its registers (rb0: resident block of the
 // tile's first token): the scores s of its two blocks and the V pairs.
-template <int HPL>
 __device__ __forceinline__ void prefix_decode(const AttnArgs& A, const TileRaw& d, int64_t rb0, int64_t t0, int64_t T,
                                               int lane, const h8_t qa[4], f4_t s[2], bool valid[2],
                                               uint32_t vp[4][8]) {
-    // dequant multipliers (s / 2 per token); the packed-multiply path is
-    // taken when every scale of the tile allows it (wave-uniform)
-    bool e0, e1, ev = true;
-    const uint32_t mk0 = half_scales((d.ks & 0xffffu) * 0x10001u, &e0);
-    const uint32_t mk1 = half_scales((d.ks >> 16) * 0x10001u, &e1);
-    const uint32_t sw[4] = {d.vs.x, d.vs.y, d.vs.z, d.vs.w};
-    uint32_t mv[4];
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        bool e;
-        mv[k] = half_scales(sw[k], &e);   // (s_2k / 2, s_2k+1 / 2)
-        ev = ev && e;
+    for (int x = 0; x < 2; x++) {
+        s[x] = f4_t{0.f, 0.f, 0.f, 0.f};
+        valid[x] = t0 + 16 * x + (lane & 15) < T;
+        if (t0 + 16 * x < T)   // wave-uniform
+            tile_k(A, d, rb0 + x, x, lane, qa, s[x]);
     }
-    const bool fast = __all(e0 && e1 && ev);
-    // one wave-uniform branch per tile: the usual all-normal-scales path carries
-    // none of the small-scale path's work
-    if (fast) {
-#pragma unroll
-        for (int x = 0; x < 2; x++) {
-            s[x] = f4_t{0.f, 0.f, 0.f, 0.f};
-            valid[x] = t0 + 16 * x + (lane & 15) < T;
-            if (t0 + 16 * x < T)   // wave-uniform
-                tile_k<true>(A, d, rb0 + x, x, lane, x ? mk1 : mk0, qa, s[x]);
-        }
-        tile_v<true>(A, d, rb0, lane, mv, vp);
-    } else {
-#pragma unroll
-        for (int x = 0; x < 2; x++) {
-            s[x] = f4_t{0.f, 0.f, 0.f, 0.f};
-            valid[x] = t0 + 16 * x + (lane & 15) < T;
-            if (t0 + 16 * x < T)
-                tile_k<false>(A, d, rb0 + x, x, lane, x ? mk1 : mk0, qa, s[x]);
-        }
-        tile_v<false>(A, d, rb0, lane, mv, vp);
-    }
+    tile_v(A, d, rb0, lane, vp);
 }
 
 // The tail tiles this wave owns: tail tile tt goes to the kv head's wave
@@ -732,7 +672,7 @@ __device__ __forceinline__ void prefix_tiles(const AttnArgs& A, int64_t kvh, int
         f4_t s[2];
         bool valid[2];
         uint32_t vp[4][8];
-        prefix_decode<HPL>(A, d, hb + ta / kRB, ta, T, lane, qa, s, valid, vp);
+        prefix_decode(A, d, hb + ta / kRB, ta, T, lane, qa, s, valid, vp);
         if (gn < npt) tile_load(A, kvh, gn * kTile, T, lane, d);
         tile_softmax_pv<HPL>(A.group, s, valid, lane, vp, pt, m_run, l_run, o);
         if (gn >= npt) break;
@@ -841,6 +781,50 @@ __global__ __launch_bounds__(kAW * 64) void k_res_attn(AttnArgs A) {
     // end) so that each thread's loads go out as one batch.
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     const float* r0 = A.rec + (int64_t)kvh * nsp * G * kRecF;
+    if (nsp <= 32) {
+        // One wave per query head, no workgroup barrier: lane p (< nsp) holds
+        // split p's (m, l); lane (half, dq) sums the O rows of splits half,
+        // half + 2, ... over dimensions 4 dq .. 4 dq + 3.  Every load (split
+        // maxima included) is issued before the first wait.
+        const int half = lane >> 5, dq = lane & 31;
+        for (int h = wave; h < G; h += kAW) {
+            const int pl = lane < nsp ? lane : nsp - 1;
+            const f4_t ml = *reinterpret_cast<const f4_t*>(r0 + (int64_t)(pl * G + h) * kRecF);
+            f4_t ov[16];
+            float mo[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const int p = half + 2 * j;
+                const int pc = p < nsp ? p : nsp - 1;
+                ov[j] = *reinterpret_cast<const f4_t*>(r0 + (int64_t)(pc * G + h) * kRecF + 4 + 4 * dq);
+                mo[j] = r0[(int64_t)(pc * G + h) * kRecF];
+            }
+            float M = lane < nsp ? ml[0] : -INFINITY;
+#pragma unroll
+            for (int o2 = 32; o2 > 0; o2 >>= 1) M = fmaxf(M, __shfl_xor(M, o2, 64));
+            float L = (lane < nsp && ml[0] != -INFINITY) ? __builtin_amdgcn_exp2f(ml[0] - M) * ml[1] : 0.f;
+#pragma unroll
+            for (int o2 = 32; o2 > 0; o2 >>= 1) L += __shfl_xor(L, o2, 64);
+            f4_t acc = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const int p = half + 2 * j;
+                const float f = (p < nsp && mo[j] != -INFINITY) ? __builtin_amdgcn_exp2f(mo[j] - M) : 0.f;
+                acc += ov[j] * f;
+            }
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc[c] += __shfl_xor(acc[c], 32, 64);
+            if (half == 0) {
+                const float inv = 1.f / L;
+                uint16_t* op = A.out + (kvh * G + h) * kHd + 4 * dq;
+                *reinterpret_cast<uint2*>(op) =
+                    make_uint2((uint32_t)f2h(acc[0] * inv) | ((uint32_t)f2h(acc[1] * inv) << 16),
+                               (uint32_t)f2h(acc[2] * inv) | ((uint32_t)f2h(acc[3] * inv) << 16));
+            }
+        }
+        if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
     float* s_cm = s_buf;
     float* s_cf = s_cm + kMaxRec;
     float* s_cl = s_cf + kMaxRec;
