@@ -369,7 +369,8 @@ __device__ __forceinline__ void wave_lds_sync() {
 struct TileRaw {
     uint32_t ka[2][4];      // K record words of blocks 0, 1, groups 0..3
     uint32_t kb[2][4];      // their low bytes
-    uint32_t ks;            // fp16 scale of the K token of block 0 (low) and 1 (high)
+    uint32_t ks[2];         // fp16 scale of the lane's K token of block 0, 1 (kept apart: combining
+                            // them at load time would wait for every load in flight)
     uint4 va0, va1;         // V records of the lane's 8 tokens (vector lane % 16)
     uint2 vb;               // their low bytes
     uint4 vs;               // fp16 scales of those 8 tokens
@@ -395,7 +396,6 @@ __device__ __forceinline__ void tile_load(const AttnArgs& A, int64_t kvh, int64_
     // and carry p = 0 into P V.
     const int64_t hb = kvh * A.k.cap_blocks;
     const int64_t last = T - kRB;
-    uint32_t ks[2];
 #pragma unroll
     for (int x = 0; x < 2; x++) {
         const int64_t tb = min(t0 + 16 * x, last);
@@ -405,9 +405,8 @@ __device__ __forceinline__ void tile_load(const AttnArgs& A, int64_t kvh, int64_
             d.ka[x][c] = A.k.a[rb * 256 + c * 64 + lane];
             d.kb[x][c] = A.k.b[rb * 256 + c * 64 + lane];
         }
-        ks[x] = A.k.scale[hb * kRB + tb + (lane & 15)];
+        d.ks[x] = A.k.scale[hb * kRB + tb + (lane & 15)];
     }
-    d.ks = ks[0] | (ks[1] << 16);
     {   // lanes 0..3 (and their copies): meta of K block 0, 1 and V block 0, 1.
         // A per-lane address keeps this a vector load: scalar loads share the
         // LDS wait counter and would stall every tile's LDS traffic.
@@ -451,7 +450,7 @@ __device__ __forceinline__ void tile_k(const AttnArgs& A, const TileRaw& d, int6
                                        const h8_t qa[4], f4_t& s) {
     const uint64_t hdr = meta_hdr(d, x);
     const int n = (int)(hdr & 0xffu);
-    const uint32_t mk = (x ? d.ks >> 16 : d.ks & 0xffffu) * 0x00010001u;   // (s, s) of the lane's token
+    const uint32_t mk = d.ks[x] * 0x00010001u;   // (s, s) of the lane's token
 #pragma unroll
     for (int c = 0; c < 4; c++) {
         uint32_t p[4];
@@ -673,7 +672,12 @@ __device__ __forceinline__ void prefix_tiles(const AttnArgs& A, int64_t kvh, int
         bool valid[2];
         uint32_t vp[4][8];
         prefix_decode(A, d, hb + ta / kRB, ta, T, lane, qa, s, valid, vp);
-        if (gn < npt) tile_load(A, kvh, gn * kTile, T, lane, d);
+        // Every use of this tile's registers is scheduled before the reload, and
+        // the reload is unconditional (past the prefix it re-reads this tile,
+        // from cache), so the next tile's loads land in place and nothing
+        // waits on them before the next decode.
+        __builtin_amdgcn_sched_barrier(0);
+        tile_load(A, kvh, (gn < npt ? gn : g) * kTile, T, lane, d);
         tile_softmax_pv<HPL>(A.group, s, valid, lane, vp, pt, m_run, l_run, o);
         if (gn >= npt) break;
         g = gn;
