@@ -63,7 +63,10 @@ __device__ __forceinline__ uint32_t unbias(uint32_t v) {
 
 // One record -> four fp16 pairs 528 + c of coordinates (0,1) (2,3) (4,5) (6,7).
 __device__ __forceinline__ void rec_pairs(uint32_t a, uint32_t b, uint32_t p[4]) {
-    const uint32_t kc = 0x60006000u | ((a & 1u) * 0x00010001u);
+    // (coset bit at bit 0 and 16) | 0x60006000: byte 0 of a copied to byte 2
+    // by one byte permute, then one AND-OR (a select between two constants
+    // would take three instructions)
+    const uint32_t kc = (__builtin_amdgcn_perm(0u, a, 0x0c000c00u) & 0x00010001u) | 0x60006000u;
     p[0] = (a & kFieldMask) | kc;
     p[1] = ((a >> 5) & kFieldMask) | kc;
     p[2] = ((a >> 10) & kFieldMask) | kc;
@@ -393,37 +396,40 @@ __device__ __forceinline__ void tile_load(const AttnArgs& A, int64_t kvh, int64_
     // Blocks past the prefix (only block 1 of the last tile, T being a
     // multiple of 16) read the last block instead: every address is valid and
     // no branch waits on the loads; their tokens are masked out of the scores
-    // and carry p = 0 into P V.
+    // and carry p = 0 into P V.  Every address is a wave-uniform base (scalar
+    // registers) plus a per-lane 32-bit offset.
     const int64_t hb = kvh * A.k.cap_blocks;
     const int64_t last = T - kRB;
+    const int64_t tb0 = min(t0, last), tb1 = min(t0 + 16, last);   // first tokens of the tile's blocks
+    const int64_t rb0 = hb + tb0 / kRB;
+    const uint32_t dblk = (uint32_t)(tb1 - tb0) / kRB;                // 1, or 0 when block 1 is clamped
 #pragma unroll
     for (int x = 0; x < 2; x++) {
-        const int64_t tb = min(t0 + 16 * x, last);
-        const int64_t rb = hb + tb / kRB;
+        const int64_t rb = x ? rb0 + dblk : rb0;
+        const uint32_t* ka = A.k.a + rb * 256;
+        const uint8_t* kb = A.k.b + rb * 256;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            d.ka[x][c] = A.k.a[rb * 256 + c * 64 + lane];
-            d.kb[x][c] = A.k.b[rb * 256 + c * 64 + lane];
+            d.ka[x][c] = ka[(uint32_t)(c * 64 + lane)];
+            d.kb[x][c] = kb[(uint32_t)(c * 64 + lane)];
         }
-        d.ks[x] = A.k.scale[hb * kRB + tb + (lane & 15)];
+        d.ks[x] = (A.k.scale + hb * kRB + (x ? tb1 : tb0))[(uint32_t)(lane & 15)];
     }
     {   // lanes 0..3 (and their copies): meta of K block 0, 1 and V block 0, 1.
         // A per-lane address keeps this a vector load: scalar loads share the
         // LDS wait counter and would stall every tile's LDS traffic.
         const int i = lane & 3;
-        const int64_t tb = min(t0 + 16 * (i & 1), last);
-        const uint32_t* mp = ((i & 2) ? A.v.meta : A.k.meta) + (hb + tb / kRB) * 4;
-        d.meta = *reinterpret_cast<const uint4*>(mp);
+        const uint32_t* mp = ((i & 2) ? A.v.meta : A.k.meta) + rb0 * 4;
+        d.meta = *reinterpret_cast<const uint4*>(mp + (i & 1) * dblk * 4);
     }
     const int n = lane & 15, k8 = lane >> 4;
-    const int64_t tb = min(t0 + 16 * (k8 >> 1), last);
-    const int64_t rb = hb + tb / kRB;
-    const int64_t r0 = rb * 256 + (n >> 2) * 64 + 16 * (n & 3) + 8 * (k8 & 1);   // 8 consecutive records
-    const uint4* ap = reinterpret_cast<const uint4*>(A.v.a + r0);
+    // records of vector n of tokens 8 k8 .. 8 k8 + 7: block k8 / 2 of the tile
+    const uint32_t r0 = (uint32_t)((k8 >> 1) * dblk * 256 + (n >> 2) * 64 + 16 * (n & 3) + 8 * (k8 & 1));
+    const uint4* ap = reinterpret_cast<const uint4*>(A.v.a + rb0 * 256 + r0);
     d.va0 = ap[0];
     d.va1 = ap[1];
-    d.vb = *reinterpret_cast<const uint2*>(A.v.b + r0);
-    d.vs = *reinterpret_cast<const uint4*>(A.v.scale + hb * kRB + tb + 8 * (k8 & 1));
+    d.vb = *reinterpret_cast<const uint2*>(A.v.b + rb0 * 256 + r0);
+    d.vs = *reinterpret_cast<const uint4*>(A.v.scale + hb * kRB + tb0 + (uint32_t)((k8 >> 1) * dblk * 16 + 8 * (k8 & 1)));
 }
 
 // exception k of a block (0 <= k < count): slot | group << 6 from the header,
