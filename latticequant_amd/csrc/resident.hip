@@ -775,11 +775,18 @@ __global__ __launch_bounds__(kAW * 64) void k_res_attn(AttnArgs A) {
             }
         }
     }
-    __builtin_amdgcn_s_waitcnt(0);   // this thread's record stores have completed
+    // Publication.  The records are agent-scope atomic stores; each thread
+    // waits for its own to complete (the barrier itself waits only for LDS
+    // traffic), the workgroup barrier orders all of them before thread 0's
+    // counter increment, and that increment is a release at agent scope (L2
+    // written back, thread 0's stores complete).  The workgroup that takes the
+    // last increment acquires at agent scope (its L2 copy invalidated) before
+    // it reads the records: release / acquire through the counter.
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     uint32_t* ctr = A.counter + kvh * kCtrStride;
     if (tid == 0) {
-        const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
         s_last = old == (uint32_t)(nsp - 1);
     }
     __syncthreads();
