@@ -758,29 +758,38 @@ __global__ __launch_bounds__(256) void k_chunk_encode(const SymT* __restrict__ s
             nq = 0;
         }
     };
-    uint64_t acc = 0;
-    uint32_t nacc = 0;
+    // Bit accumulator (ahi:alo): the emitted bits sit at the top, newest
+    // highest; a symbol's group (the k low bits of xin, bit k - 1 first in the
+    // final stream) enters by one funnel shift of (xin:ahi:alo) right by k, two
+    // v_alignbit (k <= 10; k = 0 leaves all three in place).  Below the bits a
+    // single 1 (the sentinel) marks their end, so no bit count is kept: 32 or
+    // more bits are held exactly when the low word is nonzero.  The oldest 32
+    // bits then leave as one word, bit-reversed so that the oldest bit is the
+    // word's most significant, as the stream order wants.
+    uint32_t ahi = 0x80000000u, alo = 0u;
+    auto take_word = [&]() {   // needs alo != 0
+        const uint32_t s = (uint32_t)__builtin_ctz(alo);   // sentinel position
+        const uint32_t raw = (uint32_t)((((uint64_t)ahi << 32) | alo) >> (s + 1u));
+        push(__builtin_bitreverse32(raw));
+        ahi = ((ahi >> s) | 1u) << s;   // sentinel moves up 32 bits (to bit s of the high word)
+        alo = 0u;
+    };
     for_each_rev(col.p, col.n, [&](int v, int b, bool in) {
         uint32_t k;
         const uint32_t xin = x;
         const uint32_t xn = encx_step(xin, enc(in ? v : lo_sym), &k);
         k = in ? k : 0u;
         x = in ? xn : xin;
-        // emitted group in final stream order: the k low bits of xin, most significant first
-        acc = (acc << k) | (((uint64_t)__builtin_bitreverse32(xin) << k) >> 32);
-        nacc += k;
-        // at most 3 symbols (<= 30 bits) since the last check: acc holds <= 61 bits
-        if (b % 3 == 0 && nacc >= 32) {
-            nacc -= 32;
-            push((uint32_t)(acc >> nacc));
-        }
+        alo = __builtin_amdgcn_alignbit(ahi, alo, k);
+        ahi = __builtin_amdgcn_alignbit(xin, ahi, k);
+        // at most 3 symbols (<= 30 bits) since the last check: <= 61 bits and the sentinel
+        if (b % 3 == 0 && alo != 0u) take_word();
     });
-    if (nacc >= 32) {   // the range may end between check points
-        nacc -= 32;
-        push((uint32_t)(acc >> nacc));
-    }
+    if (alo != 0u) take_word();   // the range may end between check points
+    // fewer than 32 bits left: the sentinel is in the high word
+    const uint32_t nacc = 31u - (uint32_t)__builtin_ctz(ahi);
     const uint32_t total = 32u * (uint32_t)nwords + nacc;
-    if (nacc) push((uint32_t)(acc << (32 - nacc)));
+    if (nacc) push(__builtin_bitreverse32(ahi >> (32u - nacc)));
     if (nq) {   // the last, partial group: its words sit in the top nq slots
         uint4* d = reinterpret_cast<uint4*>(scr + gbase);
         d[0] = make_uint4(qcol[0], qcol[256], qcol[512], qcol[768]);
