@@ -675,7 +675,7 @@ __global__ __launch_bounds__(256) void k_chunk_encode(const SymT* __restrict__ s
     constexpr int kCap = sizeof(SymT) == 1 ? 264 : LQ_MAXSYM;
     __shared__ uint32_t senc[LQ_STREAMS][kCap + 1];
     __shared__ int slo[LQ_STREAMS], snsym[LQ_STREAMS];
-    __shared__ uint32_t sq[8][256];   // per-lane queue of scratch words
+    __shared__ uint32_t sq[4][256];   // per-lane queue of scratch words (4: seven workgroups fit a CU's LDS)
     const int tid = threadIdx.x;
     const int64_t chunk = blockIdx.y;
     const int64_t g = (int64_t)blockIdx.x * kEncBlocks + (tid >> 4);
@@ -742,19 +742,17 @@ __global__ __launch_bounds__(256) void k_chunk_encode(const SymT* __restrict__ s
     Col<SymT> col = column(sym, blk_n1, chunk, nblk, V, g, c, idx);
     uint32_t* scr = scratch + task * (int64_t)kCapW;
     // words leave in decreasing address order from kCapW - 1; word j of the
-    // current 8-word group waits in LDS at qcol[(7 - j) * 256] (this lane's
-    // column, so a wave's writes are contiguous) and the group leaves as two
-    // 16-byte stores when full
+    // current 4-word group waits in LDS at qcol[(3 - j) * 256] (this lane's
+    // column, so a wave's writes are contiguous) and the group leaves as one
+    // 16-byte store when full
     uint32_t* const qcol = &sq[0][tid];
-    int nq = 0, gbase = kCapW - 8, nwords = 0;
+    int nq = 0, gbase = kCapW - 4, nwords = 0;
     auto push = [&](uint32_t word) {
-        qcol[(7 - nq) * 256] = word;
+        qcol[(3 - nq) * 256] = word;
         nwords++;
-        if (++nq == 8) {
-            uint4* d = reinterpret_cast<uint4*>(scr + gbase);
-            d[0] = make_uint4(qcol[0], qcol[256], qcol[512], qcol[768]);
-            d[1] = make_uint4(qcol[1024], qcol[1280], qcol[1536], qcol[1792]);
-            gbase -= 8;
+        if (++nq == 4) {
+            *reinterpret_cast<uint4*>(scr + gbase) = make_uint4(qcol[0], qcol[256], qcol[512], qcol[768]);
+            gbase -= 4;
             nq = 0;
         }
     };
@@ -791,9 +789,7 @@ __global__ __launch_bounds__(256) void k_chunk_encode(const SymT* __restrict__ s
     const uint32_t total = 32u * (uint32_t)nwords + nacc;
     if (nacc) push(__builtin_bitreverse32(ahi >> (32u - nacc)));
     if (nq) {   // the last, partial group: its words sit in the top nq slots
-        uint4* d = reinterpret_cast<uint4*>(scr + gbase);
-        d[0] = make_uint4(qcol[0], qcol[256], qcol[512], qcol[768]);
-        d[1] = make_uint4(qcol[1024], qcol[1280], qcol[1536], qcol[1792]);
+        *reinterpret_cast<uint4*>(scr + gbase) = make_uint4(qcol[0], qcol[256], qcol[512], qcol[768]);
     }
     blk_bits[task] = total;
     blk_state[task] = (uint16_t)x;
