@@ -448,13 +448,16 @@ __global__ __launch_bounds__(kQThreads, LEAN ? 7 : 1) void k_chunk_quantize(
             n1 += pc[k];
         }
         const int n0 = valid - n1;
+        // coset-1 vectors of the ballot words before this wave's (wave-uniform):
+        // word r * 4 + wave, summed with integer masks of the wave index
+        const int wm1 = -(int)(wave >= 1), wm2 = -(int)(wave >= 2), wm3 = -(int)(wave >= 3);
+        const int bef[2] = {(pc[0] & wm1) + (pc[1] & wm2) + (pc[2] & wm3),
+                            pc[0] + pc[1] + pc[2] + pc[3] + (pc[4] & wm1) + (pc[5] & wm2) + (pc[6] & wm3)};
 #pragma unroll
         for (int r = 0; r < 2; r++) {
             const int vl = r * kQThreads + tid;
             if (vl < valid) {
-                int before = 0;   // coset-1 vectors of the earlier words (wave-uniform)
-#pragma unroll
-                for (int k = 0; k < kBlk / 64; k++) before += k < r * 4 + wave ? pc[k] : 0;
+                const int before = bef[r];
                 const unsigned long long m = bal[r];
                 const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
                                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
