@@ -449,10 +449,14 @@ __global__ __launch_bounds__(kQThreads, LEAN ? 7 : 1) void k_chunk_quantize(
         }
         const int n0 = valid - n1;
         // coset-1 vectors of the ballot words before this wave's (wave-uniform):
-        // word r * 4 + wave, summed with integer masks of the wave index
-        const int wm1 = -(int)(wave >= 1), wm2 = -(int)(wave >= 2), wm3 = -(int)(wave >= 3);
-        const int bef[2] = {(pc[0] & wm1) + (pc[1] & wm2) + (pc[2] & wm3),
-                            pc[0] + pc[1] + pc[2] + pc[3] + (pc[4] & wm1) + (pc[5] & wm2) + (pc[6] & wm3)};
+        // word r * 4 + wave.  Byte-wise prefix sums by one multiply (counts are
+        // at most 64, three of them fit a byte) read at byte `wave`: scalar
+        // arithmetic on the wave index, no per-word condition kept live.
+        const uint32_t p0 = (uint32_t)pc[0] | ((uint32_t)pc[1] << 8) | ((uint32_t)pc[2] << 16);
+        const uint32_t p1 = (uint32_t)pc[4] | ((uint32_t)pc[5] << 8) | ((uint32_t)pc[6] << 16);
+        const uint32_t wsh = 8u * (uint32_t)wave;
+        const int bef[2] = {(int)(((p0 * 0x01010100u) >> wsh) & 0xffu),
+                            pc[0] + pc[1] + pc[2] + pc[3] + (int)(((p1 * 0x01010100u) >> wsh) & 0xffu)};
 #pragma unroll
         for (int r = 0; r < 2; r++) {
             const int vl = r * kQThreads + tid;
