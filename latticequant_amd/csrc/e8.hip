@@ -278,8 +278,9 @@ __device__ __forceinline__ void stage_hist(const uint4& w, int row16, int n0, in
 // spills through VGPR lanes in the block loop).  ROT: the input rows are first
 // rotated in registers (rht_lanes, sign row = the head, lpr lanes per row),
 // exactly the fp32 values a materialised forward rotation holds; no
-// dequantised output.
-template <typename SymT, bool DITHER, bool LEAN = false, bool ROT = false>
+// dequantised output.  LDT >= 0: the input dtype as a compile-time constant
+// (the lean launches), so no dtype test is kept live across the block loop.
+template <typename SymT, bool DITHER, bool LEAN = false, bool ROT = false, int LDT = -1>
 __global__ __launch_bounds__(kQThreads, LEAN ? 7 : 1) void k_chunk_quantize(
     const void* __restrict__ x, int dtype, int64_t n_heads, int64_t bph, int64_t nblk,
     const float* __restrict__ scale32, const int32_t* __restrict__ fastdiv, SymT* __restrict__ sym,
@@ -291,7 +292,7 @@ __global__ __launch_bounds__(kQThreads, LEAN ? 7 : 1) void k_chunk_quantize(
     __shared__ uint32_t shist[kWide ? 1 : LQ_STREAMS * kHRow];
     __shared__ int smin[LQ_STREAMS], smax[LQ_STREAMS];
     __shared__ __align__(16) SymT stage[kSymStride];
-    __shared__ unsigned long long masks[kBlk / 64];
+    __shared__ __align__(16) unsigned long long masks[kBlk / 64];
     __shared__ int sflag;
 
     const int tid = threadIdx.x;
@@ -366,7 +367,7 @@ __global__ __launch_bounds__(kQThreads, LEAN ? 7 : 1) void k_chunk_quantize(
                     hq = h;
                 }
                 float xv[8], t[8], ic[8], dd[8];
-                load8(x, dtype, chunk * V + v, xv);
+                load8(x, LDT >= 0 ? LDT : dtype, chunk * V + v, xv);
                 if constexpr (ROT) {
                     // rows start at multiples of lpr vectors and blocks at
                     // multiples of 512, so the lane's place in its row is tid % lpr;
@@ -394,7 +395,7 @@ __global__ __launch_bounds__(kQThreads, LEAN ? 7 : 1) void k_chunk_quantize(
                 } else {               // the rare exact path recomputes t from x
                     c = e8_nearest_fast(t, ic, [&](float tt[8]) {
                         float xx[8];
-                        load8(x, dtype, chunk * V + v, xx);
+                        load8(x, LDT >= 0 ? LDT : dtype, chunk * V + v, xx);
 #pragma unroll
                         for (int i = 0; i < 8; i++) tt[i] = div_scaled(xx[i], s, rs, fast);
                         if constexpr (DITHER) {
@@ -500,8 +501,10 @@ __global__ __launch_bounds__(kQThreads, LEAN ? 7 : 1) void k_chunk_quantize(
                 dst[i] = w;
                 if constexpr (!kWide) stage_hist(w, i, n0, n1, shist);
             }
-            unsigned long long* cb = reinterpret_cast<unsigned long long*>(coset_bits + gblk * (kBlk / 8));
-            if (tid < kBlk / 64) cb[tid] = masks[tid];
+            // the block's 64 bytes of coset bits as four 16-byte rows (lane offsets
+            // shared with the copy above)
+            uint4* cb = reinterpret_cast<uint4*>(coset_bits + gblk * (kBlk / 8));
+            if (tid < kBlk / 128) cb[tid] = reinterpret_cast<const uint4*>(masks)[tid];
             if (tid == 0) blk_n1[gblk] = (uint32_t)n1;
         }
         __syncthreads();
@@ -656,10 +659,16 @@ int lq_chunk_quantize(const void* d_x, int dtype, int64_t n_chunks, int64_t n_he
         hipLaunchKernelGGL((k_chunk_quantize<int8_t, true>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x, dtype,
                            n_heads, bph, nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, d_hist, nullptr,
                            d_status, d_deq, deq_dtype, d_dither_seed, nullptr, 1, 1.0f);
-    else if (bph >= kBlk && !d_deq)
-        hipLaunchKernelGGL((k_chunk_quantize<int8_t, false, true>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x,
-                           dtype, n_heads, bph, nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, d_hist,
-                           nullptr, d_status, nullptr, deq_dtype, nullptr, nullptr, 1, 1.0f);
+    else if (bph >= kBlk && !d_deq) {
+#define LQ_LEAN(DT)                                                                                              \
+        hipLaunchKernelGGL((k_chunk_quantize<int8_t, false, true, false, DT>), dim3((unsigned)wg), dim3(kQThreads),  \
+                           0, s, d_x, dtype, n_heads, bph, nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, \
+                           d_hist, nullptr, d_status, nullptr, deq_dtype, nullptr, nullptr, 1, 1.0f)
+        if (dtype == LQ_F16) LQ_LEAN(LQ_F16);
+        else if (dtype == LQ_BF16) LQ_LEAN(LQ_BF16);
+        else LQ_LEAN(LQ_F32);
+#undef LQ_LEAN
+    }
     else
         hipLaunchKernelGGL((k_chunk_quantize<int8_t, false>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x, dtype,
                            n_heads, bph, nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, d_hist, nullptr,
