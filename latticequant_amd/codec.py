@@ -358,7 +358,9 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
     dt = L.dtype_code(x.dtype)
     s = L.stream_ptr(dev)
     bits_t, scale32, scale16, sigma2, fastdiv = _head_scales(x, bits, scale32, rht_signs)
-    coset_bits = _zeros(C * nblk * L.LQ_BLK // 8, torch.uint8, dev)
+    # every block's 64 bytes of coset bits are written by the quantizer (bits of
+    # vectors past the end are zero), so no fill
+    coset_bits = _empty(C * nblk * L.LQ_BLK // 8, torch.uint8, dev)
     blk_n1 = _empty(C * nblk, torch.int32, dev)
     status = _zeros(C, torch.int32, dev)
     deq = torch.empty_like(x) if deq_out else None
