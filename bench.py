@@ -806,11 +806,25 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    # separate write / read timing (outside the headline loop)
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-    ev[0].record(); write(); ev[1].record(); read(); ev[2].record()
+    # separate write / read timing (outside the headline loop): each direction
+    # `steps` times back to back behind a queued spin, so that the events
+    # bracket GPU time as in the headline loop, not the host's submission of
+    # the first launches after an idle GPU
+    nrep = max(1, args.steps)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    gpu_busy()
+    ev[0].record()
+    for _ in range(nrep):
+        write()
+    ev[1].record()
     torch.cuda.synchronize()
-    t_write_ms, t_read_ms = ev[0].elapsed_time(ev[1]), ev[1].elapsed_time(ev[2])
+    gpu_busy()
+    ev[2].record()
+    for _ in range(nrep):
+        read()
+    ev[3].record()
+    torch.cuda.synchronize()
+    t_write_ms, t_read_ms = ev[0].elapsed_time(ev[1]) / nrep, ev[2].elapsed_time(ev[3]) / nrep
 
     torch.cuda.synchronize()
     t0 = time.perf_counter()
