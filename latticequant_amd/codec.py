@@ -119,9 +119,33 @@ def _empty(n, dtype, dev):
     return torch.empty(int(n), dtype=dtype, device=dev)
 
 
+def _zero_views(dev, *parts):
+    """Zeroed device arrays, one per (n, dtype) part, cut from one buffer
+    cleared by one fill; each starts 256-byte aligned."""
+    sizes = [int(n) * torch.empty((), dtype=dt).element_size() for n, dt in parts]
+    offs, total = [], 0
+    for nb in sizes:
+        offs.append(total)
+        total += (nb + 255) // 256 * 256
+    z = torch.zeros(max(total, 256), dtype=torch.uint8, device=dev)
+    return [z[o:o + nb].view(dt) for (_, dt), o, nb in zip(parts, offs, sizes)]
+
+
+_BITS_CACHE = {}
+
+
 def _bits_tensor(bits, C, dev):
+    """Per-chunk rates on the device.  A single int rate gives a cached
+    read-only tensor per (C, rate, device), so a steady stream of same-shaped
+    batches launches no fill for it."""
     if isinstance(bits, int):
-        return torch.full((C,), bits, dtype=torch.int32, device=dev)
+        key = (int(C), int(bits), torch.device(dev))
+        t = _BITS_CACHE.get(key)
+        if t is None:
+            if len(_BITS_CACHE) > 256:
+                _BITS_CACHE.clear()
+            t = _BITS_CACHE[key] = torch.full((C,), bits, dtype=torch.int32, device=dev)
+        return t
     b = torch.as_tensor(list(bits), dtype=torch.int32)
     if b.numel() != C:
         raise ValueError("bits must be an int or one value per chunk")
@@ -214,8 +238,7 @@ def quantize_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None
     sym = _empty(C * nblk * L.LQ_SYM_STRIDE, torch.int8, dev)
     coset_bits = _empty(C * nblk * L.LQ_BLK // 8, torch.uint8, dev)
     blk_n1 = _empty(C * nblk, torch.int32, dev)
-    hist = _zeros(C * L.LQ_STREAMS * 256, torch.int32, dev)
-    status = _zeros(C, torch.int32, dev)
+    status, hist = _zero_views(dev, (C, torch.int32), (C * L.LQ_STREAMS * 256, torch.int32))
     deq = torch.empty_like(x)
     L.check(lib.lq_chunk_quantize(x.data_ptr(), dt, C, nh, bph, scale32.data_ptr(), fastdiv.data_ptr(), sym.data_ptr(),
                                   coset_bits.data_ptr(), blk_n1.data_ptr(), hist.data_ptr(), status.data_ptr(),
@@ -362,7 +385,12 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
     # vectors past the end are zero), so no fill
     coset_bits = _empty(C * nblk * L.LQ_BLK // 8, torch.uint8, dev)
     blk_n1 = _empty(C * nblk, torch.int32, dev)
-    status = _zeros(C, torch.int32, dev)
+    use_wide = wide is True
+    # one zero fill: the status flags, the int8 path's histogram and a leading
+    # zero before the chunks' word counts (so that one inclusive scan of
+    # [0, w_0 .. w_{C-2}] gives the chunk bases)
+    status, hist, cwz = _zero_views(dev, (C, torch.int32), (0 if use_wide else C * L.LQ_STREAMS * 256, torch.int32),
+                                    (C + 1, torch.int64))
     deq = torch.empty_like(x) if deq_out else None
     tables = _empty(C * L.LQ_STREAMS * L.TABLE_BYTES, torch.uint8, dev)
     dseed = None
@@ -371,10 +399,8 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
         if len(ds) != C:
             raise ValueError("dither_seed must be an int or one seed per chunk")
         dseed = torch.tensor(ds, dtype=torch.int64).to(dev)
-    use_wide = wide is True
     if not use_wide:
         sym = _empty(C * nblk * L.LQ_SYM_STRIDE, torch.int8, dev)
-        hist = _zeros(C * L.LQ_STREAMS * 256, torch.int32, dev)
         if rht_signs is not None:
             L.check(lib.lq_chunk_quantize_rht(x.data_ptr(), dt, C, nh, bph, hd, rht_signs.data_ptr(),
                                               scale32.data_ptr(), sym.data_ptr(), coset_bits.data_ptr(),
@@ -421,13 +447,13 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
     stream_nbits = _empty(C * L.LQ_STREAMS, torch.int64, dev)
     stream_state = _empty(C * L.LQ_STREAMS, torch.int32, dev)
     stream_woff = _empty(C * L.LQ_STREAMS, torch.int64, dev)
-    chunk_words = _empty(C, torch.int64, dev)
+    chunk_words = cwz[1:]
     enc_fn = lib.lq_chunk_encode_wide if use_wide else lib.lq_chunk_encode
     L.check(enc_fn(sym.data_ptr(), blk_n1.data_ptr(), C, V, tables.data_ptr(), work.data_ptr(),
                    blk_off.data_ptr(), blk_state.data_ptr(), stream_nbits.data_ptr(),
                    stream_state.data_ptr(), stream_woff.data_ptr(), chunk_words.data_ptr(), s),
             "lq_chunk_encode_wide" if use_wide else "lq_chunk_encode")
-    chunk_base = torch.cumsum(chunk_words, 0) - chunk_words
+    chunk_base = torch.cumsum(cwz[:C], 0)
     bound = words_bound(C, V)
     if words_out is not None:
         if words_out.numel() < bound:

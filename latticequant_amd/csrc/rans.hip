@@ -960,7 +960,8 @@ __global__ void k_chunk_offsets(const int64_t* __restrict__ stream_nbits, const 
 // held one per lane: within a 64-word slice, the block of word w is the last
 // block with fw_i <= w, i.e. the last block starting at or before the slice
 // (a ballot count) unless one of the few blocks starting inside the slice
-// (another ballot, walked on the scalar unit) has fw_i <= w.  Stream bit
+// (another ballot, walked on the scalar unit) has fw_i <= w.  The wave of a
+// stream's last group also writes the zero word after the stream.  Stream bit
 // positions are 32-bit (blk_off is uint32).
 constexpr int kPackBlocks = 32;
 
@@ -992,6 +993,8 @@ __global__ __launch_bounds__(256) void k_chunk_pack(int64_t n_streams_total, int
     const uint32_t W0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)((myof + 31u) >> 5));
     const uint32_t W1 = (uint32_t)__builtin_amdgcn_readlane((int)((myof + 31u) >> 5), nb);
     uint32_t* out = words + chunk_base[sid / LQ_STREAMS] + stream_woff[sid];
+    // the stream's trailing zero word, from the wave of its last group
+    if (g0 + nb >= nblk && lane == 0) out[((uint64_t)nbits + 31u) >> 5] = 0u;
     const uint32_t* scr0 = scratch + (sid * nblk + g0) * (int64_t)kCapW;
     constexpr uint32_t kCapBits = (uint32_t)kCapW * 32u;
     for (uint32_t wr = W0; wr < W1; wr += 256) {
@@ -1079,15 +1082,6 @@ __global__ __launch_bounds__(256) void k_chunk_pack(int64_t n_streams_total, int
             out[w] = res;
         }
     }
-}
-
-// trailing zero word of every present stream
-__global__ void k_chunk_tail(int64_t n_streams, const lq_table* __restrict__ tables, const int64_t* __restrict__ stream_nbits,
-                             const int64_t* __restrict__ stream_woff, const int64_t* __restrict__ chunk_base,
-                             uint32_t* __restrict__ words) {
-    int64_t sid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (sid >= n_streams || tables[sid].n_sym == 0) return;
-    words[chunk_base[sid / LQ_STREAMS] + stream_woff[sid] + (stream_nbits[sid] + 31) / 32] = 0u;
 }
 
 // ------------------------------------------------------------ chunk decode --
@@ -1606,9 +1600,6 @@ int lq_chunk_pack(int64_t n_chunks, int64_t n_vectors, const lq_table* d_tables,
     const int64_t jobs = ns_total * ((nblk + kPackBlocks - 1) / kPackBlocks);
     hipLaunchKernelGGL(k_chunk_pack, dim3((unsigned)((jobs + 3) / 4)), dim3(256), 0, s, ns_total, nblk, scratch,
                        d_blk_off, d_stream_nbits, d_stream_woff, d_chunk_base, d_tables, d_words);
-    const int64_t ns = n_chunks * LQ_STREAMS;
-    hipLaunchKernelGGL(k_chunk_tail, dim3((unsigned)((ns + 255) / 256)), dim3(256), 0, s, ns, d_tables,
-                       d_stream_nbits, d_stream_woff, d_chunk_base, d_words);
     return launch_status();
 }
 
