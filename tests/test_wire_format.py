@@ -198,3 +198,33 @@ def test_wire_round_trip_decodes_bit_exact_gpu(kind):
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
     # the reference-accounted bytes are what the payload carries for them
     assert int(r.reference_bytes().sum()) == int(enc.reference_bytes().sum())
+
+
+def test_zero_views_layout_cpu():
+    """encode_batch's shared zero fill: every part zeroed, 256-byte aligned,
+    of its own dtype and size, and disjoint from the others."""
+    from latticequant_amd import codec
+    st, hist, cwz = codec._zero_views("cpu", (5, torch.int32), (3 * 256, torch.int32), (6, torch.int64))
+    assert (st.dtype, hist.dtype, cwz.dtype) == (torch.int32, torch.int32, torch.int64)
+    assert (st.numel(), hist.numel(), cwz.numel()) == (5, 768, 6)
+    base = st.data_ptr()
+    for t in (st, hist, cwz):
+        assert (t.data_ptr() - base) % 256 == 0 and int(t.abs().sum()) == 0
+    st.fill_(-1)
+    hist.fill_(-1)
+    assert int(cwz.abs().sum()) == 0   # no overlap
+    assert hist.data_ptr() >= st.data_ptr() + 5 * 4 and cwz.data_ptr() >= hist.data_ptr() + 768 * 4
+    empty, = codec._zero_views("cpu", (0, torch.int32))
+    assert empty.numel() == 0
+
+
+def test_bits_tensor_cache_cpu():
+    """A single int rate gives one cached tensor per (C, rate, device); lists
+    are converted per call and checked for length."""
+    from latticequant_amd import codec
+    a = codec._bits_tensor(4, 3, "cpu")
+    assert a is codec._bits_tensor(4, 3, "cpu") and a.tolist() == [4, 4, 4]
+    assert codec._bits_tensor(5, 3, "cpu").tolist() == [5, 5, 5]
+    assert codec._bits_tensor([3, 4], 2, "cpu").tolist() == [3, 4]
+    with pytest.raises(ValueError):
+        codec._bits_tensor([3, 4], 3, "cpu")
