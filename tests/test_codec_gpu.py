@@ -117,6 +117,23 @@ def test_chunk_batch_and_roundtrip_gpu():
         assert torch.equal(out[c].cpu(), want)
 
 
+def test_prefilled_arena_gpu():
+    """Bound-sized arena full of ones (exact_size=False, words_out): every word
+    of every chunk, the streams' trailing zero words included, is written by
+    the encoder; chunk bases are the exclusive prefix of the word counts."""
+    codec, L = _lq()
+    g = torch.Generator().manual_seed(23)
+    x = torch.randn(3, 1, 4, 200, 128, generator=g).half()
+    V = 4 * 200 * 128 // 8
+    arena = torch.full((codec.words_bound(3, V),), -1, dtype=torch.int32, device="cuda")
+    enc, _ = codec.encode_batch(x.cuda(), 4, exact_size=False, words_out=arena, wide=False)
+    cw = enc.chunk_words.cpu().numpy()
+    np.testing.assert_array_equal(enc.chunk_base.cpu().numpy(), np.cumsum(cw) - cw)
+    for c in range(3):
+        sc32 = enc.scale32.view(3, -1)[c].cpu().numpy()
+        _compare_chunk(enc, c, O.compress_chunk(x[c].float().numpy(), 4, scales_f32=sc32))
+
+
 def test_empty_coset_and_zero_head_gpu():
     codec, L = _lq()
     t = torch.zeros(1, 2, 8, 64, dtype=torch.float16)
