@@ -952,7 +952,7 @@ __global__ void k_chunk_offsets(const int64_t* __restrict__ stream_nbits, const 
 
 // One wave per (stream, group of 32 blocks).  The group owns the stream
 // words whose first bit lies in its blocks' bit range; lane l assembles words
-// W0 + l + 64 k, four per round with all their scratch loads in flight
+// W0 + l + 64 k, kPackU per round with all their scratch loads in flight
 // (256-byte coalesced stores).  A word's first bits come from the
 // right-aligned scratch of the block holding its first bit; the rare word
 // that runs past that block's end continues block by block.  The block of
@@ -964,6 +964,7 @@ __global__ void k_chunk_offsets(const int64_t* __restrict__ stream_nbits, const 
 // stream's last group also writes the zero word after the stream.  Stream bit
 // positions are 32-bit (blk_off is uint32).
 constexpr int kPackBlocks = 32;
+constexpr int kPackU = 4;   // words per lane per round, their scratch loads all in flight
 
 __global__ __launch_bounds__(256) void k_chunk_pack(int64_t n_streams_total, int64_t nblk, const uint32_t* __restrict__ scratch,
                                                     const uint32_t* __restrict__ blk_off,
@@ -997,12 +998,12 @@ __global__ __launch_bounds__(256) void k_chunk_pack(int64_t n_streams_total, int
     if (g0 + nb >= nblk && lane == 0) out[((uint64_t)nbits + 31u) >> 5] = 0u;
     const uint32_t* scr0 = scratch + (sid * nblk + g0) * (int64_t)kCapW;
     constexpr uint32_t kCapBits = (uint32_t)kCapW * 32u;
-    for (uint32_t wr = W0; wr < W1; wr += 256) {
-        uint32_t lo[4], hi[4], clo[4], chi[4];
-        int blk[4], take[4], s2[4], cs[4];
-        uint32_t pe[4], nx[4];   // bit after the word's first segment; end of the next block
+    for (uint32_t wr = W0; wr < W1; wr += 64u * kPackU) {
+        uint32_t lo[kPackU], hi[kPackU], clo[kPackU], chi[kPackU];
+        int blk[kPackU], take[kPackU], s2[kPackU], cs[kPackU];
+        uint32_t pe[kPackU], nx[kPackU];   // bit after the word's first segment; end of the next block
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < kPackU; u++) {
             const uint32_t ws = wr + 64u * u;   // first word of the slice (wave-uniform)
             const uint32_t w = ws + lane;
             const bool ok = w < W1;
@@ -1045,7 +1046,7 @@ __global__ __launch_bounds__(256) void k_chunk_pack(int64_t n_streams_total, int
             nx[u] = on;
         }
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < kPackU; u++) {
             const uint32_t w = wr + 64u * u + lane;
             if (w >= W1) continue;
             uint64_t v = ((uint64_t)hi[u] << 32 | lo[u]) >> s2[u];
