@@ -46,7 +46,7 @@ extern "C" {
 /* per-chunk status bits written by the device */
 #define LQ_ST_SYM_OVERFLOW 1   /* a lattice symbol did not fit the staging type (int8: use the wide path) */
 #define LQ_ST_ALPHABET 2       /* a stream alphabet exceeded L */
-#define LQ_ST_TIE_UNPINNED 4   /* table of > 256 symbols hit an argsort tie at a cut */
+#define LQ_ST_TIE_UNPINNED 4   /* reserved, never raised: tables follow numpy's argsort order at every size */
 
 /* dtype codes for activations */
 #define LQ_F16 0
@@ -316,7 +316,9 @@ int lq_pack_compact(const float *d_q, int bits, int64_t n, uint8_t *d_packed, in
  * packed holds n_packed rows, fallback n_fallback; ranks past them (a mask
  * that selects more rows than the caller holds) are clamped, and a block with
  * no row at all is written as zeros: garbage out, no fault, no host check.
- * d_work: lq_merge_workspace(total) bytes. */
+ * d_work: lq_merge_workspace(total) bytes.  After the call the int32 at byte
+ * offset (tiles + 1) * 8 of d_work (tiles = ceil(total / 1024)) is nonzero if
+ * a tile's look-back wait did not end; d_out is then invalid. */
 int64_t lq_merge_workspace(int64_t total_blocks);
 int lq_fused_merge(const uint8_t *d_packed, int64_t n_packed, int bits, const uint16_t *d_fallback,
                    int64_t n_fallback, const uint8_t *d_mask, const float *d_scales, int64_t total_blocks,
@@ -330,10 +332,12 @@ int lq_fused_merge(const uint8_t *d_packed, int64_t n_packed, int bits, const ui
  * d_mask gets 1 / 0 per vector, d_repr_heads (nullable) the head of each
  * packed point in packed order, d_tile_off the number of in-range points
  * before each 1024-vector tile (what lq_compact_merge takes) and d_totals
- * (n_packed, n_fallback).  d_packed / d_fallback hold room for every vector
- * (n * b and n * 16 bytes); only the first d_totals rows are written.  No host
- * sync.  A look-back wait that does not end sets the error word after d_work's
- * tile words (4 bytes at offset (tiles + 1) * 8).  d_work: lq_compact_encode_workspace(n) bytes (cleared by the call).
+ * (3 int64: n_packed, n_fallback, error word).  d_packed / d_fallback hold
+ * room for every vector (n * b and n * 16 bytes); only the first d_totals rows
+ * are written.  No host sync.  The error word is cleared by the call and set
+ * when a tile's look-back wait does not end; every output is then invalid, so
+ * a caller reads it with the counts (one copy) and discards the batch.
+ * d_work: lq_compact_encode_workspace(n) bytes (cleared by the call).
  * Replaces core/compact_storage.py:338-357 (quantize_and_pack) with the fp16
  * fallback of the fixed-rate cache (llm/fused_triton_merge.py chunk fields). */
 int64_t lq_compact_encode_workspace(int64_t n);
@@ -466,15 +470,18 @@ int lq_resident_attention(const lq_resident *k, const lq_resident *v, int64_t t_
  * allocate device memory (code under HIP graph capture, serving loops that
  * forbid hipMalloc).  No counterpart in the reference.  The counters and split
  * records live in a file-scope device array of LQ_RES_ATTN_SCRATCH_BYTES per
- * device, held until the process ends; its address is looked up (and the array
- * cleared) on the first call on each device, with that device current.  The
+ * device, held until the process ends; its address is looked up (and its
+ * counter region cleared by a fill kernel) on the first call on each device,
+ * with that device current: make that first call outside stream capture.  The
  * array holds completion counters for up to 1024 kv heads at a fixed place
  * (each completed call leaves them zero) and then the split records: a step
  * with more kv heads, or whose records exceed the rest of the array, returns
  * LQ_ERR_SCRATCH without launching.  Nothing is allocated: no hipMalloc or
  * hipFree.  Calls on one device share the array, so calls that overlap on one
  * GPU (different streams, or different host threads) race; calls in stream
- * order do not.  Results equal lq_resident_attention's. */
+ * order do not.  Results equal lq_resident_attention's within 2 fp16 ulps
+ * (prefix tiles are dealt to waves dynamically, so the summation order of a
+ * head's partial results can differ between calls). */
 int lq_resident_attention_noalloc(const lq_resident *k, const lq_resident *v, int64_t t_prefix, const uint16_t *d_q,
                                   int group, const uint16_t *d_tail_k, const uint16_t *d_tail_v, int64_t t_tail,
                                   uint16_t *d_out, hipStream_t s);

@@ -44,9 +44,8 @@ class RANSTable:
     cumfreqs: np.ndarray    # (n_symbols + 1,) int32
     alphabet: List[int]
     n_symbols: int
-    # LQ_ST_TIE_UNPINNED when an alphabet above 256 symbols hit an argsort tie
-    # at the adjustment cut: numpy's tie order there is not restated, a stable
-    # (count, index) order is used instead
+    # device status bits of the table build (0: the table equals build_rans_table's,
+    # numpy's argsort tie order included)
     status: int = 0
 
 

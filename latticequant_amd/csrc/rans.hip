@@ -16,6 +16,7 @@
 // exact, and identical to a serial encode.
 #include <climits>
 
+#include "lq_argsort.h"
 #include "lq_decode.h"
 
 using namespace lq;
@@ -37,13 +38,6 @@ inline int64_t device_cus() {
     return cache[dev];
 }
 
-// ---------------------------------------------------------------------------
-// numpy.argsort tie order.  numpy's argsort on x86 AVX512 hosts runs
-// x86-simd-sort: for n <= 256, a bitonic network over 8-lane registers padded
-// with the type maximum, in which each comparator leaves equal keys in place.
-// Executed here stage by stage in LDS, one comparator per thread.
-// ---------------------------------------------------------------------------
-
 // The table code runs on a cooperative group: a whole workgroup (one stream
 // per workgroup), or one wave (one stream per wave, wave-synchronous: no
 // workgroup barrier).  G::tid / G::size / G::sync are the group's lane, size
@@ -64,80 +58,6 @@ struct WaveGroup {
     }
     static constexpr bool kWave = true;
 };
-
-__device__ __forceinline__ void cmpx(int64_t* k, int16_t* a, int p, int q) {
-    int64_t kp = k[p], kq = k[q];
-    if (kp > kq) {
-        k[p] = kq; k[q] = kp;
-        int16_t t = a[p]; a[p] = a[q]; a[q] = t;
-    }
-}
-
-// first lane of each of the 4 comparators of an in-register stage with partner i ^ m
-__device__ __forceinline__ int pair_lane(int m, int p) {
-    switch (m) {
-        case 1: return 2 * p;                      // 0 2 4 6
-        case 2: case 3: return (p & 1) | ((p >> 1) << 2);   // 0 1 4 5
-        default: return p;                         // m = 4, 7: 0 1 2 3
-    }
-}
-
-template <typename G>
-__device__ void reg_stage(int64_t* k, int16_t* a, int nv, int m) {
-    for (int t = G::tid(); t < nv * 4; t += G::size()) {
-        int reg = t >> 2, i = pair_lane(m, t & 3);
-        cmpx(k, a, reg * 8 + i, reg * 8 + (i ^ m));
-    }
-    G::sync();
-}
-
-// keys k[0..n) (int64), pad = value larger than every key; result in a[0..n).
-template <typename G>
-__device__ void net_argsort(int64_t* k, int16_t* a, int n) {
-    int nv = 1;
-    while (nv * 8 < n) nv *= 2;
-    for (int i = G::tid(); i < nv * 8; i += G::size()) {
-        if (i >= n) k[i] = INT64_MAX;
-        a[i] = (int16_t)(i < n ? i : -1);
-    }
-    G::sync();
-    const int s8[6] = {1, 3, 1, 7, 2, 1};
-    for (int st = 0; st < 6; st++) reg_stage<G>(k, a, nv, s8[st]);
-    for (int per = 2; per <= nv; per *= 2) {
-        for (int t = G::tid(); t < nv * 4; t += G::size()) {   // mirror compare across registers
-            int grp = t / (per * 4), rem = t % (per * 4);
-            int i = rem / 8, l = rem % 8, off = grp * per;
-            cmpx(k, a, 8 * (off + i) + l, 8 * (off + per - 1 - i) + 7 - l);
-        }
-        G::sync();
-        for (int num = per / 2; num >= 2; num /= 2) {               // register half cleaners
-            for (int t = G::tid(); t < nv * 4; t += G::size()) {
-                int grp = t / (per * 4), rem = t % (per * 4);
-                int l = rem % 8, q = rem / 8;
-                int jj = q / (num / 2), i = q % (num / 2);
-                int r1 = grp * per + jj * num + i;
-                cmpx(k, a, 8 * r1 + l, 8 * (r1 + num / 2) + l);
-            }
-            G::sync();
-        }
-        reg_stage<G>(k, a, nv, 4);
-        reg_stage<G>(k, a, nv, 2);
-        reg_stage<G>(k, a, nv, 1);
-    }
-}
-
-// Stable order (key, index) for n > 256, where numpy runs a SIMD quicksort
-// whose tie order is not restated; the caller flags ties at a cut.
-template <typename G>
-__device__ void rank_argsort(const int64_t* k, int16_t* a, int n) {
-    for (int i = G::tid(); i < n; i += G::size()) {
-        int64_t ki = k[i];
-        int r = 0;
-        for (int j = 0; j < n; j++) r += (k[j] < ki) || (k[j] == ki && j < i);
-        a[r] = (int16_t)i;
-    }
-    G::sync();
-}
 
 // Block-wide sum of v (G::size() multiple of 64, <= 1024).
 template <typename G>
@@ -188,13 +108,15 @@ __device__ void bitonic_sort_u64(uint64_t* c, int N) {
     }
 }
 
-// adjust_pass for alphabets above 256 symbols: the stable (key, index) order
-// (the order the tie flag stands for) from one bitonic sort of composite keys
-// instead of per-entry rank counts.  At most one tie group straddles the cut
-// at sorted position rem: the one holding positions rem - 1 and rem.
+// adjust_pass for alphabets above 256 symbols: the members of the set
+// (the first rem entries of the argsort order) that do not depend on the tie
+// order, from one bitonic sort of composite (key, index) keys instead of
+// per-entry rank counts.  At most one tie group straddles the cut at sorted
+// position rem: the one holding positions rem - 1 and rem.  Returns (group
+// uniform) whether a different subset of that group would change a frequency.
 template <typename G>
-__device__ void adjust_pass_sorted(int n, int32_t* freqs, int diff, int full, int rem, const int64_t* kk, int16_t* a,
-                                   int8_t* inset, uint64_t* sk, int* st) {
+__device__ bool adjust_pass_sorted(int n, const int32_t* freqs, int diff, int full, int rem, const int64_t* kk,
+                                   int16_t* a, int8_t* inset, uint64_t* sk) {
     int N = 512;
     while (N < n) N <<= 1;
     for (int i = G::tid(); i < N; i += G::size())   // kk in [-(2^32 - 1), 0]: biased key in 33 bits
@@ -213,7 +135,7 @@ __device__ void adjust_pass_sorted(int n, int32_t* freqs, int diff, int full, in
         for (int p = G::tid(); p < n; p += G::size())
             if ((sk[p] >> 11) == kstar && (diff > 0 || freqs[a[p]] - full > 1)) matters = 1;
     }
-    if (block_sum<G>(matters) != 0 && G::tid() == 0) *st |= LQ_ST_TIE_UNPINNED;
+    return block_sum<G>(matters) != 0;
 }
 
 // One pass of the build_rans_table adjustment loop (core/gpu_ans.py:73-84)
@@ -222,42 +144,31 @@ __device__ void adjust_pass_sorted(int n, int32_t* freqs, int diff, int full, in
 // once more; an increment adds its visits, a decrement leaves
 // max(f - visits, 1).  The argsort tie order only matters for the tie group
 // straddling position rem, and only if a different subset of that group would
-// change a frequency; the numpy network runs only then.
+// change a frequency; numpy's argsort (np_argsort) runs only then.
 template <typename G>
-__device__ void adjust_pass(const int64_t* counts, int n, int32_t* freqs, int diff, int64_t* k, int16_t* a,
-                            int64_t* kk, int8_t* inset, int* st, uint64_t* sk) {
+__device__ void adjust_pass(const int64_t* counts, int n, int32_t* freqs, int diff, int16_t* a, int64_t* kk,
+                            int8_t* inset, NpScratch* ns, uint64_t* sk) {
     const int m = diff > 0 ? diff : -diff;
     const int full = m / n, rem = m % n;
     for (int i = G::tid(); i < n; i += G::size()) kk[i] = diff > 0 ? -counts[i] : -(int64_t)freqs[i];
     G::sync();
+    bool matters;
     if (n > 256 && sk) {
-        adjust_pass_sorted<G>(n, freqs, diff, full, rem, kk, a, inset, sk, st);
+        matters = adjust_pass_sorted<G>(n, freqs, diff, full, rem, kk, a, inset, sk);
+    } else {
+        int mt = 0;
         for (int i = G::tid(); i < n; i += G::size()) {
-            const int v = full + (inset[i] == 1 ? 1 : 0);
-            const int f = freqs[i];
-            freqs[i] = diff > 0 ? f + v : (f - v > 1 ? f - v : 1);
+            const int64_t ki = kk[i];
+            int lt = 0, eq = 0;
+            for (int j = 0; j < n; j++) { lt += kk[j] < ki; eq += kk[j] == ki; }
+            const int8_t in = lt + eq <= rem ? 1 : (lt >= rem ? 0 : 2);
+            inset[i] = in;
+            if (in == 2 && (diff > 0 || freqs[i] - full > 1)) mt = 1;
         }
-        G::sync();
-        return;
+        matters = block_sum<G>(mt) != 0;
     }
-    int matters = 0;
-    for (int i = G::tid(); i < n; i += G::size()) {
-        const int64_t ki = kk[i];
-        int lt = 0, eq = 0;
-        for (int j = 0; j < n; j++) { lt += kk[j] < ki; eq += kk[j] == ki; }
-        const int8_t in = lt + eq <= rem ? 1 : (lt >= rem ? 0 : 2);
-        inset[i] = in;
-        if (in == 2 && (diff > 0 || freqs[i] - full > 1)) matters = 1;
-    }
-    if (block_sum<G>(matters) != 0) {
-        for (int i = G::tid(); i < n; i += G::size()) k[i] = kk[i];
-        G::sync();
-        if (n <= 256) {
-            net_argsort<G>(k, a, n);
-        } else {   // numpy's quicksort tie order is not restated for n > 256
-            rank_argsort<G>(kk, a, n);
-            if (G::tid() == 0) *st |= LQ_ST_TIE_UNPINNED;
-        }
+    if (matters) {
+        np_argsort<G>(kk, a, n, ns);
         for (int p = G::tid(); p < n; p += G::size()) inset[a[p]] = p < rem ? 1 : 0;
         G::sync();
     }
@@ -270,8 +181,8 @@ __device__ void adjust_pass(const int64_t* counts, int n, int32_t* freqs, int di
 }
 
 // build_rans_table normalisation (core/gpu_ans.py:62-86) on LDS arrays:
-// counts[n] (int64) in, freqs[n] (int32) out; k, a: network scratch (256),
-// kk, inset: n entries.  Status bits (LQ_ST_TIE_UNPINNED) go to *st.
+// counts[n] (int64) in, freqs[n] (int32) out; a, kk, inset: n entries;
+// ns: argsort scratch; sk (optional, alphabets above 256): 2048 entries.
 //
 // An increment pass always reaches sum == L.  In the decrement branch the
 // excess is below n (only the max(., 1) bumps exceed L), so a pass whose
@@ -283,8 +194,8 @@ __device__ void adjust_pass(const int64_t* counts, int n, int32_t* freqs, int di
 // is nondecreasing: a binary search over t in [0, max f - 1], not one pass
 // per t (a single dominant symbol makes t as large as the excess).
 template <typename G>
-__device__ void normalise(const int64_t* counts, int n, int32_t* freqs, int64_t* k, int16_t* a, int64_t* kk,
-                          int8_t* inset, int* st, uint64_t* sk = nullptr) {
+__device__ void normalise(const int64_t* counts, int n, int32_t* freqs, int16_t* a, int64_t* kk, int8_t* inset,
+                          NpScratch* ns, uint64_t* sk = nullptr) {
     int64_t tl = 0;
     for (int i = G::tid(); i < n; i += G::size()) tl += counts[i];
     const int64_t total = block_sum<G>(tl);
@@ -301,7 +212,7 @@ __device__ void normalise(const int64_t* counts, int n, int32_t* freqs, int64_t*
     }
     const int diff = (int)(kL - block_sum<G>(fl));
     if (diff > 0) {
-        adjust_pass<G>(counts, n, freqs, diff, k, a, kk, inset, st, sk);
+        adjust_pass<G>(counts, n, freqs, diff, a, kk, inset, ns, sk);
     } else if (diff < 0) {
         const int excess0 = -diff;
         int64_t fm = 0;
@@ -324,7 +235,7 @@ __device__ void normalise(const int64_t* counts, int n, int32_t* freqs, int64_t*
         const int excess = (int)(excess0 - C(t));
         for (int i = G::tid(); i < n; i += G::size()) freqs[i] = freqs[i] - t > 1 ? freqs[i] - t : 1;
         G::sync();
-        if (excess > 0) adjust_pass<G>(counts, n, freqs, -excess, k, a, kk, inset, st, sk);
+        if (excess > 0) adjust_pass<G>(counts, n, freqs, -excess, a, kk, inset, ns, sk);
     }
 }
 
@@ -387,7 +298,7 @@ __global__ __launch_bounds__(256) void k_chunk_tables(const uint32_t* __restrict
                                                       lq_table* __restrict__ tables, int32_t* __restrict__ status) {
     __shared__ int64_t counts[LQ_MAXSYM];
     __shared__ int32_t freqs[LQ_MAXSYM];
-    __shared__ int64_t keys[256];
+    __shared__ NpScratch ns;
     __shared__ int16_t perm[LQ_MAXSYM];
     __shared__ uint32_t h[256];
     __shared__ int s_min, s_max, s_st;
@@ -438,11 +349,10 @@ __global__ __launch_bounds__(256) void k_chunk_tables(const uint32_t* __restrict
         atomicAdd(&s_tot, tl);
     }
     __syncthreads();
-    // n <= 1028; the network holds 256 keys (larger alphabets take the rank path)
     __shared__ int64_t kk[LQ_MAXSYM];
     __shared__ int8_t inset[LQ_MAXSYM];
     __shared__ uint64_t sk[WIDE ? 2048 : 1];   // wide alphabets: composite sort keys
-    normalise<BlockGroup>(counts, n, freqs, keys, perm, kk, inset, &s_st, WIDE ? sk : nullptr);
+    normalise<BlockGroup>(counts, n, freqs, perm, kk, inset, &ns, WIDE ? sk : nullptr);
     __shared__ int32_t cum[LQ_MAXSYM + 1];
     exclusive_scan_array<BlockGroup>(freqs, n, cum);
     for (int i = tid; i < n; i += 256) T->enc[i] = enc_pack((uint32_t)freqs[i], (uint32_t)cum[i]);
@@ -466,7 +376,7 @@ __global__ __launch_bounds__(64 * kTabWaves) void k_chunk_tables_wave(const uint
                                                                       int32_t* __restrict__ status) {
     __shared__ int64_t counts[kTabWaves][kCap8];
     __shared__ int32_t freqs[kTabWaves][kCap8];
-    __shared__ int64_t keys[kTabWaves][256];
+    __shared__ NpScratch ns[kTabWaves];
     __shared__ int16_t perm[kTabWaves][kCap8];
     __shared__ int64_t kk[kTabWaves][kCap8];
     __shared__ int8_t inset[kTabWaves][kCap8];
@@ -508,7 +418,7 @@ __global__ __launch_bounds__(64 * kTabWaves) void k_chunk_tables_wave(const uint
     }
     if (lane == 0) s_st[w] = 0;
     WaveGroup::sync();
-    normalise<WaveGroup>(counts[w], n, freqs[w], keys[w], perm[w], kk[w], inset[w], &s_st[w]);
+    normalise<WaveGroup>(counts[w], n, freqs[w], perm[w], kk[w], inset[w], &ns[w]);
     exclusive_scan_array<WaveGroup>(freqs[w], n, cum[w]);
     for (int i = lane; i < n; i += 64) T->enc[i] = enc_pack((uint32_t)freqs[w][i], (uint32_t)cum[w][i]);
     if (lane == 0) {
@@ -1394,7 +1304,7 @@ __global__ __launch_bounds__(256) void k_build_tables(const int64_t* __restrict_
                                                       int32_t* __restrict__ status) {
     __shared__ int64_t cnt[kL];
     __shared__ int32_t fr[kL];
-    __shared__ int64_t keys[kL];
+    __shared__ NpScratch ns;
     __shared__ int16_t perm[kL];
     __shared__ int s_st;
     const int t = blockIdx.x;
@@ -1409,7 +1319,7 @@ __global__ __launch_bounds__(256) void k_build_tables(const int64_t* __restrict_
     __syncthreads();
     __shared__ int64_t kk[kL];
     __shared__ int8_t inset[kL];
-    normalise<BlockGroup>(cnt, n, fr, keys, perm, kk, inset, &s_st);
+    normalise<BlockGroup>(cnt, n, fr, perm, kk, inset, &ns);
     __shared__ int32_t cum[kL + 1];
     exclusive_scan_array<BlockGroup>(fr, n, cum);
     for (int i = threadIdx.x; i < n; i += 256) freqs_out[o + i] = fr[i];

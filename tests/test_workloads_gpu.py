@@ -56,34 +56,40 @@ def _student_k(seed, T):
     return k.astype(np.float16)
 
 
-def test_c4_full_size_layers_gpu():
+@pytest.mark.parametrize("layer", [0, 1, 2])
+def test_c4_full_size_layers_gpu(layer):
+    """C4 at full size ([1, 4, 16384, 128] per chunk), one layer of the
+    3 / 4 / 5-bit cycle per case: V bit-exact against the oracle; K (Student-t
+    with outlier channels, int16 symbols) with every stream's table and words
+    equal to the oracle's, or AlphabetError where an alphabet exceeds L."""
     from latticequant_amd import codec
     from latticequant_amd.allocation.eval_alloc import cyclic_schedule
+    from tests.test_wide_gpu import check_chunk
     T = 16384
-    sched = cyclic_schedule(3, seed=0)
-    rng = np.random.default_rng(2026)
-    for layer, s in enumerate(sched):
-        # V: N(0,1), bit-exact against the oracle at full size
-        v = rng.standard_normal((1, 4, T, 128)).astype(np.float16)
-        ev, _ = codec.encode_batch(torch.from_numpy(v).cuda()[None], s["V"])
-        chv = O.compress_chunk(v, s["V"], scales_f32=ev.scale32.cpu().numpy())
-        np.testing.assert_array_equal(ev.words[:int(ev.chunk_words[0])].cpu().numpy().view(np.uint32), chv.bitstream)
-        # K: alphabet sizes from the device's own lattice points decide the outcome
-        k = _student_k(layer, T)
-        kk = torch.from_numpy(k).cuda()
-        q, s32, _ = codec.quantize_points(kk, s["K"])
-        coset, free, c8h = O.e8_to_symbols(q.cpu().numpy())
-        syms = np.concatenate([free, c8h[:, None]], 1)
-        widest = max(int(syms[coset == c][:, i].max() - syms[coset == c][:, i].min() + 5)
-                     for c in (0, 1) for i in range(8) if (coset == c).any())
-        if widest > O.L:
-            with pytest.raises(codec.AlphabetError):
-                codec.encode_batch(kk[None], s["K"], scale32=s32)
-            continue
-        ek, deq = codec.encode_batch(kk[None], s["K"], scale32=s32, deq_out=True)
-        assert widest <= 264 or ek.extra["wide"]
-        want = (q.view(4, -1, 8) * ek.scale16.float().view(4, 1, 1)).view(kk.shape).half()
-        assert torch.equal(codec.decode_batch(ek)[0], want)   # lossless coding of the lattice points
+    s = cyclic_schedule(3, seed=0)[layer]
+    rng = np.random.default_rng(2026 + layer)
+    v = rng.standard_normal((1, 4, T, 128)).astype(np.float16)
+    ev, _ = codec.encode_batch(torch.from_numpy(v).cuda()[None], s["V"])
+    chv = O.compress_chunk(v, s["V"], scales_f32=ev.scale32.cpu().numpy())
+    np.testing.assert_array_equal(ev.words[:int(ev.chunk_words[0])].cpu().numpy().view(np.uint32), chv.bitstream)
+    # K: alphabet sizes from the device's own lattice points decide the outcome
+    k = _student_k(layer, T)
+    kk = torch.from_numpy(k).cuda()
+    q, s32, _ = codec.quantize_points(kk, s["K"])
+    coset, free, c8h = O.e8_to_symbols(q.cpu().numpy())
+    syms = np.concatenate([free, c8h[:, None]], 1)
+    widest = max(int(syms[coset == c][:, i].max() - syms[coset == c][:, i].min() + 5)
+                 for c in (0, 1) for i in range(8) if (coset == c).any())
+    if widest > O.L:
+        with pytest.raises(codec.AlphabetError):
+            codec.encode_batch(kk[None], s["K"], scale32=s32)
+        return
+    ek, deq = codec.encode_batch(kk[None], s["K"], scale32=s32, deq_out=True)
+    assert widest <= 264 or ek.extra["wide"]
+    want = (q.view(4, -1, 8) * ek.scale16.float().view(4, 1, 1)).view(kk.shape).half()
+    assert torch.equal(codec.decode_batch(ek)[0], want)   # lossless coding of the lattice points
+    chk = O.compress_chunk(k, s["K"], scales_f32=s32.cpu().numpy())
+    assert check_chunk(ek, 0, chk) == widest
 
 
 def test_c5_full_chunk_round_trip_gpu():
