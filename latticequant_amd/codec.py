@@ -137,14 +137,20 @@ _BITS_CACHE = {}
 def _bits_tensor(bits, C, dev):
     """Per-chunk rates on the device.  A single int rate gives a cached
     read-only tensor per (C, rate, device), so a steady stream of same-shaped
-    batches launches no fill for it."""
+    batches launches no fill for it.  Kernels on any stream may read a cached
+    entry: its fill is complete before it is first returned (one stream
+    synchronisation per entry), and entries are never freed while the process
+    runs; past 256 entries a new shape gets a per-call tensor, which only the
+    current stream reads."""
     if isinstance(bits, int):
         key = (int(C), int(bits), torch.device(dev))
         t = _BITS_CACHE.get(key)
         if t is None:
-            if len(_BITS_CACHE) > 256:
-                _BITS_CACHE.clear()
-            t = _BITS_CACHE[key] = torch.full((C,), bits, dtype=torch.int32, device=dev)
+            t = torch.full((C,), bits, dtype=torch.int32, device=dev)
+            if len(_BITS_CACHE) < 256:
+                if t.is_cuda:
+                    torch.cuda.current_stream(t.device).synchronize()
+                _BITS_CACHE[key] = t
         return t
     b = torch.as_tensor(list(bits), dtype=torch.int32)
     if b.numel() != C:
@@ -270,7 +276,7 @@ class CompactBatch:
     fallback: torch.Tensor     # (V, 8) fp16; rows < totals[1] hold the out-of-range vectors
     repr_heads: torch.Tensor   # (V,) int32; rows < totals[0]: head of each packed point
     tile_off: torch.Tensor     # (tiles,) int64: packed points before each 1024-vector tile
-    totals: torch.Tensor       # (2,) int64: (n_packed, n_fallback)
+    totals: torch.Tensor       # (3,) int64: (n_packed, n_fallback, look-back error word)
     scale32: torch.Tensor      # (n_heads,) fp32 quantization scales
     scale16: torch.Tensor      # (n_heads,) fp16 stored scales
     shape: tuple
@@ -300,7 +306,7 @@ def compact_encode(t: torch.Tensor, bits: int, storage_bits: Optional[int] = Non
     fallback = _empty(V * 8, torch.float16, dev).view(V, 8)
     heads = _empty(V, torch.int32, dev)
     tile_off = _empty(tiles, torch.int64, dev)
-    totals = _empty(2, torch.int64, dev)
+    totals = _empty(3, torch.int64, dev)
     work = _empty(lib.lq_compact_encode_workspace(V), torch.uint8, dev)
     L.check(lib.lq_compact_encode(x.data_ptr(), L.dtype_code(x.dtype), nh, bph, scale32.data_ptr(), fastdiv.data_ptr(),
                                   scale16.data_ptr(), sb, mask.data_ptr(), packed.data_ptr(), fallback.data_ptr(),
@@ -308,6 +314,20 @@ def compact_encode(t: torch.Tensor, bits: int, storage_bits: Optional[int] = Non
                                   L.stream_ptr(dev)), "lq_compact_encode")
     return CompactBatch(mask=mask, packed=packed, fallback=fallback, repr_heads=heads, tile_off=tile_off,
                         totals=totals, scale32=scale32, scale16=scale16, shape=(B, H, T, hd), bph=bph, bits=sb)
+
+
+class LookbackError(RuntimeError):
+    """A chained look-back wait did not end within its spin limit: the ranks,
+    offsets and totals of that launch are invalid."""
+
+
+def compact_counts(totals) -> tuple:
+    """(n_packed, n_fallback) from a CompactBatch's totals, read to the host in
+    one copy; raises LookbackError when the launch set its error word."""
+    n_repr, n_oor, err = (int(v) for v in totals.tolist())
+    if err:
+        raise LookbackError("lq_compact_encode: a tile look-back wait did not end; the batch is invalid")
+    return n_repr, n_oor
 
 
 def compact_merge(cb: CompactBatch, out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -579,6 +599,13 @@ class PendingEncode:
 
     def _meta(self) -> torch.Tensor:
         return torch.cat([self._enc.status.to(torch.int64), self._enc.chunk_words])
+
+    def retained_bytes(self) -> int:
+        """Device bytes this unsettled batch keeps alive: the stacked input
+        (kept for an int16 re-encode) and the bound-sized bitstream arena."""
+        if self._done is not None or self._error is not None or self._enc is None:
+            return 0
+        return self._x.numel() * self._x.element_size() + self._enc.words.numel() * self._enc.words.element_size()
 
     def ready(self) -> bool:
         """Settled, or tracked and its read-back has arrived (non-blocking)."""

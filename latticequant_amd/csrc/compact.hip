@@ -155,9 +155,12 @@ __device__ int64_t tile_lookback(uint64_t* status, int64_t t, int64_t count, int
     return excl;
 }
 
-__global__ void k_zero64(uint64_t* __restrict__ p, int64_t n) {
+// Clears p[0 .. n) and, when given, the one word *extra (an error word kept
+// beside the caller's totals).
+__global__ void k_zero64(uint64_t* __restrict__ p, int64_t n, int64_t* __restrict__ extra) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
         p[i] = 0ull;
+    if (extra && blockIdx.x == 0 && threadIdx.x == 0) *extra = 0;
 }
 
 // One tile of kTile blocks per workgroup; ranks from the tile offset plus
@@ -367,7 +370,8 @@ int lq_fused_merge(const uint8_t* d_packed, int64_t n_packed, int bits, const ui
     uint64_t* status = reinterpret_cast<uint64_t*>(d_work);
     uint32_t* ticket = reinterpret_cast<uint32_t*>(status + tiles);
     int32_t* err = reinterpret_cast<int32_t*>(status + tiles + 1);
-    hipLaunchKernelGGL(k_zero64, dim3((unsigned)((tiles + 2 + 255) / 256)), dim3(256), 0, s, status, tiles + 2);
+    hipLaunchKernelGGL(k_zero64, dim3((unsigned)((tiles + 2 + 255) / 256)), dim3(256), 0, s, status, tiles + 2,
+                       (int64_t*)nullptr);
     hipLaunchKernelGGL(k_merge<true>, dim3((unsigned)tiles), dim3(kTileThreads), 0, s, d_packed, bits, d_fallback, d_mask,
                        d_scales, total_blocks, bph, n_packed, n_fallback, nullptr, d_out, status, ticket, err);
     return launch_status();
@@ -375,7 +379,7 @@ int lq_fused_merge(const uint8_t* d_packed, int64_t n_packed, int bits, const ui
 
 int64_t lq_compact_encode_workspace(int64_t n) {
     if (n < 0) return -1;
-    return ((n + kTile - 1) / kTile + 2) * 8;   // tile status words, then the ticket counter and error flag
+    return ((n + kTile - 1) / kTile + 1) * 8;   // tile status words, then the ticket counter
 }
 
 int lq_compact_encode(const void* d_x, int dtype, int64_t n_heads, int64_t bph, const float* d_scale32,
@@ -390,8 +394,9 @@ int lq_compact_encode(const void* d_x, int dtype, int64_t n_heads, int64_t bph, 
     const int64_t tiles = (n + kTile - 1) / kTile;
     uint64_t* status = reinterpret_cast<uint64_t*>(d_work);
     uint32_t* ticket = reinterpret_cast<uint32_t*>(status + tiles);
-    int32_t* err = reinterpret_cast<int32_t*>(status + tiles + 1);
-    hipLaunchKernelGGL(k_zero64, dim3((unsigned)((tiles + 2 + 255) / 256)), dim3(256), 0, s, status, tiles + 2);
+    int32_t* err = reinterpret_cast<int32_t*>(d_totals + 2);   // read back with the totals
+    hipLaunchKernelGGL(k_zero64, dim3((unsigned)((tiles + 1 + 255) / 256)), dim3(256), 0, s, status, tiles + 1,
+                       d_totals + 2);
     hipLaunchKernelGGL(k_compact_encode, dim3((unsigned)tiles), dim3(kTileThreads), 0, s, d_x, dtype, n, bph, d_scale32,
                        d_fastdiv, d_scale16, bits, d_mask, d_packed, d_fallback, d_repr_heads, d_tile_off, d_totals,
                        status, ticket, err);

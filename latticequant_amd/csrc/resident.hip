@@ -986,9 +986,10 @@ __global__ void k_zero_u32(uint32_t* p, int64_t n) {
 }
 
 // Device address of the current device's scratch array.  On the first call
-// per device: look it up and clear it (a fill kernel on s, stream-ordered
-// before the caller's launch; the counters must start at zero and every
-// completed step leaves them zero).
+// per device: look it up and clear its counter region (a fill kernel on s,
+// stream-ordered before the caller's launch; the counters must start at zero
+// and every completed step leaves them zero; the split records are written
+// before they are read).
 int scratch_ptr(void** out, hipStream_t s) {
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return LQ_ERR_ARG;
@@ -997,7 +998,7 @@ int scratch_ptr(void** out, hipStream_t s) {
         void* p = nullptr;
         if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return LQ_ERR_LAUNCH;
         hipLaunchKernelGGL(k_zero_u32, dim3(256), dim3(256), 0, s, static_cast<uint32_t*>(p),
-                           (int64_t)LQ_RES_ATTN_SCRATCH_BYTES / 4);
+                           kScratchCounterBytes / 4);
         if (hipGetLastError() != hipSuccess) return LQ_ERR_LAUNCH;
         g_scratch[dev] = p;
     }

@@ -331,13 +331,20 @@ class CompressedKVCache(DynamicCache):
             self._pending.append((pend, chunks))
         return out
 
+    # small (untracked) pending batches are settled together once this many
+    # are pending, or once they keep this many device bytes alive
+    SETTLE_SMALL_COUNT = 256
+    SETTLE_SMALL_BYTES = 256 << 20
+
     def _settle_ready(self):
         """Settle the batches whose status read-back has arrived (non-blocking),
-        and, once 256 small (untracked) batches are pending, all of those with
+        and, once SETTLE_SMALL_COUNT small (untracked) batches are pending or
+        they retain SETTLE_SMALL_BYTES of input and arena, all of those with
         one copy: their chunks move to the exact-size arena (or the int16
         re-encode)."""
         small = [p for p, _ in self._pending if not p.tracked]
-        if len(small) >= 256:
+        if small and (len(small) >= self.SETTLE_SMALL_COUNT
+                      or sum(p.retained_bytes() for p in small) >= self.SETTLE_SMALL_BYTES):
             codec.settle_many(small)
         keep = []
         for pend, chunks in self._pending:
@@ -526,13 +533,14 @@ def compress_fixed_rate(tensor: torch.Tensor, bits_per_dim: int = 4, storage_bit
     same), out-of-range vectors as fp16 fallback.  Scales are the fp16-stored
     ones widened to fp32, so merge output equals _decompress_chunk's.  One
     compaction pass on the device (codec.compact_encode); the only host sync
-    reads the two row counts that size the chunk's tensors."""
+    reads the two row counts that size the chunk's tensors, with the launch's
+    look-back error word (codec.LookbackError if it is set)."""
     B, H, T, hd = tensor.shape
     if hd % 8:
         raise ValueError("head_dim must be a multiple of 8")
     x = (tensor.cuda() if not tensor.is_cuda else tensor).contiguous()
     cb = codec.compact_encode(x, bits_per_dim, storage_bits, scale32)
-    n_repr, n_oor = (int(v) for v in cb.totals.tolist())
+    n_repr, n_oor = codec.compact_counts(cb.totals)
     nh, bph = B * H, T * hd // 8
     return CompressedChunk(repr_mask=cb.mask.bool(), packed=cb.packed[:n_repr], fallback=cb.fallback[:n_oor],
                            scales=cb.scale16.float(), repr_head_ids=cb.repr_heads[:n_repr],

@@ -18,6 +18,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib as L
+from .. import codec
 from .compressed_kv_cache import CompressedChunk, CompressedKVCache, OptimizedChunk
 
 
@@ -56,6 +57,10 @@ def fused_decompress_chunk(chunk: CompressedChunk) -> torch.Tensor:
                                        mask.data_ptr(), sc.data_ptr(), total, bph, work.data_ptr(), out.data_ptr(),
                                        L.stream_ptr(dev)),
                 "lq_fused_merge")
+    if L.debug_checks():   # the look-back error word after the tile words (a sync)
+        tiles = (total + 1023) // 1024
+        if int(work[(tiles + 1) * 8:(tiles + 1) * 8 + 4].view(torch.int32).item()):
+            raise codec.LookbackError("lq_fused_merge: a tile look-back wait did not end; the output is invalid")
     return out.reshape(batch, heads, seq, hd)
 
 

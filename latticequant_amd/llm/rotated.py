@@ -61,15 +61,20 @@ _DEV_SIGNS = {}
 
 def _device_signs(shape, layers, kvs, device) -> torch.Tensor:
     """chunk_signs on the device, kept per (geometry, layers, K/V, device): the
-    sustained write / read loops then issue no host-to-device copy per call."""
+    sustained write / read loops then issue no host-to-device copy per call.
+    Kernels on any stream may read a cached entry: its copy is complete before
+    it is first returned, and entries are never freed while the process runs;
+    past 256 entries a new key gets a per-call copy, read on the current
+    stream only."""
     C, B, H, _, hd = shape
     key = (C, B, H, hd, tuple(layers), tuple(kvs), str(device))
     t = _DEV_SIGNS.get(key)
     if t is None:
-        if len(_DEV_SIGNS) >= 256:
-            _DEV_SIGNS.clear()
         t = chunk_signs(shape, layers, kvs).to(device)
-        _DEV_SIGNS[key] = t
+        if len(_DEV_SIGNS) < 256:
+            if t.is_cuda:
+                torch.cuda.current_stream(t.device).synchronize()
+            _DEV_SIGNS[key] = t
     return t
 
 

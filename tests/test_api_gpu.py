@@ -29,18 +29,15 @@ def test_build_rans_table_golden_gpu():
     counts = [_ragged(g, "tab_counts", i) for i in range(n)]
     alph = [list(range(int(g["tab_lo"][i]), int(g["tab_lo"][i]) + len(counts[i]))) for i in range(n)]
     tabs = ga.build_rans_tables(counts, alph)
-    flagged = 0
+    wide = 0
     for i, t in enumerate(tabs):
         assert t.cumfreqs[0] == 0 and t.cumfreqs[-1] == ga.L and (t.freqs >= 1).all()
-        if t.status:
-            # numpy's tie order above 256 symbols is not restated: only such tables may differ
-            assert t.status == 4 and t.n_symbols > 256, f"table {i}"
-            flagged += 1
-            continue
+        assert t.status == 0, f"table {i}"
         np.testing.assert_array_equal(t.freqs, g["tab_freqs"][g["tab_counts_off"][i]:g["tab_counts_off"][i + 1]],
                                       err_msg=f"table {i}")
         np.testing.assert_array_equal(t.lookup, g["tab_lookup"][i])
-    assert flagged <= 8, f"{flagged} of {len(tabs)} tables hit the unpinned tie case"
+        wide += t.n_symbols > 256
+    assert wide > 0   # the golden set holds alphabets above 256 symbols (numpy's quicksort order)
     # single-table API
     t = ga.build_rans_table(counts[0], alph[0])
     np.testing.assert_array_equal(t.freqs, tabs[0].freqs)
@@ -360,7 +357,7 @@ def test_compact_encode_merge_device_gpu(bits, storage):
     t[..., :2] *= 9.0
     t = t.half()
     cb = codec.compact_encode(t.cuda(), bits, storage)
-    n_repr, n_oor = (int(v) for v in cb.totals.tolist())
+    n_repr, n_oor = codec.compact_counts(cb.totals)
     V = t.numel() // 8
     s32 = cb.scale32.cpu().numpy()
     qo = O.quantize_heads(t.float().numpy(), s32)

@@ -49,13 +49,17 @@ class _Materialising:
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("prompt,steps,tail,heads,kv", [(100, 60, 32, 4, 2), (40, 30, 0, 8, 2), (70, 25, 128, 4, 4)])
-def test_hf_decode_over_resident_prefix_gpu(prompt, steps, tail, heads, kv):
+def test_hf_decode_over_resident_prefix_gpu(prompt, steps, tail, heads, kv, monkeypatch):
     from latticequant_amd.llm.resident_cache import ResidentKVCache
     model, cfg = _model(heads=heads, kv_heads=kv)
     g = torch.Generator().manual_seed(1)
     ids = torch.randint(0, cfg.vocab_size, (1, prompt), generator=g).cuda()
     a = ResidentKVCache(bits_per_dim=4, tail_tokens=tail)
     b = _Materialising(bits_per_dim=4, tail_tokens=tail).cache
+    calls = []   # (layer, cache) of every resident-kernel call
+    orig = ResidentKVCache.attend
+    monkeypatch.setattr(ResidentKVCache, "attend",
+                        lambda self, layer, q: calls.append((layer, self)) or orig(self, layer, q))
     with torch.no_grad():
         la = model(ids, past_key_values=a, use_cache=True).logits[:, -1].float()
         lb = model(ids, past_key_values=b, use_cache=True).logits[:, -1].float()
@@ -71,6 +75,10 @@ def test_hf_decode_over_resident_prefix_gpu(prompt, steps, tail, heads, kv):
             assert err < 5e-3, err
             agree += int(la.argmax() == lb.argmax())
     assert agree >= steps - 1
+    # the unmasked decode steps ran the resident kernel in every layer of the
+    # cache under test (the materialising cache hands HF plain tensors)
+    mine = [layer for layer, c in calls if c is a]
+    assert len(mine) == steps * cfg.num_hidden_layers, (len(mine), steps)
     n = prompt + steps
     assert a.get_seq_length() == n == b.get_seq_length()
     flushed = a.res_k[0].n_tokens
