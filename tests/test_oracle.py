@@ -301,3 +301,26 @@ def test_as_written_tier_matches_oracle():
     # without injected scales the torch sigma^2 path gives the oracle's fp16 scales
     _, s16, _ = A.compress(torch.from_numpy(t), 4)
     np.testing.assert_array_equal(s16.numpy(), O.compress_chunk(t, 4).scales)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S", [(1, 32, 8, 700), (2, 8, 2, 129), (1, 4, 4, 1), (3, 6, 3, 64)])
+def test_decode_attention_matches_sdpa_float64(B, Hq, Hkv, S):
+    """oracle.decode_attention (the checker of the decode-attention kernels)
+    against torch's scaled_dot_product_attention in float64 on the CPU, with
+    GQA expanded explicitly (q head h reads kv head h // (Hq / Hkv)); large
+    logits included so the max-subtraction matters."""
+    import torch
+    rng = np.random.default_rng(B * 1000 + S)
+    q = rng.standard_normal((B, Hq, 1, 128))
+    k = rng.standard_normal((B, Hkv, S, 128)) * 3.0
+    v = rng.standard_normal((B, Hkv, S, 128))
+    k[:, :, S // 2] *= 40.0   # one dominant key per head
+    got = O.decode_attention(q, k, v)
+    g = Hq // Hkv
+    kt = torch.from_numpy(k).repeat_interleave(g, dim=1)
+    vt = torch.from_numpy(v).repeat_interleave(g, dim=1)
+    want = torch.nn.functional.scaled_dot_product_attention(torch.from_numpy(q), kt, vt).numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-13)
+    # a head whose keys are all equal averages V
+    k2 = np.repeat(k[:, :, :1], S, axis=2)
+    np.testing.assert_allclose(O.decode_attention(q, k2, v)[:, ::g, 0], v.mean(axis=2), rtol=1e-12, atol=1e-13)
