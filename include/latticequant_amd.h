@@ -148,6 +148,26 @@ int lq_chunk_quantize_wide(const void *d_x, int dtype, int64_t n_chunks, int64_t
                            uint32_t *d_blk_n1, int32_t *d_minmax, int32_t *d_status, void *d_deq, int deq_dtype,
                            const int64_t *d_dither_seed, hipStream_t s);
 
+/* Coarse / fine escape of the wide path, for streams whose alphabet exceeds
+ * L = 1024 symbols (the reference's table normalisation, core/gpu_ans.py:73-84,
+ * never terminates there; this format is defined by this build and has no
+ * reference counterpart).  Plan: per chunk and coordinate j, the least
+ * k_j in [0, 7] with (max >> k_j) - (min >> k_j) + 5 <= L for both cosets'
+ * streams of j (d_esc_k: n_chunks * 8 int32), and the coarse min / max of
+ * every stream (d_minmax_coarse, layout of d_minmax), which then feed
+ * lq_chunk_hist_wide and lq_chunk_tables_wide.  No k fits: LQ_ST_ALPHABET. */
+int lq_chunk_escape_plan(const int32_t *d_minmax, int64_t n_chunks, int32_t *d_esc_k, int32_t *d_minmax_coarse,
+                         int32_t *d_status, hipStream_t s);
+
+/* Escape split: in the int16 staging of lq_chunk_quantize_wide, every symbol
+ * s of a coordinate with k_j > 0 becomes s >> k_j (floor), and its k_j low
+ * bits go to d_fine: coordinate j of chunk c owns nblk * 16 * k_j words from
+ * word d_fine_off[c * 8 + j], vector v's bits at bit v * k_j, least
+ * significant first.  Chunks with every k_j = 0 are left untouched. */
+int lq_chunk_escape_split(int16_t *d_sym, const uint8_t *d_coset_bits, const uint32_t *d_blk_n1, int64_t n_chunks,
+                          int64_t n_vectors, const int32_t *d_esc_k, const int64_t *d_fine_off, uint32_t *d_fine,
+                          hipStream_t s);
+
 /* Wide path: per-stream histograms (n_chunks * 16 * 1024 uint32, zero on
  * entry) of the int16 symbols in the window [min, min + 1023].
  * Replaces the np.unique counting of llm/compressed_kv_cache.py:242-246. */
@@ -214,6 +234,19 @@ int lq_chunk_decode(const uint32_t *d_words, const int64_t *d_chunk_base, const 
                     const uint32_t *d_blk_n1, const lq_table *d_tables, const uint16_t *d_scale16,
                     int64_t n_chunks, int64_t n_heads, int64_t bph, uint32_t *d_lut_work, void *d_out,
                     int out_dtype, const int64_t *d_dither_seed, hipStream_t s);
+
+/* lq_chunk_decode (d_signs null) or lq_chunk_decode_rht (d_signs given) of a
+ * batch with escaped chunks (lq_chunk_escape_plan / lq_chunk_escape_split):
+ * symbol j of a vector is (decoded coarse symbol << k_j) plus its low bits
+ * from d_fine before c7 and the coset offset are applied.  Build-defined
+ * format: no reference counterpart (the reference never terminates on such
+ * streams). */
+int lq_chunk_decode_escaped(const uint32_t *d_words, const int64_t *d_chunk_base, const int64_t *d_stream_woff,
+                            const uint32_t *d_blk_off, const int64_t *d_stream_nbits, const uint16_t *d_blk_state,
+                            const uint8_t *d_coset_bits, const lq_table *d_tables, const uint16_t *d_scale16,
+                            int64_t n_chunks, int64_t n_heads, int64_t bph, int head_dim, const float *d_signs,
+                            const int32_t *d_esc_k, const int64_t *d_fine_off, const uint32_t *d_fine,
+                            uint32_t *d_lut_work, void *d_out, int out_dtype, const int64_t *d_dither_seed, hipStream_t s);
 
 /* lq_chunk_decode of chunks written by lq_chunk_quantize_rht: each row's
  * fp32 dequantised values ((q - d) * scale16) are rotated back (FWHT / sqrt(head_dim),

@@ -45,6 +45,10 @@ _SIGS = {
     "lq_chunk_tables": ([_P, _I64, _P, _P, _P], _INT),
     "lq_chunk_quantize_wide": ([_P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _INT, _P, _P], _INT),
     "lq_chunk_hist_wide": ([_P, _P, _I64, _I64, _P, _P, _P], _INT),
+    "lq_chunk_escape_plan": ([_P, _I64, _P, _P, _P, _P], _INT),
+    "lq_chunk_escape_split": ([_P, _P, _P, _I64, _I64, _P, _P, _P, _P], _INT),
+    "lq_chunk_decode_escaped": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _INT, _P, _P, _P, _P, _P, _P,
+                                 _INT, _P, _P], _INT),
     "lq_chunk_tables_wide": ([_P, _P, _I64, _P, _P, _P], _INT),
     "lq_chunk_encode_wide": ([_P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P], _INT),
     "lq_chunk_encode_workspace": ([_I64, _I64], _I64),

@@ -66,6 +66,11 @@ class EncodedBatch:
     def nblk(self) -> int:
         return (self.n_vectors + L.LQ_BLK - 1) // L.LQ_BLK
 
+    @property
+    def escape(self) -> Optional["Escape"]:
+        """Coarse / fine escape of chunks with alphabets beyond L (None: none)."""
+        return self.extra.get("esc")
+
     # ---- views ------------------------------------------------------------
     def select(self, c: int) -> "EncodedBatch":
         """Chunk c as a one-chunk batch (views, no copies; words stay shared)."""
@@ -85,13 +90,19 @@ class EncodedBatch:
             status=self.status[c:c + 1],
             hist=None if self.hist is None else self.hist.view(C, -1)[c],
             extra={**self.extra, "dither_seed": None if self.extra.get("dither_seed") is None
-                   else self.extra["dither_seed"][c:c + 1]})
+                   else self.extra["dither_seed"][c:c + 1],
+                   "esc": None if self.escape is None else self.escape.select(c)})
 
     # ---- byte accounting -------------------------------------------------
     def reference_bytes(self) -> torch.Tensor:
         """Bytes the reference counts per chunk (llm/compressed_kv_cache.py:113-119):
-        int32 bitstream words + packed coset bits + fp16 scales.  (C,) int64 on device."""
-        return self.chunk_words * 4 + (self.n_vectors + 7) // 8 + 2 * self.n_heads
+        int32 bitstream words + packed coset bits + fp16 scales, plus, for an
+        escaped chunk (alphabets beyond L, a case the reference never
+        completes), its raw low-bit words.  (C,) int64 on device."""
+        b = self.chunk_words * 4 + (self.n_vectors + 7) // 8 + 2 * self.n_heads
+        if self.escape is not None:
+            b = b + self.escape.fine_bytes(self.nblk).to(b.device)
+        return b
 
     def side_bytes(self) -> torch.Tensor:
         """Bytes this format adds per chunk: compact tables (lo, n_sym: 4 B + 2 B per
@@ -103,6 +114,48 @@ class EncodedBatch:
         tab = (4 * present + 2 * nsym).sum(1)
         ck = 6 * present.sum(1) * self.nblk
         return tab + ck + 2 * self.nblk
+
+
+@dataclass
+class Escape:
+    """Coarse / fine escape of a batch (lq_chunk_escape_plan / _split): per
+    chunk and coordinate j the shift k_j; symbol s of coordinate j is coded as
+    s >> k_j in its stream and its k_j low bits are stored raw in `fine`
+    (coordinate j of chunk c: nblk * 16 * k_j words from word off[c * 8 + j],
+    vector v's bits at bit v * k_j, least significant first).  A format of this
+    build: the reference never terminates on alphabets beyond L."""
+    k: torch.Tensor        # (C, 8) int32, device
+    off: torch.Tensor      # (C * 8,) int64 word offsets into fine, device
+    fine: torch.Tensor     # (words + 1,) int32, device (one slack word)
+    k_host: np.ndarray     # (C, 8) int32
+
+    def select(self, c: int) -> "Escape":
+        return Escape(k=self.k[c:c + 1], off=self.off[8 * c:8 * c + 8], fine=self.fine,
+                      k_host=self.k_host[c:c + 1])
+
+    def fine_bytes(self, nblk: int) -> torch.Tensor:
+        """Raw low-bit bytes per chunk, (C,) int64 (host tensor)."""
+        return torch.from_numpy(4 * 16 * nblk * self.k_host.astype(np.int64).sum(1))
+
+
+def _plan_escape(minmax, C, nblk, V, sym, coset_bits, blk_n1, status, dev, s):
+    """Escape plan and split of a wide batch (one host read of the C x 8
+    shifts).  Returns (Escape or None, the coarse per-stream min / max)."""
+    lib = L.lib()
+    esc_k = _empty(C * 8, torch.int32, dev)
+    mm_c = torch.empty_like(minmax)
+    L.check(lib.lq_chunk_escape_plan(minmax.data_ptr(), C, esc_k.data_ptr(), mm_c.data_ptr(), status.data_ptr(), s),
+            "lq_chunk_escape_plan")
+    kh = esc_k.view(C, 8).cpu().numpy()
+    if not kh.any():
+        return None, minmax
+    per = (16 * nblk * kh.astype(np.int64)).reshape(-1)
+    off = np.concatenate([[0], np.cumsum(per)[:-1]]).astype(np.int64)
+    fine = _zeros(int(per.sum()) + 1, torch.int32, dev)
+    off_d = torch.from_numpy(off).to(dev)
+    L.check(lib.lq_chunk_escape_split(sym.data_ptr(), coset_bits.data_ptr(), blk_n1.data_ptr(), C, V, esc_k.data_ptr(),
+                                      off_d.data_ptr(), fine.data_ptr(), s), "lq_chunk_escape_split")
+    return Escape(k=esc_k.view(C, 8), off=off_d, fine=fine, k_host=kh.astype(np.int32)), mm_c
 
 
 def words_bound(n_chunks: int, n_vectors: int) -> int:
@@ -361,7 +414,7 @@ class AlphabetError(ValueError):
 
 def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, deq_out: bool = False,
                  exact_size: bool = True, words_out: Optional[torch.Tensor] = None, wide="auto",
-                 dither_seed=None, rht_signs: Optional[torch.Tensor] = None):
+                 dither_seed=None, rht_signs: Optional[torch.Tensor] = None, escape: bool = True):
     """Compress a batch of chunks.
 
     x: (C, B, H, T, hd) fp16 / bf16 / fp32 CUDA tensor, hd % 8 == 0.
@@ -375,8 +428,12 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
       chunk beyond sets LQ_ST_SYM_OVERFLOW in enc.status).  True: int16, for
       alphabets up to 1024 symbols.  "auto": int8 first, and if a chunk
       overflowed (one status read-back) the batch is redone on the wide path.
-    An alphabet above 1024 symbols raises AlphabetError when the status is read
-    back (wide="auto" or True with exact_size) and is otherwise left in enc.status.
+    escape: on the wide path, a coordinate whose alphabet exceeds 1024 symbols
+      (where the reference's table normalisation never terminates) is coded
+      as coarse symbols s >> k plus k raw low bits per vector (enc.escape; a
+      format of this build, one host read of the shifts).  escape=False: such
+      an alphabet raises AlphabetError when the status is read back
+      (wide="auto" or True with exact_size) and is otherwise left in enc.status.
     dither_seed: int or (C,) ints: subtractive dither per chunk (the rotated
       path; the seeds are kept in enc.extra and decode_batch removes the dither).
     rht_signs: (C*B*H, hd) fp32 sign rows: the chunks are coded as their
@@ -393,7 +450,8 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
         fused = not deq_out and wide is not True and hd <= 128
         if not fused:
             w = rotate_rows(x, rht_signs, inverse=False)
-            return encode_batch(w, bits, scale32, deq_out, exact_size, words_out, wide, dither_seed)
+            return encode_batch(w, bits, scale32, deq_out, exact_size, words_out, wide, dither_seed,
+                                escape=escape)
     dev = x.device
     nh, bph = B * H, T * hd // 8
     V = nh * bph
@@ -406,6 +464,7 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
     coset_bits = _empty(C * nblk * L.LQ_BLK // 8, torch.uint8, dev)
     blk_n1 = _empty(C * nblk, torch.int32, dev)
     use_wide = wide is True
+    esc = None
     # one zero fill: the status flags, the int8 path's histogram and a leading
     # zero before the chunks' word counts (so that one inclusive scan of
     # [0, w_0 .. w_{C-2}] gives the chunk bases)
@@ -433,7 +492,8 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
         if wide == "auto" and _status_or(status) & L.LQ_ST_SYM_OVERFLOW:
             if rht_signs is not None:   # the int16 path reads the materialised rotation
                 w = rotate_rows(x, rht_signs, inverse=False)
-                return encode_batch(w, bits, scale32, deq_out, exact_size, words_out, wide, dither_seed)
+                return encode_batch(w, bits, scale32, deq_out, exact_size, words_out, wide, dither_seed,
+                                    escape=escape)
             use_wide = True
             status.zero_()
         else:
@@ -448,6 +508,8 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
                                            sym.data_ptr(), coset_bits.data_ptr(), blk_n1.data_ptr(), minmax.data_ptr(),
                                            status.data_ptr(), L.ptr(deq), dt, L.ptr(dseed), s),
                 "lq_chunk_quantize_wide")
+        if escape:
+            esc, minmax = _plan_escape(minmax, C, nblk, V, sym, coset_bits, blk_n1, status, dev, s)
         L.check(lib.lq_chunk_hist_wide(sym.data_ptr(), blk_n1.data_ptr(), C, V, minmax.data_ptr(), hist.data_ptr(), s),
                 "lq_chunk_hist_wide")
         L.check(lib.lq_chunk_tables_wide(hist.data_ptr(), minmax.data_ptr(), C, tables.data_ptr(), status.data_ptr(), s),
@@ -490,7 +552,7 @@ def encode_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, 
                        tables=tables, blk_off=blk_off, blk_state=blk_state, stream_nbits=stream_nbits,
                        stream_state=stream_state, stream_woff=stream_woff, chunk_words=chunk_words,
                        chunk_base=chunk_base, words=words, status=status, hist=hist,
-                       extra={"wide": use_wide, "dither_seed": dseed})
+                       extra={"wide": use_wide, "dither_seed": dseed, "esc": esc})
     return enc, deq
 
 
@@ -508,6 +570,7 @@ def decode_batch(enc: EncodedBatch, out_dtype: torch.dtype = torch.float16, out:
         out = torch.empty((C,) + tuple(enc.shape), dtype=out_dtype, device=dev)
     if lut_work is None:
         lut_work = _empty(C * L.LQ_STREAMS * L.LQ_L, torch.int32, dev)
+    esc = enc.escape
     if rht_signs is not None:
         hd = enc.shape[-1]
         rht_signs = _check_signs(rht_signs, C * enc.n_heads, hd, dev)
@@ -515,6 +578,19 @@ def decode_batch(enc: EncodedBatch, out_dtype: torch.dtype = torch.float16, out:
             w = decode_batch(enc, out_dtype=torch.float32, lut_work=lut_work)
             out.copy_(rotate_rows(w, rht_signs, inverse=True, out_dtype=out.dtype))
             return out
+    if esc is not None:   # chunks with coarse / fine coordinates
+        hd = enc.shape[-1]
+        L.check(lib.lq_chunk_decode_escaped(enc.words.data_ptr(), enc.chunk_base.data_ptr(), enc.stream_woff.data_ptr(),
+                                            enc.blk_off.data_ptr(), enc.stream_nbits.data_ptr(),
+                                            enc.blk_state.data_ptr(), enc.coset_bits.data_ptr(), enc.tables.data_ptr(),
+                                            enc.scale16.data_ptr(), C, enc.n_heads, enc.bph,
+                                            hd if rht_signs is not None else 0, L.ptr(rht_signs), esc.k.data_ptr(),
+                                            esc.off.data_ptr(), esc.fine.data_ptr(), lut_work.data_ptr(),
+                                            out.data_ptr(), L.dtype_code(out.dtype),
+                                            L.ptr(enc.extra.get("dither_seed")), L.stream_ptr(dev)),
+                "lq_chunk_decode_escaped")
+        return out
+    if rht_signs is not None:
         L.check(lib.lq_chunk_decode_rht(enc.words.data_ptr(), enc.chunk_base.data_ptr(), enc.stream_woff.data_ptr(),
                                         enc.blk_off.data_ptr(), enc.stream_nbits.data_ptr(), enc.blk_state.data_ptr(),
                                         enc.coset_bits.data_ptr(), enc.tables.data_ptr(), enc.scale16.data_ptr(), C,
@@ -698,10 +774,14 @@ def encode_batch_deferred(x: torch.Tensor, bits, deq_out: bool = False, dither_s
 # n_symbols, status + one uint16 frequency per symbol; cumulative
 # frequencies and renormalisation shifts are rebuilt on load), the block
 # checkpoints of present streams (uint32 bit offset + uint16 state), the
-# per-block coset-1 counts (uint16) and the stream metadata.
+# per-block coset-1 counts (uint16) and the stream metadata.  Version 2 adds
+# the coarse / fine escape (esc_k: 8 int32 shifts per chunk; fine: the raw
+# low-bit words of every escaped coordinate in (chunk, coordinate) order);
+# batches without escaped chunks are still written as version 1.
 
 WIRE_MAGIC = b"LQE8RANS"
-WIRE_VERSION = 1
+WIRE_VERSION = 2
+WIRE_VERSIONS_READ = (1, 2)
 
 
 class WireFormatError(ValueError):
@@ -756,10 +836,19 @@ def to_bytes(enc: EncodedBatch) -> bytes:
     if "rht" in enc.extra:
         layers, kvs = enc.extra["rht"]
         extra["rht"] = [[int(v) for v in layers], [int(v) for v in kvs]]
+    esc = enc.escape
+    if esc is not None:
+        kh = esc.k_host.astype(np.int32).reshape(-1)
+        offs = esc.off.cpu().numpy()
+        fall = esc.fine.cpu().numpy().view(np.uint32)
+        fine = [fall[o:o + 16 * nb * int(k)] for o, k in zip(offs, kh) if k]
+        fields.append(("esc_k", kh))
+        fields.append(("fine", np.concatenate(fine) if fine else np.zeros(0, np.uint32)))
     header = {"n_chunks": C, "n_heads": enc.n_heads, "bph": enc.bph, "shape": [int(v) for v in enc.shape],
               "fields": [[n, a.dtype.str, int(a.size)] for n, a in fields], "extra": extra}
     hb = json.dumps(header, separators=(",", ":")).encode()
-    parts = [WIRE_MAGIC, np.uint32(WIRE_VERSION).tobytes(), np.uint32(len(hb)).tobytes(), hb]
+    version = WIRE_VERSION if esc is not None else 1
+    parts = [WIRE_MAGIC, np.uint32(version).tobytes(), np.uint32(len(hb)).tobytes(), hb]
     pos = sum(len(p) for p in parts)
     for _, a in fields:
         pad = (-pos) % 8
@@ -788,7 +877,7 @@ def _check_wire_geometry(C, nh, bph, shape, arrs):
             raise WireFormatError(f"missing field {name}")
         if n is not None and arrs[name].size != n:
             raise WireFormatError(f"field {name} holds {arrs[name].size} values, the geometry needs {n}")
-    for name, n in (("sigma2", C * nh), ("dither_seed", C)):
+    for name, n in (("sigma2", C * nh), ("dither_seed", C), ("esc_k", C * 8)):
         if name in arrs and arrs[name].size != n:
             raise WireFormatError(f"field {name} holds {arrs[name].size} values, the geometry needs {n}")
 
@@ -838,8 +927,9 @@ def from_bytes(buf, device=None) -> EncodedBatch:
     if len(mv) < 20 or bytes(mv[:8]) != WIRE_MAGIC:
         raise WireFormatError("not an LQE8RANS chunk batch")
     version = int(np.frombuffer(mv[8:12], np.uint32)[0])
-    if version != WIRE_VERSION:
-        raise WireFormatError(f"unsupported wire format version {version} (this build reads {WIRE_VERSION})")
+    if version not in WIRE_VERSIONS_READ:
+        raise WireFormatError(f"unsupported wire format version {version} (this build reads "
+                              f"{', '.join(str(v) for v in WIRE_VERSIONS_READ)})")
     crc = int(np.frombuffer(mv[len(mv) - 4:], np.uint32)[0])
     if zlib.crc32(mv[:len(mv) - 4]) & 0xFFFFFFFF != crc:
         raise WireFormatError("checksum mismatch: the chunk batch is corrupted")
@@ -898,6 +988,12 @@ def from_bytes(buf, device=None) -> EncodedBatch:
     if arrs["words"].size != int(cw.sum()):
         raise WireFormatError("inconsistent bitstream length")
     _check_wire_streams(C, nv, nb, present.reshape(C, S), arrs, off, st)
+    if ("esc_k" in arrs) != ("fine" in arrs) or ("esc_k" in arrs and version < 2):
+        raise WireFormatError("inconsistent escape fields")
+    if "esc_k" in arrs:
+        kh = arrs["esc_k"].astype(np.int64)
+        if np.any(kh < 0) or np.any(kh > 7) or arrs["fine"].size != int(16 * nb * kh.sum()):
+            raise WireFormatError("escape shifts out of range or low-bit words of the wrong length")
     dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
 
     def T(a, dt):
@@ -922,6 +1018,13 @@ def from_bytes(buf, device=None) -> EncodedBatch:
     if "rht" in header.get("extra", {}):
         layers, kvs = header["extra"]["rht"]
         enc.extra["rht"] = (list(layers), list(kvs))
+    if "esc_k" in arrs and arrs["esc_k"].any():
+        kh = arrs["esc_k"].astype(np.int32).reshape(C, 8)
+        per = 16 * nb * kh.astype(np.int64).reshape(-1)
+        offs = np.cumsum(per) - per
+        fine = np.concatenate([arrs["fine"].astype(np.uint32), np.zeros(1, np.uint32)])
+        enc.extra["esc"] = Escape(k=T(kh, torch.int32), off=T(offs, torch.int64),
+                                  fine=torch.from_numpy(fine.view(np.int32).copy()).to(dev), k_host=kh)
     return enc
 
 

@@ -471,4 +471,38 @@ struct CosetConsts {
     }
 };
 
+// A staged vector of an escaped chunk (coarse symbol fields in r) as its
+// lattice point in fp32: coordinate j's coarse symbol is the field minus its
+// bias (512, c8h 256) when the chunk's LUTs hold biased fields, else
+// lo_j + index; the symbol is (coarse << k_j) plus its k_j raw low bits (bit
+// v * k_j of the coordinate's fine words, least significant first), then
+// c7 = 2 * c8h + (sum of the free symbols mod 2) (core/entropy_coder.py:71-89)
+// and the coset offset.
+__device__ __forceinline__ void lattice_escaped_f32(const uint4& r, const CosetConsts& cs, bool lut_biased,
+                                                    const int32_t* ek, const int64_t* fo, const uint32_t* fine,
+                                                    int64_t v, float y[8]) {
+    const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+    int sv[8];
+    int par = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int idx = (int)((j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu));
+        int val = lut_biased ? idx - (j < 7 ? 512 : 256) : cs.lo[j] + idx;
+        const int k = ek[j];
+        if (k) {
+            const int64_t bit = v * k;
+            const uint32_t* wp = fine + fo[j] + (bit >> 5);
+            const int sh = (int)(bit & 31);
+            uint32_t f = wp[0] >> sh;
+            if (sh + k > 32) f |= wp[1] << (32 - sh);
+            val = val * (1 << k) + (int)(f & ((1u << k) - 1u));
+        }
+        sv[j] = val;
+        if (j < 7) par += val;
+    }
+#pragma unroll
+    for (int j = 0; j < 7; j++) y[j] = (float)sv[j] + cs.off;
+    y[7] = (float)(2 * sv[7] + (par & 1)) + cs.off;
+}
+
 }  // namespace lq

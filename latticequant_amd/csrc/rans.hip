@@ -1066,7 +1066,8 @@ __global__ __launch_bounds__(kDecThreads) void k_chunk_decode(
         const uint16_t* __restrict__ blk_state, const uint8_t* __restrict__ coset_bits,
         const lq_table* __restrict__ tables, const uint16_t* __restrict__ scale16, const uint32_t* __restrict__ lutg,
         int64_t n_chunks, int64_t n_heads, int64_t bph, int64_t nblk, int64_t gpw, void* __restrict__ out,
-        const int64_t* __restrict__ dseed, const float* __restrict__ signs, int lpr, float rdiv) {
+        const int64_t* __restrict__ dseed, const float* __restrict__ signs, int lpr, float rdiv,
+        const int32_t* __restrict__ esc_k, const int64_t* __restrict__ fine_off, const uint32_t* __restrict__ fine) {
     __shared__ uint32_t lut[LQ_STREAMS * kL];                               // 64 KB
     __shared__ uint32_t ring[kDecThreads / 64][kLineRing][64];              // 48 KB
     __shared__ __align__(16) uint16_t stg[kDecBlocks * 2 * kDecGroupU16];   // 34 KB
@@ -1121,7 +1122,16 @@ __global__ __launch_bounds__(kDecThreads) void k_chunk_decode(
     for (int w = 0; w < kBlk / 32; w++) n1 += __builtin_popcount(bm1[b][w]);
     const int n = c ? n1 : valid - n1;
     const lq_table* T = tables + chunk * LQ_STREAMS;
-    const bool biased = chunk_biased(T);
+    // escaped chunk (coarse symbols plus raw low bits, alphabets beyond L):
+    // the generic path with the low bits merged in
+    const int32_t* const ekc = esc_k ? esc_k + chunk * 8 : nullptr;
+    bool esc = false;
+    if (ekc) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) esc = esc || ekc[j] != 0;
+    }
+    const bool lut_biased = chunk_biased(T);   // the LUT's symbol fields (k_chunk_lut decides the same way)
+    const bool biased = !esc && lut_biased;
     CosetConsts cc0, cc1;   // per-coset alphabet lows, for chunks whose fields are not biased
     if (!biased) {
         cc0.init(T, 0);
@@ -1204,6 +1214,10 @@ __global__ __launch_bounds__(kDecThreads) void k_chunk_decode(
             }
             if (biased) {
                 lattice_biased_f32(r, cp ? 0.5f : 0.f, y);
+            } else if (esc) {
+                CosetConsts cs;
+                cs.pick(cp, cc0, cc1);
+                lattice_escaped_f32(r, cs, lut_biased, ekc, fine_off + chunk * 8, fine, vfirst + p, y);
             } else {
                 CosetConsts cs;
                 cs.pick(cp, cc0, cc1);
@@ -1519,8 +1533,10 @@ static int chunk_decode_launch(const uint32_t* d_words, const int64_t* d_chunk_b
                                const uint8_t* d_coset_bits, const lq_table* d_tables, const uint16_t* d_scale16,
                                int64_t n_chunks, int64_t n_heads, int64_t bph, uint32_t* d_lut_work, void* d_out,
                                int out_dtype, const int64_t* d_dither_seed, int head_dim, const float* d_signs,
+                               const int32_t* d_esc_k, const int64_t* d_fine_off, const uint32_t* d_fine,
                                hipStream_t s) {
     if (n_chunks <= 0 || n_heads <= 0 || bph <= 0 || out_dtype < 0 || out_dtype > 2) return LQ_ERR_ARG;
+    if (d_esc_k && (!d_fine_off || !d_fine)) return LQ_ERR_ARG;
     const int64_t V = n_heads * bph;
     const int64_t nblk = (V + kBlk - 1) / kBlk;
     hipLaunchKernelGGL(k_chunk_lut, dim3((unsigned)(n_chunks * LQ_STREAMS)), dim3(256), 0, s, d_tables, d_lut_work, 1);
@@ -1534,7 +1550,8 @@ static int chunk_decode_launch(const uint32_t* d_words, const int64_t* d_chunk_b
 #define LQ_DECODE(DT, AL, DI, RO)                                                                                 \
     hipLaunchKernelGGL((k_chunk_decode<DT, AL, DI, RO>), grid, dim3(kDecThreads), 0, s, d_words, d_chunk_base,          \
                        d_stream_woff, d_blk_off, d_stream_nbits, d_blk_state, d_coset_bits, d_tables, d_scale16,       \
-                       d_lut_work, n_chunks, n_heads, bph, nblk, gpw, d_out, d_dither_seed, d_signs, lpr, div)
+                       d_lut_work, n_chunks, n_heads, bph, nblk, gpw, d_out, d_dither_seed, d_signs, lpr, div,         \
+                       d_esc_k, d_fine_off, d_fine)
 #define LQ_DECODE_DT(DT, RO)                                                                                      \
     do {                                                                                                          \
         if (d_dither_seed) { if (aligned) LQ_DECODE(DT, true, true, RO); else LQ_DECODE(DT, false, true, RO); }   \
@@ -1562,7 +1579,21 @@ int lq_chunk_decode(const uint32_t* d_words, const int64_t* d_chunk_base, const 
     (void)d_blk_n1;   // the decoder counts each block's coset-1 vectors from the bitmap
     return chunk_decode_launch(d_words, d_chunk_base, d_stream_woff, d_blk_off, d_stream_nbits, d_blk_state,
                                d_coset_bits, d_tables, d_scale16, n_chunks, n_heads, bph, d_lut_work, d_out, out_dtype,
-                               d_dither_seed, 0, nullptr, s);
+                               d_dither_seed, 0, nullptr, nullptr, nullptr, nullptr, s);
+}
+
+int lq_chunk_decode_escaped(const uint32_t* d_words, const int64_t* d_chunk_base, const int64_t* d_stream_woff,
+                            const uint32_t* d_blk_off, const int64_t* d_stream_nbits, const uint16_t* d_blk_state,
+                            const uint8_t* d_coset_bits, const lq_table* d_tables, const uint16_t* d_scale16,
+                            int64_t n_chunks, int64_t n_heads, int64_t bph, int head_dim, const float* d_signs,
+                            const int32_t* d_esc_k, const int64_t* d_fine_off, const uint32_t* d_fine,
+                            uint32_t* d_lut_work, void* d_out, int out_dtype, const int64_t* d_dither_seed, hipStream_t s) {
+    if (!d_esc_k || !d_fine_off || !d_fine) return LQ_ERR_ARG;
+    if (d_signs && (head_dim < 8 || head_dim > 128 || (head_dim & (head_dim - 1)) || bph <= 0 || bph % (head_dim / 8)))
+        return LQ_ERR_ARG;
+    return chunk_decode_launch(d_words, d_chunk_base, d_stream_woff, d_blk_off, d_stream_nbits, d_blk_state,
+                               d_coset_bits, d_tables, d_scale16, n_chunks, n_heads, bph, d_lut_work, d_out, out_dtype,
+                               d_dither_seed, d_signs ? head_dim : 0, d_signs, d_esc_k, d_fine_off, d_fine, s);
 }
 
 int lq_chunk_decode_rht(const uint32_t* d_words, const int64_t* d_chunk_base, const int64_t* d_stream_woff,
@@ -1574,7 +1605,7 @@ int lq_chunk_decode_rht(const uint32_t* d_words, const int64_t* d_chunk_base, co
         return LQ_ERR_ARG;
     return chunk_decode_launch(d_words, d_chunk_base, d_stream_woff, d_blk_off, d_stream_nbits, d_blk_state,
                                d_coset_bits, d_tables, d_scale16, n_chunks, n_heads, bph, d_lut_work, d_out, out_dtype,
-                               d_dither_seed, head_dim, d_signs, s);
+                               d_dither_seed, head_dim, d_signs, nullptr, nullptr, nullptr, s);
 }
 
 int lq_chunk_luts(const lq_table* d_tables, int64_t n_chunks, uint32_t* d_lut, hipStream_t s) {

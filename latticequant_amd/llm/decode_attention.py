@@ -45,6 +45,9 @@ def decode_attention(k: EncodedBatch, v: EncodedBatch, q: torch.Tensor, tail_k: 
     lib = L.lib()
     if k.shape != v.shape or k.n_chunks != v.n_chunks:
         raise ValueError("K and V batches must have the same geometry")
+    if k.escape is not None or v.escape is not None:
+        raise ValueError("decode attention reads the reference's chunk format; escaped chunks (alphabets beyond "
+                         "L = 1024) are decoded with codec.decode_batch")
     B, Hkv, T, hd = k.shape
     if hd != 128 or T % 32:
         raise ValueError("decode attention needs head_dim 128 and a multiple of 32 tokens per chunk")

@@ -18,6 +18,12 @@ Parity notes
     as numpy's AVX512 bitonic network.  For n > 256 this module calls the host
     numpy.argsort, so on a host whose numpy takes another code path the tie
     order there is "parity unpinned".
+  * escape_shifts / compress_chunk(escape=True) / decompress_chunk: the
+    coarse / fine escape for alphabets beyond L is a format of this build
+    (the reference's normalisation never terminates there), so its parity is
+    unpinned by the reference; it is pinned by invariants instead (lossless
+    round trip, coarse alphabets within L, minimal shift) in
+    tests/test_oracle.py.
   * sigma^2 = mean(x^2) is reduction-order dependent in the reference; the
     oracle computes it in float64 and rounds once.  Bit-exact comparisons inject
     the scale instead.
@@ -353,6 +359,8 @@ class Chunk:
     word_offsets: List[int] = field(default_factory=list)
     decompressed: np.ndarray = None
     dither_seed: Optional[int] = None
+    esc_k: Optional[np.ndarray] = None   # (8,) shifts of an escaped chunk, else None
+    fine: Optional[dict] = None          # coordinate j -> uint32 low-bit words (k_j > 0)
 
     @property
     def n_vectors(self):
@@ -360,8 +368,10 @@ class Chunk:
 
     @property
     def compressed_bytes(self):
-        """llm/compressed_kv_cache.py:113-119 accounting (bitstream + coset bits + fp16 scales)."""
-        return self.bitstream.size * 4 + self.coset_packed.size + self.scales.size * 2
+        """llm/compressed_kv_cache.py:113-119 accounting (bitstream + coset bits +
+        fp16 scales), plus an escaped chunk's low-bit words."""
+        fine = sum(w.size for w in self.fine.values()) * 4 if self.fine else 0
+        return self.bitstream.size * 4 + self.coset_packed.size + self.scales.size * 2 + fine
 
 
 def column_table(col: np.ndarray):
@@ -374,12 +384,53 @@ def column_table(col: np.ndarray):
     return lo, counts
 
 
+ESC_MAX_SHIFT = 7
+BLK = 512
+
+
+def escape_shifts(syms: np.ndarray, coset: np.ndarray) -> np.ndarray:
+    """Per coordinate j the least k in [0, 7] with (max >> k) - (min >> k) + 5 <= L
+    for the symbols of both cosets' streams of j (build-defined escape; the
+    reference's table normalisation never terminates beyond L)."""
+    ks = np.zeros(8, np.int64)
+    for j in range(8):
+        for k in range(ESC_MAX_SHIFT + 1):
+            ok = True
+            for c in (0, 1):
+                col = syms[coset == c][:, j]
+                if len(col) and (int(col.max()) >> k) - (int(col.min()) >> k) + 5 > L:
+                    ok = False
+            if ok:
+                ks[j] = k
+                break
+        else:
+            raise ValueError(f"coordinate {j}: no shift up to {ESC_MAX_SHIFT} fits the alphabet in L")
+    return ks
+
+
+def pack_fine(low: np.ndarray, k: int) -> np.ndarray:
+    """Low bits of every vector (value v at bit v * k, least significant first)
+    in uint32 words, padded to whole 512-vector blocks (16 k words each)."""
+    n = len(low)
+    nblk = (n + BLK - 1) // BLK
+    bits = ((np.asarray(low, np.int64)[:, None] >> np.arange(k)) & 1).astype(np.uint8).reshape(-1)
+    bits = np.concatenate([bits, np.zeros(nblk * BLK * k - bits.size, np.uint8)])
+    return np.packbits(bits.reshape(-1, 32), axis=1, bitorder="little").view(np.uint32).reshape(-1)
+
+
+def unpack_fine(words: np.ndarray, k: int, n: int) -> np.ndarray:
+    bits = np.unpackbits(np.asarray(words, np.uint32).view(np.uint8), bitorder="little")[:n * k]
+    return (bits.reshape(n, k).astype(np.int64) << np.arange(k)).sum(1)
+
+
 def compress_chunk(t: np.ndarray, bits: int, scales_f32: Optional[np.ndarray] = None,
-                   entropy: bool = True, dither_seed: Optional[int] = None) -> Chunk:
+                   entropy: bool = True, dither_seed: Optional[int] = None, escape: bool = False) -> Chunk:
     """CompressedKVCache._compress_tensor (llm/compressed_kv_cache.py:176-287).
 
     t: (B, H, T, hd) array in the model dtype.  scales_f32 injects the per-head
-    fp32 scale (bit-exact comparisons); otherwise the oracle's own sigma^2."""
+    fp32 scale (bit-exact comparisons); otherwise the oracle's own sigma^2.
+    escape: coordinates whose alphabet exceeds L are coded as coarse symbols
+    s >> k_j plus raw low bits (a format of this build; see escape_shifts)."""
     B, H, T, hd = t.shape
     assert hd % 8 == 0
     t32 = np.asarray(t, dtype=np.float32)
@@ -402,6 +453,12 @@ def compress_chunk(t: np.ndarray, bits: int, scales_f32: Optional[np.ndarray] = 
                dither_seed=dither_seed)
     if not entropy:
         return ch
+    if escape:
+        ks = escape_shifts(syms, coset)
+        if ks.any():
+            ch.esc_k = ks
+            ch.fine = {j: pack_fine(syms[:, j] & ((1 << int(ks[j])) - 1), int(ks[j])) for j in range(8) if ks[j]}
+            syms = syms >> ks[None, :]
     all_words = []
     for c in (0, 1):
         sc = syms[coset == c]
@@ -429,6 +486,10 @@ def decompress_chunk(ch: Chunk, out_dtype=np.float16) -> np.ndarray:
     for s in ch.streams:
         rows = np.where(cos == s.coset)[0]
         syms[rows, s.idx] = rans_decode(s.words, s.n_bits, s.state, s.table, s.n_symbols)
+    if ch.esc_k is not None:
+        for j, words in ch.fine.items():
+            k = int(ch.esc_k[j])
+            syms[:, j] = (syms[:, j] << k) + unpack_fine(words, k, n)
     q = symbols_to_e8(cos, syms[:, :7], syms[:, 7])
     if ch.dither_seed is not None:
         q = (q - dither(ch.dither_seed, n)).astype(np.float32)

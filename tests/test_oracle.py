@@ -324,3 +324,51 @@ def test_decode_attention_matches_sdpa_float64(B, Hq, Hkv, S):
     # a head whose keys are all equal averages V
     k2 = np.repeat(k[:, :, :1], S, axis=2)
     np.testing.assert_allclose(O.decode_attention(q, k2, v)[:, ::g, 0], v.mean(axis=2), rtol=1e-12, atol=1e-13)
+
+
+def _heavy_k(seed, T=700, H=4, mult=20.0):
+    rng = np.random.default_rng(seed)
+    k = rng.standard_t(3.0, size=(1, H, T, 128)).astype(np.float32)
+    for h in range(H):
+        k[:, h, :, rng.permutation(128)[:8]] *= mult
+    return k.astype(np.float16)
+
+
+def test_pack_fine_known_answer():
+    """Low bits at bit v * k, least significant first, blocks of 512 vectors
+    padded to 16 k words."""
+    w = O.pack_fine(np.array([1, 2, 3, 0, 7]), 3)
+    assert w.shape == (48,)
+    # 001 010 011 000 111 read LSB first: bits 0..14 = 1,0,0, 0,1,0, 1,1,0, 0,0,0, 1,1,1
+    assert int(w[0]) == (1 | 1 << 4 | 1 << 6 | 1 << 7 | 7 << 12) and not w[1:].any()
+    v = np.random.default_rng(3).integers(0, 1 << 5, 1500)
+    np.testing.assert_array_equal(O.unpack_fine(O.pack_fine(v, 5), 5, 1500), v)
+
+
+@pytest.mark.parametrize("seed,bits", [(0, 5), (1, 4), (2, 5), (3, 3)])
+def test_escape_round_trip_and_minimal_shift(seed, bits):
+    """The coarse / fine escape (a format of this build) is lossless, keeps
+    every coarse alphabet within L, and uses the least shift that does."""
+    k = _heavy_k(seed)
+    s32, s16 = O.cache_scales(O.head_sigma2(k.astype(np.float32)), bits)
+    q = O.quantize_heads(k.astype(np.float32), s32)
+    coset, free, c8h = O.e8_to_symbols(q)
+    syms = np.concatenate([free, c8h[:, None]], 1)
+    ks = O.escape_shifts(syms, coset)
+    for j in range(8):
+        for c in (0, 1):
+            col = syms[coset == c][:, j]
+            if len(col):
+                assert (col.max() >> ks[j]) - (col.min() >> ks[j]) + 5 <= O.L
+        if ks[j]:   # one shift less does not fit
+            assert any((syms[coset == c][:, j].max() >> (ks[j] - 1)) - (syms[coset == c][:, j].min() >> (ks[j] - 1))
+                       + 5 > O.L for c in (0, 1) if (coset == c).any())
+    ch = O.compress_chunk(k, bits, scales_f32=s32, escape=True)
+    want = (q.reshape(4, -1, 8) * s16.astype(np.float32)[:, None, None]).astype(np.float32)
+    np.testing.assert_array_equal(O.decompress_chunk(ch), want.reshape(k.shape).astype(np.float16))
+    assert all(len(s.table.freqs) <= O.L for s in ch.streams)
+    if ks.any():
+        assert ch.esc_k is not None and sorted(ch.fine) == [j for j in range(8) if ks[j]]
+    plain = O.compress_chunk(k, bits, scales_f32=s32, escape=False) if not ks.any() else None
+    if plain is not None:   # no escape needed: the reference's format, word for word
+        assert ch.esc_k is None and np.array_equal(ch.bitstream, plain.bitstream)

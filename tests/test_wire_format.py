@@ -121,6 +121,54 @@ def test_wire_rejects_corruption_and_versions_cpu(tmp_path):
         codec.from_bytes(bytes(v2), device="cpu")
 
 
+def _with_escape(e, seed=5):
+    """The fake batch with an escape on chunk 0 (coordinates 1 and 7)."""
+    rng = np.random.default_rng(seed)
+    C, nb = e.n_chunks, e.nblk
+    kh = np.zeros((C, 8), np.int32)
+    kh[0, 1], kh[0, 7] = 2, 3
+    per = 16 * nb * kh.astype(np.int64).reshape(-1)
+    off = np.cumsum(per) - per
+    fine = rng.integers(0, 2**31, int(per.sum()) + 1).astype(np.int32)
+    e.extra["esc"] = codec.Escape(k=torch.from_numpy(kh), off=torch.from_numpy(off), fine=torch.from_numpy(fine),
+                                  k_host=kh)
+    return e
+
+
+def test_wire_round_trip_escape_cpu():
+    """Escaped batches travel as version 2 with their shifts and low-bit
+    words; batches without an escape stay version 1."""
+    e = _fake_batch(seed=4)
+    assert int(np.frombuffer(codec.to_bytes(e)[8:12], np.uint32)[0]) == 1
+    e = _with_escape(e)
+    b = codec.to_bytes(e)
+    assert int(np.frombuffer(b[8:12], np.uint32)[0]) == 2
+    r = codec.from_bytes(b, device="cpu")
+    assert r.escape is not None and np.array_equal(r.escape.k_host, e.escape.k_host)
+    ef, rf = e.escape.fine.numpy(), r.escape.fine.numpy()
+    for o1, o2, k in zip(e.escape.off.numpy(), r.escape.off.numpy(), e.escape.k_host.reshape(-1)):
+        n = 16 * e.nblk * int(k)
+        assert np.array_equal(ef[o1:o1 + n], rf[o2:o2 + n])
+    assert np.array_equal(r.reference_bytes().numpy(), e.reference_bytes().numpy())
+    assert int(r.reference_bytes()[0] - r.reference_bytes()[1]) != 0
+    one = r.select(0)
+    assert one.escape is not None and one.escape.k_host.shape == (1, 8)
+
+
+def test_wire_rejects_bad_escape_cpu():
+    e = _with_escape(_fake_batch(seed=4))
+    e.escape.k_host[0, 1] = 9
+    with pytest.raises(codec.WireFormatError, match="escape"):
+        codec.from_bytes(codec.to_bytes(e), device="cpu")
+    e = _with_escape(_fake_batch(seed=4))
+    b = bytearray(codec.to_bytes(e))
+    b[8:12] = np.uint32(1).tobytes()   # escape fields in a version-1 batch
+    import zlib
+    b[-4:] = np.uint32(zlib.crc32(bytes(b[:-4])) & 0xFFFFFFFF).tobytes()
+    with pytest.raises(codec.WireFormatError, match="escape"):
+        codec.from_bytes(bytes(b), device="cpu")
+
+
 def _corrupt(field, edit):
     """A fresh valid batch with one field edited (to_bytes writes a valid CRC)."""
     e = _fake_batch(seed=3)
@@ -172,20 +220,25 @@ def test_wire_rejects_bad_sizes_and_shape_cpu():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("kind", ["normal", "outliers", "rotated"])
+@pytest.mark.parametrize("kind", ["normal", "outliers", "rotated", "escaped"])
 def test_wire_round_trip_decodes_bit_exact_gpu(kind):
     g = torch.Generator().manual_seed(7)
     x = torch.randn(3, 1, 4, 256, 128, generator=g)
     if kind == "outliers":
         x[..., :4] *= 10
+    if kind == "escaped":   # heavy-tailed K with x20 outlier channels at 5 bits: alphabets beyond L
+        rng = np.random.default_rng(7)
+        x = torch.from_numpy(rng.standard_t(3.0, size=(3, 1, 4, 1024, 128)).astype(np.float32))
+        x[..., [3, 40, 77, 100]] *= 20.0
     x = x.half().cuda()
     if kind == "rotated":
         from latticequant_amd.llm.rotated import decode_rotated, encode_rotated
         enc, _ = encode_rotated(x, 4, [0, 1, 2], [0, 1, 0])
         ref = decode_rotated(enc)
     else:
-        enc, _ = codec.encode_batch(x, 4)
+        enc, _ = codec.encode_batch(x, 5 if kind == "escaped" else 4)
         ref = codec.decode_batch(enc)
+        assert (enc.escape is not None) == (kind == "escaped")
     b = codec.to_bytes(enc)
     r = codec.from_bytes(b)
     for a, b2 in zip(_meaningful_tables(enc), _meaningful_tables(r)):

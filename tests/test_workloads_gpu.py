@@ -61,10 +61,11 @@ def test_c4_full_size_layers_gpu(layer):
     """C4 at full size ([1, 4, 16384, 128] per chunk), one layer of the
     3 / 4 / 5-bit cycle per case: V bit-exact against the oracle; K (Student-t
     with outlier channels, int16 symbols) with every stream's table and words
-    equal to the oracle's, or AlphabetError where an alphabet exceeds L."""
+    equal to the oracle's, escaped (coarse streams + raw low bits, equal to the
+    oracle's restatement) where an alphabet exceeds L."""
     from latticequant_amd import codec
     from latticequant_amd.allocation.eval_alloc import cyclic_schedule
-    from tests.test_wide_gpu import check_chunk
+    from tests.test_wide_gpu import check_chunk, check_escape
     T = 16384
     s = cyclic_schedule(3, seed=0)[layer]
     rng = np.random.default_rng(2026 + layer)
@@ -80,16 +81,15 @@ def test_c4_full_size_layers_gpu(layer):
     syms = np.concatenate([free, c8h[:, None]], 1)
     widest = max(int(syms[coset == c][:, i].max() - syms[coset == c][:, i].min() + 5)
                  for c in (0, 1) for i in range(8) if (coset == c).any())
-    if widest > O.L:
-        with pytest.raises(codec.AlphabetError):
-            codec.encode_batch(kk[None], s["K"], scale32=s32)
-        return
     ek, deq = codec.encode_batch(kk[None], s["K"], scale32=s32, deq_out=True)
     assert widest <= 264 or ek.extra["wide"]
+    assert (ek.escape is not None) == (widest > O.L)
     want = (q.view(4, -1, 8) * ek.scale16.float().view(4, 1, 1)).view(kk.shape).half()
     assert torch.equal(codec.decode_batch(ek)[0], want)   # lossless coding of the lattice points
-    chk = O.compress_chunk(k, s["K"], scales_f32=s32.cpu().numpy())
-    assert check_chunk(ek, 0, chk) == widest
+    chk = O.compress_chunk(k, s["K"], scales_f32=s32.cpu().numpy(), escape=True)
+    widest_coded = check_chunk(ek, 0, chk)
+    assert widest_coded == widest if widest <= O.L else widest_coded <= O.L
+    check_escape(ek, 0, chk)
 
 
 def test_c5_full_chunk_round_trip_gpu():
