@@ -780,6 +780,10 @@ def encode_batch_deferred(x: torch.Tensor, bits, deq_out: bool = False, dither_s
 # batches without escaped chunks are still written as version 1.
 
 WIRE_MAGIC = b"LQE8RANS"
+# the dither a seed stands for (lq_device.h dither8): 2 = 16-bit fields of two
+# SplitMix64 outputs per vector; batches with a dither seed and no scheme 2
+# were written with another dither and are refused
+DITHER_SCHEME = 2
 WIRE_VERSION = 2
 WIRE_VERSIONS_READ = (1, 2)
 
@@ -833,6 +837,7 @@ def to_bytes(enc: EncodedBatch) -> bytes:
     ds = enc.extra.get("dither_seed")
     if ds is not None:
         fields.append(("dither_seed", ds.cpu().numpy().astype(np.int64)))
+        extra["dither_scheme"] = DITHER_SCHEME
     if "rht" in enc.extra:
         layers, kvs = enc.extra["rht"]
         extra["rht"] = [[int(v) for v in layers], [int(v) for v in kvs]]
@@ -1014,6 +1019,8 @@ def from_bytes(buf, device=None) -> EncodedBatch:
         chunk_base=T(np.cumsum(cw) - cw, torch.int64),
         words=torch.from_numpy(words.view(np.int32).copy()).to(dev), status=T(arrs["status"], torch.int32))
     if "dither_seed" in arrs:
+        if header.get("extra", {}).get("dither_scheme") != DITHER_SCHEME:
+            raise WireFormatError("the batch's dither seeds stand for another dither scheme")
         enc.extra["dither_seed"] = T(arrs["dither_seed"], torch.int64)
     if "rht" in header.get("extra", {}):
         layers, kvs = header["extra"]["rht"]

@@ -145,7 +145,7 @@ __global__ __launch_bounds__(256) void k_rht(const void* __restrict__ x, int64_t
     load8(x, IN_DT, v, y);
     load_signs8(signs + ((rr / rows_per_sign) % n_sign) * (int64_t)d + 8 * part, s);
     // lanes of one row are consecutive and lpr divides 64, so rows never straddle a wave
-    rht_lanes(y, s, part, lpr, div, inverse != 0);
+    rht_lanes(y, s, part, lpr, div, 1.0f / div, inverse != 0);
     if (live) store8(out, OUT_DT, v, y);
 }
 

@@ -128,12 +128,13 @@ __global__ void k_head_sumsq(const void* __restrict__ x, int dtype, int64_t vec_
         // rows are whole within [v0, v1) and lpr divides the block size, so the
         // lanes of a row enter and leave the loop together
         const int part = (int)(threadIdx.x % lpr);
+        const float rrcp = 1.0f / rdiv;
         float sg[8];
         load_signs8(signs + h * (8 * (int64_t)lpr) + 8 * part, sg);
         for (; v < v1; v += bd) {
             float xv[8];
             load8(x, dtype, h * vec_per_head + v, xv);
-            rht_lanes(xv, sg, part, lpr, rdiv, false);
+            rht_lanes(xv, sg, part, lpr, rdiv, rrcp, false);
 #pragma unroll
             for (int i = 0; i < 8; i++) acc4[0] += (double)xv[i] * (double)xv[i];
         }
@@ -278,10 +279,11 @@ __device__ __forceinline__ void stage_hist(const uint4& w, int row16, int n0, in
 // spills through VGPR lanes in the block loop).  ROT: the input rows are first
 // rotated in registers (rht_lanes, sign row = the head, lpr lanes per row),
 // exactly the fp32 values a materialised forward rotation holds; no
-// dequantised output.  LDT >= 0: the input dtype as a compile-time constant
-// (the lean launches), so no dtype test is kept live across the block loop.
+// dequantised output, at least 5 waves per SIMD.  LDT >= 0: the input dtype as
+// a compile-time constant (the lean launches), so no dtype test is kept live
+// across the block loop.
 template <typename SymT, bool DITHER, bool LEAN = false, bool ROT = false, int LDT = -1>
-__global__ __launch_bounds__(kQThreads, LEAN ? 7 : 1) void k_chunk_quantize(
+__global__ __launch_bounds__(kQThreads, LEAN ? 7 : (ROT ? 5 : 1)) void k_chunk_quantize(
     const void* __restrict__ x, int dtype, int64_t n_heads, int64_t bph, int64_t nblk,
     const float* __restrict__ scale32, const int32_t* __restrict__ fastdiv, SymT* __restrict__ sym,
     uint8_t* __restrict__ coset_bits, uint32_t* __restrict__ blk_n1, uint32_t* __restrict__ hist,
@@ -294,6 +296,8 @@ __global__ __launch_bounds__(kQThreads, LEAN ? 7 : 1) void k_chunk_quantize(
     __shared__ __align__(16) SymT stage[kSymStride];
     __shared__ __align__(16) unsigned long long masks[kBlk / 64];
     __shared__ int sflag;
+    __shared__ __align__(16) float tslot[ROT ? 8 * kQThreads : 4];   // ROT: each lane's t for the exact path
+    const float rrcp = ROT ? 1.0f / rdiv : 1.0f;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -375,7 +379,7 @@ __global__ __launch_bounds__(kQThreads, LEAN ? 7 : 1) void k_chunk_quantize(
                     float sg[8];
                     const int part = tid & (lpr - 1);
                     load_signs8(signs + hq * (8 * (int64_t)lpr) + 8 * part, sg);
-                    rht_lanes(xv, sg, part, lpr, rdiv, false);
+                    rht_lanes(xv, sg, part, lpr, rdiv, rrcp, false);
                 }
                 if (fast) {
 #pragma unroll
@@ -390,8 +394,19 @@ __global__ __launch_bounds__(kQThreads, LEAN ? 7 : 1) void k_chunk_quantize(
                     for (int i = 0; i < 8; i++) t[i] = t[i] + dd[i];
                 }
                 int c;
-                if constexpr (ROT) {   // the rotation is cross-lane, so t cannot be recomputed in a
-                    c = e8_nearest(t, ic);   // divergent branch; keeping it live costs this variant a wave
+                if constexpr (ROT) {
+                    // the rotation is cross-lane, so the rare exact path cannot
+                    // recompute t in a divergent branch: t waits in the lane's
+                    // LDS slot instead of in registers
+                    float4* slot = reinterpret_cast<float4*>(tslot + 8 * tid);
+                    slot[0] = make_float4(t[0], t[1], t[2], t[3]);
+                    slot[1] = make_float4(t[4], t[5], t[6], t[7]);
+                    c = e8_nearest_fast(t, ic, [&](float tt[8]) {
+                        asm volatile("" ::: "memory");   // read the slot back: t is not kept live for this
+                        const float4 a = slot[0], b = slot[1];
+                        tt[0] = a.x; tt[1] = a.y; tt[2] = a.z; tt[3] = a.w;
+                        tt[4] = b.x; tt[5] = b.y; tt[6] = b.z; tt[7] = b.w;
+                    });
                 } else {               // the rare exact path recomputes t from x
                     c = e8_nearest_fast(t, ic, [&](float tt[8]) {
                         float xx[8];

@@ -329,9 +329,11 @@ __host__ __device__ void np_net_range(const int64_t* key, int16_t* arg, int len,
 }
 
 // arg[0 .. n) = numpy.argsort(key[0 .. n)) for n <= 1028 (LDS arrays; every
-// lane of the group calls it; uniform control flow).
+// lane of the group calls it; uniform control flow).  Out of line: inlined
+// into the table kernels its code costs them registers on every call path
+// (the wave-per-stream table build measured 29 -> 53 us per C2 launch).
 template <typename G>
-__host__ __device__ void np_argsort(const int64_t* key, int16_t* arg, int n, NpScratch* ns) {
+__host__ __device__ __attribute__((noinline)) void np_argsort(const int64_t* key, int16_t* arg, int n, NpScratch* ns) {
     for (int i = G::tid(); i < n; i += G::size()) arg[i] = (int16_t)i;
     G::sync();
     if (n <= 1) return;

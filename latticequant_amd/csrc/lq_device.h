@@ -303,13 +303,49 @@ __device__ __forceinline__ float div_scaled(float x, float s, float r, bool fast
 // lpr = d / 8 consecutive lanes (lpr divides 64), 8 consecutive elements per
 // lane: stages h < 8 run in registers, h >= 8 across lanes (partner lane ^ h/8).
 // Every lane of a row must execute this together.  div = f32(sqrt(d)).
+//
+// Partner lanes l ^ 1, l ^ 2, l ^ 4, l ^ 8 lie in one 16-lane DPP row and are
+// read with DPP moves (quad_perm for ^1 and ^2, two bank-masked row shifts
+// for ^4 and ^8), not through the LDS crossbar; the butterfly is then one
+// FMA, fma(y, +-1, partner) = RN(partner +- y): the lower lane of a pair gets
+// a + b, the upper a - b, bit for bit as the add / subtract.  Rows of more
+// than 16 lanes (head_dim > 128) use shuffles for the partners beyond.
+template <int HL>
+__device__ __forceinline__ float lane_xor(float v) {
+    const int i = __builtin_bit_cast(int, v);
+    int r;
+    if constexpr (HL == 1) {
+        r = __builtin_amdgcn_update_dpp(i, i, 0xB1, 0xF, 0xF, false);    // quad_perm [1, 0, 3, 2]
+    } else if constexpr (HL == 2) {
+        r = __builtin_amdgcn_update_dpp(i, i, 0x4E, 0xF, 0xF, false);    // quad_perm [2, 3, 0, 1]
+    } else if constexpr (HL == 4) {   // row_shl:4 into banks 0, 2; row_shr:4 into banks 1, 3
+        r = __builtin_amdgcn_update_dpp(__builtin_amdgcn_update_dpp(i, i, 0x104, 0xF, 0x5, false), i, 0x114, 0xF,
+                                        0xA, false);
+    } else if constexpr (HL == 8) {   // row_shl:8 into banks 0, 1; row_shr:8 into banks 2, 3
+        r = __builtin_amdgcn_update_dpp(__builtin_amdgcn_update_dpp(i, i, 0x108, 0xF, 0x3, false), i, 0x118, 0xF,
+                                        0xC, false);
+    } else {
+        return __shfl_xor(v, HL, 64);
+    }
+    return __builtin_bit_cast(float, r);
+}
+
+template <int HL>
+__device__ __forceinline__ void fwht_cross_t(float y[8], int part) {
+    const float sgn = (part & HL) ? -1.0f : 1.0f;   // upper lane of the pair: partner - own
+#pragma unroll
+    for (int i = 0; i < 8; i++) y[i] = __builtin_fmaf(y[i], sgn, lane_xor<HL>(y[i]));
+}
+
 // One butterfly stage across lanes: partner lane ^ hl (stage h = 8 hl).
 __device__ __forceinline__ void fwht_cross(float y[8], int part, int hl) {
-    const bool upper = (part & hl) != 0;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const float o = __shfl_xor(y[i], hl, 64);
-        y[i] = upper ? o - y[i] : y[i] + o;   // lower keeps a + b, upper gets a - b
+    switch (hl) {
+        case 1: fwht_cross_t<1>(y, part); break;
+        case 2: fwht_cross_t<2>(y, part); break;
+        case 4: fwht_cross_t<4>(y, part); break;
+        case 8: fwht_cross_t<8>(y, part); break;
+        case 16: fwht_cross_t<16>(y, part); break;
+        default: fwht_cross_t<32>(y, part); break;
     }
 }
 
@@ -326,19 +362,65 @@ __device__ __forceinline__ void fwht_stages(float y[8], int part, int nl) {
             y[i + h] = a - b;
         }
     }
-    for (int hl = 1; hl < nl; hl <<= 1) fwht_cross(y, part, hl);
+    if (nl > 1) fwht_cross_t<1>(y, part);
+    if (nl > 2) fwht_cross_t<2>(y, part);
+    if (nl > 4) fwht_cross_t<4>(y, part);
+    if (nl > 8) fwht_cross_t<8>(y, part);
+    if (nl > 16) fwht_cross_t<16>(y, part);
+    if (nl > 32) fwht_cross_t<32>(y, part);
 }
 
-__device__ __forceinline__ void rht_lanes(float y[8], const float s[8], int part, int lpr, float div, bool inverse) {
+// y / d as IEEE fp32 division rounds it, for the rotation's divisor
+// d = f32(sqrt(D)), D a power of two in [8, 512], in three operations given
+// r = RN(1 / d): q0 = RN(y r), the residual e = y - q0 d (exact, one FMA),
+// RN(q0 + e r).  Each such d is a power of two or 2^k f32(sqrt 2), and for
+// those divisors the three operations give RN(y / d) for every fp32
+// significand (checked exhaustively by tests/host/div_sqrt_check.cpp), hence
+// for every y whose residual stays exact: |y| >= 2^-100 suffices.  Zeros
+// (whose sign the FMA form loses), tiny, infinite and NaN y take the IEEE
+// division.
+__host__ __device__ __forceinline__ float div_sqrt_dim(float y, float d, float r) {
+    const float q0 = y * r;
+    const float e = __builtin_fmaf(-q0, d, y);
+    float q = __builtin_fmaf(e, r, q0);
+    if (!(__builtin_fabsf(y) >= 0x1p-100f && __builtin_fabsf(y) <= 0x1.fffffep127f)) q = y / d;
+    return q;
+}
+
+// div_sqrt_dim of 8 values with one test per row: the three operations when
+// every |y_i| lies in [2^-100, FLT_MAX], else IEEE division for all 8.
+__host__ __device__ __forceinline__ void div_sqrt_dim8(float y[8], float d, float r) {
+    float lo = __builtin_fabsf(y[0]), hi = lo;
+#pragma unroll
+    for (int i = 1; i < 8; i++) {
+        lo = __builtin_fminf(lo, __builtin_fabsf(y[i]));
+        hi = __builtin_fmaxf(hi, __builtin_fabsf(y[i]));
+    }
+    if (lo >= 0x1p-100f && hi <= 0x1.fffffep127f) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float q0 = y[i] * r;
+            const float e = __builtin_fmaf(-q0, d, y[i]);
+            y[i] = __builtin_fmaf(e, r, q0);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) y[i] = y[i] / d;
+    }
+}
+
+// rcp = RN(1 / div) (the caller's, computed once per launch).
+__device__ __forceinline__ void rht_lanes(float y[8], const float s[8], int part, int lpr, float div, float rcp,
+                                          bool inverse) {
     if (!inverse) {
 #pragma unroll
         for (int i = 0; i < 8; i++) y[i] = y[i] * s[i];
     }
     fwht_stages(y, part, lpr);
+    div_sqrt_dim8(y, div, rcp);
+    if (inverse) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        y[i] = y[i] / div;
-        if (inverse) y[i] = y[i] * s[i];
+        for (int i = 0; i < 8; i++) y[i] = y[i] * s[i];
     }
 }
 
@@ -352,12 +434,13 @@ __device__ __forceinline__ void load_signs8(const float* p, float s[8]) {
 //
 // Subtractive dither of the rotated path (build-defined: the reference has no
 // E8 dither).  Vector v of a chunk with seed s gets d in [-1, 1)^8, uniform on
-// a 2^-23 grid: a fundamental domain of 2Z^8, a sublattice of E8, so modulo E8
+// a 2^-15 grid: a fundamental domain of 2Z^8, a sublattice of E8, so modulo E8
 // the dither is uniform on the Voronoi cell and the error Q(t + d) - d - t is
-// uniform on the cell and independent of t.  Coordinates 2p, 2p + 1 come from
-// 24-bit fields of h = mix64(mix64(s) + 4 v + p), mix64 the SplitMix64 output
-// function (Steele, Lea, Flood 2014).  The quantizer adds d to x / scale; the
-// decoder subtracts it from the lattice point before scaling.
+// uniform on the cell (on the grid's resolution) and independent of t.
+// Coordinates 4p .. 4p + 3 are the four 16-bit fields (least significant
+// first) of h_p = mix64(mix64(s) + 2 v + p), p = 0, 1, with mix64 the
+// SplitMix64 output function (Steele, Lea, Flood 2014).  The quantizer adds d
+// to x / scale; the decoder subtracts it from the lattice point before scaling.
 __host__ __device__ inline uint64_t mix64(uint64_t z) {
     z += 0x9E3779B97F4A7C15ull;
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -368,10 +451,13 @@ __host__ __device__ inline uint64_t mix64(uint64_t z) {
 // key = mix64(seed); d = dither of vector v (exact in fp32)
 __device__ __forceinline__ void dither8(uint64_t key, int64_t v, float d[8]) {
 #pragma unroll
-    for (int p = 0; p < 4; p++) {
-        const uint64_t h = mix64(key + (uint64_t)v * 4u + (uint64_t)p);
-        d[2 * p] = (float)((int32_t)((h >> 40) & 0xFFFFFFu) - (1 << 23)) * 0x1p-23f;
-        d[2 * p + 1] = (float)((int32_t)((h >> 16) & 0xFFFFFFu) - (1 << 23)) * 0x1p-23f;
+    for (int p = 0; p < 2; p++) {
+        const uint64_t h = mix64(key + (uint64_t)v * 2u + (uint64_t)p);
+        const uint32_t lo = (uint32_t)h, hi = (uint32_t)(h >> 32);
+        d[4 * p + 0] = (float)((int32_t)(lo & 0xFFFFu) - (1 << 15)) * 0x1p-15f;
+        d[4 * p + 1] = (float)((int32_t)(lo >> 16) - (1 << 15)) * 0x1p-15f;
+        d[4 * p + 2] = (float)((int32_t)(hi & 0xFFFFu) - (1 << 15)) * 0x1p-15f;
+        d[4 * p + 3] = (float)((int32_t)(hi >> 16) - (1 << 15)) * 0x1p-15f;
     }
 }
 

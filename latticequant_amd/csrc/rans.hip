@@ -168,8 +168,15 @@ __device__ void adjust_pass(const int64_t* counts, int n, int32_t* freqs, int di
         matters = block_sum<G>(mt) != 0;
     }
     if (matters) {
-        np_argsort<G>(kk, a, n, ns);
-        for (int p = G::tid(); p < n; p += G::size()) inset[a[p]] = p < rem ? 1 : 0;
+        if (n <= 256) {   // numpy's network directly (np_argsort's first and only frame)
+            for (int i = G::tid(); i < n; i += G::size()) { ns->k[i] = kk[i]; ns->a[i] = (int16_t)i; }
+            G::sync();
+            np_net_sort<G>(ns->k, ns->a, n);
+            for (int p = G::tid(); p < n; p += G::size()) inset[ns->a[p]] = p < rem ? 1 : 0;
+        } else {
+            np_argsort<G>(kk, a, n, ns);
+            for (int p = G::tid(); p < n; p += G::size()) inset[a[p]] = p < rem ? 1 : 0;
+        }
         G::sync();
     }
     for (int i = G::tid(); i < n; i += G::size()) {
@@ -1073,6 +1080,7 @@ __global__ __launch_bounds__(kDecThreads) void k_chunk_decode(
     __shared__ __align__(16) uint16_t stg[kDecBlocks * 2 * kDecGroupU16];   // 34 KB
     __shared__ uint32_t bm1[kDecBlocks][kBlk / 32 + 1];                     // coset-1 bits, one zero word after each row
     const int tid = threadIdx.x;
+    const float rrcp = ROT ? 1.0f / rdiv : 1.0f;   // the rotation's RN(1 / sqrt(head_dim))
     const int64_t V = n_heads * bph;
     const int64_t groups = (nblk + kDecBlocks - 1) / kDecBlocks;   // per chunk
     const int64_t total = n_chunks * groups;
@@ -1251,7 +1259,7 @@ __global__ __launch_bounds__(kDecThreads) void k_chunk_decode(
                 load_signs8(sgp + 8 * (l16 & (lpr - 1)), sg);
                 if (lpr < 16) {
                     if (mine) {
-                        rht_lanes(y, sg, l16 & (lpr - 1), lpr, rdiv, true);
+                        rht_lanes(y, sg, l16 & (lpr - 1), lpr, rdiv, rrcp, true);
                         store8(ob, OUT_DT, p, y);
                     }
                 } else {
@@ -1269,8 +1277,9 @@ __global__ __launch_bounds__(kDecThreads) void k_chunk_decode(
                             for (int j = 0; j < 8; j++) y[j] = pend[j];
                         }
                         fwht_cross(y, l16, 8);
+                        div_sqrt_dim8(y, rdiv, rrcp);
 #pragma unroll
-                        for (int j = 0; j < 8; j++) y[j] = (y[j] / rdiv) * sg[j];
+                        for (int j = 0; j < 8; j++) y[j] = y[j] * sg[j];
                         store8(ob, OUT_DT, base + l16, y);
                     }
                 }

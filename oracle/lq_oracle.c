@@ -116,15 +116,15 @@ uint64_t lqo_mix64(uint64_t z) {
 }
 
 /* Dither of vectors v0 .. v0 + n - 1 of a chunk with seed `seed`: coordinates
- * 2p, 2p + 1 from bits 40..63 and 16..39 of mix64(mix64(seed) + 4 v + p),
- * each (k - 2^23) * 2^-23 in [-1, 1). */
+ * 4p .. 4p + 3 from the four 16-bit fields (least significant first) of
+ * mix64(mix64(seed) + 2 v + p), p = 0, 1, each (k - 2^15) * 2^-15 in [-1, 1). */
 void lqo_dither(int64_t seed, int64_t v0, int64_t n, float *d) {
     const uint64_t key = lqo_mix64((uint64_t)seed);
     for (int64_t v = 0; v < n; v++) {
-        for (int p = 0; p < 4; p++) {
-            const uint64_t h = lqo_mix64(key + (uint64_t)(v0 + v) * 4u + (uint64_t)p);
-            d[8 * v + 2 * p] = (float)((int32_t)((h >> 40) & 0xFFFFFFu) - (1 << 23)) * 0x1p-23f;
-            d[8 * v + 2 * p + 1] = (float)((int32_t)((h >> 16) & 0xFFFFFFu) - (1 << 23)) * 0x1p-23f;
+        for (int p = 0; p < 2; p++) {
+            const uint64_t h = lqo_mix64(key + (uint64_t)(v0 + v) * 2u + (uint64_t)p);
+            for (int j = 0; j < 4; j++)
+                d[8 * v + 4 * p + j] = (float)((int32_t)((h >> (16 * j)) & 0xFFFFu) - (1 << 15)) * 0x1p-15f;
         }
     }
 }

@@ -174,12 +174,21 @@ def test_rht_golden_gpu():
     np.testing.assert_array_equal(back.cpu().numpy(), O.rht_f32(g["y"], g["signs"][2], inverse=True))
     # head-batched transform, every power-of-two width the kernel takes
     rng = np.random.default_rng(4)
-    for d in (8, 16, 64, 128, 256, 512):
+    for d in (8, 16, 32, 64, 128, 256, 512):
         x = rng.standard_normal((2, 3, 5, d)).astype(np.float32)
+        # rows that take the division's IEEE branch: zeros (their sign), tiny and huge values
+        x[0, 0, 0] = 0.0
+        x[0, 0, 1] = -0.0
+        x[0, 1, 2] = 1e-33
+        x[1, 2, 3, : d // 2] = 1.0e35   # large, and the sums stay finite
+        x[1, 1, 4, 0] = -2.0 ** -120
         signs = pl.head_signs(d, 3, 3, 1)
         y = pl.rht_heads(torch.from_numpy(x).cuda(), signs)
         want = np.stack([O.rht_f32(x[:, h], signs[h].numpy()) for h in range(3)], 1)
-        np.testing.assert_array_equal(y.cpu().numpy(), want)
+        np.testing.assert_array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
+        back = pl.rht_heads(y, signs, inverse=True)
+        wantb = np.stack([O.rht_f32(want[:, h], signs[h].numpy(), inverse=True) for h in range(3)], 1)
+        np.testing.assert_array_equal(back.cpu().numpy().view(np.uint32), wantb.view(np.uint32))
         x16 = torch.from_numpy(x).half()
         y16 = pl.rht_heads(x16.cuda(), signs, out_dtype=torch.float16)
         want16 = np.stack([O.rht_f32(x16[:, h].float().numpy(), signs[h].numpy()) for h in range(3)], 1)

@@ -36,13 +36,15 @@ def test_dither_fields_and_distribution():
     d = O.dither(12345, n)
     assert d.dtype == np.float32 and d.shape == (n, 8)
     assert d.min() >= -1.0 and d.max() < 1.0
-    # coordinates 2p, 2p+1 are bits 40..63 and 16..39 of mix64(mix64(seed) + 4 v + p)
+    # coordinates 4p .. 4p+3 are the 16-bit fields of mix64(mix64(seed) + 2 v + p), low field first
     key = _mix64_py(12345)
     for v in (0, 1, 777, n - 1):
-        for p in range(4):
-            h = _mix64_py((key + 4 * v + p) & M64)
-            assert d[v, 2 * p] == np.float32((((h >> 40) & 0xFFFFFF) - (1 << 23)) * 2.0**-23)
-            assert d[v, 2 * p + 1] == np.float32((((h >> 16) & 0xFFFFFF) - (1 << 23)) * 2.0**-23)
+        for p in range(2):
+            h = _mix64_py((key + 2 * v + p) & M64)
+            for j in range(4):
+                assert d[v, 4 * p + j] == np.float32((((h >> (16 * j)) & 0xFFFF) - (1 << 15)) * 2.0**-15)
+    # every value lies on the 2^-15 grid of [-1, 1)
+    assert np.array_equal(d * 2**15, np.round(d * 2**15))
     assert abs(d.mean()) < 4 * np.sqrt(1 / 3 / d.size)
     np.testing.assert_allclose(d.var(axis=0), 1 / 3, rtol=0.01)
     c = np.corrcoef(d[:, :4].T)

@@ -281,3 +281,17 @@ def test_bits_tensor_cache_cpu():
     assert codec._bits_tensor([3, 4], 2, "cpu").tolist() == [3, 4]
     with pytest.raises(ValueError):
         codec._bits_tensor([3, 4], 3, "cpu")
+
+
+def test_wire_refuses_other_dither_scheme_cpu(monkeypatch):
+    """A batch whose dither seeds stand for another dither scheme is refused
+    (its decode would subtract the wrong dither)."""
+    e = _fake_batch(seed=6)
+    e.extra["dither_seed"] = torch.tensor([11, 12], dtype=torch.int64)
+    r = codec.from_bytes(codec.to_bytes(e), device="cpu")
+    assert torch.equal(r.extra["dither_seed"], e.extra["dither_seed"])
+    monkeypatch.setattr(codec, "DITHER_SCHEME", 1)
+    b = codec.to_bytes(e)
+    monkeypatch.undo()
+    with pytest.raises(codec.WireFormatError, match="dither"):
+        codec.from_bytes(b, device="cpu")
