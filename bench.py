@@ -28,6 +28,7 @@ slice), the core count, torch's threads and the CPU model.
     python bench.py --e2e                   model decode tok/s through the HF cache interface
 """
 import argparse
+import dataclasses
 import hashlib
 import json
 import os
@@ -215,12 +216,14 @@ def bench_c1(dev, iters=20):
     fallback for the rest, 1-bit mask, per-head scales) -> fused merge back to
     fp16.  B = 4 D + 2 P, P = 4 V_in + 16 V_oor + ceil(V/8) + 2 H.
 
-    Timed: the device round trip (per-head scales, codec.compact_encode: one
-    quantize + compaction pass, codec.compact_merge: no host sync); the round
-    trip through the API (compress_fixed_rate, whose one host sync reads the
-    row counts that size the chunk's tensors, then fused_decompress_chunk); and
-    the merge kernel alone (the reference's own throughput method,
-    core/triton_dequant.py:238-286); each after a 512 MiB cache flush and warm
+    Timed: the device round trip (codec.compact_encode: sigma^2 partial sums,
+    then one pass that finalises the scales, quantizes, packs and compacts;
+    codec.compact_merge: no host sync); the round trip through the API
+    (compress_fixed_rate, whose one host sync reads the row counts that size
+    the chunk's tensors, then fused_decompress_chunk); and the merge kernel
+    alone (the reference's own throughput method,
+    core/triton_dequant.py:238-286), with its own look-back over the mask and
+    with the encoder's tile offsets; each after a 512 MiB cache flush and warm
     (the 12 MB working set then sits in the 256 MB MALL)."""
     from latticequant_amd import codec
     from latticequant_amd.llm.compressed_kv_cache import compress_fixed_rate
@@ -256,22 +259,31 @@ def bench_c1(dev, iters=20):
     flush = CacheFlush(dev)
     dv = lambda: codec.compact_merge(codec.compact_encode(kd, 4), out=dout)
     rt = lambda: fused_decompress_chunk(compress_fixed_rate(kd, 4))
-    mg = lambda: fused_decompress_chunk(ch)
+    ch_lb = dataclasses.replace(ch, tile_offsets=None)   # the merge then scans the mask itself
+    exact = exact and bool(np.array_equal(fused_decompress_chunk(ch_lb).cpu().numpy(), want))
+    mg = lambda: fused_decompress_chunk(ch_lb)
+    mt = lambda: fused_decompress_chunk(ch)
     us_dv_f, us_dv_w = timed_median(dv, iters, flush), timed_median(dv, iters)
     us_rt_f, us_rt_w = timed_median(rt, iters, flush), timed_median(rt, iters)
     us_mg_f, us_mg_w = timed_median(mg, iters, flush), timed_median(mg, iters)
+    us_mt_f = timed_median(mt, iters, flush)
     del flush
     return {"workload": "C1: K [1,8,2048,128] fp16 (randn seed 0, CPU), 4 b/d, compact 4-byte form + fp16 "
                         "fallback, no entropy coding", "input_sha256": sha, "bit_exact": exact,
             "in_range_frac": round(v_in / V, 4), "P_bytes": P, "B_bytes": B,
-            "round_trip_flushed": _roof(B, us_dv_f, "head scales + compact_encode (quantize, pack, compact in one "
-                                                   "pass) + compact_merge, no host sync; 512 MiB flush before each run"),
+            "round_trip_flushed": _roof(B, us_dv_f, "compact_encode (sigma^2 partials; then scales, quantize, pack, "
+                                                   "compact in one pass) + compact_merge, no host sync; 512 MiB "
+                                                   "flush before each run"),
             "round_trip_warm": _roof(B, us_dv_w, "same, warm (MALL-resident working set)"),
             "api_round_trip_flushed": _roof(B, us_rt_f, "compress_fixed_rate + fused_decompress_chunk (one host "
                                                        "sync for the row counts), flushed"),
             "api_round_trip_warm": _roof(B, us_rt_w, "same, warm"),
-            "merge_flushed": _roof(P + 2 * D, us_mg_f, "lq_fused_merge alone (reads P, writes 2 D), flushed"),
-            "merge_warm": _roof(P + 2 * D, us_mg_w, "lq_fused_merge alone, warm (MALL-resident)")}
+            "merge_flushed": _roof(P + 2 * D, us_mg_f, "lq_fused_merge alone (reads P, writes 2 D; look-back "
+                                                       "over the mask), flushed"),
+            "merge_warm": _roof(P + 2 * D, us_mg_w, "lq_fused_merge alone, warm (MALL-resident)"),
+            "merge_tile_offsets_flushed": _roof(P + 2 * D, us_mt_f, "lq_compact_merge with the encoder's tile "
+                                                                   "offsets (a chunk from compress_fixed_rate), "
+                                                                   "flushed")}
 
 
 def _student_t(shape, g):

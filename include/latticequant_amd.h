@@ -379,6 +379,23 @@ int lq_compact_encode(const void *d_x, int dtype, int64_t n_heads, int64_t bph, 
                       uint8_t *d_packed, uint16_t *d_fallback, int32_t *d_repr_heads, int64_t *d_tile_off,
                       int64_t *d_totals, void *d_work, hipStream_t s);
 
+/* lq_compact_encode with the per-head scales computed on the way (two
+ * launches in all): sigma^2 as lq_head_scales forms it (same partial sums,
+ * same order, so bit-identical), scale = sqrt(f32(2 pi e) sigma^2 4^-scale_bits)
+ * (1 where sigma^2 < 1e-12), its fp16 copy, float(scale16) for the merge, and
+ * the fast-division flags, all finalised inside the encoder, whose tiles of
+ * 1024 vectors then span at most two heads: bph >= 1024 is required
+ * (LQ_ERR_ARG otherwise; lq_head_scales + lq_compact_encode serve the rest).
+ * d_sigma2 may be NULL.  d_work: lq_compact_encode_scaled_workspace bytes,
+ * cleared by the call.  Outputs, totals and error word as lq_compact_encode.
+ * Replaces llm/compressed_kv_cache.py:188-196 (scales) with
+ * core/compact_storage.py:338-357 as lq_compact_encode does. */
+int64_t lq_compact_encode_scaled_workspace(int64_t n_heads, int64_t bph);
+int lq_compact_encode_scaled(const void *d_x, int dtype, int64_t n_heads, int64_t bph, int scale_bits, int bits,
+                             float *d_sigma2, float *d_scale32, uint16_t *d_scale16, float *d_scale16f,
+                             uint8_t *d_mask, uint8_t *d_packed, uint16_t *d_fallback, int32_t *d_repr_heads,
+                             int64_t *d_tile_off, int64_t *d_totals, void *d_work, hipStream_t s);
+
 /* lq_fused_merge with the tile offsets lq_compact_encode wrote (no count or
  * scan pass).  Replaces llm/fused_triton_merge.py:33-172 as lq_fused_merge. */
 int lq_compact_merge(const uint8_t *d_packed, int64_t n_packed, int bits, const uint16_t *d_fallback,

@@ -63,6 +63,9 @@ _SIGS = {
     "lq_merge_workspace": ([_I64], _I64),
     "lq_compact_encode_workspace": ([_I64], _I64),
     "lq_compact_encode": ([_P, _INT, _I64, _I64, _P, _P, _P, _INT, _P, _P, _P, _P, _P, _P, _P, _P], _INT),
+    "lq_compact_encode_scaled_workspace": ([_I64, _I64], _I64),
+    "lq_compact_encode_scaled": ([_P, _INT, _I64, _I64, _INT, _INT, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+                                 _INT),
     "lq_compact_merge": ([_P, _I64, _INT, _P, _I64, _P, _P, _I64, _I64, _P, _P, _P], _INT),
     "lq_fused_merge": ([_P, _I64, _INT, _P, _I64, _P, _P, _I64, _I64, _P, _P, _P], _INT),
     "lq_e8_validate": ([_P, _I64, ctypes.c_float, _INT, _P, _P], _INT),

@@ -335,6 +335,7 @@ class CompactBatch:
     shape: tuple
     bph: int
     bits: int
+    merge_scales: Optional[torch.Tensor] = None   # (n_heads,) fp32: float(scale16), the merge's scales
 
 
 def compact_encode(t: torch.Tensor, bits: int, storage_bits: Optional[int] = None,
@@ -342,7 +343,10 @@ def compact_encode(t: torch.Tensor, bits: int, storage_bits: Optional[int] = Non
     """Fixed-rate compression of one (B, H, T, hd) tensor without a host sync:
     scales at `bits` (or the caller's scale32), lattice points packed at
     `storage_bits` (default `bits`) where they fit, fp16 fallback elsewhere,
-    compacted in one pass (lq_compact_encode)."""
+    compacted in one pass.  Device scales with T * hd / 8 >= 1024 vectors per
+    head: two launches (lq_compact_encode_scaled finalises the scales inside
+    the encoder); otherwise lq_head_scales (or lq_scale_fastdiv) and
+    lq_compact_encode."""
     lib = L.lib()
     sb = storage_bits or bits
     if sb not in (3, 4, 5):
@@ -352,7 +356,6 @@ def compact_encode(t: torch.Tensor, bits: int, storage_bits: Optional[int] = Non
     nh, bph = B * H, T * hd // 8
     V = nh * bph
     dev = x.device
-    _, scale32, scale16, _, fastdiv = _head_scales(x, bits, scale32)
     tiles = (V + 1023) // 1024
     mask = _empty(V, torch.uint8, dev)
     packed = _empty(V * sb, torch.uint8, dev).view(V, sb)
@@ -360,13 +363,28 @@ def compact_encode(t: torch.Tensor, bits: int, storage_bits: Optional[int] = Non
     heads = _empty(V, torch.int32, dev)
     tile_off = _empty(tiles, torch.int64, dev)
     totals = _empty(3, torch.int64, dev)
-    work = _empty(lib.lq_compact_encode_workspace(V), torch.uint8, dev)
-    L.check(lib.lq_compact_encode(x.data_ptr(), L.dtype_code(x.dtype), nh, bph, scale32.data_ptr(), fastdiv.data_ptr(),
-                                  scale16.data_ptr(), sb, mask.data_ptr(), packed.data_ptr(), fallback.data_ptr(),
-                                  heads.data_ptr(), tile_off.data_ptr(), totals.data_ptr(), work.data_ptr(),
-                                  L.stream_ptr(dev)), "lq_compact_encode")
+    st = L.stream_ptr(dev)
+    if scale32 is None and bph >= 1024 and isinstance(bits, int):
+        scale32 = _empty(nh, torch.float32, dev)
+        scale16 = _empty(nh, torch.float16, dev)
+        merge_scales = _empty(nh, torch.float32, dev)
+        work = _empty(lib.lq_compact_encode_scaled_workspace(nh, bph), torch.uint8, dev)
+        L.check(lib.lq_compact_encode_scaled(x.data_ptr(), L.dtype_code(x.dtype), nh, bph, bits, sb, None,
+                                             scale32.data_ptr(), scale16.data_ptr(), merge_scales.data_ptr(),
+                                             mask.data_ptr(), packed.data_ptr(), fallback.data_ptr(), heads.data_ptr(),
+                                             tile_off.data_ptr(), totals.data_ptr(), work.data_ptr(), st),
+                "lq_compact_encode_scaled")
+    else:
+        _, scale32, scale16, _, fastdiv = _head_scales(x, bits, scale32)
+        work = _empty(lib.lq_compact_encode_workspace(V), torch.uint8, dev)
+        L.check(lib.lq_compact_encode(x.data_ptr(), L.dtype_code(x.dtype), nh, bph, scale32.data_ptr(),
+                                      fastdiv.data_ptr(), scale16.data_ptr(), sb, mask.data_ptr(), packed.data_ptr(),
+                                      fallback.data_ptr(), heads.data_ptr(), tile_off.data_ptr(), totals.data_ptr(),
+                                      work.data_ptr(), st), "lq_compact_encode")
+        merge_scales = scale16.float()
     return CompactBatch(mask=mask, packed=packed, fallback=fallback, repr_heads=heads, tile_off=tile_off,
-                        totals=totals, scale32=scale32, scale16=scale16, shape=(B, H, T, hd), bph=bph, bits=sb)
+                        totals=totals, scale32=scale32, scale16=scale16, shape=(B, H, T, hd), bph=bph, bits=sb,
+                        merge_scales=merge_scales)
 
 
 class LookbackError(RuntimeError):
@@ -392,7 +410,7 @@ def compact_merge(cb: CompactBatch, out: Optional[torch.Tensor] = None) -> torch
     dev = cb.mask.device
     if out is None:
         out = torch.empty(B, H, T, hd, dtype=torch.float16, device=dev)
-    sc = cb.scale16.float()
+    sc = cb.merge_scales if cb.merge_scales is not None else cb.scale16.float()
     L.check(lib.lq_compact_merge(cb.packed.data_ptr(), V, cb.bits, cb.fallback.data_ptr(), V, cb.mask.data_ptr(),
                                  sc.data_ptr(), V, cb.bph, cb.tile_off.data_ptr(), out.data_ptr(), L.stream_ptr(dev)),
             "lq_compact_merge")

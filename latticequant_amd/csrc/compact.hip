@@ -5,7 +5,7 @@
 // word per vector, [coset(1) | c0..c6 (b each) | c7 >> 1 (b-1)], coordinates
 // biased by R = 2^(b-1).  c7's low bit is recovered from the parity of
 // c0 + .. + c6 (floor-mod, as unpack_e8 does).
-#include "lq_device.h"
+#include "lq_scales.h"
 
 using namespace lq;
 
@@ -163,6 +163,19 @@ __global__ void k_zero64(uint64_t* __restrict__ p, int64_t n, int64_t* __restric
     if (extra && blockIdx.x == 0 && threadIdx.x == 0) *extra = 0;
 }
 
+// sigma^2 partial sums per (head, part), exactly as lq_head_scales forms them
+// (lq_scales.h head_sumsq_part, same part count), and, on the side, the clear
+// of the fixed-rate encoder's look-back words clear[0 .. n_clear) and *extra.
+__global__ __launch_bounds__(256) void k_compact_sumsq(const void* __restrict__ x, int dtype, int64_t bph, int parts,
+                                                       double* __restrict__ work, uint64_t* __restrict__ clear,
+                                                       int64_t n_clear, int64_t* __restrict__ extra) {
+    __shared__ double red[256];
+    const int64_t wg = (int64_t)blockIdx.y * gridDim.x + blockIdx.x, n_wg = (int64_t)gridDim.x * gridDim.y;
+    for (int64_t i = wg * 256 + threadIdx.x; i < n_clear; i += n_wg * 256) clear[i] = 0ull;
+    if (wg == 0 && threadIdx.x == 0) *extra = 0;
+    head_sumsq_part<false>(x, dtype, bph, parts, blockIdx.x, blockIdx.y, work, red, nullptr, 1, 1.0f);
+}
+
 // One tile of kTile blocks per workgroup; ranks from the tile offset plus
 // wave ballots, then either unpack the packed word or copy the fp16 fallback.
 // LB: the tile offsets come from the chained look-back (tile = ticket order)
@@ -241,20 +254,81 @@ __global__ __launch_bounds__(kTileThreads) void k_merge(const uint8_t* __restric
 // in-range vectors, else q * float(scale16[head]) in fp16 at its rank among
 // the others; the mask byte; the head of each packed point (optional); tile
 // offsets for the merge; the two totals.
+//
+// SC: the scales are not given but finalised here from the sigma^2 partial
+// sums work[head * parts + p] of k_compact_sumsq, for the (at most two, as
+// bph >= kTile) heads the tile spans, by the code of k_head_finalize (the
+// parts summed in order p = 0, 1, .., lq_scales.h head_scale, the exhaustive
+// fast-division check); the tile that holds a head's first vector stores its
+// sigma^2 (optional), scale32, scale16 and float(scale16).
+struct AutoScales {
+    const double* work;
+    int parts;
+    int scale_bits;
+    float* sigma2;
+    float* scale32;
+    uint16_t* scale16;
+    float* scale16f;
+};
+
+template <bool SC>
 __global__ __launch_bounds__(kTileThreads) void k_compact_encode(
         const void* __restrict__ x, int dtype, int64_t n, int64_t bph, const float* __restrict__ scale32,
         const int32_t* __restrict__ fastdiv, const uint16_t* __restrict__ scale16, int bits,
         uint8_t* __restrict__ mask, uint8_t* __restrict__ packed, uint16_t* __restrict__ fallback,
         int32_t* __restrict__ repr_heads, int64_t* __restrict__ tile_off, int64_t* __restrict__ totals,
         uint64_t* __restrict__ status,
-        uint32_t* __restrict__ ticket, int32_t* __restrict__ err) {
+        uint32_t* __restrict__ ticket, int32_t* __restrict__ err, AutoScales as) {
     __shared__ int s_t, s_wcnt[kTile / 64];
     __shared__ int64_t s_excl;
+    __shared__ float s_sc[2], s_sf[2];
+    __shared__ int s_fd[2], s_bad[2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid == 0) s_t = (int)atomicAdd(ticket, 1u);
     __syncthreads();
     const int64_t t = s_t;
     const int64_t ntiles = (n + kTile - 1) / kTile;
+    int64_t h0 = 0;
+    if (SC) {
+        const int64_t first = t * kTile, last = (first + kTile < n ? first + kTile : n) - 1;
+        h0 = first / bph;
+        const int nhd = (int)(last / bph - h0) + 1;   // 1 or 2
+        if (wave < nhd) {
+            const int64_t h = h0 + wave;
+            const double* wp = as.work + h * as.parts;
+            double acc = 0.0;
+            for (int p0 = 0; p0 < as.parts; p0 += 64) {
+                const double v = p0 + lane < as.parts ? wp[p0 + lane] : 0.0;
+                const int m = as.parts - p0 < 64 ? as.parts - p0 : 64;
+                const uint64_t vb = __builtin_bit_cast(uint64_t, v);
+                const int lo = (int)(uint32_t)vb, hi = (int)(uint32_t)(vb >> 32);
+                for (int i = 0; i < m; i++) {
+                    const uint64_t b = (uint64_t)(uint32_t)__builtin_amdgcn_readlane(lo, i) |
+                                       ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(hi, i) << 32);
+                    acc += __builtin_bit_cast(double, b);
+                }
+            }
+            if (lane == 0) {
+                float s2;
+                const float s = head_scale(acc, bph * 8, as.scale_bits, &s2);
+                const uint16_t s16 = f2h(s);
+                s_sc[wave] = s;
+                s_sf[wave] = h2f(s16);
+                if (h * bph >= first) {   // the head starts in this tile
+                    if (as.sigma2) as.sigma2[h] = s2;
+                    as.scale32[h] = s;
+                    as.scale16[h] = s16;
+                    as.scale16f[h] = h2f(s16);
+                }
+            }
+        }
+        __syncthreads();
+        for (int k = 0; k < nhd; k++) {
+            const int f = dtype == LQ_F16 ? fastdiv_flag(s_sc[k], &s_bad[k]) : 0;
+            if (tid == 0) s_fd[k] = f;
+        }
+        __syncthreads();
+    }
     const int R = 1 << (bits - 1);
     uint64_t word[kTileRounds];
     float y[kTileRounds][8];
@@ -266,8 +340,8 @@ __global__ __launch_bounds__(kTileThreads) void k_compact_encode(
         word[r] = 0;
         if (v < n) {
             const int64_t h = v / bph;
-            const float s = scale32[h];
-            const bool fast = fastdiv[h] != 0;
+            const float s = SC ? s_sc[h - h0] : scale32[h];
+            const bool fast = SC ? s_fd[h - h0] != 0 : fastdiv[h] != 0;
             const float rs = 1.0f / s;
             float xv[8], tq[8], ic[8];
             load8(x, dtype, v, xv);
@@ -290,7 +364,7 @@ __global__ __launch_bounds__(kTileThreads) void k_compact_encode(
             }
             m[r] = in ? 1 : 0;
             word[r] = w;
-            const float sf = h2f(scale16[h]), off = c ? 0.5f : 0.f;
+            const float sf = SC ? s_sf[h - h0] : h2f(scale16[h]), off = c ? 0.5f : 0.f;
 #pragma unroll
             for (int i = 0; i < 8; i++) y[r][i] = (ic[i] + off) * sf;
         }
@@ -397,9 +471,41 @@ int lq_compact_encode(const void* d_x, int dtype, int64_t n_heads, int64_t bph, 
     int32_t* err = reinterpret_cast<int32_t*>(d_totals + 2);   // read back with the totals
     hipLaunchKernelGGL(k_zero64, dim3((unsigned)((tiles + 1 + 255) / 256)), dim3(256), 0, s, status, tiles + 1,
                        d_totals + 2);
-    hipLaunchKernelGGL(k_compact_encode, dim3((unsigned)tiles), dim3(kTileThreads), 0, s, d_x, dtype, n, bph, d_scale32,
-                       d_fastdiv, d_scale16, bits, d_mask, d_packed, d_fallback, d_repr_heads, d_tile_off, d_totals,
-                       status, ticket, err);
+    hipLaunchKernelGGL(k_compact_encode<false>, dim3((unsigned)tiles), dim3(kTileThreads), 0, s, d_x, dtype, n, bph,
+                       d_scale32, d_fastdiv, d_scale16, bits, d_mask, d_packed, d_fallback, d_repr_heads, d_tile_off,
+                       d_totals, status, ticket, err, AutoScales{});
+    return launch_status();
+}
+
+int64_t lq_compact_encode_scaled_workspace(int64_t n_heads, int64_t bph) {
+    if (n_heads <= 0 || bph <= 0) return -1;
+    const int parts = head_parts(n_heads, bph);
+    return n_heads * parts * 8 + lq_compact_encode_workspace(n_heads * bph);
+}
+
+int lq_compact_encode_scaled(const void* d_x, int dtype, int64_t n_heads, int64_t bph, int scale_bits, int bits,
+                             float* d_sigma2, float* d_scale32, uint16_t* d_scale16, float* d_scale16f,
+                             uint8_t* d_mask, uint8_t* d_packed, uint16_t* d_fallback, int32_t* d_repr_heads,
+                             int64_t* d_tile_off, int64_t* d_totals, void* d_work, hipStream_t s) {
+    if (bits < 3 || bits > 5 || scale_bits < 1 || scale_bits > 16 || n_heads <= 0 || bph < kTile || dtype < 0 ||
+        dtype > 2)
+        return LQ_ERR_ARG;
+    if (!d_x || !d_scale32 || !d_scale16 || !d_scale16f || !d_mask || !d_packed || !d_fallback || !d_tile_off ||
+        !d_totals || !d_work)
+        return LQ_ERR_ARG;
+    const int64_t n = n_heads * bph;
+    const int64_t tiles = (n + kTile - 1) / kTile;
+    const int parts = head_parts(n_heads, bph);
+    double* partial = reinterpret_cast<double*>(d_work);
+    uint64_t* status = reinterpret_cast<uint64_t*>(partial + n_heads * parts);
+    uint32_t* ticket = reinterpret_cast<uint32_t*>(status + tiles);
+    int32_t* err = reinterpret_cast<int32_t*>(d_totals + 2);   // read back with the totals
+    hipLaunchKernelGGL(k_compact_sumsq, dim3((unsigned)n_heads, parts), dim3(256), 0, s, d_x, dtype, bph, parts,
+                       partial, status, tiles + 1, d_totals + 2);
+    const AutoScales as{partial, parts, scale_bits, d_sigma2, d_scale32, d_scale16, d_scale16f};
+    hipLaunchKernelGGL(k_compact_encode<true>, dim3((unsigned)tiles), dim3(kTileThreads), 0, s, d_x, dtype, n, bph,
+                       (const float*)nullptr, (const int32_t*)nullptr, (const uint16_t*)nullptr, bits, d_mask,
+                       d_packed, d_fallback, d_repr_heads, d_tile_off, d_totals, status, ticket, err, as);
     return launch_status();
 }
 

@@ -519,6 +519,10 @@ class CompressedChunk:
     blocks_per_head: int
     bits_per_dim: int = 4
     orig_dtype: torch.dtype = torch.float16
+    # (ceil(N / 1024),) int64 on the device: packed vectors before each
+    # 1024-vector tile of repr_mask, when known (compress_fixed_rate sets it;
+    # the merge then reads it instead of scanning the mask).  Not stored.
+    tile_offsets: Optional[torch.Tensor] = None
 
     @property
     def total_bytes(self) -> int:
@@ -542,7 +546,7 @@ def compress_fixed_rate(tensor: torch.Tensor, bits_per_dim: int = 4, storage_bit
     cb = codec.compact_encode(x, bits_per_dim, storage_bits, scale32)
     n_repr, n_oor = codec.compact_counts(cb.totals)
     nh, bph = B * H, T * hd // 8
-    return CompressedChunk(repr_mask=cb.mask.bool(), packed=cb.packed[:n_repr], fallback=cb.fallback[:n_oor],
-                           scales=cb.scale16.float(), repr_head_ids=cb.repr_heads[:n_repr],
+    return CompressedChunk(repr_mask=cb.mask.view(torch.bool), packed=cb.packed[:n_repr], fallback=cb.fallback[:n_oor],
+                           scales=cb.merge_scales, repr_head_ids=cb.repr_heads[:n_repr],
                            orig_shape=(B, H, T, hd), n_vectors=nh * bph, n_heads=nh, blocks_per_head=bph,
-                           bits_per_dim=cb.bits, orig_dtype=torch.float16)
+                           bits_per_dim=cb.bits, orig_dtype=torch.float16, tile_offsets=cb.tile_off)

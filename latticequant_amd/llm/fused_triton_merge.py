@@ -32,7 +32,8 @@ def fused_decompress_chunk(chunk: CompressedChunk) -> torch.Tensor:
     total = batch * heads * bph
     assert total * 8 == batch * heads * seq * hd
     bits = chunk.bits_per_dim
-    mask = chunk.repr_mask.to(torch.uint8).contiguous()
+    rm = chunk.repr_mask
+    mask = rm.view(torch.uint8) if rm.dtype == torch.bool and rm.is_contiguous() else rm.to(torch.uint8).contiguous()
     if mask.numel() != total:
         raise ValueError("repr_mask must hold one flag per block")
     packed = chunk.packed.contiguous()
@@ -51,6 +52,16 @@ def fused_decompress_chunk(chunk: CompressedChunk) -> torch.Tensor:
     if sc.numel() < batch * heads:
         raise ValueError("one scale per head required")
     out = torch.empty(total * 8, dtype=torch.float16, device=dev)
+    toff = chunk.tile_offsets
+    if toff is not None:   # tile offsets from the encoder: no look-back pass
+        if toff.dtype != torch.int64 or toff.numel() != (total + 1023) // 1024 or toff.device != dev:
+            raise ValueError("tile_offsets must hold one int64 per 1024-vector tile on the chunk's device")
+        with torch.cuda.device(dev):
+            L.check(L.lib().lq_compact_merge(packed.data_ptr(), n_repr, bits, fallback.data_ptr(),
+                                             int(fallback.shape[0]), mask.data_ptr(), sc.data_ptr(), total, bph,
+                                             toff.contiguous().data_ptr(), out.data_ptr(), L.stream_ptr(dev)),
+                    "lq_compact_merge")
+        return out.reshape(batch, heads, seq, hd)
     work = torch.empty(max(int(L.lib().lq_merge_workspace(total)), 8), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         L.check(L.lib().lq_fused_merge(packed.data_ptr(), n_repr, bits, fallback.data_ptr(), int(fallback.shape[0]),

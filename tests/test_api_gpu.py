@@ -385,3 +385,103 @@ def test_compact_encode_merge_device_gpu(bits, storage):
     np.testing.assert_array_equal(cb.tile_off.cpu().numpy(), want_off)
     out = codec.compact_merge(cb)
     np.testing.assert_array_equal(out.cpu().numpy().reshape(-1, 8), full)
+
+
+def _compact_two_ways(x, bits, storage):
+    """(scaled, separate): the outputs of lq_compact_encode_scaled and of
+    lq_head_scales + lq_compact_encode on one (n_heads, bph, 8) input."""
+    from latticequant_amd import _lib as L
+    from latticequant_amd import codec
+    lib = L.lib()
+    nh, bph = x.shape[0], x.shape[1]
+    V = nh * bph
+    dev = x.device
+    dt = L.dtype_code(x.dtype)
+    s = L.stream_ptr(dev)
+    tiles = (V + 1023) // 1024
+
+    def outs():
+        return dict(mask=torch.full((V,), 7, dtype=torch.uint8, device=dev),
+                    packed=torch.zeros(V * storage, dtype=torch.uint8, device=dev),
+                    fallback=torch.zeros(V * 8, dtype=torch.float16, device=dev),
+                    heads=torch.full((V,), -1, dtype=torch.int32, device=dev),
+                    tile_off=torch.full((tiles,), -1, dtype=torch.int64, device=dev),
+                    totals=torch.full((3,), -1, dtype=torch.int64, device=dev))
+
+    a = outs()
+    a["sigma2"] = torch.full((nh,), -1.0, device=dev)
+    a["scale32"] = torch.full((nh,), -1.0, device=dev)
+    a["scale16"] = torch.zeros(nh, dtype=torch.float16, device=dev)
+    a["scale16f"] = torch.full((nh,), -1.0, device=dev)
+    work = torch.full((lib.lq_compact_encode_scaled_workspace(nh, bph),), 0xAB, dtype=torch.uint8, device=dev)
+    L.check(lib.lq_compact_encode_scaled(x.data_ptr(), dt, nh, bph, bits, storage, a["sigma2"].data_ptr(),
+                                         a["scale32"].data_ptr(), a["scale16"].data_ptr(), a["scale16f"].data_ptr(),
+                                         a["mask"].data_ptr(), a["packed"].data_ptr(), a["fallback"].data_ptr(),
+                                         a["heads"].data_ptr(), a["tile_off"].data_ptr(), a["totals"].data_ptr(),
+                                         work.data_ptr(), s), "lq_compact_encode_scaled")
+    b = outs()
+    bits_t = torch.full((1,), bits, dtype=torch.int32, device=dev)
+    hw = torch.empty(4096 + nh, dtype=torch.float64, device=dev)
+    b["sigma2"] = torch.empty(nh, device=dev)
+    b["scale32"] = torch.empty(nh, device=dev)
+    b["scale16"] = torch.empty(nh, dtype=torch.float16, device=dev)
+    fd = torch.empty(nh, dtype=torch.int32, device=dev)
+    L.check(lib.lq_head_scales(x.data_ptr(), dt, 1, nh, bph, bits_t.data_ptr(), hw.data_ptr(), b["sigma2"].data_ptr(),
+                               b["scale32"].data_ptr(), b["scale16"].data_ptr(), fd.data_ptr(), s), "lq_head_scales")
+    wb = torch.full((lib.lq_compact_encode_workspace(V),), 0xAB, dtype=torch.uint8, device=dev)
+    L.check(lib.lq_compact_encode(x.data_ptr(), dt, nh, bph, b["scale32"].data_ptr(), fd.data_ptr(),
+                                  b["scale16"].data_ptr(), storage, b["mask"].data_ptr(), b["packed"].data_ptr(),
+                                  b["fallback"].data_ptr(), b["heads"].data_ptr(), b["tile_off"].data_ptr(),
+                                  b["totals"].data_ptr(), wb.data_ptr(), s), "lq_compact_encode")
+    b["scale16f"] = b["scale16"].float()
+    for d in (a, b):
+        n_repr, n_oor = codec.compact_counts(d["totals"])
+        d["packed"] = d["packed"][:n_repr * storage]
+        d["heads"] = d["heads"][:n_repr]
+        d["fallback"] = d["fallback"][:n_oor * 8]
+    return a, b
+
+
+@pytest.mark.parametrize("nh,bph,dtype,bits,storage", [
+    (8, 32768, torch.float16, 4, 4),      # C1's shape: one head per tile
+    (3, 1025, torch.float16, 4, 3),       # every tile but one spans two heads
+    (5, 1024, torch.bfloat16, 3, 3),      # bph at the limit
+    (1, 65536, torch.float32, 5, 5),      # one head: 128 sigma^2 parts (two waves of lanes)
+    (4, 3000, torch.float16, 4, 5),       # a zero head (scale 1) among others
+])
+def test_compact_encode_scaled_equals_separate_gpu(nh, bph, dtype, bits, storage):
+    """lq_compact_encode_scaled (scales finalised inside the encoder) writes
+    the same sigma^2, scales, fp16 scales, mask, packed words, fallback rows,
+    head ids, tile offsets and totals as lq_head_scales + lq_compact_encode,
+    byte for byte, with float(scale16) beside them; twice in a row on one
+    workspace (its look-back words are cleared by the call)."""
+    gen = torch.Generator().manual_seed(nh * 7 + bph)
+    x = torch.randn(nh, bph, 8, generator=gen)
+    x[:, :, :2] *= 6.0
+    if nh == 4:
+        x[2] = 0.0
+    x = x.to(dtype).cuda()
+    for _ in range(2):
+        a, b = _compact_two_ways(x, bits, storage)
+        for k in a:
+            assert torch.equal(a[k].cpu(), b[k].cpu()), k
+    n_repr = int(a["totals"][0])
+    assert 0 < n_repr < nh * bph
+
+
+def test_compact_encode_scaled_rejects_short_heads_gpu():
+    """Fewer than 1024 vectors per head: LQ_ERR_ARG (a tile could span more
+    than two heads); codec.compact_encode then takes the separate path and
+    still matches the oracle."""
+    from latticequant_amd import _lib as L
+    from latticequant_amd import codec
+    lib = L.lib()
+    x = torch.randn(4, 1023, 8).half().cuda()
+    z = torch.zeros(16, dtype=torch.int64, device="cuda")
+    rc = lib.lq_compact_encode_scaled(x.data_ptr(), L.LQ_F16, 4, 1023, 4, 4, None, z.data_ptr(), z.data_ptr(),
+                                      z.data_ptr(), z.data_ptr(), z.data_ptr(), z.data_ptr(), None, z.data_ptr(),
+                                      z.data_ptr(), z.data_ptr(), L.stream_ptr())
+    assert rc == -1   # LQ_ERR_ARG
+    cb = codec.compact_encode(x.view(1, 4, 1023, 8), 4)
+    qo = O.quantize_heads(x.view(1, 4, 1023, 8).float().cpu().numpy(), cb.scale32.cpu().numpy())
+    np.testing.assert_array_equal(cb.mask.cpu().numpy().astype(bool), O.check_representable(qo, 4))
