@@ -83,7 +83,10 @@ int lq_symbols_to_e8(const int32_t *d_coset, const int32_t *d_sym8, int64_t n, f
 
 /* Per-head sigma^2 = mean(x^2), fp32 scale sqrt(2*pi*e*sigma^2*4^-b) (1 if
  * sigma^2 < 1e-12) and its fp16 copy; bits per chunk.  Also the per-head
- * fast-division flag consumed by lq_chunk_quantize.  d_work: 4096 + n_heads_total doubles.
+ * fast-division word consumed by lq_chunk_quantize: 0 (IEEE division), or,
+ * when x * r corrected by one FMA equals x / scale for every fp16 input, the
+ * fp32 bit pattern of r = RN(1 / scale) (never 0; consumers test != 0 and
+ * take r from it).  d_work: 4096 + n_heads_total doubles.
  * Replaces llm/compressed_kv_cache.py:188-196. */
 int lq_head_scales(const void *d_x, int dtype, int64_t n_chunks, int64_t n_heads, int64_t bph,
                    const int32_t *d_chunk_bits, double *d_work, float *d_sigma2, float *d_scale32,
@@ -101,8 +104,8 @@ int lq_head_scales_rht(const void *d_x, int dtype, int64_t n_chunks, int64_t n_h
                        const float *d_signs, const int32_t *d_chunk_bits, double *d_work, float *d_sigma2,
                        float *d_scale32, uint16_t *d_scale16, int32_t *d_fastdiv, hipStream_t s);
 
-/* Fast-division flags for caller-supplied fp32 scales (exhaustive check of all
- * 2048 fp16 significands per head).  Same d_fastdiv layout as above. */
+/* Fast-division words for caller-supplied fp32 scales (exhaustive check of all
+ * 2048 fp16 significands per head).  Same d_fastdiv words as above. */
 int lq_scale_fastdiv(const float *d_scale32, int64_t n_heads_total, int dtype, int32_t *d_fastdiv,
                      hipStream_t s);
 

@@ -324,7 +324,7 @@ __global__ __launch_bounds__(kTileThreads) void k_compact_encode(
         }
         __syncthreads();
         for (int k = 0; k < nhd; k++) {
-            const int f = dtype == LQ_F16 ? fastdiv_flag(s_sc[k], &s_bad[k]) : 0;
+            const int32_t f = dtype == LQ_F16 ? fastdiv_word(s_sc[k], &s_bad[k]) : 0;
             if (tid == 0) s_fd[k] = f;
         }
         __syncthreads();
@@ -341,8 +341,9 @@ __global__ __launch_bounds__(kTileThreads) void k_compact_encode(
         if (v < n) {
             const int64_t h = v / bph;
             const float s = SC ? s_sc[h - h0] : scale32[h];
-            const bool fast = SC ? s_fd[h - h0] != 0 : fastdiv[h] != 0;
-            const float rs = 1.0f / s;
+            const int32_t fw = SC ? s_fd[h - h0] : fastdiv[h];
+            const bool fast = fw != 0;
+            const float rs = __int_as_float(fw);   // RN(1 / s) when fast
             float xv[8], tq[8], ic[8];
             load8(x, dtype, v, xv);
 #pragma unroll

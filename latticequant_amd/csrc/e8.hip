@@ -68,8 +68,9 @@ __global__ void k_quantize_heads(const void* __restrict__ x, int dtype, int64_t 
     if (v >= n) return;
     const int64_t h = v / bph;
     const float s = scale32[h];
-    const bool fast = fastdiv[h] != 0;
-    const float rs = 1.0f / s;
+    const int32_t fw = fastdiv[h];
+    const bool fast = fw != 0;
+    const float rs = __int_as_float(fw);   // RN(1 / s) when fast
     float xv[8], t[8], ic[8];
     load8(x, dtype, v, xv);
 #pragma unroll
@@ -91,10 +92,10 @@ __global__ void k_head_sumsq(const void* __restrict__ x, int dtype, int64_t vec_
     head_sumsq_part<ROT>(x, dtype, vec_per_head, parts, blockIdx.x, blockIdx.y, work, red, signs, lpr, rdiv);
 }
 
-__device__ void fastdiv_check(float s, int32_t* flag) {
+__device__ void fastdiv_check(float s, int32_t* word) {
     __shared__ int bad;
-    const int f = fastdiv_flag(s, &bad);
-    if (threadIdx.x == 0) *flag = f;
+    const int32_t w = fastdiv_word(s, &bad);
+    if (threadIdx.x == 0) *word = w;
 }
 
 // sigma^2, scales (llm/compressed_kv_cache.py:189-196) and fast-division flag.
@@ -241,8 +242,11 @@ __global__ __launch_bounds__(kQThreads, LEAN ? 7 : (ROT ? 5 : 1)) void k_chunk_q
         bool f0 = false, f1 = false;
         if (two_heads) {
             s0 = scale32[hq0]; s1 = scale32[hq1];
-            rs0 = 1.0f / s0; rs1 = 1.0f / s1;
-            f0 = !ROT && fastdiv[hq0] != 0; f1 = !ROT && fastdiv[hq1] != 0;   // rotated values are fp32
+            if (!ROT) {   // rotated values are fp32: IEEE division
+                const int32_t w0 = fastdiv[hq0], w1 = fastdiv[hq1];
+                f0 = w0 != 0; f1 = w1 != 0;
+                rs0 = __int_as_float(w0); rs1 = __int_as_float(w1);   // RN(1 / s) where fast
+            }
         }
         int32_t sy[2][8];
         int cs[2];
@@ -268,8 +272,9 @@ __global__ __launch_bounds__(kQThreads, LEAN ? 7 : (ROT ? 5 : 1)) void k_chunk_q
                     int64_t h = hq0;
                     while (rr >= (int)bph) { rr -= (int)bph; h++; }
                     s = scale32[h];
-                    rs = 1.0f / s;
-                    fast = !ROT && fastdiv[h] != 0;
+                    const int32_t w = ROT ? 0 : fastdiv[h];
+                    rs = __int_as_float(w);
+                    fast = w != 0;
                     hq = h;
                 }
                 float xv[8], t[8], ic[8], dd[8];

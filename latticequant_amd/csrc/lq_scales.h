@@ -116,6 +116,13 @@ __device__ __forceinline__ int fastdiv_flag(float s, int* bad) {
     return *bad ? 0 : 1;
 }
 
+// The fast-division word of scale s: 0, or the bits of r = RN(1 / s) (a
+// positive float, so never 0) when fastdiv_flag passes.
+__device__ __forceinline__ int32_t fastdiv_word(float s, int* bad) {
+    const int f = fastdiv_flag(s, bad);
+    return f ? __float_as_int(1.0f / s) : 0;
+}
+
 // sumsq parts per head (about 4096 workgroups in all, at most one per 512 vectors)
 inline int head_parts(int64_t H, int64_t bph) {
     const int64_t want = (4096 + H - 1) / H, cap = bph / 512 > 1 ? bph / 512 : 1;
