@@ -176,6 +176,43 @@ __device__ __forceinline__ void stage_hist(const uint4& w, int row16, int n0, in
     }
 }
 
+// Wide path: min / max of the int16 symbols of one staged 16-byte row (8
+// symbols of one column), folded into the copying thread's running values of
+// the row's coset.  Row j of the staging holds column (j / 2) % 8 of its coset
+// region (regions start at multiples of 128 symbols, a column chunk spans two
+// rows), so the rows a thread copies (j = tid + 256 k) share one coordinate.
+// Rows past the column's count hold stale staging and are skipped.
+typedef short short2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void stage_minmax(const uint4& w, int row16, int n0, int n1, int tmin[2], int tmax[2]) {
+    const int e = row16 * 8;   // first symbol of the row
+    const int r1 = sym_region(1, n0);
+    const int c = e >= r1;
+    const int q = e - (c ? r1 : 0);
+    const int left = (c ? n1 : n0) - (16 * (q >> 7) + (q & 15));   // symbols of this column from the row on
+    if (left <= 0) return;
+    int lo, hi;
+    if (left >= 8) {
+        const short2_t a = __builtin_bit_cast(short2_t, w.x), b = __builtin_bit_cast(short2_t, w.y);
+        const short2_t cc = __builtin_bit_cast(short2_t, w.z), d = __builtin_bit_cast(short2_t, w.w);
+        const short2_t mn = __builtin_elementwise_min(__builtin_elementwise_min(a, b), __builtin_elementwise_min(cc, d));
+        const short2_t mx = __builtin_elementwise_max(__builtin_elementwise_max(a, b), __builtin_elementwise_max(cc, d));
+        lo = min((int)mn.x, (int)mn.y);
+        hi = max((int)mx.x, (int)mx.y);
+    } else {
+        const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+        lo = INT_MAX;
+        hi = INT_MIN;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int v = (int)(int16_t)(d[k >> 1] >> ((k & 1) * 16));
+            if (k < left) { lo = min(lo, v); hi = max(hi, v); }
+        }
+    }
+    if (c) { tmin[1] = min(tmin[1], lo); tmax[1] = max(tmax[1], hi); }
+    else { tmin[0] = min(tmin[0], lo); tmax[0] = max(tmax[0], hi); }
+}
+
 // k_chunk_quantize (described above).  LEAN: the host guarantees bph >= LQ_BLK
 // (a block spans at most two heads) and no dequantised output; the general
 // paths are compiled out, which frees the scalar registers they held (fewer
@@ -216,12 +253,9 @@ __global__ __launch_bounds__(kQThreads, LEAN ? 7 : (ROT ? 5 : 1)) void k_chunk_q
     if (tid < LQ_STREAMS) { smin[tid] = INT_MAX; smax[tid] = INT_MIN; }
     if (tid == 0) sflag = 0;
     __syncthreads();
-    // wide path: this thread's running min / max per stream
-    int tmin[kWide ? LQ_STREAMS : 1], tmax[kWide ? LQ_STREAMS : 1];
-    if constexpr (kWide) {
-#pragma unroll
-        for (int i = 0; i < LQ_STREAMS; i++) { tmin[i] = INT_MAX; tmax[i] = INT_MIN; }
-    }
+    // wide path: this thread's running min / max per coset of its coordinate
+    // (stage_minmax: the staged rows a thread copies all hold one coordinate)
+    int tmin[2] = {INT_MAX, INT_MAX}, tmax[2] = {INT_MIN, INT_MIN};
 
     int flag = 0;
     for (int bi = 0; bi < kQBlocksPerWG; bi++) {
@@ -398,16 +432,7 @@ __global__ __launch_bounds__(kQThreads, LEAN ? 7 : (ROT ? 5 : 1)) void k_chunk_q
                     for (int i = 0; i < 8; i++) sp[16 * i] = (SymT)sy[r][i];
                 } else {
 #pragma unroll
-                    for (int i = 0; i < 8; i++) {
-                        sp[16 * i] = (SymT)sy[r][i];
-                        // c is 0 or 1: update both halves with selects (registers stay static)
-#pragma unroll
-                        for (int cc = 0; cc < 2; cc++) {
-                            const int st = cc * 8 + i;
-                            tmin[st] = c == cc ? min(tmin[st], sy[r][i]) : tmin[st];
-                            tmax[st] = c == cc ? max(tmax[st], sy[r][i]) : tmax[st];
-                        }
-                    }
+                    for (int i = 0; i < 8; i++) sp[16 * i] = (SymT)sy[r][i];
                 }
             }
         }
@@ -422,6 +447,7 @@ __global__ __launch_bounds__(kQThreads, LEAN ? 7 : (ROT ? 5 : 1)) void k_chunk_q
                 const uint4 w = src[i];
                 dst[i] = w;
                 if constexpr (!kWide) stage_hist(w, i, n0, n1, shist);
+                else stage_minmax(w, i, n0, n1, tmin, tmax);
             }
             // the block's 64 bytes of coset bits as four 16-byte rows (lane offsets
             // shared with the copy above)
@@ -432,11 +458,12 @@ __global__ __launch_bounds__(kQThreads, LEAN ? 7 : (ROT ? 5 : 1)) void k_chunk_q
         __syncthreads();
     }
     if (flag) atomicOr(&sflag, 1);
-    if constexpr (kWide) {
+    if constexpr (kWide) {   // this thread's coordinate, both cosets
+        const int idx = (tid >> 1) & 7;
 #pragma unroll
-        for (int i = 0; i < LQ_STREAMS; i++) {
-            if (tmin[i] != INT_MAX) atomicMin(&smin[i], tmin[i]);
-            if (tmax[i] != INT_MIN) atomicMax(&smax[i], tmax[i]);
+        for (int c = 0; c < 2; c++) {
+            if (tmin[c] != INT_MAX) atomicMin(&smin[c * 8 + idx], tmin[c]);
+            if (tmax[c] != INT_MIN) atomicMax(&smax[c * 8 + idx], tmax[c]);
         }
     }
     __syncthreads();
@@ -458,17 +485,20 @@ __global__ __launch_bounds__(kQThreads, LEAN ? 7 : (ROT ? 5 : 1)) void k_chunk_q
 // Wide path, second pass: histograms of the int16 symbols in the window
 // [min, min + 1023] of each stream (a stream whose max exceeds the window has
 // an alphabet beyond L and is flagged by the table stage).  Workgroup: 16
-// blocks x 16 streams of one chunk, one lane per (block, stream) column;
-// counts accumulate in LDS (16 x 1024) and are added to hist once.
+// blocks x 16 streams of one chunk, one lane per (block, stream) column, read
+// 16 symbols (32 bytes) at a time with the next chunk's loads in flight.
+// Counts accumulate in LDS as 16-bit halves, two bins per word (a bin counts
+// at most 16 x 512 symbols of a workgroup), and are added to hist once.
 constexpr int kHBlocks = 16;
 
 __global__ __launch_bounds__(256) void k_chunk_hist_wide(const int16_t* __restrict__ sym, const uint32_t* __restrict__ blk_n1,
                                                          int64_t nblk, int64_t V, const int32_t* __restrict__ minmax,
                                                          uint32_t* __restrict__ hist) {
-    __shared__ uint32_t sh[LQ_STREAMS * LQ_L];
+    static_assert(kHBlocks * kBlk < 65536, "16-bit LDS counters");
+    __shared__ uint32_t sh[LQ_STREAMS * LQ_L / 2];
     const int tid = threadIdx.x;
     const int64_t chunk = blockIdx.y;
-    for (int i = tid; i < LQ_STREAMS * LQ_L; i += 256) sh[i] = 0;
+    for (int i = tid; i < LQ_STREAMS * LQ_L / 2; i += 256) sh[i] = 0;
     __syncthreads();
     const int64_t g = (int64_t)blockIdx.x * kHBlocks + (tid >> 4);
     const int st = tid & 15;
@@ -480,17 +510,27 @@ __global__ __launch_bounds__(256) void k_chunk_hist_wide(const int16_t* __restri
         const int n = c ? n1 : n0;
         const int lo = minmax[(chunk * LQ_STREAMS + st) * 2];
         const int16_t* col = sym + (chunk * nblk + g) * (int64_t)kSymStride + sym_region(c, n0) + 16 * idx;
-        uint32_t* hs = sh + st * LQ_L;
-        for (int r = 0; r < n; r++) {
-            const int v = col[((r >> 4) << 7) + (r & 15)] - lo;
-            if (v < LQ_L) atomicAdd(hs + v, 1u);
+        uint32_t* hs = sh + st * (LQ_L / 2);
+        const int nk = (n + 15) >> 4;   // column chunks (the last one may be partial)
+        Chunk16<int16_t> cur = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)}, nxt = cur;
+        if (nk > 0) cur = gload_chunk(col);
+        for (int k = 0; k < nk; k++) {
+            if (k + 1 < nk) nxt = gload_chunk(col + 128 * (int64_t)(k + 1));
+            const int m = n - 16 * k < 16 ? n - 16 * k : 16;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int v = cur.get(i) - lo;
+                if (i < m && (unsigned)v < (unsigned)LQ_L) atomicAdd(hs + (v >> 1), 1u << ((v & 1) * 16));
+            }
+            cur = nxt;
         }
     }
     __syncthreads();
     uint32_t* gh = hist + chunk * (LQ_STREAMS * LQ_L);
-    for (int i = tid; i < LQ_STREAMS * LQ_L; i += 256) {
-        const uint32_t cnt = sh[i];
-        if (cnt) atomicAdd(gh + i, cnt);
+    for (int i = tid; i < LQ_STREAMS * LQ_L / 2; i += 256) {
+        const uint32_t w = sh[i];
+        if (w & 0xffffu) atomicAdd(gh + 2 * i, w & 0xffffu);
+        if (w >> 16) atomicAdd(gh + 2 * i + 1, w >> 16);
     }
 }
 
@@ -635,6 +675,16 @@ int lq_chunk_quantize_wide(const void* d_x, int dtype, int64_t n_chunks, int64_t
         hipLaunchKernelGGL((k_chunk_quantize<int16_t, true>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x, dtype,
                            n_heads, bph, nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, nullptr, d_minmax,
                            d_status, d_deq, deq_dtype, d_dither_seed, nullptr, 1, 1.0f);
+    else if (bph >= kBlk && !d_deq) {
+#define LQ_LEAN(DT)                                                                                               \
+        hipLaunchKernelGGL((k_chunk_quantize<int16_t, false, true, false, DT>), dim3((unsigned)wg), dim3(kQThreads),  \
+                           0, s, d_x, dtype, n_heads, bph, nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1,  \
+                           nullptr, d_minmax, d_status, nullptr, deq_dtype, nullptr, nullptr, 1, 1.0f)
+        if (dtype == LQ_F16) LQ_LEAN(LQ_F16);
+        else if (dtype == LQ_BF16) LQ_LEAN(LQ_BF16);
+        else LQ_LEAN(LQ_F32);
+#undef LQ_LEAN
+    }
     else
         hipLaunchKernelGGL((k_chunk_quantize<int16_t, false>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x, dtype,
                            n_heads, bph, nblk, d_scale32, d_fastdiv, d_sym, d_coset_bits, d_blk_n1, nullptr, d_minmax,

@@ -30,6 +30,41 @@ __device__ __forceinline__ int sym_pos(int c, int i, int r, int n0) {
     return sym_region(c, n0) + ((((r >> 4) << 3) + i) << 4) + (r & 15);
 }
 
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const u32x4_t gconst_u32x4;
+
+// 16-byte load through a global (address space 1) pointer: a global_load, not
+// a flat load, so it does not hold up waits on LDS results.
+__device__ __forceinline__ uint4 gload16(uintptr_t a) {
+    u32x4_t v = *reinterpret_cast<gconst_u32x4*>(a);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// 16 symbols of one column chunk (int8: one 16-byte load, int16: two).
+template <typename SymT>
+struct Chunk16 {
+    uint4 a, b;
+    __device__ __forceinline__ int get(int i) const {
+        if constexpr (sizeof(SymT) == 1) {
+            const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+            return (int)(int8_t)(w[i >> 2] >> ((i & 3) * 8));
+        } else {
+            const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            return (int)(int16_t)(w[i >> 1] >> ((i & 1) * 16));
+        }
+    }
+};
+
+template <typename SymT>
+__device__ __forceinline__ Chunk16<SymT> gload_chunk(const SymT* p) {
+    Chunk16<SymT> c;
+    const uintptr_t a = (uintptr_t)p;
+    c.a = gload16(a);
+    if constexpr (sizeof(SymT) == 2) c.b = gload16(a + 16);
+    else c.b = make_uint4(0, 0, 0, 0);
+    return c;
+}
+
 // torch.arange(8, dtype=f32) * 1e-7  ==  RN32(i * f32(1e-7))   (core/e8_quantizer.py:42-44)
 __host__ __device__ __forceinline__ float tiebreak(int i) {
     constexpr float tb[8] = {0.0f,           0x1.ad7f2ap-24f, 0x1.ad7f2ap-23f, 0x1.421f60p-22f,

@@ -493,41 +493,6 @@ __device__ __forceinline__ void hull_step(uint32_t& lo, uint32_t& hi, uint32_t e
     }
 }
 
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(1))) const u32x4_t gconst_u32x4;
-
-// 16-byte load through a global (address space 1) pointer: a global_load, not
-// a flat load, so it does not hold up waits on LDS results.
-__device__ __forceinline__ uint4 gload16(uintptr_t a) {
-    u32x4_t v = *reinterpret_cast<gconst_u32x4*>(a);
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-
-// 16 symbols of one column chunk (int8: one 16-byte load, int16: two).
-template <typename SymT>
-struct Chunk16 {
-    uint4 a, b;
-    __device__ __forceinline__ int get(int i) const {
-        if constexpr (sizeof(SymT) == 1) {
-            const uint32_t w[4] = {a.x, a.y, a.z, a.w};
-            return (int)(int8_t)(w[i >> 2] >> ((i & 3) * 8));
-        } else {
-            const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-            return (int)(int16_t)(w[i >> 1] >> ((i & 1) * 16));
-        }
-    }
-};
-
-template <typename SymT>
-__device__ __forceinline__ Chunk16<SymT> gload_chunk(const SymT* p) {
-    Chunk16<SymT> c;
-    const uintptr_t a = (uintptr_t)p;
-    c.a = gload16(a);
-    if constexpr (sizeof(SymT) == 2) c.b = gload16(a + 16);
-    else c.b = make_uint4(0, 0, 0, 0);
-    return c;
-}
-
 // f(v, b, in) for the column symbols of ranks n-1, n-2, .., 0 (the column's
 // 16-symbol chunk k sits at p + 128 k), read with 16-byte loads issued one
 // chunk ahead.  b is the symbol's index in its chunk (a compile-time
@@ -587,10 +552,15 @@ __global__ __launch_bounds__(256) void k_chunk_encode(const SymT* __restrict__ s
                                                       int64_t nblk, int64_t V, const lq_table* __restrict__ tables,
                                                       uint32_t* __restrict__ blk_bits, uint32_t* __restrict__ scratch,
                                                       uint16_t* __restrict__ blk_state) {
-    // odd row stride: the 16 stream tables start in different LDS banks
-    // alphabet capacity: int8 symbols fit 260 entries, wide streams up to L + 4
-    constexpr int kCap = sizeof(SymT) == 1 ? 264 : LQ_MAXSYM;
-    __shared__ uint32_t senc[LQ_STREAMS][kCap + 1];
+    // odd row stride: the 16 stream tables start in different LDS banks.
+    // int8 symbols span at most 260 alphabet entries, all held in LDS.  Wide
+    // (int16) alphabets reach L + 4 entries: LDS holds a window of kWin
+    // entries per stream around symbol 0 (lattice coordinates centre there),
+    // and the rare symbol outside it reads its entry from the table in global
+    // memory, so the workgroup's LDS stays that of the int8 encoder.
+    constexpr bool kWide = sizeof(SymT) == 2;
+    constexpr int kWin = kWide ? 256 : 264;
+    __shared__ uint32_t senc[LQ_STREAMS][kWin + 1];
     __shared__ int slo[LQ_STREAMS], snsym[LQ_STREAMS];
     __shared__ uint32_t sq[4][256];   // per-lane queue of scratch words (4: seven workgroups fit a CU's LDS)
     const int tid = threadIdx.x;
@@ -598,11 +568,17 @@ __global__ __launch_bounds__(256) void k_chunk_encode(const SymT* __restrict__ s
     const int64_t g = (int64_t)blockIdx.x * kEncBlocks + (tid >> 4);
     const int st = tid & 15;
     const lq_table* T = tables + chunk * LQ_STREAMS;
-    for (int i = tid; i < LQ_STREAMS * kCap; i += 256) {
-        int s = i / kCap, j = i % kCap;
-        senc[s][j] = j < T[s].n_sym ? encx_of(T[s].enc[j]) : 0u;
+    // first alphabet entry of stream s's LDS window
+    auto win0 = [&](int s) -> int {
+        if constexpr (!kWide) return 0;
+        const int n = T[s].n_sym, w = -T[s].lo - kWin / 2;
+        return n <= kWin || w <= 0 ? 0 : (w < n - kWin ? w : n - kWin);
+    };
+    for (int i = tid; i < LQ_STREAMS * kWin; i += 256) {
+        const int s = i / kWin, j = i % kWin, w0 = win0(s);
+        senc[s][j] = j + w0 < T[s].n_sym ? encx_of(T[s].enc[j + w0]) : 0u;
     }
-    if (tid < LQ_STREAMS) { slo[tid] = T[tid].lo; snsym[tid] = T[tid].n_sym; }
+    if (tid < LQ_STREAMS) { slo[tid] = T[tid].lo + win0(tid); snsym[tid] = T[tid].n_sym; }
     __syncthreads();
     if (g >= nblk) return;
     const int64_t task = (chunk * LQ_STREAMS + st) * nblk + g;
@@ -613,8 +589,19 @@ __global__ __launch_bounds__(256) void k_chunk_encode(const SymT* __restrict__ s
     }
     const int c = st >> 3, idx = st & 7;
     const uint32_t* encs = senc[st];
-    const int lo_sym = slo[st];
-    auto enc = [&](int v) { return encs[v - lo_sym]; };   // entry of symbol value v
+    const int lo_sym = slo[st];   // symbol of the window's first entry (a valid symbol)
+    const uint32_t* const genc = T[st].enc;
+    const int glo = T[st].lo;
+    auto enc = [&](int v) -> uint32_t {   // entry of symbol value v
+        const uint32_t j = (uint32_t)(v - lo_sym);
+        if constexpr (!kWide) {
+            return encs[j];
+        } else {
+            uint32_t e = encs[j < (uint32_t)kWin ? j : (uint32_t)kWin - 1u];
+            if (j >= (uint32_t)kWin) e = encx_of(genc[v - glo]);   // outside the window (rare)
+            return e;
+        }
+    };
 
     // ---- state entering block g (encode order runs from the stream end down)
     uint32_t x = kL;
