@@ -471,6 +471,23 @@ struct CosetConsts {
     }
 };
 
+// Per-chunk escape constants, wave-uniform: the shift k_j of each coordinate
+// and the first of its fine words.
+struct EscCoords {
+    int k[8];
+    const uint32_t* w[8];
+    __device__ __forceinline__ void init(const int32_t* ek, const int64_t* fo, const uint32_t* fine) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            k[j] = __builtin_amdgcn_readfirstlane(ek[j]);
+            const int64_t o = fo[j];
+            const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)o);
+            const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)o >> 32));
+            w[j] = fine + (int64_t)(((uint64_t)hi << 32) | lo);
+        }
+    }
+};
+
 // A staged vector of an escaped chunk (coarse symbol fields in r) as its
 // lattice point in fp32: coordinate j's coarse symbol is the field minus its
 // bias (512, c8h 256) when the chunk's LUTs hold biased fields, else
@@ -479,8 +496,7 @@ struct CosetConsts {
 // c7 = 2 * c8h + (sum of the free symbols mod 2) (core/entropy_coder.py:71-89)
 // and the coset offset.
 __device__ __forceinline__ void lattice_escaped_f32(const uint4& r, const CosetConsts& cs, bool lut_biased,
-                                                    const int32_t* ek, const int64_t* fo, const uint32_t* fine,
-                                                    int64_t v, float y[8]) {
+                                                    const EscCoords& ec, int64_t v, float y[8]) {
     const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
     int sv[8];
     int par = 0;
@@ -488,10 +504,10 @@ __device__ __forceinline__ void lattice_escaped_f32(const uint4& r, const CosetC
     for (int j = 0; j < 8; j++) {
         const int idx = (int)((j & 1) ? (w4[j >> 1] >> 16) : (w4[j >> 1] & 0xffffu));
         int val = lut_biased ? idx - (j < 7 ? 512 : 256) : cs.lo[j] + idx;
-        const int k = ek[j];
+        const int k = ec.k[j];
         if (k) {
             const int64_t bit = v * k;
-            const uint32_t* wp = fine + fo[j] + (bit >> 5);
+            const uint32_t* wp = ec.w[j] + (bit >> 5);
             const int sh = (int)(bit & 31);
             uint32_t f = wp[0] >> sh;
             if (sh + k > 32) f |= wp[1] << (32 - sh);

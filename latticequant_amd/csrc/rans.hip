@@ -1053,7 +1053,7 @@ __device__ __forceinline__ int dpp_ror8(int v) {   // lane l <- lane l ^ 8 withi
     return __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false);
 }
 
-template <int OUT_DT, bool HEADS_ALIGNED, bool DITHER, bool ROT = false>
+template <int OUT_DT, bool HEADS_ALIGNED, bool DITHER, bool ROT = false, bool ESC = false>
 __global__ __launch_bounds__(kDecThreads) void k_chunk_decode(
         const uint32_t* __restrict__ words, const int64_t* __restrict__ chunk_base, const int64_t* __restrict__ stream_woff,
         const uint32_t* __restrict__ blk_off, const int64_t* __restrict__ stream_nbits,
@@ -1119,11 +1119,13 @@ __global__ __launch_bounds__(kDecThreads) void k_chunk_decode(
     const lq_table* T = tables + chunk * LQ_STREAMS;
     // escaped chunk (coarse symbols plus raw low bits, alphabets beyond L):
     // the generic path with the low bits merged in
-    const int32_t* const ekc = esc_k ? esc_k + chunk * 8 : nullptr;
+    const int32_t* const ekc = ESC && esc_k ? esc_k + chunk * 8 : nullptr;
     bool esc = false;
-    if (ekc) {
+    EscCoords ec;
+    if (ESC && ekc) {
+        ec.init(ekc, fine_off + chunk * 8, fine);
 #pragma unroll
-        for (int j = 0; j < 8; j++) esc = esc || ekc[j] != 0;
+        for (int j = 0; j < 8; j++) esc = esc || ec.k[j] != 0;
     }
     const bool lut_biased = chunk_biased(T);   // the LUT's symbol fields (k_chunk_lut decides the same way)
     const bool biased = !esc && lut_biased;
@@ -1209,10 +1211,10 @@ __global__ __launch_bounds__(kDecThreads) void k_chunk_decode(
             }
             if (biased) {
                 lattice_biased_f32(r, cp ? 0.5f : 0.f, y);
-            } else if (esc) {
+            } else if (ESC && esc) {
                 CosetConsts cs;
                 cs.pick(cp, cc0, cc1);
-                lattice_escaped_f32(r, cs, lut_biased, ekc, fine_off + chunk * 8, fine, vfirst + p, y);
+                lattice_escaped_f32(r, cs, lut_biased, ec, vfirst + p, y);
             } else {
                 CosetConsts cs;
                 cs.pick(cp, cc0, cc1);
@@ -1543,11 +1545,17 @@ static int chunk_decode_launch(const uint32_t* d_words, const int64_t* d_chunk_b
     const bool aligned = bph % kBlk == 0;
     const int lpr = d_signs ? head_dim / 8 : 1;
     const float div = d_signs ? (float)sqrt((double)head_dim) : 1.0f;
-#define LQ_DECODE(DT, AL, DI, RO)                                                                                 \
-    hipLaunchKernelGGL((k_chunk_decode<DT, AL, DI, RO>), grid, dim3(kDecThreads), 0, s, d_words, d_chunk_base,          \
+    // escaped chunks get their own instantiations (the escape constants would
+    // otherwise cost registers in every decoder)
+#define LQ_DECODE_E(DT, AL, DI, RO, ES)                                                                           \
+    hipLaunchKernelGGL((k_chunk_decode<DT, AL, DI, RO, ES>), grid, dim3(kDecThreads), 0, s, d_words, d_chunk_base,      \
                        d_stream_woff, d_blk_off, d_stream_nbits, d_blk_state, d_coset_bits, d_tables, d_scale16,       \
                        d_lut_work, n_chunks, n_heads, bph, nblk, gpw, d_out, d_dither_seed, d_signs, lpr, div,         \
                        d_esc_k, d_fine_off, d_fine)
+#define LQ_DECODE(DT, AL, DI, RO)                                                                                 \
+    do {                                                                                                          \
+        if (d_esc_k) LQ_DECODE_E(DT, AL, DI, RO, true); else LQ_DECODE_E(DT, AL, DI, RO, false);                  \
+    } while (0)
 #define LQ_DECODE_DT(DT, RO)                                                                                      \
     do {                                                                                                          \
         if (d_dither_seed) { if (aligned) LQ_DECODE(DT, true, true, RO); else LQ_DECODE(DT, false, true, RO); }   \
@@ -1564,6 +1572,7 @@ static int chunk_decode_launch(const uint32_t* d_words, const int64_t* d_chunk_b
     }
 #undef LQ_DECODE_DT
 #undef LQ_DECODE
+#undef LQ_DECODE_E
     return launch_status();
 }
 
