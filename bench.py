@@ -711,6 +711,46 @@ def summarize_pmc(fetch_csv, write_csv, out_path, calib_bytes=1 << 30):
     print(json.dumps(res))
 
 
+def summarize_counters(counter_csv, simds=1024, xcds=8):
+    """Per-kernel means of every counter in a rocprofv3 --pmc
+    counter_collection.csv (the largest-grid dispatches of each kernel), as a
+    markdown table, plus two issue figures where the counters are present.
+    GRBM_GUI_ACTIVE comes summed over the XCDs (each has its own GRBM), so a
+    launch's busy cycles at its actual clock are GRBM_GUI_ACTIVE / xcds:
+      issue_frac = 4 SQ_INSTS_VALU / (simds x GRBM_GUI_ACTIVE / xcds): the share
+                   of those cycles the launch's VALU instructions occupy at one
+                   wave64 instruction per 4 cycles per SIMD (1.0 = issue bound);
+      valu_busy  = the same with SQ_ACTIVE_INST_VALU (rocprof's VALUBusy)."""
+    import pandas as pd
+    df = pd.read_csv(counter_csv)
+    df = df.assign(base=df["Kernel_Name"].map(_kernel_base))
+    rows = {}
+    for (name, ctr), d in df.groupby(["base", "Counter_Name"]):
+        if not name.startswith("k_"):
+            continue
+        d = d[d["Grid_Size"] == d["Grid_Size"].max()]
+        r = rows.setdefault(name, {"grid": int(d["Grid_Size"].max()), "dispatches": 0})
+        per = d.groupby("Dispatch_Id")["Counter_Value"].sum() if "Dispatch_Id" in d else d["Counter_Value"]
+        r[ctr] = float(per.mean())
+        r["dispatches"] = max(r["dispatches"], int(len(per)))
+    ctrs = sorted({c for r in rows.values() for c in r if c not in ("grid", "dispatches")})
+    extra = []
+    if {"SQ_INSTS_VALU", "GRBM_GUI_ACTIVE"} <= set(ctrs):
+        extra.append("issue_frac")
+    if {"SQ_ACTIVE_INST_VALU", "GRBM_GUI_ACTIVE"} <= set(ctrs):
+        extra.append("valu_busy")
+    print("| kernel | grid | dispatches | " + " | ".join(ctrs + extra) + " |")
+    print("|---|---:|---:|" + "---:|" * (len(ctrs) + len(extra)))
+    for name, r in sorted(rows.items()):
+        vals = [f"{r.get(c, float('nan')):.4g}" for c in ctrs]
+        g = r.get("GRBM_GUI_ACTIVE")
+        if "issue_frac" in extra:
+            vals.append(f"{4 * r.get('SQ_INSTS_VALU', 0) / (simds * g / xcds):.3f}" if g else "")
+        if "valu_busy" in extra:
+            vals.append(f"{4 * r.get('SQ_ACTIVE_INST_VALU', 0) / (simds * g / xcds):.3f}" if g else "")
+        print(f"| {name} | {r['grid']} | {r['dispatches']} | " + " | ".join(vals) + " |")
+
+
 def summarize_trace(trace_csv, top=16):
     """Per (kernel, grid size) launch counts and durations from a rocprofv3
     --kernel-trace kernel_trace.csv, as a markdown table (longest total first)."""
@@ -753,7 +793,13 @@ def main():
                          "architecture; fp16, rANS and resident caches) and print one JSON line")
     ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
                     help="only print per-(kernel, grid) launch durations of a rocprofv3 --kernel-trace run and exit")
+    ap.add_argument("--summarize-counters", metavar="COUNTER_CSV",
+                    help="only print per-kernel means of the counters of a rocprofv3 --pmc run (and the VALU issue "
+                         "share when SQ_INSTS_VALU / SQ_ACTIVE_INST_VALU and GRBM_GUI_ACTIVE are among them) and exit")
     args = ap.parse_args()
+    if args.summarize_counters:
+        summarize_counters(args.summarize_counters)
+        return
     if args.summarize_pmc:
         summarize_pmc(*args.summarize_pmc)
         return
