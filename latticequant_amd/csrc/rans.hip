@@ -442,8 +442,9 @@ __global__ __launch_bounds__(64 * kTabWaves) void k_chunk_tables_wave(const uint
 //
 // Task = (chunk, stream st = coset * 8 + coord, block g), one lane each; a
 // 256-thread workgroup holds 16 consecutive blocks x 16 streams of one chunk,
-// so the 8 lanes of a (block, coset) read the 8 interleaved columns of that
-// coset one 128-byte line at a time (sym_pos layout).
+// a wave one coset of 8 blocks, so the 8 lanes of a (block, coset) read the 8
+// interleaved columns of that coset one 128-byte line at a time (sym_pos
+// layout).
 
 template <typename SymT>
 struct Col {
@@ -565,8 +566,10 @@ __global__ __launch_bounds__(256) void k_chunk_encode(const SymT* __restrict__ s
     __shared__ uint32_t sq[4][256];   // per-lane queue of scratch words (4: seven workgroups fit a CU's LDS)
     const int tid = threadIdx.x;
     const int64_t chunk = blockIdx.y;
-    const int64_t g = (int64_t)blockIdx.x * kEncBlocks + (tid >> 4);
-    const int st = tid & 15;
+    // wave = one coset of 8 blocks (lanes: block-major, coordinate-minor), so
+    // a wave's columns hold one coset's counts and run about equally long
+    const int64_t g = (int64_t)blockIdx.x * kEncBlocks + ((tid >> 3) & 15);
+    const int st = ((tid >> 7) << 3) | (tid & 7);
     const lq_table* T = tables + chunk * LQ_STREAMS;
     // first alphabet entry of stream s's LDS window
     auto win0 = [&](int s) -> int {
