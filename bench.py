@@ -320,10 +320,13 @@ def make_c4():
     return ks, vs, sched, h.hexdigest()
 
 
-def bench_c4(dev, steps=5):
+def bench_c4(dev, steps=5, n_streams=3):
     """C4: the 28-layer Qwen2.5-7B-shaped cache at its 3/4/5-bit schedule, one
     chunk per (layer, K/V), per-chunk tables, every chunk coded.  Chunks are
-    grouped by rate (K on the int16 staging path, V on int8).  K coordinates
+    grouped by rate (K on the int16 staging path, V on int8); the groups are
+    independent and are dealt to n_streams streams (V groups first: their
+    launches fill the chip while a K group's latency-bound table build and
+    its one host read of the escape shifts run beside them).  K coordinates
     whose stream alphabet exceeds L = 1024 symbols (the reference's table
     normalisation never terminates there) are escaped: coarse symbols through
     the same tables and streams plus raw low bits (a format of this build; the
@@ -346,12 +349,27 @@ def bench_c4(dev, steps=5):
     arenas = [torch.empty(codec.words_bound(g[0].shape[0], g[0][0].numel() // 8), dtype=torch.int32, device=dev)
               for g in groups]
     encs = [None] * len(groups)
+    side = [torch.cuda.Stream(device=dev) for _ in range(n_streams)] if n_streams > 1 else []
+    order = sorted(range(len(groups)), key=lambda i: groups[i][2])   # int8 groups first
+
+    def one(i):
+        x, r, wide, _ = groups[i]
+        encs[i], _ = codec.encode_batch(x, r, exact_size=False, words_out=arenas[i], wide=wide)
+        codec.decode_batch(encs[i], out=outs[i])
 
     def step():
-        for i, (x, r, wide, _) in enumerate(groups):
-            encs[i], _ = codec.encode_batch(x, r, exact_size=False, words_out=arenas[i], wide=wide)
-        for i in range(len(groups)):
-            codec.decode_batch(encs[i], out=outs[i])
+        if not side:
+            for i in order:
+                one(i)
+            return
+        main = torch.cuda.current_stream(dev)
+        for st in side:
+            st.wait_stream(main)
+        for j, i in enumerate(order):   # group i always runs on the same stream
+            with torch.cuda.stream(side[j % len(side)]):
+                one(i)
+        for st in side:
+            main.wait_stream(st)
 
     step()
     torch.cuda.synchronize()
@@ -408,7 +426,7 @@ def bench_c4(dev, steps=5):
             "k_layers_escaped": sorted(l for _, _, l in escaped), "status_flags": st,
             "bit_exact_v_chunk": exact, "k_chunks_lossless": lossless,
             "escaped_k_chunk_equals_oracle_escape": esc_exact,
-            "step_us": round(us, 1), "D": D, "compressed_bytes": Cb,
+            "step_us": round(us, 1), "streams": max(n_streams, 1), "D": D, "compressed_bytes": Cb,
             "effective_bits_per_dim": round(8 * Cb / D, 4),
             "roofline": _roof(B, us, "encode + decode of every coded chunk, B = 4 D + 2 C over them")}
 
@@ -784,6 +802,7 @@ def main():
     ap.add_argument("--only", choices=["c1", "c3", "c4", "c5"],
                     help="run one leg alone and print its JSON (the profiling entry points)")
     ap.add_argument("--c5-layers", type=int, default=32, help="layers of the C5 cache (x K,V chunks of 2 GiB)")
+    ap.add_argument("--c4-streams", type=int, default=3, help="streams the C4 rate groups are dealt to (1: one stream)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run one 1 GiB device copy (the HBM-counter calibration kernel under rocprofv3 --pmc)")
     ap.add_argument("--summarize-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "OUT_JSON"),
@@ -822,7 +841,7 @@ def main():
                           "dtype": "fp16", "config": {"model": "Llama-3.1-8B architecture, random weights",
                                                      "bits_per_dim": BITS}, "results": r}))
         return
-    legs = {"c1": lambda: bench_c1(dev), "c3": lambda: bench_decode_step(dev), "c4": lambda: bench_c4(dev),
+    legs = {"c1": lambda: bench_c1(dev), "c3": lambda: bench_decode_step(dev), "c4": lambda: bench_c4(dev, n_streams=args.c4_streams),
             "c5": lambda: bench_c5(dev, args.c5_layers)}
     if args.only:
         res = legs[args.only]()
@@ -981,7 +1000,7 @@ def main():
         extra["c1"] = bench_c1(dev)
     if "c4" not in skip:
         progress("C4 28-layer schedule")
-        extra["c4"] = bench_c4(dev)
+        extra["c4"] = bench_c4(dev, n_streams=args.c4_streams)
     if "c5" not in skip:
         del x, out
         torch.cuda.empty_cache()
