@@ -10,6 +10,9 @@ compresses every update and hands HF attention fully decompressed fp16 K / V
     format: the at-rest form, what ``compressed_bytes`` counts), and
   - the resident fixed-width form of the same lattice points
     (:class:`ResidentKV`) that decode attention reads;
+* the at-rest chunks are not read by decode steps: ``offload_at_rest()``
+  moves them to host memory in the wire form (the device then keeps the
+  resident form and the tail), ``restore_at_rest()`` brings them back;
 * ``update`` returns, for a one-token step, marker views that carry the cache
   and layer, and the registered attention ``"lq_resident"`` runs
   ``lq_resident_attention`` over resident prefix + tail (no fp16 prefix is
@@ -160,11 +163,34 @@ class ResidentKVCache(DynamicCache):
     def is_compileable(self) -> bool:
         return False
 
+    # -- at-rest chunks ---------------------------------------------------
+    def offload_at_rest(self) -> int:
+        """Move every at-rest chunk pair flushed so far to host memory in the
+        wire form (codec.to_bytes: the reference's bitstream words, coset bits
+        and fp16 scales plus tables, checkpoints and a CRC-32), releasing its
+        device copy: decode steps read only the resident form and the tail, so
+        the device then holds about the resident bytes and the tail.  Settles
+        pending encodes (one host sync).  Returns the host bytes held."""
+        for ch in self.chunks:
+            for i, pair in enumerate(ch):
+                ch[i] = tuple(e if isinstance(e, _HostAtRest) else _HostAtRest(e.batch) for e in pair)
+        return self.at_rest_host_bytes()
+
+    def restore_at_rest(self):
+        """Bring offloaded chunk pairs back to the device (codec.from_bytes)."""
+        for ch in self.chunks:
+            for i, pair in enumerate(ch):
+                ch[i] = tuple(_DeviceAtRest(e.batch) if isinstance(e, _HostAtRest) else e for e in pair)
+
+    def at_rest_host_bytes(self) -> int:
+        return sum(e.nbytes for ch in self.chunks for pair in ch for e in pair if isinstance(e, _HostAtRest))
+
     # -- reporting --------------------------------------------------------
     def compressed_bytes(self) -> int:
         """Bytes of the at-rest chunks as the reference counts them
-        (bitstream + coset bits + fp16 scales, llm/compressed_kv_cache.py:113-119)."""
-        return sum(int(e.batch.reference_bytes().sum()) for ch in self.chunks for pair in ch for e in pair)
+        (bitstream + coset bits + fp16 scales, llm/compressed_kv_cache.py:113-119),
+        wherever they are held."""
+        return sum(e.reference_bytes() for ch in self.chunks for pair in ch for e in pair)
 
     def resident_bytes(self) -> int:
         """Bytes of the resident decode form (records, meta, scales, exceptions)."""
@@ -183,6 +209,36 @@ class _AtRest:
     @property
     def batch(self):
         return self._pend.result().select(self._index)
+
+    def reference_bytes(self) -> int:
+        return int(self.batch.reference_bytes().sum())
+
+
+class _DeviceAtRest:
+    """An at-rest half held on the device as a settled batch."""
+
+    def __init__(self, batch):
+        self.batch = batch
+
+    def reference_bytes(self) -> int:
+        return int(self.batch.reference_bytes().sum())
+
+
+class _HostAtRest:
+    """An at-rest half held in host memory in the wire form; .batch restores
+    it to the current device (a new device copy per access)."""
+
+    def __init__(self, batch):
+        self.blob = codec.to_bytes(batch)
+        self.nbytes = len(self.blob)
+        self._ref = int(batch.reference_bytes().sum())
+
+    @property
+    def batch(self):
+        return codec.from_bytes(self.blob)
+
+    def reference_bytes(self) -> int:
+        return self._ref
 
 
 def attn_workspace_size(n_heads: int, group: int, t_prefix: int, t_tail: int) -> int:

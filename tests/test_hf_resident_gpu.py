@@ -115,3 +115,43 @@ def test_hf_left_padded_batch_uses_masked_sdpa_gpu(monkeypatch):
             assert torch.equal(la, lb)
     assert calls == []
     assert a.res_k[0].n_tokens > 0   # the prefix was compressed and is read through materialise()
+
+
+@pytest.mark.gpu
+def test_resident_cache_offload_at_rest_gpu():
+    """offload_at_rest moves the flushed rANS chunk pairs to host bytes (the
+    wire form): decode attention and the materialised K / V are unchanged,
+    compressed_bytes is unchanged, the device releases the chunks, and a
+    chunk restored from the host decodes to the same K / V the resident prefix
+    holds (the values _decompress_chunk writes)."""
+    from latticequant_amd import codec
+    from latticequant_amd.llm.resident_cache import ResidentKVCache
+    g = torch.Generator().manual_seed(5)
+    c = ResidentKVCache(bits_per_dim=4, tail_tokens=32)
+    k = torch.randn(1, 2, 232, 128, generator=g).half().cuda()
+    v = torch.randn(1, 2, 232, 128, generator=g).half().cuda()
+    c.update(k[:, :, :200], v[:, :, :200], 0)           # prompt: 160 tokens flushed
+    for t in range(200, 232):                           # decode steps: another 32
+        c.update(k[:, :, t:t + 1], v[:, :, t:t + 1], 0)
+    assert len(c.chunks[0]) == 3 and c.res_k[0].n_tokens == 192
+    q = torch.randn(1, 4, 1, 128, generator=g).half().cuda()
+    before = c.attend(0, q)
+    mk, mv = c.materialise(0)
+    ref = c.compressed_bytes()
+    torch.cuda.synchronize()
+    m0 = torch.cuda.memory_allocated()
+    held = c.offload_at_rest()
+    torch.cuda.synchronize()
+    assert held > 0 and c.at_rest_host_bytes() == held
+    assert torch.cuda.memory_allocated() < m0
+    assert torch.equal(c.attend(0, q), before)
+    mk2, mv2 = c.materialise(0)
+    assert torch.equal(mk2, mk) and torch.equal(mv2, mv)
+    assert c.compressed_bytes() == ref
+    n0 = 160
+    for half, full in ((0, mk), (1, mv)):
+        dec = codec.decode_batch(c.chunks[0][0][half].batch)
+        assert torch.equal(dec.reshape(1, 2, n0, 128), full[:, :, :n0])
+    c.restore_at_rest()
+    assert c.at_rest_host_bytes() == 0 and c.compressed_bytes() == ref
+    assert torch.equal(codec.decode_batch(c.chunks[0][1][0].batch).reshape(1, 2, 16, 128), mk[:, :, n0:n0 + 16])
