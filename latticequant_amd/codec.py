@@ -282,10 +282,11 @@ def _check_input(x: torch.Tensor) -> torch.Tensor:
     return x.contiguous()
 
 
-def quantize_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None):
+def quantize_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None, with_sigma2: bool = False):
     """E8-quantize a batch of chunks without entropy coding (the reference's
     eval_only_no_entropy path, llm/compressed_kv_cache.py:199-221).
-    Returns (scale32, scale16, deq) with deq = q * scale32 in x's dtype."""
+    Returns (scale32, scale16, deq) with deq = q * scale32 in x's dtype, and
+    sigma2 after them when with_sigma2 (None for caller scales)."""
     lib = L.lib()
     x = _check_input(x)
     C, B, H, T, hd = x.shape
@@ -293,7 +294,7 @@ def quantize_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None
     nh, bph = B * H, T * hd // 8
     nblk = (nh * bph + L.LQ_BLK - 1) // L.LQ_BLK
     dt = L.dtype_code(x.dtype)
-    _, scale32, scale16, _, fastdiv = _head_scales(x, bits, scale32)
+    _, scale32, scale16, sigma2, fastdiv = _head_scales(x, bits, scale32)
     sym = _empty(C * nblk * L.LQ_SYM_STRIDE, torch.int8, dev)
     coset_bits = _empty(C * nblk * L.LQ_BLK // 8, torch.uint8, dev)
     blk_n1 = _empty(C * nblk, torch.int32, dev)
@@ -302,7 +303,7 @@ def quantize_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None
     L.check(lib.lq_chunk_quantize(x.data_ptr(), dt, C, nh, bph, scale32.data_ptr(), fastdiv.data_ptr(), sym.data_ptr(),
                                   coset_bits.data_ptr(), blk_n1.data_ptr(), hist.data_ptr(), status.data_ptr(),
                                   deq.data_ptr(), dt, None, L.stream_ptr(dev)), "lq_chunk_quantize")
-    return scale32, scale16, deq
+    return (scale32, scale16, deq, sigma2) if with_sigma2 else (scale32, scale16, deq)
 
 
 def quantize_points(t: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None):
@@ -734,6 +735,7 @@ class PendingEncode:
         if st & L.LQ_ST_SYM_OVERFLOW:
             done, _ = encode_batch(self._x, self._bits, scale32=enc.scale32, exact_size=True, wide=True,
                                    dither_seed=self._seed)
+            done.sigma2 = enc.sigma2   # the scales' sigma^2, as the first encode had them
         else:
             if st & L.LQ_ST_ALPHABET:
                 raise AlphabetError("a stream's alphabet exceeds L = 1024 symbols (the reference's table "
@@ -766,13 +768,19 @@ def settle_many(pends) -> None:
         o += n
 
 
-def encode_batch_deferred(x: torch.Tensor, bits, deq_out: bool = False, dither_seed=None):
+def encode_batch_deferred(x: torch.Tensor, bits, deq_out: bool = False, dither_seed=None,
+                          scale32: Optional[torch.Tensor] = None, sigma2: Optional[torch.Tensor] = None):
     """encode_batch with no host sync (int8 staging, bound-sized arena):
     returns (enc, deq, PendingEncode).  enc may be used for device work in
     stream order right away unless a chunk overflowed int8; the pending
-    handle's result() is the batch to keep (see PendingEncode)."""
+    handle's result() is the batch to keep (see PendingEncode).  scale32 (and
+    their sigma2): the chunks' scales when they were already computed
+    (quantize_batch)."""
     x = _check_input(x)
-    enc, deq = encode_batch(x, bits, deq_out=deq_out, exact_size=False, wide=False, dither_seed=dither_seed)
+    enc, deq = encode_batch(x, bits, scale32=scale32, deq_out=deq_out, exact_size=False, wide=False,
+                            dither_seed=dither_seed)
+    if scale32 is not None:
+        enc.sigma2 = sigma2
     return enc, deq, PendingEncode(enc, x, bits, dither_seed)
 
 

@@ -172,6 +172,51 @@ class OptimizedChunk:
         return 0 if self._one is None else int(self._one.side_bytes()[0].item())
 
 
+class _DeferredGroup:
+    """Same-shaped small updates whose entropy coding is batched: their inputs,
+    rates and fp32 scales, kept until flush() queues one encode_batch_deferred
+    over all of them.  Behaves as the chunks' pending handle: result() flushes
+    (if not yet) and settles the batch (a host read of its status and sizes)."""
+
+    def __init__(self):
+        self.xs, self.bits, self.scales, self.sigma2, self.chunks = [], [], [], [], []
+        self.n = 0
+        self._pend = None
+
+    def full(self, limit: int) -> bool:
+        return self._pend is not None or self.n >= limit
+
+    def add(self, x: torch.Tensor, bits, scale32: torch.Tensor, sigma2: torch.Tensor) -> int:
+        i0 = self.n
+        self.xs.append(x)
+        self.bits.extend([bits] * x.shape[0] if isinstance(bits, int) else list(bits))
+        self.scales.append(scale32)
+        self.sigma2.append(sigma2)
+        self.n += x.shape[0]
+        return i0
+
+    def flush(self) -> Optional[codec.PendingEncode]:
+        if self._pend is None and self.n:
+            x = self.xs[0] if len(self.xs) == 1 else torch.cat(self.xs)
+            bits = self.bits[0] if len(set(self.bits)) == 1 else list(self.bits)
+            _, _, self._pend = codec.encode_batch_deferred(x, bits, scale32=torch.cat(self.scales),
+                                                          sigma2=torch.cat(self.sigma2))
+            self.xs, self.scales, self.sigma2 = [], [], []
+            return self._pend
+        return None
+
+    @property
+    def tracked(self) -> bool:
+        return self._pend is not None and self._pend.tracked
+
+    def ready(self) -> bool:
+        return self._pend is not None and self._pend.ready()
+
+    def result(self) -> codec.EncodedBatch:
+        self.flush()
+        return self._pend.result()
+
+
 class CompressedKVLayer:
     """Chunks of one layer's K or V (llm/compressed_kv_cache.py:96-126)."""
 
@@ -295,11 +340,21 @@ class CompressedKVCache(DynamicCache):
         self.total_vectors = 0
         self._model_dtype = None
         self._pending: list = []   # (PendingEncode, chunks) written without host syncs, not yet settled
+        self._groups: dict = {}    # (shape, dtype, device) -> open _DeferredGroup of small updates
 
     # -- compression ----------------------------------------------------
     def _compress_many(self, tensors: List[torch.Tensor], bits=None):
         """Compress same-shaped (B, H, T, hd) tensors in one batched launch.
-        Returns [(chunk, decompressed)] in input order."""
+        Returns [(chunk, decompressed)] in input order.
+
+        Small updates (decode steps) are quantized at once -- the returned K / V
+        are final -- while their entropy coding waits in a shared group: once
+        DEFER_CHUNKS chunks of one shape are pending (the K and V of every
+        layer of a step, typically), or one of them is read, the group is
+        encoded in one batch with the scales already computed.  rANS coding is
+        lossless and every chunk keeps its own tables and streams, so the
+        chunks are the ones a per-update encode writes, with one encode
+        launch sequence per group instead of one per update."""
         t0 = tensors[0]
         batch, heads, seq, hd = t0.shape
         if hd % 8 != 0:
@@ -310,6 +365,24 @@ class CompressedKVCache(DynamicCache):
         bph = seq * (hd // 8)
         n_vectors = n_heads * bph
         pend = None
+        if not self.eval_only_no_entropy and n_vectors <= self.DEFER_MAX_VECTORS:
+            scale32, scale16, deq, sigma2 = codec.quantize_batch(x, bits, with_sigma2=True)
+            key = (tuple(x.shape[1:]), x.dtype, x.device)
+            grp = self._groups.get(key)
+            if grp is None or grp.full(self.DEFER_CHUNKS):
+                if grp is not None:
+                    self._flush_group(grp)
+                grp = self._groups[key] = _DeferredGroup()
+            i0 = grp.add(x, bits, scale32, sigma2)
+            per = scale16.view(len(tensors), -1)
+            out = []
+            for i, t in enumerate(tensors):
+                b = bits if isinstance(bits, int) else bits[i]
+                ch = OptimizedChunk(None, i0 + i, per[i], t.shape, n_vectors, n_heads, bph, b, t.dtype, pending=grp)
+                self.total_vectors += n_vectors
+                grp.chunks.append(ch)
+                out.append((ch, deq[i]))
+            return out
         if self.eval_only_no_entropy:
             _, scale16, deq = codec.quantize_batch(x, bits)
             enc = None
@@ -335,6 +408,17 @@ class CompressedKVCache(DynamicCache):
     # are pending, or once they keep this many device bytes alive
     SETTLE_SMALL_COUNT = 256
     SETTLE_SMALL_BYTES = 256 << 20
+    # updates of at most this many vectors per chunk defer their entropy
+    # coding to a shared group of at most DEFER_CHUNKS chunks
+    DEFER_MAX_VECTORS = 1 << 14
+    DEFER_CHUNKS = 64
+
+    def _flush_group(self, grp: "_DeferredGroup"):
+        """Queue the group's batched encode (no host sync) and track it like
+        any other pending batch."""
+        pend = grp.flush()
+        if pend is not None:
+            self._pending.append((pend, grp.chunks))
 
     def _settle_ready(self):
         """Settle the batches whose status read-back has arrived (non-blocking),

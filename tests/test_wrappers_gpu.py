@@ -127,3 +127,46 @@ def test_check_representable_inrange_fixture_gpu():
         q = O.encode_e8(x)
         got = cs.check_representable(torch.from_numpy(q).cuda(), b).cpu().numpy()
         np.testing.assert_array_equal(got, g[f"inrange{b}"])
+
+
+def test_deferred_entropy_coding_equals_per_update_gpu():
+    """Small updates (decode steps) quantize at once and entropy-code in shared
+    groups: the K / V update() returns and every chunk's words, streams, byte
+    counts and decoded tensor equal those of a cache that encodes each update
+    on its own, over a prefill plus decode steps of three layers with a group
+    limit small enough to flush several groups; a chunk of a group that is
+    still open is read (and settled) mid-run; one chunk against the oracle."""
+    from latticequant_amd.llm.compressed_kv_cache import CompressedKVCache
+    gen = torch.Generator().manual_seed(29)
+    a = CompressedKVCache(bits_per_dim=4)
+    a.DEFER_CHUNKS = 8
+    b = CompressedKVCache(bits_per_dim=4)
+    b.DEFER_MAX_VECTORS = 0
+    layers, heads = 3, 2
+    xs = {}
+    for step in range(12):
+        T = 40 if step == 0 else 1
+        for l in range(layers):
+            k = torch.randn(1, heads, T, 128, generator=gen)
+            k[..., :3] *= 6.0
+            k = k.half().cuda()
+            v = torch.randn(1, heads, T, 128, generator=gen).half().cuda()
+            xs[(step, l)] = k
+            ka, va = a.update(k, v, l)
+            kb, vb = b.update(k, v, l)
+            assert torch.equal(ka, kb) and torch.equal(va, vb)
+        if step == 5:   # read a chunk of the open group: it is encoded and settled now
+            assert a._comp_keys[0].chunks[-1].reference_bytes() == b._comp_keys[0].chunks[-1].reference_bytes()
+    assert a.compressed_bytes() == b.compressed_bytes()
+    for l in range(layers):
+        for ca, cb in zip(a._comp_keys[l].chunks + a._comp_values[l].chunks,
+                          b._comp_keys[l].chunks + b._comp_values[l].chunks):
+            assert torch.equal(ca.gpu_bitstream, cb.gpu_bitstream)
+            assert torch.equal(ca.coset_packed, cb.coset_packed)
+            assert ca.side_info_bytes() == cb.side_info_bytes()
+            assert [s.n_bits for s in ca.streams] == [s.n_bits for s in cb.streams]
+            assert torch.equal(a._decompress_chunk(ca), b._decompress_chunk(cb))
+    ch = a._comp_keys[1].chunks[7]   # layer 1, decode step 7
+    s32 = ch.encoded.scale32.cpu().numpy()
+    ref = O.compress_chunk(xs[(7, 1)].cpu().numpy(), 4, scales_f32=s32)
+    np.testing.assert_array_equal(ch.gpu_bitstream.cpu().numpy().view(np.uint32), ref.bitstream.astype(np.uint32))
