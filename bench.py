@@ -470,6 +470,8 @@ def bench_c5(dev, layers):
     pool.shutdown()
     sha = hashlib.sha256("".join(shas).encode()).hexdigest()
     outs = [torch.empty(shape, dtype=torch.float16, device=dev) for _ in range(2)]
+    for i, x in enumerate(xs):   # each (layer, K/V)'s HeadRHT signs, drawn once as the reference's HeadRHT does
+        R.prepare_signs(x.shape, [names[i][0]], [names[i][1]], dev)
     enc0, _ = R.encode_rotated(xs[0], BITS, [0], [0], exact_size=True, wide=False)   # warm-up
     R.decode_rotated(enc0, out=outs[0])
     del enc0

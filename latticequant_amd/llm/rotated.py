@@ -78,6 +78,16 @@ def _device_signs(shape, layers, kvs, device) -> torch.Tensor:
     return t
 
 
+def prepare_signs(shape, layers, kvs, device) -> torch.Tensor:
+    """Draw and upload the sign rows of a chunk geometry once (the reference
+    builds its HeadRHT signs when the object is made,
+    llm/perplexity_eval.py:35-61); later encode_rotated / decode_rotated calls
+    with the same (geometry, layers, K/V) find them on the device."""
+    C = shape[0]
+    layers, kvs = _lists(C, layers, kvs)
+    return _device_signs(shape, layers, kvs, device)
+
+
 def default_dither_seed(layer: int, kv: int) -> int:
     return layer * 10000 + kv * 10 + 7
 
