@@ -339,26 +339,20 @@ __device__ __forceinline__ float div_scaled(float x, float s, float r, bool fast
 // lane: stages h < 8 run in registers, h >= 8 across lanes (partner lane ^ h/8).
 // Every lane of a row must execute this together.  div = f32(sqrt(d)).
 //
-// Partner lanes l ^ 1, l ^ 2, l ^ 4, l ^ 8 lie in one 16-lane DPP row and are
-// read with DPP moves (quad_perm for ^1 and ^2, two bank-masked row shifts
-// for ^4 and ^8), not through the LDS crossbar; the butterfly is then one
+// Partner lanes l ^ 1 .. l ^ 16 are read with one ds_swizzle each (bitmask
+// mode, within 32 lanes), which issues on the LDS pipe and leaves the VALU to
+// the arithmetic (these kernels are VALU-bound); the butterfly is then one
 // FMA, fma(y, +-1, partner) = RN(partner +- y): the lower lane of a pair gets
-// a + b, the upper a - b, bit for bit as the add / subtract.  Rows of more
-// than 16 lanes (head_dim > 128) use shuffles for the partners beyond.
+// a + b, the upper a - b, bit for bit as the add / subtract.  Rows of 64
+// lanes (head_dim 512) read partner l ^ 32 with a shuffle.
 template <int HL>
 __device__ __forceinline__ float lane_xor(float v) {
     const int i = __builtin_bit_cast(int, v);
     int r;
-    if constexpr (HL == 1) {
-        r = __builtin_amdgcn_update_dpp(i, i, 0xB1, 0xF, 0xF, false);    // quad_perm [1, 0, 3, 2]
-    } else if constexpr (HL == 2) {
-        r = __builtin_amdgcn_update_dpp(i, i, 0x4E, 0xF, 0xF, false);    // quad_perm [2, 3, 0, 1]
-    } else if constexpr (HL == 4) {   // row_shl:4 into banks 0, 2; row_shr:4 into banks 1, 3
-        r = __builtin_amdgcn_update_dpp(__builtin_amdgcn_update_dpp(i, i, 0x104, 0xF, 0x5, false), i, 0x114, 0xF,
-                                        0xA, false);
-    } else if constexpr (HL == 8) {   // row_shl:8 into banks 0, 1; row_shr:8 into banks 2, 3
-        r = __builtin_amdgcn_update_dpp(__builtin_amdgcn_update_dpp(i, i, 0x108, 0xF, 0x3, false), i, 0x118, 0xF,
-                                        0xC, false);
+    if constexpr (HL <= 16) {
+        // ds_swizzle in bitmask mode (offset bit 15 clear): lane (l & 0x1f) ^ HL
+        // of its 32-lane half, on the LDS pipe, not the VALU
+        r = __builtin_amdgcn_ds_swizzle(i, (HL << 10) | 0x1f);
     } else {
         return __shfl_xor(v, HL, 64);
     }
