@@ -218,12 +218,13 @@ __device__ __forceinline__ void stage_minmax(const uint4& w, int row16, int n0, 
 // paths are compiled out, which frees the scalar registers they held (fewer
 // spills through VGPR lanes in the block loop).  ROT: the input rows are first
 // rotated in registers (rht_lanes, sign row = the head, lpr lanes per row),
-// exactly the fp32 values a materialised forward rotation holds; no
-// dequantised output, at least 5 waves per SIMD.  LDT >= 0: the input dtype as
-// a compile-time constant (the lean launches), so no dtype test is kept live
-// across the block loop.
+// exactly the fp32 values a materialised forward rotation holds, and divided
+// by the scale as IEEE division rounds (div_exact where the row and the scale
+// lie in its range); no dequantised output, at least 5 waves per SIMD.
+// LDT >= 0: the input dtype as a compile-time constant (the lean launches),
+// so no dtype test is kept live across the block loop.
 template <typename SymT, bool DITHER, bool LEAN = false, bool ROT = false, int LDT = -1>
-__global__ __launch_bounds__(kQThreads, LEAN ? 7 : (ROT ? 5 : 1)) void k_chunk_quantize(
+__global__ __launch_bounds__(kQThreads, ROT ? 5 : (LEAN ? 7 : 1)) void k_chunk_quantize(
     const void* __restrict__ x, int dtype, int64_t n_heads, int64_t bph, int64_t nblk,
     const float* __restrict__ scale32, const int32_t* __restrict__ fastdiv, SymT* __restrict__ sym,
     uint8_t* __restrict__ coset_bits, uint32_t* __restrict__ blk_n1, uint32_t* __restrict__ hist,
@@ -276,7 +277,11 @@ __global__ __launch_bounds__(kQThreads, LEAN ? 7 : (ROT ? 5 : 1)) void k_chunk_q
         bool f0 = false, f1 = false;
         if (two_heads) {
             s0 = scale32[hq0]; s1 = scale32[hq1];
-            if (!ROT) {   // rotated values are fp32: IEEE division
+            if (ROT) {    // rotated values are fp32: div_exact where in range
+                rs0 = 1.0f / s0; rs1 = 1.0f / s1;
+                f0 = s0 >= 0x1p-60f && s0 <= 0x1p60f;
+                f1 = s1 >= 0x1p-60f && s1 <= 0x1p60f;
+            } else {
                 const int32_t w0 = fastdiv[hq0], w1 = fastdiv[hq1];
                 f0 = w0 != 0; f1 = w1 != 0;
                 rs0 = __int_as_float(w0); rs1 = __int_as_float(w1);   // RN(1 / s) where fast
@@ -306,9 +311,14 @@ __global__ __launch_bounds__(kQThreads, LEAN ? 7 : (ROT ? 5 : 1)) void k_chunk_q
                     int64_t h = hq0;
                     while (rr >= (int)bph) { rr -= (int)bph; h++; }
                     s = scale32[h];
-                    const int32_t w = ROT ? 0 : fastdiv[h];
-                    rs = __int_as_float(w);
-                    fast = w != 0;
+                    if (ROT) {
+                        rs = 1.0f / s;
+                        fast = s >= 0x1p-60f && s <= 0x1p60f;
+                    } else {
+                        const int32_t w = fastdiv[h];
+                        rs = __int_as_float(w);
+                        fast = w != 0;
+                    }
                     hq = h;
                 }
                 float xv[8], t[8], ic[8], dd[8];
@@ -320,9 +330,15 @@ __global__ __launch_bounds__(kQThreads, LEAN ? 7 : (ROT ? 5 : 1)) void k_chunk_q
                     float sg[8];
                     const int part = tid & (lpr - 1);
                     load_signs8(signs + hq * (8 * (int64_t)lpr) + 8 * part, sg);
-                    rht_lanes(xv, sg, part, lpr, rdiv, rrcp, false);
-                }
-                if (fast) {
+                    const bool narrow = rht_lanes(xv, sg, part, lpr, rdiv, rrcp, false);
+                    if (fast && narrow) {
+#pragma unroll
+                        for (int i = 0; i < 8; i++) t[i] = div_exact(xv[i], s, rs);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 8; i++) t[i] = xv[i] / s;
+                    }
+                } else if (fast) {
 #pragma unroll
                     for (int i = 0; i < 8; i++) t[i] = div_scaled(xv[i], s, rs, true);
                 } else {
@@ -638,7 +654,7 @@ int lq_chunk_quantize(const void* d_x, int dtype, int64_t n_chunks, int64_t n_he
 
 // Rotated rows: as lq_chunk_quantize on w = RHT(x) (sign row = the head,
 // head_dim a power of two in [8, 128], bph a multiple of head_dim / 8), with
-// IEEE division by the scale and no dequantised output.
+// the scale division rounded as IEEE division and no dequantised output.
 int lq_chunk_quantize_rht(const void* d_x, int dtype, int64_t n_chunks, int64_t n_heads, int64_t bph, int head_dim,
                           const float* d_signs, const float* d_scale32, int8_t* d_sym, uint8_t* d_coset_bits,
                           uint32_t* d_blk_n1, uint32_t* d_hist, int32_t* d_status, const int64_t* d_dither_seed,
@@ -651,14 +667,19 @@ int lq_chunk_quantize_rht(const void* d_x, int dtype, int64_t n_chunks, int64_t 
     const int64_t wg = n_chunks * ((nblk + kQBlocksPerWG - 1) / kQBlocksPerWG);
     const float div = (float)sqrt((double)head_dim);
     const int lpr = head_dim / 8;
-    if (d_dither_seed)
-        hipLaunchKernelGGL((k_chunk_quantize<int8_t, true, false, true>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x,
-                           dtype, n_heads, bph, nblk, d_scale32, nullptr, d_sym, d_coset_bits, d_blk_n1, d_hist, nullptr,
-                           d_status, nullptr, (int)LQ_F32, d_dither_seed, d_signs, lpr, div);
-    else
-        hipLaunchKernelGGL((k_chunk_quantize<int8_t, false, false, true>), dim3((unsigned)wg), dim3(kQThreads), 0, s,
-                           d_x, dtype, n_heads, bph, nblk, d_scale32, nullptr, d_sym, d_coset_bits, d_blk_n1, d_hist,
-                           nullptr, d_status, nullptr, (int)LQ_F32, nullptr, d_signs, lpr, div);
+#define LQ_ROT(DI, LE, DT)                                                                                        \
+    hipLaunchKernelGGL((k_chunk_quantize<int8_t, DI, LE, true, DT>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x, \
+                       dtype, n_heads, bph, nblk, d_scale32, nullptr, d_sym, d_coset_bits, d_blk_n1, d_hist, nullptr,  \
+                       d_status, nullptr, (int)LQ_F32, d_dither_seed, d_signs, lpr, div)
+#define LQ_ROT_DT(DI)                                                                                             \
+    if (bph < kBlk) LQ_ROT(DI, false, -1);                                                                        \
+    else if (dtype == LQ_F16) LQ_ROT(DI, true, LQ_F16);                                                           \
+    else if (dtype == LQ_BF16) LQ_ROT(DI, true, LQ_BF16);                                                         \
+    else LQ_ROT(DI, true, LQ_F32)
+    if (d_dither_seed) { LQ_ROT_DT(true); }
+    else { LQ_ROT_DT(false); }
+#undef LQ_ROT_DT
+#undef LQ_ROT
     return launch_status();
 }
 

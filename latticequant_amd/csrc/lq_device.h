@@ -416,9 +416,27 @@ __host__ __device__ __forceinline__ float div_sqrt_dim(float y, float d, float r
     return q;
 }
 
+// x / s as IEEE fp32 division rounds it, in five operations given
+// r = RN(1 / s), for |x| and s in [2^-60, 2^60] (every intermediate is then a
+// normal number and each remainder x - q s is computed exactly): q0 = RN(x r)
+// lies within 1.5 ulp of x / s, one correction q1 = RN(q0 + RN(x - q0 s) r)
+// within one ulp, and a second correction of a quotient within one ulp with r
+// within half an ulp of 1 / s is correctly rounded (Markstein 1990, IBM J. Res.
+// Dev. 34(1); Muller et al., Handbook of Floating-Point Arithmetic, the
+// theorem on Newton-Raphson based division).  tests/host/div_exact_check.cpp
+// compares it with IEEE division on every fp32 significand of x for the
+// divisors whose reciprocal rounds worst.
+__host__ __device__ __forceinline__ float div_exact(float x, float s, float r) {
+    const float q0 = x * r;
+    const float q1 = __builtin_fmaf(__builtin_fmaf(-q0, s, x), r, q0);
+    return __builtin_fmaf(__builtin_fmaf(-q1, s, x), r, q1);
+}
+
 // div_sqrt_dim of 8 values with one test per row: the three operations when
 // every |y_i| lies in [2^-100, FLT_MAX], else IEEE division for all 8.
-__host__ __device__ __forceinline__ void div_sqrt_dim8(float y[8], float d, float r) {
+// Returns whether every |y_i| lies in [2^-55, 2^55], so that every quotient
+// (d in [f32(sqrt 8), f32(sqrt 512)]) lies in div_exact's range [2^-60, 2^60].
+__host__ __device__ __forceinline__ bool div_sqrt_dim8(float y[8], float d, float r) {
     float lo = __builtin_fabsf(y[0]), hi = lo;
 #pragma unroll
     for (int i = 1; i < 8; i++) {
@@ -436,21 +454,25 @@ __host__ __device__ __forceinline__ void div_sqrt_dim8(float y[8], float d, floa
 #pragma unroll
         for (int i = 0; i < 8; i++) y[i] = y[i] / d;
     }
+    return lo >= 0x1p-55f && hi <= 0x1p55f;
 }
 
-// rcp = RN(1 / div) (the caller's, computed once per launch).
-__device__ __forceinline__ void rht_lanes(float y[8], const float s[8], int part, int lpr, float div, float rcp,
+// rcp = RN(1 / div) (the caller's, computed once per launch).  Returns
+// div_sqrt_dim8's range flag: forward (sign before the transform), every
+// output lies in [2^-60, 2^60].
+__device__ __forceinline__ bool rht_lanes(float y[8], const float s[8], int part, int lpr, float div, float rcp,
                                           bool inverse) {
     if (!inverse) {
 #pragma unroll
         for (int i = 0; i < 8; i++) y[i] = y[i] * s[i];
     }
     fwht_stages(y, part, lpr);
-    div_sqrt_dim8(y, div, rcp);
+    const bool narrow = div_sqrt_dim8(y, div, rcp);
     if (inverse) {
 #pragma unroll
         for (int i = 0; i < 8; i++) y[i] = y[i] * s[i];
     }
+    return narrow;
 }
 
 __device__ __forceinline__ void load_signs8(const float* p, float s[8]) {

@@ -3,7 +3,9 @@ lq_chunk_decode_rht) against the materialised rotation (lq_rht, then the
 plain codec) and the oracle: the same fp32 scales, coset bits and stream
 words, and the same decoded rows in every output dtype.  Cases: head_dim
 128 / 64 / 32, with and without dither, heads whose vector count is not a
-multiple of the 512-vector block (rows and heads cross block boundaries)."""
+multiple of the 512-vector block (rows and heads cross block boundaries),
+heads of fewer than 512 vectors (the quantizer's general launch), and rows
+and heads outside the five-operation division's range (IEEE division)."""
 import numpy as np
 import pytest
 import torch
@@ -24,7 +26,8 @@ def _oracle_rotate(x, layers, kvs, inverse=False):
 
 
 CASES = [((2, 2, 3, 64, 128), True), ((1, 2, 2, 40, 128), True), ((2, 1, 4, 96, 64), False),
-         ((1, 1, 2, 256, 32), True), ((1, 3, 2, 72, 128), False)]
+         ((1, 1, 2, 256, 32), True), ((1, 3, 2, 72, 128), False),
+         ((2, 1, 3, 24, 128), True), ((1, 2, 5, 12, 64), False)]   # heads below 512 vectors
 
 
 @pytest.mark.parametrize("shape,dither", CASES)
@@ -65,6 +68,43 @@ def test_fused_rotation_matches_materialised_and_oracle_gpu(shape, dither):
         want = codec.rotate_rows(wd, signs, inverse=True, out_dtype=dt)
         assert torch.equal(got, want), dt
     np.testing.assert_array_equal(codec.decode_batch(fused, rht_signs=signs)[0].cpu().numpy(), want0)
+
+
+@pytest.mark.parametrize("dither", [True, False])
+def test_fused_rotation_division_fallbacks_gpu(dither):
+    """Rotated rows whose values leave [2^-60, 2^60] (zeros, 1e-20, 1e18) and a
+    head whose (finite) scale exceeds 2^60 (values ~3e18 at 3 bits: at 4 bits
+    every finite scale lies below 2^60) divide by the scale with IEEE division;
+    rows in range use the five-operation form.  Both give the materialised
+    rotation's words and the oracle's."""
+    from latticequant_amd import codec
+    from latticequant_amd.llm import rotated as R
+    C, B, H, T, hd = 1, 1, 3, 64, 128
+    print(f"fallback case dither={dither}", flush=True)
+    g = torch.Generator().manual_seed(77)
+    x = torch.randn(C, B, H, T, hd, generator=g)
+    x[0, 0, 0, 3] = 0.0
+    x[0, 0, 0, 5] = 1e-20 * torch.randn(hd, generator=g)
+    x[0, 0, 0, 9] = 1e18 * torch.randn(hd, generator=g)
+    x[0, 0, 1, 7, :5] = 0.0
+    x[0, 0, 2] *= 3e18
+    layers, kvs = [4], [1]
+    signs = R.chunk_signs(x.shape, layers, kvs).cuda()
+    seeds = [R.default_dither_seed(4, 1)] if dither else None
+    xc = x.cuda()
+    fused, _ = codec.encode_batch(xc, 3, dither_seed=seeds, rht_signs=signs, wide=False)
+    w = codec.rotate_rows(xc, signs, inverse=False)
+    mat, _ = codec.encode_batch(w, 3, dither_seed=seeds, wide=False)
+    s32 = fused.scale32.cpu().numpy()
+    assert np.isfinite(s32).all() and s32[2] > 2.0 ** 60 and s32[0] < 2.0 ** 60, s32
+    assert int(fused.status.max()) == 0 and int(mat.status.max()) == 0
+    assert torch.equal(fused.scale32, mat.scale32)
+    assert torch.equal(fused.coset_bits, mat.coset_bits)
+    nw = int(fused.chunk_words.sum())
+    assert torch.equal(fused.words[:nw], mat.words[:nw])
+    w_or = _oracle_rotate(x.numpy(), layers, kvs)
+    ch = O.compress_chunk(w_or[0], 3, scales_f32=s32, dither_seed=seeds[0] if dither else None)
+    np.testing.assert_array_equal(fused.words[:nw].cpu().numpy().view(np.uint32), ch.bitstream)
 
 
 def test_encode_decode_rotated_use_fused_path_gpu(monkeypatch):
