@@ -84,12 +84,12 @@ __global__ void k_quantize_heads(const void* __restrict__ x, int dtype, int64_t 
 // ---------------------------------------------------------- head scales --
 
 // Partial sums of x^2 per head in double: grid (heads, parts).  ROT: of the
-// forward-rotated rows (lq_scales.h head_sumsq_part).
-template <bool ROT>
+// forward-rotated rows (lq_scales.h head_sumsq_part); LPR > 0: lpr known.
+template <bool ROT, int LPR = 0>
 __global__ void k_head_sumsq(const void* __restrict__ x, int dtype, int64_t vec_per_head, int parts,
                              double* __restrict__ work, const float* __restrict__ signs, int lpr, float rdiv) {
     __shared__ double red[256];
-    head_sumsq_part<ROT>(x, dtype, vec_per_head, parts, blockIdx.x, blockIdx.y, work, red, signs, lpr, rdiv);
+    head_sumsq_part<ROT, LPR>(x, dtype, vec_per_head, parts, blockIdx.x, blockIdx.y, work, red, signs, lpr, rdiv);
 }
 
 __device__ void fastdiv_check(float s, int32_t* word) {
@@ -222,8 +222,10 @@ __device__ __forceinline__ void stage_minmax(const uint4& w, int row16, int n0, 
 // by the scale as IEEE division rounds (div_exact where the row and the scale
 // lie in its range); no dequantised output, at least 5 waves per SIMD.
 // LDT >= 0: the input dtype as a compile-time constant (the lean launches),
-// so no dtype test is kept live across the block loop.
-template <typename SymT, bool DITHER, bool LEAN = false, bool ROT = false, int LDT = -1>
+// so no dtype test is kept live across the block loop.  LPR > 0: the rotation's
+// lanes per row as a compile-time constant, so the butterfly stages are
+// straight-line code (no per-stage branch and register copies).
+template <typename SymT, bool DITHER, bool LEAN = false, bool ROT = false, int LDT = -1, int LPR = 0>
 __global__ __launch_bounds__(kQThreads, ROT ? 5 : (LEAN ? 7 : 1)) void k_chunk_quantize(
     const void* __restrict__ x, int dtype, int64_t n_heads, int64_t bph, int64_t nblk,
     const float* __restrict__ scale32, const int32_t* __restrict__ fastdiv, SymT* __restrict__ sym,
@@ -328,9 +330,10 @@ __global__ __launch_bounds__(kQThreads, ROT ? 5 : (LEAN ? 7 : 1)) void k_chunk_q
                     // multiples of 512, so the lane's place in its row is tid % lpr;
                     // valid is a multiple of lpr, so whole rows are live together
                     float sg[8];
-                    const int part = tid & (lpr - 1);
-                    load_signs8(signs + hq * (8 * (int64_t)lpr) + 8 * part, sg);
-                    const bool narrow = rht_lanes(xv, sg, part, lpr, rdiv, rrcp, false);
+                    const int lw = LPR > 0 ? LPR : lpr;
+                    const int part = tid & (lw - 1);
+                    load_signs8(signs + hq * (8 * (int64_t)lw) + 8 * part, sg);
+                    const bool narrow = rht_lanes(xv, sg, part, lw, rdiv, rrcp, false);
                     if (fast && narrow) {
 #pragma unroll
                         for (int i = 0; i < 8; i++) t[i] = div_exact(xv[i], s, rs);
@@ -601,8 +604,12 @@ int lq_head_scales_rht(const void* d_x, int dtype, int64_t n_chunks, int64_t n_h
     const int64_t H = n_chunks * n_heads;
     const int parts = head_parts(H, bph);
     const float div = (float)sqrt((double)head_dim);
-    hipLaunchKernelGGL(k_head_sumsq<true>, dim3((unsigned)H, parts), dim3(256), 0, s, d_x, dtype, bph, parts, d_work,
-                       d_signs, head_dim / 8, div);
+    if (head_dim == 128)
+        hipLaunchKernelGGL((k_head_sumsq<true, 16>), dim3((unsigned)H, parts), dim3(256), 0, s, d_x, dtype, bph, parts,
+                           d_work, d_signs, 16, div);
+    else
+        hipLaunchKernelGGL((k_head_sumsq<true, 0>), dim3((unsigned)H, parts), dim3(256), 0, s, d_x, dtype, bph, parts,
+                           d_work, d_signs, head_dim / 8, div);
     hipLaunchKernelGGL(k_head_finalize, dim3((unsigned)H), dim3(256), 0, s, d_work, parts, bph * 8, n_heads,
                        d_chunk_bits, (int)LQ_F32, d_sigma2, d_scale32, d_scale16, d_fastdiv);
     return launch_status();
@@ -667,18 +674,22 @@ int lq_chunk_quantize_rht(const void* d_x, int dtype, int64_t n_chunks, int64_t 
     const int64_t wg = n_chunks * ((nblk + kQBlocksPerWG - 1) / kQBlocksPerWG);
     const float div = (float)sqrt((double)head_dim);
     const int lpr = head_dim / 8;
-#define LQ_ROT(DI, LE, DT)                                                                                        \
-    hipLaunchKernelGGL((k_chunk_quantize<int8_t, DI, LE, true, DT>), dim3((unsigned)wg), dim3(kQThreads), 0, s, d_x, \
-                       dtype, n_heads, bph, nblk, d_scale32, nullptr, d_sym, d_coset_bits, d_blk_n1, d_hist, nullptr,  \
-                       d_status, nullptr, (int)LQ_F32, d_dither_seed, d_signs, lpr, div)
+#define LQ_ROT(DI, LE, DT, LP)                                                                                    \
+    hipLaunchKernelGGL((k_chunk_quantize<int8_t, DI, LE, true, DT, LP>), dim3((unsigned)wg), dim3(kQThreads), 0, s,  \
+                       d_x, dtype, n_heads, bph, nblk, d_scale32, nullptr, d_sym, d_coset_bits, d_blk_n1, d_hist,      \
+                       nullptr, d_status, nullptr, (int)LQ_F32, d_dither_seed, d_signs, lpr, div)
+#define LQ_ROT_LP(DI, DT)                                                                                         \
+    if (lpr == 16) LQ_ROT(DI, true, DT, 16);                                                                      \
+    else LQ_ROT(DI, true, DT, 0)
 #define LQ_ROT_DT(DI)                                                                                             \
-    if (bph < kBlk) LQ_ROT(DI, false, -1);                                                                        \
-    else if (dtype == LQ_F16) LQ_ROT(DI, true, LQ_F16);                                                           \
-    else if (dtype == LQ_BF16) LQ_ROT(DI, true, LQ_BF16);                                                         \
-    else LQ_ROT(DI, true, LQ_F32)
+    if (bph < kBlk) LQ_ROT(DI, false, -1, 0);                                                                     \
+    else if (dtype == LQ_F16) { LQ_ROT_LP(DI, LQ_F16); }                                                          \
+    else if (dtype == LQ_BF16) { LQ_ROT_LP(DI, LQ_BF16); }                                                        \
+    else { LQ_ROT_LP(DI, LQ_F32); }
     if (d_dither_seed) { LQ_ROT_DT(true); }
     else { LQ_ROT_DT(false); }
 #undef LQ_ROT_DT
+#undef LQ_ROT_LP
 #undef LQ_ROT
     return launch_status();
 }

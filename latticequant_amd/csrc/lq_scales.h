@@ -38,7 +38,8 @@ __device__ __forceinline__ float sq_vec16(const u32x4 w, bool f16) {
 // row; the parts split on row boundaries), summed exactly like an fp32 input
 // holding w, so the scales equal those of the materialised rotation.
 // One (head h, part p) on a 256-thread workgroup; red: 256 doubles of LDS.
-template <bool ROT>
+// LPR > 0: lpr as a compile-time constant (straight-line butterfly stages).
+template <bool ROT, int LPR = 0>
 __device__ __forceinline__ void head_sumsq_part(const void* __restrict__ x, int dtype, int64_t vec_per_head,
                                                 int parts, int64_t h, int p, double* __restrict__ work, double* red,
                                                 const float* __restrict__ signs, int lpr, float rdiv) {
@@ -53,14 +54,15 @@ __device__ __forceinline__ void head_sumsq_part(const void* __restrict__ x, int 
     if (ROT) {
         // rows are whole within [v0, v1) and lpr divides the block size, so the
         // lanes of a row enter and leave the loop together
-        const int part = (int)(threadIdx.x % lpr);
+        const int lw = LPR > 0 ? LPR : lpr;
+        const int part = (int)(threadIdx.x % lw);
         const float rrcp = 1.0f / rdiv;
         float sg[8];
-        load_signs8(signs + h * (8 * (int64_t)lpr) + 8 * part, sg);
+        load_signs8(signs + h * (8 * (int64_t)lw) + 8 * part, sg);
         for (; v < v1; v += bd) {
             float xv[8];
             load8(x, dtype, h * vec_per_head + v, xv);
-            rht_lanes(xv, sg, part, lpr, rdiv, rrcp, false);
+            rht_lanes(xv, sg, part, lw, rdiv, rrcp, false);
 #pragma unroll
             for (int i = 0; i < 8; i++) acc4[0] += (double)xv[i] * (double)xv[i];
         }
