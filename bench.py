@@ -325,13 +325,15 @@ def bench_c4(dev, steps=5, n_streams=3):
     chunk per (layer, K/V), per-chunk tables, every chunk coded.  Chunks are
     grouped by rate (K on the int16 staging path, V on int8); the groups are
     independent and are dealt to n_streams streams (V groups first: their
-    launches fill the chip while a K group's latency-bound table build and
-    its one host read of the escape shifts run beside them).  K coordinates
-    whose stream alphabet exceeds L = 1024 symbols (the reference's table
-    normalisation never terminates there) are escaped: coarse symbols through
-    the same tables and streams plus raw low bits (a format of this build; the
-    wide path reads the C x 8 shifts back once per batch).  One step = encode
-    every group + decode every group.  B = 4 D + 2 C over all chunks."""
+    launches fill the chip while a K group's latency-bound table build runs
+    beside them).  K coordinates whose stream alphabet exceeds L = 1024
+    symbols (the reference's table normalisation never terminates there) are
+    escaped: coarse symbols through the same tables and streams plus raw low
+    bits (a format of this build).  The escape plan stays on the device; its
+    C x 8 shifts reach the host when a K group's decode asks for them, so
+    every group's encode is queued before the first K decode waits for its
+    plan.  One step = encode every group + decode every group.  B = 4 D + 2 C
+    over all chunks."""
     from latticequant_amd import codec
     from oracle import oracle as O
     ks_h, vs_h, sched, sha = make_c4()
@@ -352,22 +354,34 @@ def bench_c4(dev, steps=5, n_streams=3):
     side = [torch.cuda.Stream(device=dev) for _ in range(n_streams)] if n_streams > 1 else []
     order = sorted(range(len(groups)), key=lambda i: groups[i][2])   # int8 groups first
 
-    def one(i):
+    def enc(i):
         x, r, wide, _ = groups[i]
         encs[i], _ = codec.encode_batch(x, r, exact_size=False, words_out=arenas[i], wide=wide)
+
+    def dec(i):
         codec.decode_batch(encs[i], out=outs[i])
 
     def step():
         if not side:
             for i in order:
-                one(i)
+                enc(i)
+                dec(i)
             return
         main = torch.cuda.current_stream(dev)
         for st in side:
             st.wait_stream(main)
-        for j, i in enumerate(order):   # group i always runs on the same stream
+        # group i always runs on the same stream; an int8 group is decoded
+        # right after its encode, the wide groups only once every encode is
+        # queued (their decode waits on the host for the escape plan)
+        for j, i in enumerate(order):
             with torch.cuda.stream(side[j % len(side)]):
-                one(i)
+                enc(i)
+                if not groups[i][2]:
+                    dec(i)
+        for j, i in enumerate(order):
+            if groups[i][2]:
+                with torch.cuda.stream(side[j % len(side)]):
+                    dec(i)
         for st in side:
             main.wait_stream(st)
 

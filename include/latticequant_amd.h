@@ -30,6 +30,7 @@ extern "C" {
 
 #define LQ_L 1024          /* rANS precision (reference core/gpu_ans.py:44-45) */
 #define LQ_BLK 512         /* vectors per checkpoint block */
+#define LQ_ESC_MAX_SHIFT 7 /* largest escape shift k_j (lq_chunk_escape_plan) */
 #define LQ_SYM_STRIDE 4352 /* symbols per block in the staging layout (8 * LQ_BLK + 2 x 128 padding);
                               bytes: x 1 for int8 symbols, x 2 for the wide (int16) path */
 #define LQ_MAXSYM 1028     /* alphabet capacity of a table: the reference's L = 1024 + 4 guard entries */

@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(_HERE, "liblatticequant_amd.so")
 
 LQ_L = 1024
 LQ_BLK = 512
+LQ_ESC_MAX_SHIFT = 7
 LQ_SYM_STRIDE = 4352
 LQ_MAXSYM = 1028
 LQ_STREAMS = 16

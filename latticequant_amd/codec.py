@@ -68,8 +68,13 @@ class EncodedBatch:
 
     @property
     def escape(self) -> Optional["Escape"]:
-        """Coarse / fine escape of chunks with alphabets beyond L (None: none)."""
-        return self.extra.get("esc")
+        """Coarse / fine escape of chunks with alphabets beyond L (None: none).
+        The wide path plans escapes on the device; the first access reads the
+        plan's shifts back (waiting for the plan, not for the whole encode)."""
+        esc = self.extra.get("esc")
+        if esc is not None and not esc.any():
+            self.extra["esc"] = esc = None
+        return esc
 
     # ---- views ------------------------------------------------------------
     def select(self, c: int) -> "EncodedBatch":
@@ -116,22 +121,49 @@ class EncodedBatch:
         return tab + ck + 2 * self.nblk
 
 
-@dataclass
 class Escape:
     """Coarse / fine escape of a batch (lq_chunk_escape_plan / _split): per
     chunk and coordinate j the shift k_j; symbol s of coordinate j is coded as
     s >> k_j in its stream and its k_j low bits are stored raw in `fine`
     (coordinate j of chunk c: nblk * 16 * k_j words from word off[c * 8 + j],
     vector v's bits at bit v * k_j, least significant first).  A format of this
-    build: the reference never terminates on alphabets beyond L."""
-    k: torch.Tensor        # (C, 8) int32, device
-    off: torch.Tensor      # (C * 8,) int64 word offsets into fine, device
-    fine: torch.Tensor     # (words + 1,) int32, device (one slack word)
-    k_host: np.ndarray     # (C, 8) int32
+    build: the reference never terminates on alphabets beyond L.
+
+    k: (C, 8) int32, device; off: (C * 8,) int64 word offsets into fine,
+    device; fine: int32 words, device (one slack word past the last).  A plan
+    made on the device (`pending`: the pinned copy of the shifts, the event
+    after it, the stream that wrote `fine`, nblk) keeps `fine` at its upper
+    bound until k_host is first read; then a batch with escapes keeps only its
+    words (copied on the writing stream, so after the split that fills them)."""
+
+    def __init__(self, k: torch.Tensor, off: torch.Tensor, fine: torch.Tensor,
+                 k_host: Optional[np.ndarray] = None, pending=None):
+        self.k, self.off, self.fine = k, off, fine
+        self._k_host = k_host
+        self._pending = pending
+        if k_host is None and pending is None:
+            raise ValueError("Escape needs the host shifts or a pending device plan")
+
+    @property
+    def k_host(self) -> np.ndarray:
+        """(C, 8) int32 shifts on the host."""
+        if self._k_host is None:
+            host, event, stream, nblk = self._pending
+            event.synchronize()
+            kh = host.numpy().reshape(-1, 8).astype(np.int32)
+            total = int((16 * nblk * kh.astype(np.int64)).sum())
+            if total and total + 1 < self.fine.numel():
+                with torch.cuda.stream(stream):
+                    self.fine = self.fine[:total + 1].clone()
+            self._k_host, self._pending = kh, None
+        return self._k_host
+
+    def any(self) -> bool:
+        return bool(self.k_host.any())
 
     def select(self, c: int) -> "Escape":
-        return Escape(k=self.k[c:c + 1], off=self.off[8 * c:8 * c + 8], fine=self.fine,
-                      k_host=self.k_host[c:c + 1])
+        kh = self.k_host[c:c + 1]   # first: reading the plan may compact fine
+        return Escape(k=self.k[c:c + 1], off=self.off[8 * c:8 * c + 8], fine=self.fine, k_host=kh)
 
     def fine_bytes(self, nblk: int) -> torch.Tensor:
         """Raw low-bit bytes per chunk, (C,) int64 (host tensor)."""
@@ -139,23 +171,27 @@ class Escape:
 
 
 def _plan_escape(minmax, C, nblk, V, sym, coset_bits, blk_n1, status, dev, s):
-    """Escape plan and split of a wide batch (one host read of the C x 8
-    shifts).  Returns (Escape or None, the coarse per-stream min / max)."""
+    """Escape plan and split of a wide batch, with no host read: the fine-word
+    offsets are an exclusive scan of 16 nblk k_j on the device, the fine
+    buffer has its upper bound (k_j <= LQ_ESC_MAX_SHIFT), and the shifts
+    reach the host through a pinned copy that Escape.k_host waits for.
+    Returns (Escape, the coarse per-stream min / max)."""
     lib = L.lib()
     esc_k = _empty(C * 8, torch.int32, dev)
     mm_c = torch.empty_like(minmax)
     L.check(lib.lq_chunk_escape_plan(minmax.data_ptr(), C, esc_k.data_ptr(), mm_c.data_ptr(), status.data_ptr(), s),
             "lq_chunk_escape_plan")
-    kh = esc_k.view(C, 8).cpu().numpy()
-    if not kh.any():
-        return None, minmax
-    per = (16 * nblk * kh.astype(np.int64)).reshape(-1)
-    off = np.concatenate([[0], np.cumsum(per)[:-1]]).astype(np.int64)
-    fine = _zeros(int(per.sum()) + 1, torch.int32, dev)
-    off_d = torch.from_numpy(off).to(dev)
+    stream = torch.cuda.current_stream(dev)
+    host = torch.empty(C * 8, dtype=torch.int32, pin_memory=True)
+    host.copy_(esc_k, non_blocking=True)
+    event = torch.cuda.Event()
+    event.record(stream)
+    per = esc_k.to(torch.int64) * (16 * nblk)
+    off_d = torch.cumsum(per, 0) - per
+    fine = _empty(C * 8 * 16 * nblk * L.LQ_ESC_MAX_SHIFT + 1, torch.int32, dev)
     L.check(lib.lq_chunk_escape_split(sym.data_ptr(), coset_bits.data_ptr(), blk_n1.data_ptr(), C, V, esc_k.data_ptr(),
                                       off_d.data_ptr(), fine.data_ptr(), s), "lq_chunk_escape_split")
-    return Escape(k=esc_k.view(C, 8), off=off_d, fine=fine, k_host=kh.astype(np.int32)), mm_c
+    return Escape(k=esc_k.view(C, 8), off=off_d, fine=fine, pending=(host, event, stream, nblk)), mm_c
 
 
 def words_bound(n_chunks: int, n_vectors: int) -> int:

@@ -22,7 +22,7 @@ namespace {
 
 inline int launch_status() { return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_LAUNCH; }
 
-constexpr int kMaxShift = 7;   // int16 symbols span < 2^16: k = 7 leaves at most 512 + 5 coarse symbols
+constexpr int kMaxShift = LQ_ESC_MAX_SHIFT;   // int16 symbols span < 2^16: k = 7 leaves at most 512 + 5 coarse symbols
 
 __device__ __forceinline__ int64_t span_after(int mn, int mx, int k) {
     return (int64_t)(mx >> k) - (int64_t)(mn >> k) + 5;
