@@ -161,6 +161,10 @@ class Escape:
     def any(self) -> bool:
         return bool(self.k_host.any())
 
+    def ready(self) -> bool:
+        """The shifts are on the host, or their copy has arrived (non-blocking)."""
+        return self._pending is None or self._pending[1].query()
+
     def select(self, c: int) -> "Escape":
         kh = self.k_host[c:c + 1]   # first: reading the plan may compact fine
         return Escape(k=self.k[c:c + 1], off=self.off[8 * c:8 * c + 8], fine=self.fine, k_host=kh)
@@ -625,7 +629,11 @@ def decode_batch(enc: EncodedBatch, out_dtype: torch.dtype = torch.float16, out:
         out = torch.empty((C,) + tuple(enc.shape), dtype=out_dtype, device=dev)
     if lut_work is None:
         lut_work = _empty(C * L.LQ_STREAMS * L.LQ_L, torch.int32, dev)
-    esc = enc.escape
+    # an escape plan still on its way to the host is not waited for: the
+    # escaped decoder reads the shifts on the device (k_j = 0 decodes plainly)
+    esc = enc.extra.get("esc")
+    if esc is not None and esc.ready():
+        esc = enc.escape
     if rht_signs is not None:
         hd = enc.shape[-1]
         rht_signs = _check_signs(rht_signs, C * enc.n_heads, hd, dev)

@@ -149,3 +149,33 @@ def test_variable_rate_cache_heavy_tailed_gpu():
         chv = O.compress_chunk(v, sched[layer]["V"], scales_f32=cv.encoded.scale32.cpu().numpy())
         np.testing.assert_array_equal(cv.gpu_bitstream.cpu().numpy().view(np.uint32), chv.bitstream)
     assert escaped >= 1 and len(cache._comp_keys[0].chunks) == 1
+
+
+def test_pending_escape_plan_decodes_like_resolved_gpu(monkeypatch):
+    """The wide path's escape plan reaches the host only when first read, and
+    decode_batch does not wait for it: an unread plan takes the escaped
+    decoder, which reads the shifts on the device (a chunk with every k_j = 0
+    decodes plainly).  Both forms give the same rows, for a batch with an
+    escaped chunk and one without; reading the plan trims the fine words to
+    the batch's own."""
+    from latticequant_amd import codec
+    print("pending escape plan", flush=True)
+    # 4 bits: seed 0's widest alphabet is 538 symbols, seed 1's 1130 (escaped);
+    # 3 bits, seed 2: 360 (wide, nothing escaped)
+    x_esc = torch.from_numpy(np.stack([student_k(0), student_k(1)])).cuda()
+    x_plain = torch.from_numpy(student_k(2)[None]).cuda()
+    for x, bits in ((x_esc, 4), (x_plain, 3)):
+        enc, _ = codec.encode_batch(x, bits, exact_size=False, wide=True)
+        monkeypatch.setattr(codec.Escape, "ready", lambda self: False)
+        pend = codec.decode_batch(enc)
+        monkeypatch.undo()
+        bound = enc.extra["esc"].fine.numel()
+        esc = enc.escape   # reads the plan back
+        res = codec.decode_batch(enc)
+        torch.cuda.synchronize()
+        assert torch.equal(pend, res)
+        if esc is None:
+            assert bits == 3
+        else:
+            used = int((16 * enc.nblk * esc.k_host.astype(np.int64)).sum())
+            assert esc.any() and esc.fine.numel() == used + 1 < bound
