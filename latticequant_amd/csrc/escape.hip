@@ -64,14 +64,18 @@ __global__ __launch_bounds__(64) void k_chunk_esc_plan(const int32_t* __restrict
 
 // One workgroup per (block, chunk), one thread per vector of the block: the
 // int16 staging of every escaped coordinate becomes its coarse symbols in
-// place, and the low bits go to the block's 16 k_j words of that coordinate
-// (assembled in LDS, then stored whole).
+// place, and each vector's low bits wait in LDS (one byte per vector and
+// coordinate, k <= 7); then every thread assembles whole fine words -- word t
+// of coordinate j holds bits 32 t .. 32 t + 31 of the coordinate's bit string,
+// vector v's k bits at bit v k -- from the vectors those bits come from, and
+// stores them (no LDS atomics: vectors sharing a word would serialise on
+// its address).  Vectors past the chunk's end contribute zero bits.
 __global__ __launch_bounds__(kBlk) void k_chunk_esc_split(int16_t* __restrict__ sym, const uint8_t* __restrict__ coset_bits,
                                                           const uint32_t* __restrict__ blk_n1, int64_t nblk, int64_t V,
                                                           const int32_t* __restrict__ esc_k,
                                                           const int64_t* __restrict__ fine_off,
                                                           uint32_t* __restrict__ fine) {
-    __shared__ uint32_t fb[8][16 * kMaxShift];
+    __shared__ uint8_t fv[8][kBlk];
     __shared__ uint32_t bm[kBlk / 32];
     const int64_t chunk = blockIdx.y, g = blockIdx.x;
     const int tid = threadIdx.x;
@@ -83,13 +87,12 @@ __global__ __launch_bounds__(kBlk) void k_chunk_esc_split(int16_t* __restrict__ 
         any |= kk[j];
     }
     if (!any) return;   // chunk-uniform
-    for (int i = tid; i < 8 * 16 * kMaxShift; i += kBlk) (&fb[0][0])[i] = 0u;
     if (tid < kBlk / 32) bm[tid] = reinterpret_cast<const uint32_t*>(coset_bits + (chunk * nblk + g) * (kBlk / 8))[tid];
     __syncthreads();
-    const int64_t valid = V - g * kBlk < kBlk ? V - g * kBlk : kBlk;
+    const int valid = (int)(V - g * kBlk < kBlk ? V - g * kBlk : kBlk);
     if (tid < valid) {
         const int n1 = (int)blk_n1[chunk * nblk + g];
-        const int n0 = (int)valid - n1;
+        const int n0 = valid - n1;
         const int w = tid >> 5;
         int below = 0;   // coset-1 vectors of the block before this one
         for (int i = 0; i < w; i++) below += __builtin_popcount(bm[i]);
@@ -104,19 +107,28 @@ __global__ __launch_bounds__(kBlk) void k_chunk_esc_split(int16_t* __restrict__ 
             int16_t* p = blk + sym_pos(c, j, r, n0);
             const int s = *p;
             *p = (int16_t)(s >> k);
-            const uint32_t f = (uint32_t)s & ((1u << k) - 1u);
-            const int bit = tid * k;
-            atomicOr(&fb[j][bit >> 5], f << (bit & 31));
-            if ((bit & 31) + k > 32) atomicOr(&fb[j][(bit >> 5) + 1], f >> (32 - (bit & 31)));
+            fv[j][tid] = (uint8_t)((uint32_t)s & ((1u << k) - 1u));
         }
     }
     __syncthreads();
+    // the block's fine words, coordinates in order: 16 k_j words each
+    int nw = 0;
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
+    for (int j = 0; j < 8; j++) nw += 16 * kk[j];
+    for (int t = tid; t < nw; t += kBlk) {
+        int j = 0, tj = t;
+        while (tj >= 16 * kk[j]) { tj -= 16 * kk[j]; j++; }   // kk[j] > 0 where the loop stops
         const int k = kk[j];
-        if (k == 0) continue;
-        uint32_t* dst = fine + fine_off[chunk * 8 + j] + g * 16 * k;
-        for (int i = tid; i < 16 * k; i += kBlk) dst[i] = fb[j][i];
+        const int b0 = 32 * tj;
+        const int v0 = b0 / k;
+        const int v1 = (b0 + 31) / k < valid - 1 ? (b0 + 31) / k : valid - 1;
+        uint32_t word = 0u;
+        for (int v = v0; v <= v1; v++) {
+            const int sh = v * k - b0;   // position of vector v's lowest bit in the word
+            const uint32_t f = fv[j][v];
+            word |= sh >= 0 ? f << sh : f >> -sh;
+        }
+        fine[fine_off[chunk * 8 + j] + g * 16 * k + tj] = word;
     }
 }
 
