@@ -129,8 +129,20 @@ int lq_chunk_quantize(const void *d_x, int dtype, int64_t n_chunks, int64_t n_he
                       uint8_t *d_coset_bits, uint32_t *d_blk_n1, uint32_t *d_hist, int32_t *d_status,
                       void *d_deq, int deq_dtype, const int64_t *d_dither_seed, hipStream_t s);
 
+/* Small updates without entropy coding (a decode step's K / V): the scales of
+ * lq_head_scales and the dequantised rows q * scale32 of lq_chunk_quantize
+ * (d_deq, x's dtype and layout) in one call.  d_work: scratch of
+ * lq_quantize_deq_workspace(n_chunks, n_heads, bph) bytes (-1: invalid
+ * geometry), 256-byte aligned, contents need not be cleared; calls sharing it
+ * must be ordered on one stream.  Replaces llm/compressed_kv_cache.py:188-221
+ * for the eval_only_no_entropy path and the quantize half of update(). */
+int64_t lq_quantize_deq_workspace(int64_t n_chunks, int64_t n_heads, int64_t bph);
+int lq_quantize_deq(const void *d_x, int dtype, int64_t n_chunks, int64_t n_heads, int64_t bph,
+                    const int32_t *d_chunk_bits, void *d_work, float *d_sigma2, float *d_scale32,
+                    uint16_t *d_scale16, void *d_deq, hipStream_t s);
+
 /* Rotated rows: lq_chunk_quantize of w = RHT(x) (as lq_head_scales_rht), the
- * rotation in registers, IEEE division by scale32, optional dither; no
+ * rotation in registers, the scale division rounded as IEEE division, optional dither; no
  * dequantised output.  Same outputs and layouts as lq_chunk_quantize on a
  * materialised fp32 rotation.  Replaces core/pipeline.py:100-108 +
  * llm/perplexity_eval.py:35-61 feeding llm/compressed_kv_cache.py:199-231,270. */

@@ -41,6 +41,8 @@ _SIGS = {
     "lq_e8_to_symbols": ([_P, _I64, _P, _P, _P], _INT),
     "lq_symbols_to_e8": ([_P, _P, _I64, _P, _P], _INT),
     "lq_head_scales": ([_P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P], _INT),
+    "lq_quantize_deq_workspace": ([_I64, _I64, _I64], _I64),
+    "lq_quantize_deq": ([_P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P], _INT),
     "lq_scale_fastdiv": ([_P, _I64, _INT, _P, _P], _INT),
     "lq_chunk_quantize": ([_P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _INT, _P, _P], _INT),
     "lq_chunk_tables": ([_P, _I64, _P, _P, _P], _INT),

@@ -346,6 +346,46 @@ def quantize_batch(x: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None
     return (scale32, scale16, deq, sigma2) if with_sigma2 else (scale32, scale16, deq)
 
 
+class QuantizeScratch:
+    """Device scratch of quantize_deq, grown on demand and reused: calls that
+    share one must run on one stream (in order)."""
+
+    def __init__(self):
+        self.buf: Optional[torch.Tensor] = None
+
+    def get(self, C: int, nh: int, bph: int, dev) -> torch.Tensor:
+        n = int(L.lib().lq_quantize_deq_workspace(C, nh, bph))
+        if n < 0:
+            raise ValueError("invalid chunk geometry")
+        b = self.buf
+        if b is None or b.device != torch.device(dev) or b.numel() < n:
+            self.buf = b = torch.empty(max(n, 2 * b.numel() if b is not None else 0), dtype=torch.uint8, device=dev)
+        return b
+
+
+def quantize_deq(x: torch.Tensor, bits, scratch: QuantizeScratch):
+    """quantize_batch(x, bits, with_sigma2=True) in one native call
+    (lq_quantize_deq): (scale32, scale16, deq, sigma2), with the symbol
+    staging and the other by-products in the caller's scratch, so a decode
+    step's update allocates only its outputs."""
+    lib = L.lib()
+    x = _check_input(x)
+    C, B, H, T, hd = x.shape
+    dev = x.device
+    nh, bph = B * H, T * hd // 8
+    work = scratch.get(C, nh, bph, dev)
+    n = C * nh
+    sc = torch.empty(3 * n, dtype=torch.float32, device=dev)   # sigma2 | scale32 | scale16 (fp16, front half)
+    sigma2, scale32 = sc[:n], sc[n:2 * n]
+    scale16 = sc[2 * n:].view(torch.float16)[:n]
+    deq = torch.empty_like(x)
+    bits_t = _bits_tensor(bits, C, dev)
+    L.check(lib.lq_quantize_deq(x.data_ptr(), L.dtype_code(x.dtype), C, nh, bph, bits_t.data_ptr(), work.data_ptr(),
+                                sigma2.data_ptr(), scale32.data_ptr(), scale16.data_ptr(), deq.data_ptr(),
+                                L.stream_ptr(dev)), "lq_quantize_deq")
+    return scale32, scale16, deq, sigma2
+
+
 def quantize_points(t: torch.Tensor, bits, scale32: Optional[torch.Tensor] = None):
     """Lattice points of one (B, H, T, hd) tensor as _compress_tensor computes
     them (x / scale[head] -> E8).  Returns (q (B*H*T*hd/8, 8) fp32, scale32, scale16)."""

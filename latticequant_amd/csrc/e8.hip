@@ -593,6 +593,41 @@ int lq_head_scales(const void* d_x, int dtype, int64_t n_chunks, int64_t n_heads
     return launch_status();
 }
 
+// Small updates without entropy coding: lq_head_scales, then the quantizer
+// with the dequantised output; its symbol staging, bitmap, counts, histogram
+// and status land in the caller's scratch and are not read (the histogram
+// and status words need no clearing: they are only added to).
+static inline int64_t qd_align(int64_t b) { return (b + 255) / 256 * 256; }
+
+int64_t lq_quantize_deq_workspace(int64_t n_chunks, int64_t n_heads, int64_t bph) {
+    if (n_chunks <= 0 || n_heads <= 0 || bph <= 0 || bph > kMaxBph) return -1;
+    const int64_t H = n_chunks * n_heads, nblk = (n_heads * bph + kBlk - 1) / kBlk;
+    return qd_align((4096 + H) * 8) + qd_align(H * 4) + qd_align(n_chunks * nblk * kSymStride) +
+           qd_align(n_chunks * nblk * (kBlk / 8)) + qd_align(n_chunks * nblk * 4) +
+           qd_align(n_chunks * LQ_STREAMS * 256 * 4) + qd_align(n_chunks * 4);
+}
+
+int lq_quantize_deq(const void* d_x, int dtype, int64_t n_chunks, int64_t n_heads, int64_t bph,
+                    const int32_t* d_chunk_bits, void* d_work, float* d_sigma2, float* d_scale32,
+                    uint16_t* d_scale16, void* d_deq, hipStream_t s) {
+    if (!d_x || !d_chunk_bits || !d_work || !d_sigma2 || !d_scale32 || !d_scale16 || !d_deq) return LQ_ERR_ARG;
+    if (lq_quantize_deq_workspace(n_chunks, n_heads, bph) < 0 || dtype < 0 || dtype > 2) return LQ_ERR_ARG;
+    const int64_t H = n_chunks * n_heads, nblk = (n_heads * bph + kBlk - 1) / kBlk;
+    char* p = static_cast<char*>(d_work);
+    double* work = reinterpret_cast<double*>(p);             p += qd_align((4096 + H) * 8);
+    int32_t* fastdiv = reinterpret_cast<int32_t*>(p);        p += qd_align(H * 4);
+    int8_t* sym = reinterpret_cast<int8_t*>(p);              p += qd_align(n_chunks * nblk * kSymStride);
+    uint8_t* coset = reinterpret_cast<uint8_t*>(p);          p += qd_align(n_chunks * nblk * (kBlk / 8));
+    uint32_t* n1 = reinterpret_cast<uint32_t*>(p);           p += qd_align(n_chunks * nblk * 4);
+    uint32_t* hist = reinterpret_cast<uint32_t*>(p);         p += qd_align(n_chunks * LQ_STREAMS * 256 * 4);
+    int32_t* status = reinterpret_cast<int32_t*>(p);
+    const int rc = lq_head_scales(d_x, dtype, n_chunks, n_heads, bph, d_chunk_bits, work, d_sigma2, d_scale32,
+                                  d_scale16, fastdiv, s);
+    if (rc != LQ_OK) return rc;
+    return lq_chunk_quantize(d_x, dtype, n_chunks, n_heads, bph, d_scale32, fastdiv, sym, coset, n1, hist, status,
+                             d_deq, dtype, nullptr, s);
+}
+
 // Rotated rows (head_dim a power of two in [8, 128], bph a multiple of
 // head_dim / 8): the scales of w = RHT(x) without materialising w; the
 // fast-division flags are 0 (w is fp32).

@@ -341,6 +341,8 @@ class CompressedKVCache(DynamicCache):
         self._model_dtype = None
         self._pending: list = []   # (PendingEncode, chunks) written without host syncs, not yet settled
         self._groups: dict = {}    # (shape, dtype, device) -> open _DeferredGroup of small updates
+        self._qscratch = codec.QuantizeScratch()   # small updates' quantizer scratch (the model's stream)
+        self._last_layer = -1      # layer of the previous update (a smaller or equal one starts a step)
 
     # -- compression ----------------------------------------------------
     def _compress_many(self, tensors: List[torch.Tensor], bits=None):
@@ -366,7 +368,7 @@ class CompressedKVCache(DynamicCache):
         n_vectors = n_heads * bph
         pend = None
         if not self.eval_only_no_entropy and n_vectors <= self.DEFER_MAX_VECTORS:
-            scale32, scale16, deq, sigma2 = codec.quantize_batch(x, bits, with_sigma2=True)
+            scale32, scale16, deq, sigma2 = codec.quantize_deq(x, bits, self._qscratch)
             key = (tuple(x.shape[1:]), x.dtype, x.device)
             grp = self._groups.get(key)
             if grp is None or grp.full(self.DEFER_CHUNKS):
@@ -474,7 +476,11 @@ class CompressedKVCache(DynamicCache):
         device = key_states.device
         if self._model_dtype is None:
             self._model_dtype = key_states.dtype
-        self._settle_ready()
+        # once per step (the layer index stops increasing when a new forward
+        # starts): settle the batches whose read-back has arrived
+        if layer_idx <= self._last_layer:
+            self._settle_ready()
+        self._last_layer = layer_idx
         bk, bv = self._layer_bits(layer_idx)
         if key_states.shape == value_states.shape:
             (comp_k, k_new), (comp_v, v_new) = self._compress_many([key_states, value_states],

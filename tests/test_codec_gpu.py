@@ -206,3 +206,29 @@ def test_long_stream_tiled_scan_vs_oracle_gpu():
     nb = enc.stream_nbits.cpu().numpy()
     assert (np.diff(off, axis=1) >= 0).all() and (off[:, 0] == 0).all() and (off[:, -1] <= nb).all()
     np.testing.assert_array_equal(codec.decode_batch(enc)[0].cpu().numpy(), O.decompress_chunk(ch))
+
+
+def test_quantize_deq_matches_quantize_batch_gpu():
+    """lq_quantize_deq (the scales and the dequantised rows of a small update
+    in one call, by-products in the caller's scratch) returns what
+    quantize_batch returns, over calls in a row that share one scratch (the
+    later ones smaller, so stale scratch is read back only if the kernel
+    wrongly depends on it), fp16 / bf16 / fp32, per-chunk rates, and the
+    dequantised rows equal the oracle's."""
+    codec, _ = _lq()
+    sc = codec.QuantizeScratch()
+    cases = [((2, 1, 8, 40, 128), torch.float16, 4), ((2, 1, 8, 1, 128), torch.float16, [3, 5]),
+             ((2, 2, 4, 3, 64), torch.bfloat16, 4), ((1, 1, 2, 1, 128), torch.float32, 5)]
+    for shape, dt, bits in cases:
+        print(f"case {shape} {dt} {bits}", flush=True)
+        x = torch.randn(*shape, generator=torch.Generator().manual_seed(sum(shape))).mul(3.0).to(dt).cuda()
+        got = codec.quantize_deq(x, bits, sc)
+        want = codec.quantize_batch(x, bits, with_sigma2=True)
+        for g, w, name in zip(got, want, ("scale32", "scale16", "deq", "sigma2")):
+            assert torch.equal(g, w), name
+    # the oracle's dequantised rows for the last fp16 case
+    x = torch.randn(2, 1, 8, 1, 128, generator=torch.Generator().manual_seed(3)).half()
+    s32, _, deq, _ = codec.quantize_deq(x.cuda(), 4, sc)
+    for c in range(2):
+        ch = O.compress_chunk(x[c].numpy(), 4, scales_f32=s32.view(2, -1)[c].cpu().numpy())
+        np.testing.assert_array_equal(deq[c].cpu().numpy(), ch.decompressed)
