@@ -320,6 +320,21 @@ def make_c4():
     return ks, vs, sched, h.hexdigest()
 
 
+_SIDE_STREAMS = []
+
+
+def side_streams(dev, n):
+    """The first n side streams of the process (default priority), created
+    once and shared by every leg.  HIP places a process's streams on its
+    hardware queues (4 per process on these boxes) in creation order, so a leg
+    that creates fresh streams after another leg's may find two of them on
+    one queue, serialised; reusing the same streams keeps C4's three side
+    streams on distinct queues whatever ran before."""
+    while len(_SIDE_STREAMS) < n:
+        _SIDE_STREAMS.append(torch.cuda.Stream(device=dev))
+    return _SIDE_STREAMS[:n]
+
+
 def bench_c4(dev, steps=5, n_streams=3):
     """C4: the 28-layer Qwen2.5-7B-shaped cache at its 3/4/5-bit schedule, one
     chunk per (layer, K/V), per-chunk tables, every chunk coded.  Chunks are
@@ -351,7 +366,7 @@ def bench_c4(dev, steps=5, n_streams=3):
     arenas = [torch.empty(codec.words_bound(g[0].shape[0], g[0][0].numel() // 8), dtype=torch.int32, device=dev)
               for g in groups]
     encs = [None] * len(groups)
-    side = [torch.cuda.Stream(device=dev) for _ in range(n_streams)] if n_streams > 1 else []
+    side = side_streams(dev, n_streams) if n_streams > 1 else []
     order = sorted(range(len(groups)), key=lambda i: groups[i][2])   # int8 groups first
 
     def enc(i):
@@ -882,7 +897,7 @@ def main():
     arenas = [torch.empty(bound, dtype=torch.int32, device=dev) for _ in groups]
     out = torch.empty_like(x)
     NS = max(1, args.streams)
-    streams = [torch.cuda.Stream(device=dev) for _ in range(NS)]   # default priority
+    streams = side_streams(dev, NS)
     luts = [torch.empty(G * L.LQ_STREAMS * L.LQ_L, dtype=torch.int32, device=dev) for _ in range(NS)]
     encs = [None] * len(groups)
 
