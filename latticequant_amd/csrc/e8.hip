@@ -333,7 +333,9 @@ __global__ __launch_bounds__(kQThreads, ROT ? 5 : (LEAN ? 7 : 1)) void k_chunk_q
                     const int lw = LPR > 0 ? LPR : lpr;
                     const int part = tid & (lw - 1);
                     load_signs8(signs + hq * (8 * (int64_t)lw) + 8 * part, sg);
-                    const bool narrow = rht_lanes(xv, sg, part, lw, rdiv, rrcp, false);
+                    // fp16 rows: no range test (every quotient is in range; the
+                    // sign of a zero t does not change its lattice point)
+                    const bool narrow = rht_lanes<LDT == LQ_F16>(xv, sg, part, lw, rdiv, rrcp, false);
                     if (fast && narrow) {
 #pragma unroll
                         for (int i = 0; i < 8; i++) t[i] = div_exact(xv[i], s, rs);

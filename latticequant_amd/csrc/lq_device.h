@@ -436,7 +436,28 @@ __host__ __device__ __forceinline__ float div_exact(float x, float s, float r) {
 // every |y_i| lies in [2^-100, FLT_MAX], else IEEE division for all 8.
 // Returns whether every |y_i| lies in [2^-55, 2^55], so that every quotient
 // (d in [f32(sqrt 8), f32(sqrt 512)]) lies in div_exact's range [2^-60, 2^60].
+//
+// F16IN: the rows were fp16 before the transform, so no test is made.  Every
+// fp16 value is an integer multiple of 2^-24 below 2^16 in magnitude; sums,
+// differences and sign flips of such values keep every fp32 intermediate a
+// multiple of 2^-24 (below 1 such a value is exactly representable, above 1
+// the rounding grid is coarser than 2^-24), and 128 of them stay below 2^24.
+// So y is 0 or |y| in [2^-24, 2^24]: the three operations are exact, the
+// quotients lie in [2^-29, 2^23] inside div_exact's range, and only y = -0
+// comes out +0 (IEEE gives -0).  The callers that take F16IN only square the
+// quotient or quantize it (E8 rounds +-0 and +-0 + d alike), so the sign of a
+// zero never reaches their outputs.
+template <bool F16IN = false>
 __host__ __device__ __forceinline__ bool div_sqrt_dim8(float y[8], float d, float r) {
+    if constexpr (F16IN) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float q0 = y[i] * r;
+            const float e = __builtin_fmaf(-q0, d, y[i]);
+            y[i] = __builtin_fmaf(e, r, q0);
+        }
+        return true;
+    }
     float lo = __builtin_fabsf(y[0]), hi = lo;
 #pragma unroll
     for (int i = 1; i < 8; i++) {
@@ -459,7 +480,9 @@ __host__ __device__ __forceinline__ bool div_sqrt_dim8(float y[8], float d, floa
 
 // rcp = RN(1 / div) (the caller's, computed once per launch).  Returns
 // div_sqrt_dim8's range flag: forward (sign before the transform), every
-// output lies in [2^-60, 2^60].
+// output lies in [2^-60, 2^60].  F16IN: as div_sqrt_dim8 (fp16 rows, the
+// sign of a zero output unspecified).
+template <bool F16IN = false>
 __device__ __forceinline__ bool rht_lanes(float y[8], const float s[8], int part, int lpr, float div, float rcp,
                                           bool inverse) {
     if (!inverse) {
@@ -467,7 +490,7 @@ __device__ __forceinline__ bool rht_lanes(float y[8], const float s[8], int part
         for (int i = 0; i < 8; i++) y[i] = y[i] * s[i];
     }
     fwht_stages(y, part, lpr);
-    const bool narrow = div_sqrt_dim8(y, div, rcp);
+    const bool narrow = div_sqrt_dim8<F16IN>(y, div, rcp);
     if (inverse) {
 #pragma unroll
         for (int i = 0; i < 8; i++) y[i] = y[i] * s[i];

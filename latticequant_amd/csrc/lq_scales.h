@@ -59,12 +59,22 @@ __device__ __forceinline__ void head_sumsq_part(const void* __restrict__ x, int 
         const float rrcp = 1.0f / rdiv;
         float sg[8];
         load_signs8(signs + h * (8 * (int64_t)lw) + 8 * part, sg);
-        for (; v < v1; v += bd) {
-            float xv[8];
-            load8(x, dtype, h * vec_per_head + v, xv);
-            rht_lanes(xv, sg, part, lw, rdiv, rrcp, false);
+        if (dtype == LQ_F16) {   // no range test: zero's sign does not change its square
+            for (; v < v1; v += bd) {
+                float xv[8];
+                load8(x, LQ_F16, h * vec_per_head + v, xv);
+                rht_lanes<true>(xv, sg, part, lw, rdiv, rrcp, false);
 #pragma unroll
-            for (int i = 0; i < 8; i++) acc4[0] += (double)xv[i] * (double)xv[i];
+                for (int i = 0; i < 8; i++) acc4[0] += (double)xv[i] * (double)xv[i];
+            }
+        } else {
+            for (; v < v1; v += bd) {
+                float xv[8];
+                load8(x, dtype, h * vec_per_head + v, xv);
+                rht_lanes(xv, sg, part, lw, rdiv, rrcp, false);
+#pragma unroll
+                for (int i = 0; i < 8; i++) acc4[0] += (double)xv[i] * (double)xv[i];
+            }
         }
     } else if (dtype == LQ_F32) {   // fp32 squares are not exact: keep every product in fp64
         for (; v < v1; v += bd) {

@@ -372,3 +372,42 @@ def test_escape_round_trip_and_minimal_shift(seed, bits):
     plain = O.compress_chunk(k, bits, scales_f32=s32, escape=False) if not ks.any() else None
     if plain is not None:   # no escape needed: the reference's format, word for word
         assert ch.esc_k is None and np.array_equal(ch.bitstream, plain.bitstream)
+
+
+def test_fp16_rows_keep_the_2pow24_grid_through_the_rotation():
+    """The rotated kernels skip the range test of the division by f32(sqrt d)
+    for fp16 rows because every value of the transform then lies on the 2^-24
+    grid, below 2^24 in magnitude: zero, or in [2^-24, 2^24], where the
+    three-operation division is exact.  Each butterfly stage of the
+    reference's fp32 transform (core/pipeline.py:49-69) is replayed here on
+    fp16 rows of extreme values (subnormals, signed zeros, +-65504) and
+    random ones, and every intermediate is checked against that grid."""
+    rng = np.random.default_rng(11)
+    for d in (8, 32, 128, 512):
+        rows = [np.clip(rng.standard_normal(d) * s, -65504.0, 65504.0) for s in (1e-7, 1e-3, 1.0, 300.0, 6e4)]
+        rows += [np.full(d, 2.0 ** -24), np.zeros(d), -np.zeros(d), np.full(d, 65504.0),
+                 np.where(np.arange(d) % 2, 65504.0, -65504.0), np.where(np.arange(d) % 3, 2.0 ** -24, -0.0)]
+        x = np.stack(rows).astype(np.float16).astype(np.float32)
+        sg = np.where(rng.random(d) < 0.5, -1.0, 1.0).astype(np.float32)
+        y = (x * sg).astype(np.float32)
+        h = 1
+        while h < d:
+            y = y.reshape(-1, d // (2 * h), 2, h)
+            a, b = y[:, :, 0, :].copy(), y[:, :, 1, :].copy()
+            y[:, :, 0, :] = a + b
+            y[:, :, 1, :] = a - b
+            y = y.reshape(-1, d)
+            k = y.astype(np.float64) * 2.0 ** 24
+            assert np.array_equal(k, np.round(k)), (d, h)
+            assert np.abs(y).max() < 2.0 ** 24
+            nz = np.abs(y[y != 0])
+            assert nz.size == 0 or nz.min() >= 2.0 ** -24
+            h *= 2
+        # the division the kernels skip the test for equals IEEE division there (but the sign of zero)
+        dd = np.float32(np.sqrt(d))
+        r = np.float32(1.0) / dd
+        q0 = (y * r).astype(np.float32)
+        e = (y.astype(np.float64) - q0.astype(np.float64) * np.float64(dd)).astype(np.float32)   # exact: fma
+        q = (q0.astype(np.float64) + e.astype(np.float64) * np.float64(r)).astype(np.float32)    # one rounding
+        want = (y / dd).astype(np.float32)
+        assert np.array_equal(q, want)   # -0 and +0 compare equal

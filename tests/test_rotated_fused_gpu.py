@@ -133,3 +133,40 @@ def test_encode_decode_rotated_use_fused_path_gpu(monkeypatch):
     assert calls   # the reconstruction path materialises the rotation
     monkeypatch.undo()
     assert torch.equal(R.decode_rotated(enc), y)
+
+
+@pytest.mark.parametrize("dither", [True, False])
+def test_fused_rotation_fp16_extremes_gpu(dither):
+    """fp16 rows take the rotation without the division's range test (their
+    transform stays on the 2^-24 grid): rows of zeros and negative zeros,
+    fp16 subnormals, +-65504 and ordinary rows give the materialised
+    rotation's scales, coset bits and words, and the oracle's."""
+    from latticequant_amd import codec
+    from latticequant_amd.llm import rotated as R
+    C, B, H, T, hd = 1, 1, 2, 64, 128
+    print(f"fp16 extremes dither={dither}", flush=True)
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(C, B, H, T, hd, generator=g)
+    x[0, 0, 0, 0] = 0.0
+    x[0, 0, 0, 1] = -0.0
+    x[0, 0, 0, 2, ::2] = -0.0
+    x[0, 0, 0, 3] = 2.0 ** -24
+    x[0, 0, 0, 4] = torch.where(torch.arange(hd) % 3 == 0, torch.tensor(-(2.0 ** -24)), torch.tensor(2.0 ** -23))
+    x[0, 0, 1, 5] = 65504.0
+    x[0, 0, 1, 6] = torch.where(torch.arange(hd) % 2 == 0, torch.tensor(65504.0), torch.tensor(-65504.0))
+    x = x.half()
+    layers, kvs = [2], [0]
+    signs = R.chunk_signs(x.shape, layers, kvs).cuda()
+    seeds = [R.default_dither_seed(2, 0)] if dither else None
+    xc = x.cuda()
+    fused, _ = codec.encode_batch(xc, 4, dither_seed=seeds, rht_signs=signs, wide=False)
+    w = codec.rotate_rows(xc, signs, inverse=False)
+    mat, _ = codec.encode_batch(w, 4, dither_seed=seeds, wide=False)
+    assert int(fused.status.max()) == 0
+    assert torch.equal(fused.scale32, mat.scale32)
+    assert torch.equal(fused.coset_bits, mat.coset_bits)
+    nw = int(fused.chunk_words.sum())
+    assert torch.equal(fused.words[:nw], mat.words[:nw])
+    w_or = _oracle_rotate(x.float().numpy(), layers, kvs)
+    ch = O.compress_chunk(w_or[0], 4, scales_f32=fused.scale32.cpu().numpy(), dither_seed=seeds[0] if dither else None)
+    np.testing.assert_array_equal(fused.words[:nw].cpu().numpy().view(np.uint32), ch.bitstream)
