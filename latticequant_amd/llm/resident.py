@@ -51,16 +51,27 @@ class ResidentKV:
         cap = exc_cap if exc_cap is not None else max(256, n_heads * nb * 4)
         self.exc = torch.zeros(cap * 8, dtype=torch.int16, device=dev)
         self.n_tokens = 0
+        # exception count as the host knows it without waiting: a count read
+        # back earlier (pinned copy + event), the vectors appended after it
+        # (each may add one exception), and the newest read still in flight
+        self._exc_known = 0
+        self._exc_since = 0
+        self._exc_read = None   # (pinned count, event, vectors appended after its snapshot)
+        self._st = None         # the ctypes view of the buffers, rebuilt when one is reallocated
 
     @property
     def exc_cap(self) -> int:
         return self.exc.numel() // 8
 
     def struct(self) -> L.Resident:
-        return L.Resident(a=self.a.data_ptr(), b=self.b.data_ptr(), mask=self.mask.data_ptr(),
-                          meta=self.meta.data_ptr(), exc=self.exc.data_ptr(), scale=self.scale.data_ptr(),
-                          n_exc=self.n_exc.data_ptr(), status=self.status.data_ptr(), n_heads=self.n_heads,
-                          cap_blocks=self.cap_blocks, exc_cap=self.exc_cap)
+        """The buffers as the C ABI's lq_resident (cached: the pointers and
+        capacities change only when reserve() or the exception list grows)."""
+        if self._st is None:
+            self._st = L.Resident(a=self.a.data_ptr(), b=self.b.data_ptr(), mask=self.mask.data_ptr(),
+                                  meta=self.meta.data_ptr(), exc=self.exc.data_ptr(), scale=self.scale.data_ptr(),
+                                  n_exc=self.n_exc.data_ptr(), status=self.status.data_ptr(), n_heads=self.n_heads,
+                                  cap_blocks=self.cap_blocks, exc_cap=self.exc_cap)
+        return self._st
 
     def nbytes(self) -> int:
         """Bytes a decode step reads per token range: records, masks, bases, scales, exceptions in use."""
@@ -86,12 +97,20 @@ class ResidentKV:
         self.meta = grow(self.meta, 4)
         self.scale = grow(self.scale, RB)
         self.cap_blocks = nb
+        self._st = None
+
+    # appends of at most this many vectors run without a host read: the
+    # exception list is grown (device copy) whenever the host's upper bound of
+    # the count could pass its capacity; larger appends (a prefill) read the
+    # count back instead, so that the list does not grow to the bound
+    ASYNC_MAX_VECTORS = 1 << 14
 
     def append(self, x: torch.Tensor, scale32: torch.Tensor, scale16: torch.Tensor) -> None:
         """Quantize x (B, H, T, 128) with the per-head scales of its chunk
         (B*H of each; the points are those the chunk codec codes with the same
-        scale32) and append it: T must be a multiple of 16.  Grows the
-        exception list if needed (one host read of the exception count)."""
+        scale32) and append it: T must be a multiple of 16.  Small appends (a
+        decode step's flush) make no host read; larger ones grow the exception
+        list to its exact need (one or two host reads of the count)."""
         if x.dim() != 4 or x.shape[3] != HD:
             raise ValueError("x must be (B, H, T, 128)")
         B, H, T, _ = x.shape
@@ -111,23 +130,53 @@ class ResidentKV:
             raise ValueError("one scale per head expected")
         work = torch.empty(int(lib.lq_resident_workspace(self.n_heads, T)), dtype=torch.uint8, device=self.device)
         blk0 = self.n_tokens // RB
-        n0 = int(self.n_exc.item())
+        n_new = self.n_heads * T * (HD // 8)   # vectors appended: each can be one exception
+
+        def launch():
+            st = self.struct()
+            L.check(lib.lq_resident_quantize(xc.data_ptr(), L.dtype_code(xc.dtype), self.n_heads, T,
+                                             s32.data_ptr(), s16.data_ptr(), ctypes.addressof(st), 0, blk0,
+                                             work.data_ptr(), L.stream_ptr(self.device)), "lq_resident_quantize")
+
         with torch.cuda.device(self.device):
-            for attempt in range(2):
-                st = self.struct()
-                L.check(lib.lq_resident_quantize(xc.data_ptr(), L.dtype_code(xc.dtype), self.n_heads, T,
-                                                 s32.data_ptr(), s16.data_ptr(), ctypes.addressof(st), 0, blk0,
-                                                 work.data_ptr(), L.stream_ptr(self.device)), "lq_resident_quantize")
-                n1 = int(self.n_exc.item())
-                if n1 <= self.exc_cap:
-                    break
-                # grow the exception list to the exact need and redo this append
-                grown = torch.zeros(max(n1, 2 * self.exc_cap) * 8, dtype=torch.int16, device=self.device)
-                grown[:n0 * 8] = self.exc[:n0 * 8]
-                self.exc = grown
-                self.n_exc.fill_(n0)
-                self.status.zero_()
+            if n_new <= self.ASYNC_MAX_VECTORS:
+                if self._exc_read is not None and self._exc_read[1].query():
+                    host, _, after = self._exc_read
+                    self._exc_known, self._exc_since, self._exc_read = int(host[0]), after, None
+                need = self._exc_known + self._exc_since + n_new
+                if need > self.exc_cap:
+                    self._grow_exc(max(2 * self.exc_cap, need), self.exc_cap)
+                launch()
+                self._exc_since += n_new
+                if self._exc_read is not None:
+                    host, ev, after = self._exc_read
+                    self._exc_read = (host, ev, after + n_new)
+                else:
+                    host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+                    host.copy_(self.n_exc, non_blocking=True)
+                    ev = torch.cuda.Event()
+                    ev.record(torch.cuda.current_stream(self.device))
+                    self._exc_read = (host, ev, 0)
+            else:
+                n0 = int(self.n_exc.item())
+                for attempt in range(2):
+                    launch()
+                    n1 = int(self.n_exc.item())
+                    if n1 <= self.exc_cap:
+                        break
+                    # grow the exception list to the exact need and redo this append
+                    self._grow_exc(max(n1, 2 * self.exc_cap), n0)
+                    self.n_exc.fill_(n0)
+                    self.status.zero_()
+                self._exc_known, self._exc_since, self._exc_read = n1, 0, None
         self.n_tokens += T
+
+    def _grow_exc(self, cap: int, keep: int) -> None:
+        """A longer exception list holding the first `keep` entries."""
+        grown = torch.zeros(cap * 8, dtype=torch.int16, device=self.device)
+        grown[:keep * 8] = self.exc[:keep * 8]
+        self.exc = grown
+        self._st = None
 
     def dequant(self, out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
         """(n_heads, n_tokens, 128): lattice point times the stored fp16 scale,
@@ -204,8 +253,14 @@ def resident_decode_attention(k: ResidentKV, v: ResidentKV, q: torch.Tensor, tai
     if out is None:
         out = torch.empty(B, Hq, 1, HD, dtype=torch.float16, device=dev)
     ks, vs = k.struct(), v.struct()
-    with torch.cuda.device(dev):
+
+    def call():
         L.check(lib.lq_resident_attention(ctypes.addressof(ks), ctypes.addressof(vs), tp, qc.data_ptr(), group,
                                           L.ptr(pk), L.ptr(pv), tt, work.data_ptr(), out.data_ptr(),
                                           L.stream_ptr(dev)), "lq_resident_attention")
+    if dev.index == torch.cuda.current_device():
+        call()
+    else:
+        with torch.cuda.device(dev):
+            call()
     return out

@@ -75,15 +75,15 @@ class ResidentKVCache(DynamicCache):
         xk, xv = tk[:, :, :n].contiguous(), tv[:, :, :n].contiguous()
         # no host sync: the at-rest chunks are settled on first access
         enc, _, pend = codec.encode_batch_deferred(torch.stack([xk, xv]), self.bits)
-        ek, ev = enc.select(0), enc.select(1)
-        for i, (res, x, e) in enumerate(((self.res_k, xk, ek), (self.res_v, xv, ev))):
+        s32, s16 = enc.scale32.view(2, -1), enc.scale16.view(2, -1)   # the K and V chunks' head scales
+        for i, (res, x) in enumerate(((self.res_k, xk), (self.res_v, xv))):
             r = res[layer_idx]
             if r is None:
                 r = ResidentKV(B * H, max(4 * n, 1024), device=x.device)
                 res[layer_idx] = r
             elif r.n_tokens + n > r.cap_blocks * RB:
                 r.reserve(max(2 * r.cap_blocks * RB, r.n_tokens + n))
-            r.append(x, e.scale32, e.scale16)
+            r.append(x, s32[i], s16[i])
         self.chunks[layer_idx].append((_AtRest(pend, 0), _AtRest(pend, 1)))
         self.tail_k[layer_idx] = tk[:, :, n:].contiguous()
         self.tail_v[layer_idx] = tv[:, :, n:].contiguous()
