@@ -240,3 +240,41 @@ def test_resident_attention_long_prefix_split_cap_gpu():
     ref = torch.matmul(torch.softmax(s, -1), V)
     err = ((out - ref).abs().amax(1) / ref.abs().amax(1)).max().item()
     assert err <= 1e-3, err
+
+
+def test_resident_small_appends_without_host_reads_gpu():
+    """Appends of at most ASYNC_MAX_VECTORS vectors read no count back: the
+    exception list grows ahead of the host's upper bound of the count (the
+    last count read through a pinned copy, plus every vector appended since).
+    Many 16-token appends of heavy-tailed data, starting from a one-entry
+    list, leave the same records, exception list, scales and dequantised
+    values as one large append of the same tokens (which reads the count
+    back), and the oracle's values."""
+    from latticequant_amd.llm.resident import ResidentKV
+    H, n, T = 4, 12, 16
+    x = _data((1, H, n * T, 128), 41, "outliers")
+    ch = O.compress_chunk(x[0].numpy()[None], 4)
+    s32 = torch.from_numpy(ch.scales_f32)
+    s16 = torch.from_numpy(ch.scales.astype(np.float16))
+    xc = x.cuda()
+    small = ResidentKV(H, n * T, device="cuda", exc_cap=1)
+    assert H * T * 16 <= small.ASYNC_MAX_VECTORS
+    for i in range(n):
+        small.append(xc[:, :, i * T:(i + 1) * T], s32, s16)
+    big = ResidentKV(H, n * T, device="cuda", exc_cap=1)
+    big.ASYNC_MAX_VECTORS = 0   # the read-back path for every append
+    big.append(xc, s32, s16)
+    torch.cuda.synchronize()
+    ne = int(small.n_exc.item())
+    assert ne == int(big.n_exc.item()) > 0 and small.exc_cap >= ne
+    assert int(small.status.item()) == 0 and int(big.status.item()) == 0
+    # records, exception masks and scales are placed per block; the list
+    # order of the exceptions (and so the offsets in the meta words) follows
+    # the order in which workgroups reserve their slots, so the exceptions are
+    # compared through the dequantised values
+    for name in ("a", "b", "mask", "scale"):
+        assert torch.equal(getattr(small, name), getattr(big, name)), name
+    assert torch.equal(small.dequant(), big.dequant())
+    got = small.dequant().cpu().numpy()
+    ref = O.decompress_chunk(ch).reshape(H, n * T, 128)
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
