@@ -2,7 +2,7 @@
 lq_chunk_decode_rht) against the materialised rotation (lq_rht, then the
 plain codec) and the oracle: the same fp32 scales, coset bits and stream
 words, and the same decoded rows in every output dtype.  Cases: head_dim
-128 / 64 / 32, with and without dither, heads whose vector count is not a
+128 / 64 / 32, fp16 and bf16 rows, with and without dither, heads whose vector count is not a
 multiple of the 512-vector block (rows and heads cross block boundaries),
 heads of fewer than 512 vectors (the quantizer's general launch), and rows
 and heads outside the five-operation division's range (IEEE division)."""
@@ -30,13 +30,15 @@ CASES = [((2, 2, 3, 64, 128), True), ((1, 2, 2, 40, 128), True), ((2, 1, 4, 96, 
          ((2, 1, 3, 24, 128), True), ((1, 2, 5, 12, 64), False)]   # heads below 512 vectors
 
 
-@pytest.mark.parametrize("shape,dither", CASES)
-def test_fused_rotation_matches_materialised_and_oracle_gpu(shape, dither):
+@pytest.mark.parametrize("shape,dither,dtype", [(s, d, torch.float16) for s, d in CASES] +
+                         [((1, 2, 2, 40, 128), True, torch.bfloat16), ((2, 1, 3, 24, 128), False, torch.bfloat16),
+                          ((1, 1, 2, 64, 64), True, torch.bfloat16)])
+def test_fused_rotation_matches_materialised_and_oracle_gpu(shape, dither, dtype):
     from latticequant_amd import codec
     from latticequant_amd.llm import rotated as R
     C, B, H, T, hd = shape
-    print(f"case {shape} dither={dither}", flush=True)
-    x = torch.randn(*shape, generator=torch.Generator().manual_seed(T + hd)).half()
+    print(f"case {shape} dither={dither} {dtype}", flush=True)
+    x = torch.randn(*shape, generator=torch.Generator().manual_seed(T + hd)).to(dtype)
     layers, kvs = list(range(3, 3 + C)), [c & 1 for c in range(C)]
     signs = R.chunk_signs(x.shape, layers, kvs).cuda()
     seeds = [R.default_dither_seed(l, k) for l, k in zip(layers, kvs)] if dither else None
