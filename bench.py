@@ -820,8 +820,10 @@ def summarize_trace(trace_csv, top=16):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=5)
-    ap.add_argument("--warmup", type=int, default=2)
+    # 20 timed steps after 5 warm-up steps: shorter runs read the first steps
+    # of a cold GPU (clocks still ramping: 2.02 against 1.90 ms per C2 step)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--group", type=int, default=64, help="chunks per kernel launch in the timed step")
     ap.add_argument("--streams", type=int, default=1,
                     help="streams the chunk groups of a step are dealt to (measured: one 64-chunk group on one "

@@ -356,6 +356,7 @@ __global__ __launch_bounds__(kQThreads, ROT ? 5 : (LEAN ? 7 : 1)) void k_chunk_q
                     for (int i = 0; i < 8; i++) t[i] = t[i] + dd[i];
                 }
                 int c;
+                float tm;   // max(1, max |t_i|)
                 if constexpr (ROT) {
                     // the rotation is cross-lane, so the rare exact path cannot
                     // recompute t in a divergent branch: t waits in the lane's
@@ -368,7 +369,7 @@ __global__ __launch_bounds__(kQThreads, ROT ? 5 : (LEAN ? 7 : 1)) void k_chunk_q
                         const float4 a = slot[0], b = slot[1];
                         tt[0] = a.x; tt[1] = a.y; tt[2] = a.z; tt[3] = a.w;
                         tt[4] = b.x; tt[5] = b.y; tt[6] = b.z; tt[7] = b.w;
-                    });
+                    }, &tm);
                 } else {               // the rare exact path recomputes t from x
                     c = e8_nearest_fast(t, ic, [&](float tt[8]) {
                         float xx[8];
@@ -381,22 +382,31 @@ __global__ __launch_bounds__(kQThreads, ROT ? 5 : (LEAN ? 7 : 1)) void k_chunk_q
 #pragma unroll
                             for (int i = 0; i < 8; i++) tt[i] = tt[i] + d2[i];
                         }
-                    });
+                    }, &tm);
                 }
                 cs[r] = c;
-                int32_t lo = INT_MAX, hi = INT_MIN;
 #pragma unroll
                 for (int i = 0; i < 8; i++) {
                     const int32_t iv = (int32_t)ic[i];
                     sy[r][i] = i < 7 ? iv : (iv >> 1);
-                    lo = min(lo, sy[r][i]);
-                    hi = max(hi, sy[r][i]);
                 }
-                // out-of-range symbols are flagged and clamped (histogram indices stay in range)
-                if (lo < kSymMin || hi > kSymMax) {
-                    flag = 1;
+                // max |t_i| < kSymMax - 1 puts every coordinate in
+                // [-kSymMax, kSymMax] (e8_nearest_fast), so the symbols are in
+                // range; only vectors with a larger (or infinite) |t_i| are
+                // checked.  Out-of-range symbols are flagged and clamped
+                // (histogram indices stay in range).
+                if (!(tm < (float)(kSymMax - 1))) {
+                    int32_t lo = INT_MAX, hi = INT_MIN;
 #pragma unroll
-                    for (int i = 0; i < 8; i++) sy[r][i] = min(max(sy[r][i], kSymMin), kSymMax);
+                    for (int i = 0; i < 8; i++) {
+                        lo = min(lo, sy[r][i]);
+                        hi = max(hi, sy[r][i]);
+                    }
+                    if (lo < kSymMin || hi > kSymMax) {
+                        flag = 1;
+#pragma unroll
+                        for (int i = 0; i < 8; i++) sy[r][i] = min(max(sy[r][i], kSymMin), kSymMax);
+                    }
                 }
                 if (!LEAN && !ROT && deq) {
                     float off = c ? 0.5f : 0.f, y[8];

@@ -274,9 +274,14 @@ __host__ __device__ __forceinline__ bool e8_choose_exact(const float x[8], const
 }
 
 // reload(float x[8]) writes x again for the rare exact path, so that x need
-// not stay live through the common path.
+// not stay live through the common path.  tmax (optional) receives
+// max(1, max_i |x_i|) (NaN coordinates ignored).  When tmax < T for an
+// integer T, every returned coordinate lies in [-(T + 1), T + 1]: rint(x_i)
+// lies in [-T, T], rint(x_i - 1/2) in [-T, T - 1], and a flip adds +-1.
+// Callers can skip the range checks of their symbols then.
 template <typename Reload>
-__host__ __device__ __forceinline__ int e8_nearest_fast(const float x[8], float ic[8], Reload&& reload) {
+__host__ __device__ __forceinline__ int e8_nearest_fast(const float x[8], float ic[8], Reload&& reload,
+                                                        float* tmax = nullptr) {
     D8Half a, b;
     d8_half<true>(x, a);
     float y[8];
@@ -300,6 +305,7 @@ __host__ __device__ __forceinline__ int e8_nearest_fast(const float x[8], float 
         reload(xr);
         use1 = e8_choose_exact(xr, a, b, fa, fb);
     }
+    if (tmax) *tmax = t;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const float ca = a.r[i] + (a.sel[i] ? fa : 0.f);
