@@ -543,14 +543,58 @@ __device__ __forceinline__ void dither8(uint64_t key, int64_t v, float d[8]) {
 
 // ---------------------------------------------------------------- rANS ---
 
-__device__ __forceinline__ uint32_t enc_pack(uint32_t f, uint32_t cum) {
-    uint32_t bl = 32u - (uint32_t)__clz((int)f);   // bit length of f
+__host__ __device__ __forceinline__ uint32_t enc_pack(uint32_t f, uint32_t cum) {
+    const uint32_t bl = f ? 32u - (uint32_t)__builtin_clz(f) : 0u;   // bit length of f
     uint32_t nb = 11u - bl;
     return f | (cum << 11) | (nb << 21);
 }
-__device__ __forceinline__ uint32_t enc_f(uint32_t e) { return e & 0x7ffu; }
-__device__ __forceinline__ uint32_t enc_c(uint32_t e) { return (e >> 11) & 0x3ffu; }
-__device__ __forceinline__ uint32_t enc_nb(uint32_t e) { return (e >> 21) & 0xfu; }
+__host__ __device__ __forceinline__ uint32_t enc_f(uint32_t e) { return e & 0x7ffu; }
+__host__ __device__ __forceinline__ uint32_t enc_c(uint32_t e) { return (e >> 11) & 0x3ffu; }
+__host__ __device__ __forceinline__ uint32_t enc_nb(uint32_t e) { return (e >> 21) & 0xfu; }
+
+// Encoder table entry of the parallel chunk encoder, for the reference's
+// step (core/gpu_ans.py:124-128: shift x right, emitting its low bits, while
+// x >= 2 f, then x = L (x // f) + cum + x % f): F | base << 16, with
+// nb = 11 - bitlen(f), thr = f << nb (the renormalisation threshold, in
+// [L, 2L)),
+// F = nb * 2^11 - thr (as int16) and base = L + cum - f (< 2^11).  A step on a
+// state x in [L, 2L) is
+//   k = nb - 1 + (x >= thr) = (x + F) >> 11;   x = (x >> k) + base
+// (x - thr lies in (-2^11, 2^11), so the shift leaves nb - 1 or nb), and
+// each half-word is read in place: two instructions for k instead of a
+// field extract, a compare and an add with carry.  F is sign-extended, so a
+// single-symbol table (f = L, nb = 0) steps too: k = 0, x unchanged.
+__host__ __device__ __forceinline__ uint32_t encx_of(uint32_t e) {
+    const uint32_t f = enc_f(e), c = enc_c(e), nb = enc_nb(e);
+    const int32_t F = (int32_t)(nb << 11) - (int32_t)(f << nb);
+    return ((uint32_t)F & 0xffffu) | (((uint32_t)kL + c - f) << 16);
+}
+__host__ __device__ __forceinline__ uint32_t encx_k(uint32_t x, uint32_t e) {
+    return (uint32_t)((int32_t)x + (int32_t)(int16_t)(e & 0xffffu)) >> 11;
+}
+__host__ __device__ __forceinline__ uint32_t encx_step(uint32_t x, uint32_t e, uint32_t* k_out) {
+    const uint32_t k = encx_k(x, e);
+    *k_out = k;
+    return (x >> k) + (e >> 16);
+}
+
+// Interval step: every state in [lo, hi] encodes the symbol; the image is
+// exact when the interval lies on one side of the renormalisation threshold
+// (both ends take the same k), otherwise the whole image range of the
+// symbol: (x >> k) covers [f, 2f), with nb = k of the upper end and
+// f = thr >> nb = ((nb << 11) - F) >> nb.
+__host__ __device__ __forceinline__ void hull_step(uint32_t& lo, uint32_t& hi, uint32_t e) {
+    const uint32_t klo = encx_k(lo, e), khi = encx_k(hi, e), base = e >> 16;
+    if (klo == khi) {
+        lo = (lo >> klo) + base;
+        hi = (hi >> klo) + base;
+    } else {
+        const uint32_t thr = (uint32_t)((int32_t)(khi << 11) - (int32_t)(int16_t)(e & 0xffffu));
+        const uint32_t f = thr >> khi;
+        lo = f + base;
+        hi = 2u * f - 1u + base;
+    }
+}
 
 // One encoder step (core/gpu_ans.py:124-128): k renormalisation bits leave
 // through *k / *bits (low k bits of x), then x = L + cum + (x >> k) - f.
