@@ -7,9 +7,10 @@ compared against.  Only tests/, ``__graft_entry__.smoke()`` and the
 
 It restates the reference algorithm (yoon9728/LatticeQuant) in numpy on top of
 the plain-C kernels in lq_oracle.c.  Each function names the reference
-file:line it follows.  Pinning is described in lq_oracle.c and DESIGN.md;
-everything here is additionally checked against the golden vectors under
-tests/golden/, which were written by the reference itself.
+file:line it follows.  Pinning is described in lq_oracle.c; everything here
+is additionally checked against the golden vectors under tests/golden/,
+which were written by the reference itself, and against closed forms,
+brute force and invariants (tests/test_oracle.py).
 
 Parity notes
   * torch.round is round-half-even, argmin takes the first index, torch's CPU

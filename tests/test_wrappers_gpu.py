@@ -1,6 +1,7 @@
-"""GPU parity of the public module-level entry points that INTEGRATION.md
-advertises as module swaps, called exactly as the reference's callers call
-them (not through the fused chunk kernels):
+"""GPU parity of the public module-level entry points that stand in for the
+reference's modules (latticequant_amd.core.*, latticequant_amd.llm.*),
+called exactly as the reference's callers call them (not through the fused
+chunk kernels):
 
 * core.e8_quantizer.quantize_e8 (core/e8_quantizer.py:90-110):
   Q_E8(x / scale) * scale in fp32, against the oracle's encode_e8 (pinned by
