@@ -232,3 +232,39 @@ def test_quantize_deq_matches_quantize_batch_gpu():
     for c in range(2):
         ch = O.compress_chunk(x[c].numpy(), 4, scales_f32=s32.view(2, -1)[c].cpu().numpy())
         np.testing.assert_array_equal(deq[c].cpu().numpy(), ch.decompressed)
+
+
+@pytest.mark.parametrize("peak", [125.6, 126.4, 127.3, 128.6])
+def test_int8_range_check_near_its_bound_gpu(peak):
+    """The quantizer checks the int8 range of a vector's symbols only when the
+    vector's max |x / scale| reaches 126 (below that every coordinate, flip
+    included, lies within +-127).  Vectors with one coordinate at +-peak times
+    its head's scale (the scale settled by iterating, since the peaks move
+    sigma^2), the rest Gaussian: at 125.6 the check is skipped with symbols
+    up to +-126, at 126.4 and 127.3 it runs with symbols up to -128 / 127 (in
+    range), at 128.6 a symbol reaches 129.  The overflow flag is set exactly
+    when the oracle's symbols leave int8, and the chunk equals the oracle's
+    when they do not."""
+    codec, L = _lq()
+    rng = np.random.default_rng(int(peak * 10))
+    x = rng.standard_normal((1, 2, 256, 128)).astype(np.float32)
+    sel = [(0, 5, 3), (0, 17, 64 + 7), (1, 40, 8 * 5 + 1), (1, 63, 127), (0, 130, 12), (1, 200, 100)]
+    for _ in range(12):
+        s = O.compress_chunk(x.astype(np.float16).astype(np.float32), 4).scales_f32
+        for k, (h, t, d) in enumerate(sel):
+            x[0, h, t, d] = (peak if k % 2 == 0 else -peak) * s[h]
+    xh = x.astype(np.float16)
+    enc, _ = codec.encode_batch(torch.from_numpy(xh).cuda()[None], 4, wide=False, exact_size=False)
+    # the oracle at the device's scales (sigma^2 sums in another order can move
+    # a scale's last bit, and with it a point near a decision boundary)
+    sc32 = enc.scale32.cpu().numpy()
+    ch = O.compress_chunk(xh.astype(np.float32), 4, scales_f32=sc32)
+    ts = [abs(float(xh[0, h, t, d]) / float(sc32[h])) for h, t, d in sel]
+    assert max(abs(t - peak) for t in ts) < 0.1
+    lo = min(st.table.alphabet[0] + 2 for st in ch.streams)    # alphabets are padded by 2 on each side
+    hi = max(st.table.alphabet[-1] - 2 for st in ch.streams)
+    over = lo < -128 or hi > 127
+    assert over == (peak > 128)
+    assert bool(int(enc.status[0]) & L.LQ_ST_SYM_OVERFLOW) == over
+    if not over:
+        _compare_chunk(enc, 0, ch)
