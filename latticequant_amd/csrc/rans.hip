@@ -517,7 +517,7 @@ __host__ __device__ inline EncWork enc_layout(int64_t n_chunks, int64_t n_vector
 constexpr int kEncBlocks = 16;   // blocks per encode workgroup (x 16 streams)
 
 // Grid: (block groups, chunks).  The scratch words of a task are collected in
-// an 8-word LDS queue and stored as aligned 32-byte pieces.
+// a 4-word LDS queue per lane and stored as aligned 16-byte pieces.
 template <typename SymT>
 __global__ __launch_bounds__(256) void k_chunk_encode(const SymT* __restrict__ sym, const uint32_t* __restrict__ blk_n1,
                                                       int64_t nblk, int64_t V, const lq_table* __restrict__ tables,
