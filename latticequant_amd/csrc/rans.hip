@@ -1005,8 +1005,11 @@ __global__ __launch_bounds__(256) void k_chunk_lut(const lq_table* __restrict__ 
 // coset bitmap per symbol.  After each phase the block's 16 lanes flush the
 // output in whole 128-byte lines (8 vectors): a line is flushed once both
 // cosets have staged every vector in it; a flushed vector's rank in its coset
-// is the flushed count plus a popcount of the coset-1 bitmap below it.  Each
-// flush round writes up to 16 consecutive vectors (256 bytes) of a block.
+// is the flushed count plus a popcount of the coset-1 bitmap below it.  A
+// phase flushes at most two lines (16 consecutive vectors, 256 bytes, one
+// per lane of the block's row): a second round for lines 3 and 4 left most
+// of its lanes idle and cost more than the extra phases the cap adds (the
+// first flushable line is always taken, so the cap never stalls the loop).
 // A coset runs a phase only if the 8 vectors it stages fit the ring next to
 // its unflushed ones (st - flushed <= 8).  That never blocks for good: the
 // first unflushed line holds at most 8 vectors of each coset, so a coset
@@ -1138,7 +1141,7 @@ __global__ __launch_bounds__(kDecThreads) void k_chunk_decode(
     const uint64_t dkey = DITHER ? mix64((uint64_t)dseed[chunk]) : 0u;
     const uint32_t* const bmr = bm1[b];
     uint16_t* const my_stg = &stg[(b * 2 + c) * kDecGroupU16 + idx];
-    const int u = (l16 & 3) + 1;     // lines of the flush candidate this lane checks
+    const int u = (l16 & 1) + 1;     // lines of the flush candidate this lane checks
 
     float pend[ROT ? 8 : 1];         // ROT: butterfly stages of a deferred first half-row (lanes 0..7)
     int st = 0;                      // vectors of my coset staged (symbols of my stream decoded)
@@ -1157,18 +1160,18 @@ __global__ __launch_bounds__(kDecThreads) void k_chunk_decode(
         __builtin_amdgcn_wave_barrier();
         const int st_o = dpp_ror8(st);
         const int s0 = c ? st_o : st, s1 = c ? st : st_o;
-        // coset-1 bits of positions fpos .. fpos + 31; lanes 0..3 of the block's
-        // row check whether the first 1..4 lines can be flushed (the answers are
-        // monotone, so their count is the number of flushable lines)
+        // coset-1 bits of positions fpos .. fpos + 31; lanes 0 and 1 of the
+        // block's row check whether the first 1 and 2 lines can be flushed (the
+        // answers are monotone, so their count is the number of lines flushed)
         const int wi = fpos >> 5;
         const uint32_t W = __builtin_amdgcn_alignbit(bmr[wi + 1], bmr[wi], (uint32_t)(fpos & 31));
         const int rest = valid - fpos;
-        const int np = rest < 8 * u ? rest : 8 * u;                  // 1 <= np <= 32
+        const int np = rest < 8 * u ? rest : 8 * u;                  // 1 <= np <= 16
         const int p1 = __builtin_popcount(W << ((32 - np) & 31));   // coset-1 vectors among them
         const bool ok = 8 * (u - 1) < rest && fr0 + np - p1 <= s0 && fr1 + p1 <= s1;
         const uint64_t bal = __builtin_amdgcn_ballot_w64(ok);
-        const int nl = __builtin_popcountll((bal >> (tid & 48)) & 0xfull);
-        const int F = 8 * nl < rest ? 8 * nl : rest;   // positions flushed this phase (<= 32)
+        const int nl = __builtin_popcountll((bal >> (tid & 48)) & 0x3ull);   // 0, 1 or 2 lines
+        const int F = 8 * nl < rest ? 8 * nl : rest;   // positions flushed this phase (<= 16)
         // fp32 output row of position p (fpos <= p < fpos + F): the lattice
         // point from its staged symbols, dither removed, times the head's scale
         auto lattice_y = [&](int p, float y[8]) {
@@ -1272,7 +1275,7 @@ __global__ __launch_bounds__(kDecThreads) void k_chunk_decode(
                 }
             }
         }
-        const int f1 = __builtin_popcount(W) - __builtin_popcount((uint32_t)((uint64_t)W >> F));   // 0 <= F <= 32
+        const int f1 = __builtin_popcount(W) - __builtin_popcount((uint32_t)((uint64_t)W >> F));   // 0 <= F <= 16
         fr1 += f1;
         fr0 += F - f1;
         fpos += F;
