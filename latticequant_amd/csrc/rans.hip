@@ -1170,7 +1170,12 @@ __global__ __launch_bounds__(kDecThreads) void k_chunk_decode(
         const int p1 = __builtin_popcount(W << ((32 - np) & 31));   // coset-1 vectors among them
         const bool ok = 8 * (u - 1) < rest && fr0 + np - p1 <= s0 && fr1 + p1 <= s1;
         const uint64_t bal = __builtin_amdgcn_ballot_w64(ok);
-        const int nl = __builtin_popcountll((bal >> (tid & 48)) & 0x3ull);   // 0, 1 or 2 lines
+        int nl = __builtin_popcountll((bal >> (tid & 48)) & 0x3ull);   // 0, 1 or 2 lines
+        // ROT: a flush that starts in the middle of a 16-vector row takes one
+        // line, the row's second half, so the next flushes start on a row
+        // again (a 16-vector flush from the middle of a row runs the
+        // butterflies of two rows for one row's stores)
+        if (ROT && (fpos & 8) && nl > 1) nl = 1;
         const int F = 8 * nl < rest ? 8 * nl : rest;   // positions flushed this phase (<= 16)
         // fp32 output row of position p (fpos <= p < fpos + F): the lattice
         // point from its staged symbols, dither removed, times the head's scale
