@@ -469,9 +469,10 @@ __device__ __forceinline__ Col<SymT> column(const SymT* sym, const uint32_t* blk
 // chunk ahead.  b is the symbol's index in its chunk (a compile-time
 // constant after unrolling).  Only a column's top chunk can be partial.
 // Control flow is wave-uniform: the loop runs while any lane has chunks left,
-// takes the unconditional path when every lane holds a full chunk and
-// otherwise passes a per-lane predicate; f must leave its state unchanged
-// when in == false.
+// takes the unconditional path when every lane holds a full chunk, the same
+// path with finished lanes masked off when every lane holds a full chunk or
+// none, and otherwise passes a per-lane predicate; f must leave its state
+// unchanged when in == false.
 template <typename SymT, typename F>
 __device__ __forceinline__ void for_each_rev(const SymT* p, int n, F&& f) {
     int k = n > 0 ? (n - 1) >> 4 : -1;   // current chunk
@@ -483,6 +484,14 @@ __device__ __forceinline__ void for_each_rev(const SymT* p, int n, F&& f) {
         if (__all(hi_b == 16)) {
 #pragma unroll
             for (int b = 15; b >= 0; b--) f(cur.get(b), b, true);
+        } else if (__all(hi_b == 16 || hi_b == 0)) {
+            // every lane holds a full chunk or has none left (the columns of a
+            // wave end at different chunks): the full path, finished lanes
+            // masked off
+            if (hi_b == 16) {
+#pragma unroll
+                for (int b = 15; b >= 0; b--) f(cur.get(b), b, true);
+            }
         } else {
 #pragma unroll
             for (int b = 15; b >= 0; b--) f(cur.get(b), b, b < hi_b);
