@@ -840,8 +840,12 @@ __global__ void k_chunk_offsets(const int64_t* __restrict__ stream_nbits, const 
 // words whose first bit lies in its blocks' bit range; lane l assembles words
 // W0 + l + 64 k, kPackU per round with all their scratch loads in flight
 // (256-byte coalesced stores).  A word's first bits come from the
-// right-aligned scratch of the block holding its first bit; the rare word
-// that runs past that block's end continues block by block.  The block of
+// right-aligned scratch of the block holding its first bit (one funnel
+// shift), the rest, when the word runs past that block's end, from the first
+// bits of the next block (loaded only in those lanes, merged with a select);
+// the rare word that also runs past that block, or is the stream's last and
+// partly past its end, is assembled block by block.  Scratch and output words
+// are addressed with 32-bit byte offsets from wave-uniform bases.  The block of
 // each word comes from the blocks' first owned words fw_i = ceil(off_i / 32),
 // held one per lane: within a 64-word slice, the block of word w is the last
 // block with fw_i <= w, i.e. the last block starting at or before the slice
@@ -884,10 +888,16 @@ __global__ __launch_bounds__(256) void k_chunk_pack(int64_t n_streams_total, int
     if (g0 + nb >= nblk && lane == 0) out[((uint64_t)nbits + 31u) >> 5] = 0u;
     const uint32_t* scr0 = scratch + (sid * nblk + g0) * (int64_t)kCapW;
     constexpr uint32_t kCapBits = (uint32_t)kCapW * 32u;
+    // scratch word i of the group (i < (nb + 1) * kCapW), as a 32-bit byte
+    // offset from the wave-uniform base; likewise the stream's output words
+    auto scr = [&](uint32_t i) -> uint32_t {
+        return *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(scr0) + (i << 2));
+    };
     for (uint32_t wr = W0; wr < W1; wr += 64u * kPackU) {
         uint32_t lo[kPackU], hi[kPackU], clo[kPackU], chi[kPackU];
         int blk[kPackU], take[kPackU], s2[kPackU], cs[kPackU];
-        uint32_t pe[kPackU], nx[kPackU];   // bit after the word's first segment; end of the next block
+        uint32_t pe[kPackU];
+        bool nxt[kPackU], rare[kPackU];
 #pragma unroll
         for (int u = 0; u < kPackU; u++) {
             const uint32_t ws = wr + 64u * u;   // first word of the slice (wave-uniform)
@@ -909,47 +919,53 @@ __global__ __launch_bounds__(256) void k_chunk_pack(int64_t n_streams_total, int
             const uint32_t end = p + 32u < nbits ? p + 32u : nbits;
             const uint32_t e1 = end < oe ? end : oe;
             const uint32_t sp = kCapBits - (oe - ob) + (p - ob);   // scratch bit of p
-            const uint32_t* sc = scr0 + (int64_t)b * kCapW;
             const uint32_t k0 = sp >> 5;
-            lo[u] = sc[k0];
-            hi[u] = sc[k0 + 1 < (uint32_t)kCapW ? k0 + 1 : k0];
+            const uint32_t i0 = (uint32_t)b * (uint32_t)kCapW + k0;
+            lo[u] = scr(i0);
+            hi[u] = scr(k0 + 1 < (uint32_t)kCapW ? i0 + 1 : i0);
             // a word running past its block's end continues with the first bits
-            // of block b + 1: load them now, in the lanes that need them
+            // of block b + 1 (when that block is not empty): load them in the
+            // lanes that need them; they are consumed unconditionally below, so
+            // no load is left pending into the next round
             const uint32_t sp1 = kCapBits - (on - oe);            // scratch bit of block b + 1's first bit
+            const uint32_t k1 = sp1 >> 5;
+            const bool cont = ok && e1 < end;
+            nxt[u] = cont && on > oe;
             clo[u] = 0u;
             chi[u] = 0u;
-            if (ok && e1 < end && on > oe) {
-                const uint32_t* sc1 = sc + kCapW;
-                const uint32_t k1 = sp1 >> 5;
-                clo[u] = sc1[k1];
-                chi[u] = sc1[k1 + 1 < (uint32_t)kCapW ? k1 + 1 : k1];
+            if (nxt[u]) {
+                const uint32_t i1 = (uint32_t)(b + 1) * (uint32_t)kCapW + k1;
+                clo[u] = scr(i1);
+                chi[u] = scr(k1 + 1 < (uint32_t)kCapW ? i1 + 1 : i1);
             }
+            const uint32_t e2 = end < on ? end : on;
+            // rare: block b + 1 is empty, ends inside the word too, or the word
+            // is the stream's last and partly past its end (its unused bits
+            // must be zero); otherwise the two segments fill all 32 bits
+            rare[u] = cont && e2 != p + 32u;
             blk[u] = b;
-            take[u] = (int)(e1 - p);
+            take[u] = (int)(e1 - p);   // 1 .. 32
             s2[u] = (int)(sp & 31u);
             cs[u] = (int)(sp1 & 31u);
             pe[u] = e1;
-            nx[u] = on;
         }
 #pragma unroll
         for (int u = 0; u < kPackU; u++) {
             const uint32_t w = wr + 64u * u + lane;
-            if (w >= W1) continue;
-            uint64_t v = ((uint64_t)hi[u] << 32 | lo[u]) >> s2[u];
-            int got = take[u];
-            uint32_t res = got == 32 ? (uint32_t)v : (uint32_t)v & ((1u << got) - 1u);
-            uint32_t p = pe[u];
-            const uint32_t end = 32u * w + 32u < nbits ? 32u * w + 32u : nbits;
-            if (p < end) {
-                // block b + 1 (its first bits were loaded above when it is not empty)
-                const uint32_t e2 = end < nx[u] ? end : nx[u];
-                const int tk = (int)(e2 - p);
-                const uint64_t x = ((uint64_t)chi[u] << 32 | clo[u]) >> cs[u];
-                res |= (tk == 32 ? (uint32_t)x : (uint32_t)x & ((1u << tk) - 1u)) << got;
-                got += tk;
-                p = e2;
-                int b = blk[u] + 2;
-                while (p < end) {   // rare: block b + 1 ends inside the word too
+            const int got = take[u];
+            uint32_t res = __builtin_amdgcn_alignbit(hi[u], lo[u], (uint32_t)s2[u]) & (0xffffffffu >> ((32 - got) & 31));
+            // the next block's first bits fill the rest of the word (got < 32 there)
+            const uint32_t seg2 = __builtin_amdgcn_alignbit(chi[u], clo[u], (uint32_t)cs[u]) << (got & 31);
+            res |= nxt[u] ? seg2 : 0u;
+            if (rare[u]) {
+                // block by block from block b + 1: empty blocks are skipped,
+                // a block ending inside the word gives only its bits
+                res &= 0xffffffffu >> ((32 - got) & 31);
+                const uint32_t end = 32u * w + 32u < nbits ? 32u * w + 32u : nbits;
+                uint32_t p = pe[u];
+                int gb = got;
+                int b = blk[u] + 1;
+                while (p < end) {
                     const uint32_t ob = off_at(b), oe = off_at(b + 1);
                     if (oe > ob) {
                         const uint32_t e1 = end < oe ? end : oe;
@@ -959,14 +975,14 @@ __global__ __launch_bounds__(256) void k_chunk_pack(int64_t n_streams_total, int
                         uint64_t y = sc[sp >> 5];
                         if ((int)(sp & 31u) + tk2 > 32) y |= (uint64_t)sc[(sp >> 5) + 1] << 32;
                         y >>= (sp & 31u);
-                        res |= (tk2 == 32 ? (uint32_t)y : (uint32_t)y & ((1u << tk2) - 1u)) << got;
-                        got += tk2;
+                        res |= (tk2 == 32 ? (uint32_t)y : (uint32_t)y & ((1u << tk2) - 1u)) << gb;
+                        gb += tk2;
                         p = e1;
                     }
                     b++;
                 }
             }
-            out[w] = res;
+            if (w < W1) *reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(out) + (w << 2)) = res;
         }
     }
 }
