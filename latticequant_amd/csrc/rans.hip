@@ -686,7 +686,22 @@ __global__ __launch_bounds__(256) void k_chunk_encode(const SymT* __restrict__ s
 // scan plus the running carry), n_bits and final state; then the chunk's word
 // offsets (n_words + 1 words per present stream) and total.  Replaces
 // k_chunk_scan + k_chunk_offsets for such batches.
-constexpr int kScanRounds = 16;   // rounds of 64 blocks whose loads are in flight together
+constexpr int kScanRounds = 32;   // rounds of 64 blocks whose loads are in flight together
+
+// Inclusive scan over the 64 lanes of a wave in DPP moves: Hillis-Steele
+// within each 16-lane row (row_shr 1, 2, 4, 8; lanes shifted in from outside
+// the row read 0), then row 0's last lane added to row 1 and row 2's to row 3
+// (row_bcast:15), then lane 31 added to rows 2 and 3 (row_bcast:31).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
+    int v = (int)x;
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);   // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);   // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);   // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);   // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15, rows 1 and 3
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31, rows 2 and 3
+    return (uint32_t)v;
+}
 
 __global__ __launch_bounds__(1024) void k_chunk_scan_offsets(const uint32_t* __restrict__ blk_bits,
                                                              const uint16_t* __restrict__ blk_state,
@@ -713,15 +728,10 @@ __global__ __launch_bounds__(1024) void k_chunk_scan_offsets(const uint32_t* __r
         }
 #pragma unroll
         for (int k = 0; k < kScanRounds; k++) {
-            uint32_t x = v[k];   // inclusive wave scan (counts < 2^13, sums < 2^19)
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const uint32_t y = __shfl_up(x, o, 64);
-                x += lane >= o ? y : 0u;
-            }
+            const uint32_t x = wave_incl_scan(v[k]);   // counts < 2^13, sums < 2^19
             const int64_t b = r0 + 64 * k + lane;
             if (b < nblk) bo[b] = (uint32_t)(carry + x - v[k]);
-            carry += (uint32_t)__shfl(x, 63, 64);
+            carry += (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
         }
     }
     if (lane == 0) {
